@@ -1,0 +1,123 @@
+"""ctypes binding of libmi_ops.so (the C ABI in include/mi_ops.h).
+
+The shared library is built in-tree (``make -C hbd-acestep.cpp_amd``) and is
+the only compute path: if it cannot be loaded, importing this module raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.normpath(os.path.join(_PKG_DIR, "..", "lib"))
+LIB_PATH = os.environ.get("MI_OPS_LIB", os.path.join(LIB_DIR, "libmi_ops.so"))
+
+# enum mi_type (values equal enum ggml_type)
+F32, F16, Q8_0, I32, BF16 = 0, 1, 8, 26, 30
+# enum mi_q8_0_rounding
+Q8_0_CPU_X86, Q8_0_REF = 0, 1
+
+STATUS = {
+    0: "MI_OK",
+    -1: "MI_ERR_NULL",
+    -2: "MI_ERR_TYPE",
+    -3: "MI_ERR_SHAPE",
+    -4: "MI_ERR_STRIDE",
+    -5: "MI_ERR_ALIGN",
+    -6: "MI_ERR_PARAM",
+    -7: "MI_ERR_UNSUPPORTED",
+    -8: "MI_ERR_HIP",
+}
+
+
+class MiTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("type", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nb", ctypes.c_uint64 * 4),
+    ]
+
+
+_TP = ctypes.POINTER(MiTensor)
+_VP = ctypes.c_void_p
+_F = ctypes.c_float
+_I = ctypes.c_int
+
+
+class MiDitBlockIO(ctypes.Structure):
+    _fields_ = [(n, MiTensor) for n in (
+        "hidden", "adaln", "sa_norm_w", "ffn_norm_w", "norm_sa",
+        "q", "k", "q_w", "k_w", "q_out", "k_out", "pos",
+        "sa_out", "ca_norm_w", "norm_ca", "ca_q", "ca_q_w", "ca_q_out", "ca_out",
+        "norm_ffn", "gate_up", "ff", "ffn_out")] + [
+        ("eps", ctypes.c_float), ("rope_freq_base", ctypes.c_float),
+        ("n_dims", ctypes.c_int), ("use_cross_attn", ctypes.c_int)]
+
+
+class MiQwen3LayerIO(ctypes.Structure):
+    _fields_ = [(n, MiTensor) for n in (
+        "hidden", "in_norm_w", "post_norm_w", "norm", "norm2",
+        "q", "k", "v", "q_w", "k_w", "q_out", "k_out", "pos",
+        "k_cache", "v_cache", "pos0", "sets", "attn_out", "gate_up", "ff", "mlp_out")] + [
+        ("eps", ctypes.c_float), ("rope_freq_base", ctypes.c_float), ("n_dims", ctypes.c_int),
+        ("clamp_fp16", ctypes.c_int), ("kv_rounding", ctypes.c_int), ("d_err", ctypes.c_void_p)]
+
+
+# name -> argtypes, exactly the prototypes of include/mi_ops.h
+PROTOTYPES = {
+    "mi_abi_version": [],
+    "mi_status_str": [_I],
+    "mi_rms_norm": [_TP, _TP, _F, _TP, _VP],
+    "mi_rms_norm_modulate": [_TP, _TP, _TP, _TP, _F, _TP, _VP],
+    "mi_rope_ext": [_TP, _TP, _I, _I, _F, _F, _F, _F, _TP, _VP],
+    "mi_qk_norm_rope": [_TP, _TP, _TP, _TP, _TP, _TP, _TP, _F, _I, _F, _F, _F, _VP],
+    "mi_swiglu": [_TP, _I, _TP, _VP],
+    "mi_swiglu_split": [_TP, _TP, _TP, _VP],
+    "mi_add": [_TP, _TP, _TP, _VP],
+    "mi_mul": [_TP, _TP, _TP, _VP],
+    "mi_add_clamp": [_TP, _TP, _F, _F, _TP, _VP],
+    "mi_gated_add": [_TP, _TP, _TP, _TP, _VP],
+    "mi_modulate": [_TP, _TP, _TP, _TP, _VP],
+    "mi_get_rows": [_TP, _TP, _TP, _VP, _VP],
+    "mi_cpy": [_TP, _TP, _VP],
+    "mi_cpy_q8_0": [_TP, _TP, _I, _VP],
+    "mi_kv_store": [_TP, _TP, _TP, _TP, _TP, _TP, _I, _VP, _VP],
+    "mi_timestep_embedding": [_TP, _I, _I, _TP, _VP],
+    "mi_dit_block_ops": [ctypes.POINTER(MiDitBlockIO), _VP],
+    "mi_qwen3_layer_ops": [ctypes.POINTER(MiQwen3LayerIO), _VP],
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libmi_ops.so; raise if it is missing (no fallback path exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"libmi_ops.so not found at {LIB_PATH}; build it with `make -C hbd-acestep.cpp_amd` "
+                          "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, argtypes in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    lib.mi_status_str.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+class MiError(RuntimeError):
+    def __init__(self, fn: str, rc: int):
+        msg = load().mi_status_str(rc).decode()
+        super().__init__(f"{fn} failed: {STATUS.get(rc, rc)} ({msg})")
+        self.rc = rc
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        raise MiError(name, rc)

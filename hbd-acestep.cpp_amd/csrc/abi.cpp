@@ -1,0 +1,582 @@
+// abi.cpp -- the extern "C" entry points declared in include/mi_ops.h.
+//
+// Every entry validates its descriptors on the host (types, shapes, strides,
+// alignment, scalar parameters) with the shape rules of the ggml op it
+// replaces, returns a negative mi_status instead of asserting, and only then
+// launches on the caller's stream. Nothing here allocates or synchronizes.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+
+#include "launch.h"
+
+namespace mi {
+
+int num_cus() {
+    static std::atomic<int> cache[64];
+    int                     dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        return 256;
+    }
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) {
+            v = 256;
+        }
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+namespace {
+
+constexpr int64_t kMaxRows = (int64_t) 1 << 31;
+
+// Common descriptor checks. `inner` requires nb[0] == element (block) size.
+int check(const mi_tensor * t, bool inner = true) {
+    if (!t) {
+        return MI_ERR_NULL;
+    }
+    if (t->reserved != 0) {
+        return MI_ERR_PARAM;
+    }
+    const int es = type_size(t->type);
+    if (es == 0) {
+        return MI_ERR_TYPE;
+    }
+    for (int d = 0; d < 4; ++d) {
+        if (t->ne[d] < 0) {
+            return MI_ERR_SHAPE;
+        }
+    }
+    if (t->type == MI_TYPE_Q8_0 && t->ne[0] % 32 != 0) {
+        return MI_ERR_SHAPE;
+    }
+    if (nelements(*t) > 0 && !t->data) {
+        return MI_ERR_NULL;
+    }
+    const size_t al = t->type == MI_TYPE_Q8_0 ? 2 : (size_t) es;
+    if (!aligned(t->data, al)) {
+        return MI_ERR_ALIGN;
+    }
+    if (inner && t->ne[0] > 1 && t->nb[0] != (uint64_t) es) {
+        return MI_ERR_STRIDE;
+    }
+    for (int d = 1; d < 4; ++d) {
+        if (t->nb[d] % al != 0) {
+            return MI_ERR_ALIGN;
+        }
+    }
+    if (t->ne[0] >= kMaxRows || nrows(*t) >= kMaxRows) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    return MI_OK;
+}
+
+int check_act(const mi_tensor * t) {
+    const int rc = check(t);
+    if (rc != MI_OK) {
+        return rc;
+    }
+    return is_act(t->type) ? MI_OK : MI_ERR_TYPE;
+}
+
+// F32 [n] vector (a contiguous ggml 1-D tensor, or [n,1,1,1] view)
+int check_vec(const mi_tensor * v, int64_t n) {
+    const int rc = check(v);
+    if (rc != MI_OK) {
+        return rc;
+    }
+    if (v->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (v->ne[0] != n || v->ne[1] != 1 || v->ne[2] != 1 || v->ne[3] != 1) {
+        return MI_ERR_SHAPE;
+    }
+    return MI_OK;
+}
+
+// rows uniformly strided by nb[1] (ggml_is_contiguous_1 style flattening)
+bool uniform_rows(const mi_tensor & t) {
+    return (t.ne[2] <= 1 || t.nb[2] == t.nb[1] * (uint64_t) t.ne[1]) &&
+           (t.ne[3] <= 1 || t.nb[3] == t.nb[2] * (uint64_t) t.ne[2]);
+}
+
+bool can_repeat(const mi_tensor & b, const mi_tensor & a) {
+    for (int d = 0; d < 4; ++d) {
+        if (b.ne[d] == 0 || a.ne[d] % b.ne[d] != 0) {
+            return false;
+        }
+    }
+    return true;
+}
+
+int finish(int rc) {
+    if (rc != MI_OK) {
+        return rc;
+    }
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_HIP;
+}
+
+#define MI_TRY(expr)              \
+    do {                          \
+        const int _rc = (expr);   \
+        if (_rc != MI_OK) {       \
+            return _rc;           \
+        }                         \
+    } while (0)
+
+HeadSeg make_seg(const mi_tensor & x, const mi_tensor & y, const mi_tensor * w) {
+    HeadSeg s;
+    s.x     = (const char *) x.data;
+    s.y     = (char *) y.data;
+    s.heads = (uint32_t) x.ne[1];
+    s.xs1   = (int64_t) x.nb[1];
+    s.xs2   = (int64_t) x.nb[2];
+    s.xs3   = (int64_t) x.nb[3];
+    s.ys1   = (int64_t) y.nb[1];
+    s.ys2   = (int64_t) y.nb[2];
+    s.ys3   = (int64_t) y.nb[3];
+    s.w     = w ? (const float *) w->data : nullptr;
+    return s;
+}
+
+int binary_entry(int op, const mi_tensor * a, const mi_tensor * b, bool clamp, float lo, float hi,
+                 const mi_tensor * y, mi_stream stream) {
+    MI_TRY(check_act(a));
+    MI_TRY(check_act(y));
+    if (!same_shape(*a, *y)) {
+        return MI_ERR_SHAPE;
+    }
+    hipStream_t s = (hipStream_t) stream;
+    if (!b) {
+        return finish(launch_binary(op, *a, nullptr, nullptr, nullptr, clamp, lo, hi, *y, s));
+    }
+    MI_TRY(check_act(b));
+    if (same_shape(*a, *b)) {
+        return finish(launch_binary(op, *a, b, nullptr, nullptr, clamp, lo, hi, *y, s));
+    }
+    if (check_vec(b, a->ne[0]) == MI_OK) {
+        return finish(launch_binary(op, *a, nullptr, (const float *) b->data, nullptr, clamp, lo, hi, *y, s));
+    }
+    if (!can_repeat(*b, *a)) {
+        return MI_ERR_SHAPE;
+    }
+    return finish(launch_binary_bcast(op, *a, *b, clamp, lo, hi, *y, s));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_abi_version(void) {
+    return MI_OPS_ABI_VERSION;
+}
+
+const char * mi_status_str(int status) {
+    switch (status) {
+        case MI_OK:
+            return "ok";
+        case MI_ERR_NULL:
+            return "null tensor or data pointer";
+        case MI_ERR_TYPE:
+            return "unsupported type";
+        case MI_ERR_SHAPE:
+            return "inconsistent shapes";
+        case MI_ERR_STRIDE:
+            return "unsupported stride";
+        case MI_ERR_ALIGN:
+            return "misaligned pointer or stride";
+        case MI_ERR_PARAM:
+            return "invalid parameter";
+        case MI_ERR_UNSUPPORTED:
+            return "unsupported configuration";
+        case MI_ERR_HIP:
+            return "HIP runtime error";
+        default:
+            return "unknown status";
+    }
+}
+
+int mi_rms_norm(const mi_tensor * x, const mi_tensor * w, float eps, const mi_tensor * y, mi_stream stream) {
+    MI_TRY(check_act(x));
+    MI_TRY(check_act(y));
+    if (!same_shape(*x, *y)) {
+        return MI_ERR_SHAPE;
+    }
+    if (w) {
+        MI_TRY(check_vec(w, x->ne[0]));
+    }
+    if (!(eps >= 0.0f) || std::isinf(eps)) {
+        return MI_ERR_PARAM;
+    }
+    hipStream_t s = (hipStream_t) stream;
+    if (x->ne[0] == 64 || x->ne[0] == 128 || x->ne[0] == 256) {
+        // head-sized rows: sub-wave groups per row
+        HeadArgs a;
+        a.seg[0] = make_seg(*x, *y, w);
+        a.nseg   = 1;
+        a.ntok   = (uint32_t) (x->ne[2] * x->ne[3]);
+        a.ne2    = (uint32_t) x->ne[2];
+        a.pos    = nullptr;
+        a.theta_scale = a.freq_scale = a.mscale = 1.0f;
+        a.eps    = eps;
+        a.ne0    = (int) x->ne[0];
+        a.n_dims = (int) x->ne[0];
+        a.norm   = 1;
+        if (x->ne[1] * x->ne[2] * x->ne[3] >= kMaxRows || x->ne[1] * 4 >= kMaxRows) {
+            return MI_ERR_UNSUPPORTED;
+        }
+        return finish(launch_heads(a, x->type, y->type, s));
+    }
+    return finish(launch_rms_norm(*x, w ? (const float *) w->data : nullptr, nullptr, nullptr, eps, *y, s));
+}
+
+int mi_rms_norm_modulate(const mi_tensor * x, const mi_tensor * w, const mi_tensor * scale, const mi_tensor * shift,
+                         float eps, const mi_tensor * y, mi_stream stream) {
+    MI_TRY(check_act(x));
+    MI_TRY(check_act(y));
+    if (!same_shape(*x, *y)) {
+        return MI_ERR_SHAPE;
+    }
+    MI_TRY(check_vec(w, x->ne[0]));
+    MI_TRY(check_vec(scale, x->ne[0]));
+    MI_TRY(check_vec(shift, x->ne[0]));
+    if (!(eps >= 0.0f) || std::isinf(eps)) {
+        return MI_ERR_PARAM;
+    }
+    return finish(launch_rms_norm(*x, (const float *) w->data, (const float *) scale->data,
+                                  (const float *) shift->data, eps, *y, (hipStream_t) stream));
+}
+
+static int rope_common(const mi_tensor * q, const mi_tensor * q_w, const mi_tensor * q_out, const mi_tensor * k,
+                       const mi_tensor * k_w, const mi_tensor * k_out, const mi_tensor * pos, float eps, int n_dims,
+                       float freq_base, float freq_scale, float attn_factor, bool norm, bool rope,
+                       mi_stream stream) {
+    MI_TRY(check_act(q));
+    MI_TRY(check_act(q_out));
+    if (!same_shape(*q, *q_out)) {
+        return MI_ERR_SHAPE;
+    }
+    if ((k == nullptr) != (k_out == nullptr)) {
+        return MI_ERR_NULL;
+    }
+    if (k) {
+        MI_TRY(check_act(k));
+        MI_TRY(check_act(k_out));
+        if (!same_shape(*k, *k_out) || k->ne[0] != q->ne[0] || k->ne[2] != q->ne[2] || k->ne[3] != q->ne[3]) {
+            return MI_ERR_SHAPE;
+        }
+        if (k->type != q->type || k_out->type != q_out->type) {
+            return MI_ERR_TYPE;  // one launch serves both: same in/out types
+        }
+    }
+    const int64_t D = q->ne[0];
+    if (norm) {
+        if (q_w) {
+            MI_TRY(check_vec(q_w, D));
+        }
+        if (k && k_w) {
+            MI_TRY(check_vec(k_w, D));
+        }
+        if (!(eps >= 0.0f) || std::isinf(eps)) {
+            return MI_ERR_PARAM;
+        }
+    }
+    if (rope) {
+        MI_TRY(check(pos));
+        if (pos->type != MI_TYPE_I32) {
+            return MI_ERR_TYPE;
+        }
+        if (pos->ne[0] != q->ne[2] || pos->ne[1] != 1 || pos->ne[2] != 1 || pos->ne[3] != 1) {
+            return MI_ERR_SHAPE;
+        }
+        if (n_dims <= 0 || n_dims % 2 != 0 || n_dims > D) {
+            return MI_ERR_PARAM;
+        }
+        if (!(freq_base > 0.0f) || !std::isfinite(freq_scale) || !std::isfinite(attn_factor)) {
+            return MI_ERR_PARAM;
+        }
+    }
+    if (q->ne[2] * q->ne[3] >= kMaxRows || q->ne[1] * 256 >= kMaxRows || (k && k->ne[1] * 256 >= kMaxRows)) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    HeadArgs a;
+    a.seg[0] = make_seg(*q, *q_out, norm ? q_w : nullptr);
+    a.nseg   = 1;
+    if (k) {
+        a.seg[1] = make_seg(*k, *k_out, norm ? k_w : nullptr);
+        a.nseg   = 2;
+    }
+    a.ntok        = (uint32_t) (q->ne[2] * q->ne[3]);
+    a.ne2         = (uint32_t) q->ne[2];
+    a.pos         = rope ? (const int32_t *) pos->data : nullptr;
+    // ggml-cpu derives theta_scale on the host CPU with libm powf
+    a.theta_scale = rope ? powf(freq_base, -2.0f / (float) n_dims) : 1.0f;
+    a.freq_scale  = freq_scale;
+    a.mscale      = attn_factor;
+    a.eps         = eps;
+    a.ne0         = (int) D;
+    a.n_dims      = rope ? n_dims : (int) D;
+    a.norm        = norm ? 1 : 0;
+    return finish(launch_heads(a, q->type, q_out->type, (hipStream_t) stream));
+}
+
+int mi_rope_ext(const mi_tensor * x, const mi_tensor * pos, int n_dims, int mode, float freq_base, float freq_scale,
+                float ext_factor, float attn_factor, const mi_tensor * y, mi_stream stream) {
+    if (mode != 2 || ext_factor != 0.0f) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    return rope_common(x, nullptr, y, nullptr, nullptr, nullptr, pos, 0.0f, n_dims, freq_base, freq_scale,
+                       attn_factor, false, true, stream);
+}
+
+int mi_qk_norm_rope(const mi_tensor * q, const mi_tensor * q_w, const mi_tensor * q_out, const mi_tensor * k,
+                    const mi_tensor * k_w, const mi_tensor * k_out, const mi_tensor * pos, float eps, int n_dims,
+                    float freq_base, float freq_scale, float attn_factor, mi_stream stream) {
+    const bool norm = q_w != nullptr;
+    if (k && ((k_w != nullptr) != norm)) {
+        return MI_ERR_PARAM;
+    }
+    return rope_common(q, q_w, q_out, k, k_w, k_out, pos, eps, n_dims, freq_base, freq_scale, attn_factor, norm,
+                       true, stream);
+}
+
+static int swiglu_common(const mi_tensor * g, const mi_tensor * u, const char * gp, const char * up, int64_t n,
+                         const mi_tensor * y, mi_stream stream) {
+    MI_TRY(check_act(y));
+    if (y->ne[0] != n || y->ne[1] != g->ne[1] || y->ne[2] != g->ne[2] || y->ne[3] != g->ne[3]) {
+        return MI_ERR_SHAPE;
+    }
+    if (!uniform_rows(*g) || !uniform_rows(*u) || !uniform_rows(*y)) {
+        return MI_ERR_STRIDE;
+    }
+    const int64_t rows = nrows(*g);
+    return finish(launch_swiglu(gp, up, (int64_t) g->nb[1], (int64_t) u->nb[1], g->type, (char *) y->data,
+                                (int64_t) y->nb[1], y->type, rows, n, true, (hipStream_t) stream));
+}
+
+int mi_swiglu(const mi_tensor * gu, int swapped, const mi_tensor * y, mi_stream stream) {
+    MI_TRY(check_act(gu));
+    if (gu->ne[0] % 2 != 0) {
+        return MI_ERR_SHAPE;
+    }
+    const int64_t n  = gu->ne[0] / 2;
+    const size_t  hb = (size_t) n * type_size(gu->type);
+    const char *  b  = (const char *) gu->data;
+    return swiglu_common(gu, gu, swapped ? b + hb : b, swapped ? b : b + hb, n, y, stream);
+}
+
+int mi_swiglu_split(const mi_tensor * g, const mi_tensor * u, const mi_tensor * y, mi_stream stream) {
+    MI_TRY(check_act(g));
+    MI_TRY(check_act(u));
+    if (!same_shape(*g, *u)) {
+        return MI_ERR_SHAPE;
+    }
+    if (g->type != u->type) {
+        return MI_ERR_TYPE;
+    }
+    return swiglu_common(g, u, (const char *) g->data, (const char *) u->data, g->ne[0], y, stream);
+}
+
+int mi_add(const mi_tensor * a, const mi_tensor * b, const mi_tensor * y, mi_stream stream) {
+    if (!b) {
+        return MI_ERR_NULL;
+    }
+    return binary_entry(OP_ADD, a, b, false, 0.0f, 0.0f, y, stream);
+}
+
+int mi_mul(const mi_tensor * a, const mi_tensor * b, const mi_tensor * y, mi_stream stream) {
+    if (!b) {
+        return MI_ERR_NULL;
+    }
+    return binary_entry(OP_MUL, a, b, false, 0.0f, 0.0f, y, stream);
+}
+
+int mi_add_clamp(const mi_tensor * a, const mi_tensor * b, float lo, float hi, const mi_tensor * y,
+                 mi_stream stream) {
+    if (std::isnan(lo) || std::isnan(hi)) {
+        return MI_ERR_PARAM;
+    }
+    return binary_entry(b ? OP_ADD : OP_NONE, a, b, true, lo, hi, y, stream);
+}
+
+int mi_gated_add(const mi_tensor * residual, const mi_tensor * x, const mi_tensor * gate, const mi_tensor * y,
+                 mi_stream stream) {
+    MI_TRY(check_act(residual));
+    MI_TRY(check_act(x));
+    MI_TRY(check_act(y));
+    if (!same_shape(*residual, *x) || !same_shape(*residual, *y)) {
+        return MI_ERR_SHAPE;
+    }
+    MI_TRY(check_vec(gate, residual->ne[0]));
+    return finish(launch_binary(OP_GATED, *residual, x, (const float *) gate->data, nullptr, false, 0.0f, 0.0f, *y,
+                                (hipStream_t) stream));
+}
+
+int mi_modulate(const mi_tensor * x, const mi_tensor * scale, const mi_tensor * shift, const mi_tensor * y,
+                mi_stream stream) {
+    MI_TRY(check_act(x));
+    MI_TRY(check_act(y));
+    if (!same_shape(*x, *y)) {
+        return MI_ERR_SHAPE;
+    }
+    MI_TRY(check_vec(scale, x->ne[0]));
+    MI_TRY(check_vec(shift, x->ne[0]));
+    return finish(launch_binary(OP_MOD, *x, nullptr, (const float *) scale->data, (const float *) shift->data, false,
+                                0.0f, 0.0f, *y, (hipStream_t) stream));
+}
+
+int mi_get_rows(const mi_tensor * table, const mi_tensor * ids, const mi_tensor * y, int32_t * d_err,
+                mi_stream stream) {
+    MI_TRY(check(table));
+    MI_TRY(check(ids));
+    MI_TRY(check(y));
+    if (table->type != MI_TYPE_Q8_0 && !is_act(table->type)) {
+        return MI_ERR_TYPE;
+    }
+    if (ids->type != MI_TYPE_I32 || (y->type != MI_TYPE_F32 && y->type != MI_TYPE_BF16)) {
+        return MI_ERR_TYPE;
+    }
+    if (table->ne[2] != 1 || table->ne[3] != 1 || ids->ne[1] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1) {
+        return MI_ERR_UNSUPPORTED;  // batched tables (ne02/ne03 > 1) are not used by the reference
+    }
+    if (y->ne[0] != table->ne[0] || y->ne[1] != ids->ne[0] || y->ne[2] != 1 || y->ne[3] != 1) {
+        return MI_ERR_SHAPE;
+    }
+    if (!aligned(d_err, 4)) {
+        return MI_ERR_ALIGN;
+    }
+    return finish(launch_get_rows(*table, (const int32_t *) ids->data, ids->ne[0], 1, *y, d_err,
+                                  (hipStream_t) stream));
+}
+
+static RowCopy plain_copy(const mi_tensor & src, const mi_tensor & dst) {
+    RowCopy r{};
+    r.src  = (const char *) src.data;
+    r.sr   = make_rows3(src);
+    r.rows = (uint32_t) nrows(src);
+    r.ne0  = (int) src.ne[0];
+    r.dst  = (char *) dst.data;
+    r.dr   = make_rows3(dst);
+    r.kv   = 0;
+    return r;
+}
+
+int mi_cpy_q8_0(const mi_tensor * src, const mi_tensor * dst, int rounding, mi_stream stream) {
+    MI_TRY(check_act(src));
+    MI_TRY(check(dst));
+    if (dst->type != MI_TYPE_Q8_0 && !is_act(dst->type)) {
+        return MI_ERR_TYPE;
+    }
+    if (!same_shape(*src, *dst)) {
+        return MI_ERR_SHAPE;
+    }
+    if (rounding != MI_Q8_0_CPU_X86 && rounding != MI_Q8_0_REF) {
+        return MI_ERR_PARAM;
+    }
+    const RowCopy k = plain_copy(*src, *dst);
+    return finish(launch_row_copy(k, nullptr, src->type, dst->type, rounding, (hipStream_t) stream));
+}
+
+int mi_cpy(const mi_tensor * src, const mi_tensor * dst, mi_stream stream) {
+    return mi_cpy_q8_0(src, dst, MI_Q8_0_CPU_X86, stream);
+}
+
+static int kv_desc(const mi_tensor * x, const mi_tensor * cache, const mi_tensor * pos0, const mi_tensor * sets,
+                   int32_t * d_err, RowCopy & r) {
+    MI_TRY(check_act(x));
+    MI_TRY(check(cache));
+    if (cache->type != MI_TYPE_Q8_0 && !is_act(cache->type)) {
+        return MI_ERR_TYPE;
+    }
+    if (cache->ne[0] != x->ne[0] || cache->ne[2] != x->ne[1]) {
+        return MI_ERR_SHAPE;
+    }
+    r      = RowCopy{};
+    r.src  = (const char *) x->data;
+    r.sr   = make_rows3(*x);
+    r.rows = (uint32_t) nrows(*x);
+    r.ne0  = (int) x->ne[0];
+    r.dst  = (char *) cache->data;
+    r.kv   = 1;
+    r.ne1  = (uint32_t) x->ne[1];
+    r.ne2  = (uint32_t) x->ne[2];
+    r.d1   = FastDiv(r.ne1);
+    r.d12  = FastDiv(r.ne1 * r.ne2);
+    r.pos0 = (const int32_t *) pos0->data;
+    r.sets = sets ? (const int32_t *) sets->data : nullptr;
+    r.cnb1 = (int64_t) cache->nb[1];
+    r.cnb2 = (int64_t) cache->nb[2];
+    r.cnb3 = (int64_t) cache->nb[3];
+    r.max_seq = cache->ne[1];
+    r.n_sets  = cache->ne[3];
+    r.d_err   = d_err;
+    return MI_OK;
+}
+
+int mi_kv_store(const mi_tensor * k, const mi_tensor * k_cache, const mi_tensor * v, const mi_tensor * v_cache,
+                const mi_tensor * pos0, const mi_tensor * sets, int rounding, int32_t * d_err, mi_stream stream) {
+    if (!k || !k_cache || !pos0) {
+        return MI_ERR_NULL;
+    }
+    if ((v == nullptr) != (v_cache == nullptr)) {
+        return MI_ERR_NULL;
+    }
+    MI_TRY(check(pos0));
+    if (pos0->type != MI_TYPE_I32) {
+        return MI_ERR_TYPE;
+    }
+    if (pos0->ne[0] != k->ne[3] || pos0->ne[1] != 1 || pos0->ne[2] != 1 || pos0->ne[3] != 1) {
+        return MI_ERR_SHAPE;
+    }
+    if (sets) {
+        MI_TRY(check(sets));
+        if (sets->type != MI_TYPE_I32) {
+            return MI_ERR_TYPE;
+        }
+        if (sets->ne[0] != k->ne[3] || sets->ne[1] != 1 || sets->ne[2] != 1 || sets->ne[3] != 1) {
+            return MI_ERR_SHAPE;
+        }
+    }
+    if (rounding != MI_Q8_0_CPU_X86 && rounding != MI_Q8_0_REF) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(d_err, 4)) {
+        return MI_ERR_ALIGN;
+    }
+    RowCopy rk, rv;
+    MI_TRY(kv_desc(k, k_cache, pos0, sets, d_err, rk));
+    if (v) {
+        MI_TRY(kv_desc(v, v_cache, pos0, sets, d_err, rv));
+        if (!same_shape(*k, *v) || !same_shape(*k_cache, *v_cache) || k->type != v->type ||
+            k_cache->type != v_cache->type) {
+            return MI_ERR_SHAPE;
+        }
+    }
+    return finish(launch_row_copy(rk, v ? &rv : nullptr, k->type, k_cache->type, rounding, (hipStream_t) stream));
+}
+
+int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi_tensor * y, mi_stream stream) {
+    MI_TRY(check(t));
+    MI_TRY(check(y));
+    if (t->type != MI_TYPE_F32 || y->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (dim <= 0 || max_period <= 0) {
+        return MI_ERR_PARAM;
+    }
+    if (t->ne[1] != 1 || t->ne[2] != 1 || t->ne[3] != 1 || y->ne[0] != dim || y->ne[1] != t->ne[0] ||
+        y->ne[2] != 1 || y->ne[3] != 1) {
+        return MI_ERR_SHAPE;
+    }
+    return finish(launch_timestep_embedding((const float *) t->data, t->ne[0], 1, dim, max_period, (char *) y->data,
+                                            (int64_t) y->nb[1], (hipStream_t) stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,109 @@
+// launch.h -- host-side launchers shared between the kernel files and the
+// C-ABI layer. Arguments reaching these functions have been validated.
+#pragma once
+
+#include "common.h"
+
+namespace mi {
+
+// ---- vector helpers ------------------------------------------------------
+template <int TO, int N> __device__ __forceinline__ void store_vec(char * p, const float * f) {
+    if constexpr (TO == MI_TYPE_F32) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            st16(p + 16 * i, pack16<MI_TYPE_F32>(f + 4 * i));
+        }
+    } else if constexpr (N == 8) {
+        st16(p, pack16<TO>(f));
+    } else {
+        static_assert(N == 4, "4 or 8 half-width elements per store");
+        uint2 v;
+        if constexpr (TO == MI_TYPE_BF16) {
+            v = make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
+        } else {
+            v = make_uint2(pack_f16x2(f[0], f[1]), pack_f16x2(f[2], f[3]));
+        }
+        *(uint2 *) p = v;
+    }
+}
+
+// ---- norm.hip --------------------------------------------------------------
+// mode 0: rms_norm; 1: rms_norm * w; 2: (rms_norm * w) * (sc + 1) + sh
+int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, const float * sh, float eps,
+                    const mi_tensor & y, hipStream_t s);
+
+// ---- rope.hip --------------------------------------------------------------
+struct HeadSeg {
+    const char * x;
+    char *       y;
+    uint32_t     heads;
+    FastDiv      hdiv;  // rows per WG -> (token, head) split
+    int64_t      xs1, xs2, xs3, ys1, ys2, ys3;
+    const float * w;
+};
+
+struct HeadArgs {
+    HeadSeg         seg[2];
+    int             nseg;
+    uint32_t        ntok;  // ne2 * ne3
+    uint32_t        ne2;
+    FastDiv         dne2;
+    const int32_t * pos;   // nullptr: no rope
+    float           theta_scale, freq_scale, mscale, eps;
+    int             ne0, n_dims;
+    int             norm;  // apply rms_norm (* w when seg.w)
+};
+
+// q and (optionally) k share positions and head size. Returns mi_status.
+int launch_heads(HeadArgs & a, int tin, int tout, hipStream_t s);
+
+// ---- glu.hip ---------------------------------------------------------------
+int launch_swiglu(const char * g, const char * u, int64_t gs, int64_t us, int tin, char * y, int64_t ys, int tout,
+                  int64_t rows, int64_t n, bool vec_ok, hipStream_t s);
+
+// ---- binary.hip ------------------------------------------------------------
+enum BinOp { OP_ADD = 0, OP_MUL = 1, OP_GATED = 2, OP_MOD = 3, OP_NONE = 4 };
+
+// y = op(a, b | v0, v1), then optional clamp. b is a full tensor of a's shape
+// (brow) or nullptr; v0/v1 are F32 [ne0] column vectors.
+int launch_binary(int op, const mi_tensor & a, const mi_tensor * b, const float * v0, const float * v1, bool clamp,
+                  float lo, float hi, const mi_tensor & y, hipStream_t s);
+
+// generic ggml_can_repeat broadcast (any b shape)
+int launch_binary_bcast(int op, const mi_tensor & a, const mi_tensor & b, bool clamp, float lo, float hi,
+                        const mi_tensor & y, hipStream_t s);
+
+// ---- getrows.hip -----------------------------------------------------------
+int launch_get_rows(const mi_tensor & table, const int32_t * ids, int64_t n_ids, int64_t ids_stride,
+                    const mi_tensor & y, int32_t * d_err, hipStream_t s);
+
+// ---- quant.hip -------------------------------------------------------------
+// Rows of src [ne0, ne1, ne2, ne3] copied/converted into dst rows. Row r of
+// src = (i1, i2, i3); dst row address:
+//   plain cpy : dst + i1*nb1 + i2*nb2 + i3*nb3
+//   kv store  : cache + (pos0[i3] + i2)*nb1 + i1*nb2 + set[i3]*nb3
+struct RowCopy {
+    const char *    src;
+    Rows3           sr;
+    uint32_t        rows;
+    int             ne0;
+    char *          dst;
+    Rows3           dr;         // plain cpy
+    // kv store
+    int             kv;
+    uint32_t        ne1, ne2;   // src heads, tokens per sequence
+    FastDiv         d1, d12;
+    const int32_t * pos0;
+    const int32_t * sets;
+    int64_t         cnb1, cnb2, cnb3;
+    int64_t         max_seq, n_sets;
+    int32_t *       d_err;
+};
+
+int launch_row_copy(const RowCopy & k, const RowCopy * v, int tin, int tout, int rounding, hipStream_t s);
+
+// ---- tsembd.hip ------------------------------------------------------------
+int launch_timestep_embedding(const float * t, int64_t n, int64_t ts, int dim, int max_period, char * y,
+                              int64_t ys, hipStream_t s);
+
+}  // namespace mi

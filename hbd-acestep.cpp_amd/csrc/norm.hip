@@ -1,0 +1,322 @@
+// norm.hip -- RMSNorm over long rows (hidden size), optionally fused with the
+// weight multiply and the DiT AdaLN modulate.
+//
+// ggml node chain reproduced (reference: qwen3-enc.h:114-120,
+// dit-graph.h:24-30 and 54-64):
+//   n = rms_norm(x, eps)          sum_i (double)(x_i*x_i); mean = (float)(sum/ne0);
+//                                 scale = 1.0f/sqrtf(mean + eps); n_i = x_i*scale
+//   n = n * w                     (ggml_mul, [ne0] broadcast)
+//   m = (n * (scale_v + 1)) + shift_v   (dit_ggml_adaln)
+// Every intermediate stays fp32 in registers, rounded exactly as the ggml
+// nodes round it; only the final value is converted to the output type.
+//
+// Fast path: one workgroup owns whole rows. Each thread always handles the
+// same C 16-byte column vectors, so the F32 weight / (scale+1) / shift
+// vectors are loaded once into registers and reused for every row the
+// workgroup processes. R rows are loaded before any is reduced so each lane
+// keeps R*C 128-bit loads in flight; per-row partial sums (double) are
+// reduced in-wave with DPP, then across waves through LDS in a fixed order.
+#include "launch.h"
+
+namespace mi {
+
+struct NormArgs {
+    const char *  x;
+    char *        y;
+    Rows3         xr, yr;
+    uint32_t      rows;
+    int           n;
+    float         eps;
+    const float * w;
+    const float * sc;
+    const float * sh;
+};
+
+template <int TI, int TO, int MODE, int C, int R>
+__global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
+    constexpr int VI = TT<TI>::VEC;
+    constexpr int EI = TT<TI>::ES;
+    constexpr int EO = TT<TO>::ES;
+    const int     T    = blockDim.x;
+    const int     tid  = threadIdx.x;
+    const int     wave = tid >> 6;
+    const int     lane = tid & 63;
+    const int     nw   = T >> 6;
+
+    __shared__ double part[2][R][8];
+
+    float wv[C][VI], sv[C][VI], hv[C][VI];
+    if constexpr (MODE >= 1) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const int col = (j * T + tid) * VI;
+#pragma unroll
+            for (int e = 0; e < VI; e += 4) {
+                const float4 w4 = *(const float4 *) (a.w + col + e);
+                wv[j][e + 0]    = w4.x;
+                wv[j][e + 1]    = w4.y;
+                wv[j][e + 2]    = w4.z;
+                wv[j][e + 3]    = w4.w;
+                if constexpr (MODE == 2) {
+                    const float4 s4 = *(const float4 *) (a.sc + col + e);
+                    const float4 h4 = *(const float4 *) (a.sh + col + e);
+                    sv[j][e + 0]    = s4.x + 1.0f;
+                    sv[j][e + 1]    = s4.y + 1.0f;
+                    sv[j][e + 2]    = s4.z + 1.0f;
+                    sv[j][e + 3]    = s4.w + 1.0f;
+                    hv[j][e + 0]    = h4.x;
+                    hv[j][e + 1]    = h4.y;
+                    hv[j][e + 2]    = h4.z;
+                    hv[j][e + 3]    = h4.w;
+                }
+            }
+        }
+    }
+
+    int it = 0;
+    for (uint32_t rbase = blockIdx.x * R; rbase < a.rows; rbase += gridDim.x * R, ++it) {
+        uint4 raw[R][C];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = rbase + r;
+            if (row < a.rows) {
+                const char * xp = a.x + a.xr.off(row);
+#pragma unroll
+                for (int j = 0; j < C; ++j) {
+                    raw[r][j] = ld16(xp + (size_t) ((j * T + tid) * VI) * EI);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < C; ++j) {
+                    raw[r][j] = make_uint4(0, 0, 0, 0);
+                }
+            }
+        }
+        double s[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            s[r] = 0.0;
+#pragma unroll
+            for (int j = 0; j < C; ++j) {
+                float f[VI];
+                unpack16<TI>(raw[r][j], f);
+#pragma unroll
+                for (int e = 0; e < VI; ++e) {
+                    s[r] += (double) (f[e] * f[e]);
+                }
+            }
+            s[r] = group_sum<64>(s[r]);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                part[it & 1][r][wave] = s[r];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = rbase + r;
+            if (row >= a.rows) {
+                continue;
+            }
+            double tot = 0.0;
+            for (int q = 0; q < nw; ++q) {
+                tot += part[it & 1][r][q];
+            }
+            const float scale = rms_scale(tot, a.n, a.eps);
+            char *      yp    = a.y + a.yr.off(row);
+#pragma unroll
+            for (int j = 0; j < C; ++j) {
+                float f[VI];
+                unpack16<TI>(raw[r][j], f);
+#pragma unroll
+                for (int e = 0; e < VI; ++e) {
+                    float v = f[e] * scale;
+                    if constexpr (MODE >= 1) {
+                        v = v * wv[j][e];
+                    }
+                    if constexpr (MODE == 2) {
+                        v = v * sv[j][e];
+                        v = v + hv[j][e];
+                    }
+                    f[e] = v;
+                }
+                store_vec<TO, VI>(yp + (size_t) ((j * T + tid) * VI) * EO, f);
+            }
+        }
+    }
+}
+
+// Any row length, element-aligned rows: one wave per row, scalar accesses.
+template <int TI, int TO, int MODE>
+__global__ void __launch_bounds__(256) k_rms_rows_generic(const NormArgs a) {
+    constexpr int EI    = TT<TI>::ES;
+    constexpr int EO    = TT<TO>::ES;
+    const int     lane  = threadIdx.x & 63;
+    const int     wpb   = blockDim.x >> 6;
+    for (uint32_t row = blockIdx.x * wpb + (threadIdx.x >> 6); row < a.rows; row += gridDim.x * wpb) {
+        const char * xp = a.x + a.xr.off(row);
+        char *       yp = a.y + a.yr.off(row);
+        double       s  = 0.0;
+        for (int i = lane; i < a.n; i += 64) {
+            const float f = load_elem<TI>(xp + (size_t) i * EI);
+            s += (double) (f * f);
+        }
+        s                 = group_sum<64>(s);
+        const float scale = rms_scale(s, a.n, a.eps);
+        for (int i = lane; i < a.n; i += 64) {
+            float v = load_elem<TI>(xp + (size_t) i * EI) * scale;
+            if constexpr (MODE >= 1) {
+                v = v * a.w[i];
+            }
+            if constexpr (MODE == 2) {
+                v = v * (a.sc[i] + 1.0f);
+                v = v + a.sh[i];
+            }
+            store_elem<TO>(yp + (size_t) i * EO, v);
+        }
+    }
+}
+
+// Workgroups for a grid-stride loop over ceil(rows/R) row groups, capped at
+// about 16 resident waves per CU, with the groups spread evenly (every
+// workgroup runs the same number of iterations, +-1).
+static uint32_t balanced_grid(uint32_t rows, int R, int nw) {
+    const uint32_t iters  = (rows + R - 1) / R;
+    const uint32_t max_wg = (uint32_t) num_cus() * (uint32_t) (16 / nw > 0 ? 16 / nw : 1);
+    const uint32_t per    = (iters + max_wg - 1) / max_wg;
+    return (iters + per - 1) / per;
+}
+
+template <int TI, int TO, int MODE>
+static int dispatch_fast(const NormArgs & a, int T, int C, hipStream_t s) {
+    const int nw = T / 64;
+    switch (C) {
+        case 1:
+            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, 1, 4>), dim3(balanced_grid(a.rows, 4, nw)), dim3(T), 0, s,
+                               a);
+            break;
+        case 2:
+            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, 2, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0, s,
+                               a);
+            break;
+        case 3:
+            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, 3, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0, s,
+                               a);
+            break;
+        case 4:
+            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, 4, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0, s,
+                               a);
+            break;
+        default:
+            return MI_ERR_UNSUPPORTED;
+    }
+    return MI_OK;
+}
+
+template <int TI, int TO>
+static int dispatch_types(const NormArgs & a, int mode, bool fast, int T, int C, hipStream_t s) {
+    if (fast) {
+        switch (mode) {
+            case 0:
+                return dispatch_fast<TI, TO, 0>(a, T, C, s);
+            case 1:
+                return dispatch_fast<TI, TO, 1>(a, T, C, s);
+            default:
+                return dispatch_fast<TI, TO, 2>(a, T, C, s);
+        }
+    }
+    const uint32_t wpb  = 4;
+    uint32_t       grid = (a.rows + wpb - 1) / wpb;
+    const uint32_t cap  = (uint32_t) num_cus() * 8;
+    grid                = grid > cap ? cap : grid;
+    switch (mode) {
+        case 0:
+            hipLaunchKernelGGL((k_rms_rows_generic<TI, TO, 0>), dim3(grid), dim3(256), 0, s, a);
+            break;
+        case 1:
+            hipLaunchKernelGGL((k_rms_rows_generic<TI, TO, 1>), dim3(grid), dim3(256), 0, s, a);
+            break;
+        default:
+            hipLaunchKernelGGL((k_rms_rows_generic<TI, TO, 2>), dim3(grid), dim3(256), 0, s, a);
+            break;
+    }
+    return MI_OK;
+}
+
+int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, const float * sh, float eps,
+                    const mi_tensor & y, hipStream_t s) {
+    NormArgs a;
+    a.x    = (const char *) x.data;
+    a.y    = (char *) y.data;
+    a.xr   = make_rows3(x);
+    a.yr   = make_rows3(y);
+    a.rows = (uint32_t) nrows(x);
+    a.n    = (int) x.ne[0];
+    a.eps  = eps;
+    a.w    = w;
+    a.sc   = sc;
+    a.sh   = sh;
+    if (a.rows == 0 || a.n == 0) {
+        return MI_OK;
+    }
+    const int mode = sh ? 2 : (w ? 1 : 0);
+
+    // fast path: rows split into 64*nw lanes x C vectors of 16 bytes
+    bool      fast = x.type == y.type;
+    const int VI   = 16 / type_size(x.type);
+    int       T = 0, C = 0;
+    if (fast && a.n % (64 * VI) == 0) {
+        const int k = a.n / (64 * VI);
+        int       nw = 1;
+        for (int d = 8; d >= 1; --d) {
+            if (k % d == 0) {
+                nw = d;
+                break;
+            }
+        }
+        T = nw * 64;
+        C = k / nw;
+    }
+    fast = fast && C >= 1 && C <= 4;
+    for (int d = 0; d < 4 && fast; ++d) {
+        if (d > 0 && ((x.nb[d] % 16) || (y.nb[d] % 16))) {
+            fast = false;
+        }
+    }
+    fast = fast && aligned(x.data, 16) && aligned(y.data, 16) && (!w || aligned(w, 16)) &&
+           (!sc || aligned(sc, 16)) && (!sh || aligned(sh, 16));
+
+    switch (x.type) {
+        case MI_TYPE_F32:
+            switch (y.type) {
+                case MI_TYPE_F32:
+                    return dispatch_types<MI_TYPE_F32, MI_TYPE_F32>(a, mode, fast, T, C, s);
+                case MI_TYPE_BF16:
+                    return dispatch_types<MI_TYPE_F32, MI_TYPE_BF16>(a, mode, false, T, C, s);
+                default:
+                    return dispatch_types<MI_TYPE_F32, MI_TYPE_F16>(a, mode, false, T, C, s);
+            }
+        case MI_TYPE_BF16:
+            switch (y.type) {
+                case MI_TYPE_F32:
+                    return dispatch_types<MI_TYPE_BF16, MI_TYPE_F32>(a, mode, false, T, C, s);
+                case MI_TYPE_BF16:
+                    return dispatch_types<MI_TYPE_BF16, MI_TYPE_BF16>(a, mode, fast, T, C, s);
+                default:
+                    return dispatch_types<MI_TYPE_BF16, MI_TYPE_F16>(a, mode, false, T, C, s);
+            }
+        default:
+            switch (y.type) {
+                case MI_TYPE_F32:
+                    return dispatch_types<MI_TYPE_F16, MI_TYPE_F32>(a, mode, false, T, C, s);
+                case MI_TYPE_BF16:
+                    return dispatch_types<MI_TYPE_F16, MI_TYPE_BF16>(a, mode, false, T, C, s);
+                default:
+                    return dispatch_types<MI_TYPE_F16, MI_TYPE_F16>(a, mode, fast, T, C, s);
+            }
+    }
+}
+
+}  // namespace mi

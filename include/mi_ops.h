@@ -1,0 +1,251 @@
+/*
+ * mi_ops.h -- C ABI of the MI355X (gfx950) per-layer fused ops.
+ *
+ * Each entry point takes ggml-style tensor views (ne[0] innermost, byte
+ * strides nb[]) and reproduces the ggml op, or the chain of ggml ops, that
+ * acestep.cpp's graph builders emit at that point of the graph, so host code
+ * can call it at the same graph boundary. All calls are asynchronous and
+ * stream-ordered on the given HIP stream (NULL = the null stream). The
+ * library never allocates, frees or retains caller memory; arguments are
+ * validated on the host before any launch, and no entry point aborts: a
+ * non-zero mi_status is returned instead.
+ *
+ * Types: MI_TYPE_* values equal the matching enum ggml_type values, so a
+ * ggml backend can pass tensor->type, tensor->ne and tensor->nb through.
+ *
+ * Q8_0 tensors follow ggml: ne[0] counts elements (a multiple of 32), nb[0]
+ * is the 34-byte block size, a block is { fp16 d; int8 qs[32] }.
+ *
+ * Activation tensors may be F32 or BF16 (BF16 is computed as bf16 -> f32,
+ * the fp32 op chain, f32 -> bf16 round-to-nearest-even at the output).
+ * Norm weights and AdaLN vectors are F32, as the reference stores them.
+ */
+#ifndef MI_OPS_H
+#define MI_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_OPS_ABI_VERSION 1
+
+enum mi_type {
+    MI_TYPE_F32  = 0,
+    MI_TYPE_F16  = 1,
+    MI_TYPE_Q8_0 = 8,
+    MI_TYPE_I32  = 26,
+    MI_TYPE_BF16 = 30,
+};
+
+enum mi_status {
+    MI_OK              = 0,
+    MI_ERR_NULL        = -1, /* a required tensor or data pointer is NULL        */
+    MI_ERR_TYPE        = -2, /* unsupported type or type combination             */
+    MI_ERR_SHAPE       = -3, /* shapes are inconsistent for the op               */
+    MI_ERR_STRIDE      = -4, /* unsupported stride (e.g. nb[0] != element size)  */
+    MI_ERR_ALIGN       = -5, /* data pointer or stride misaligned for its type   */
+    MI_ERR_PARAM       = -6, /* invalid scalar parameter                         */
+    MI_ERR_UNSUPPORTED = -7, /* valid ggml op configuration this library lacks   */
+    MI_ERR_HIP         = -8, /* the HIP runtime reported an error at launch      */
+};
+
+/* Q8_0 quantizer rounding variants (both are ggml's own):
+ *   MI_Q8_0_CPU_X86: ggml-cpu x86 from_float: id = 127/amax, round half to even
+ *   MI_Q8_0_REF:     quantize_row_q8_0_ref:  id = 1/(amax/127), roundf (half away) */
+enum mi_q8_0_rounding {
+    MI_Q8_0_CPU_X86 = 0,
+    MI_Q8_0_REF     = 1,
+};
+
+typedef struct mi_tensor {
+    void *   data;
+    int32_t  type;     /* enum mi_type */
+    int32_t  reserved; /* must be 0 */
+    int64_t  ne[4];    /* elements per dimension, ne[0] innermost */
+    uint64_t nb[4];    /* byte strides */
+} mi_tensor;
+
+typedef void * mi_stream; /* hipStream_t */
+
+int          mi_abi_version(void);
+const char * mi_status_str(int status);
+
+/* ggml_rms_norm(x, eps), followed by ggml_mul(., w) when w != NULL.
+ * Replaces qwen3_rms_norm (qwen3-enc.h:114-120; called at qwen3-lm.h:471,
+ * 485, 494, 632, 736, 745), dit_ggml_rms_norm_weighted (dit-graph.h:24-30;
+ * 429 cross-attn norm) and the QK-norm without rope of the DiT cross
+ * attention (dit-graph.h:328-331).
+ * x, y: [n, ...] F32/BF16, rows may be strided (nb[0] = element size);
+ * w: F32 [n] or NULL. Reduction: float squares summed in double,
+ * mean = (float)(sum/n), scale = 1.0f/sqrtf(mean + eps). */
+int mi_rms_norm(const mi_tensor * x, const mi_tensor * w, float eps, const mi_tensor * y, mi_stream stream);
+
+/* RMSNorm * w then AdaLN modulate, fused:
+ * y = ((rms_norm(x) * w) * (scale + 1)) + shift.
+ * Replaces dit_ggml_rms_norm_weighted + dit_ggml_adaln (dit-graph.h:404-405,
+ * 442-443, 605-606; adaln at 54-64). scale, shift: F32 [n]. */
+int mi_rms_norm_modulate(const mi_tensor * x, const mi_tensor * w, const mi_tensor * scale, const mi_tensor * shift,
+                         float eps, const mi_tensor * y, mi_stream stream);
+
+/* ggml_rope_ext(x, pos, NULL, n_dims, mode, n_ctx_orig=0, freq_base, freq_scale,
+ * ext_factor, attn_factor, beta_fast, beta_slow) for mode 2 (NEOX).
+ * Replaces the rope nodes at qwen3-enc.h:173-174, qwen3-lm.h:378-379,
+ * 666-667, dit-graph.h:194-196. x, y: [ne0, heads, n_pos, ne3] F32/BF16,
+ * pos: I32 [n_pos] (one position per ne2 index, reused across ne3).
+ * Supported: mode == 2, ext_factor == 0 (the only values the reference
+ * passes), n_dims even and <= ne0 (remaining dims are copied). */
+int mi_rope_ext(const mi_tensor * x, const mi_tensor * pos, int n_dims, int mode, float freq_base, float freq_scale,
+                float ext_factor, float attn_factor, const mi_tensor * y, mi_stream stream);
+
+/* Per-head QK-RMSNorm then NEOX rope for Q and K in one launch:
+ *   q_out = rope(rms_norm(q) * q_w),  k_out = rope(rms_norm(k) * k_w)
+ * Replaces rms_norm + mul + rope (x2) at qwen3-lm.h:372-379, 660-667,
+ * qwen3-enc.h:165-174, dit-graph.h:183-196. q/k may be strided views of the
+ * fused QKV projection output (the ggml_cont copies at qwen3-lm.h:640-642,
+ * dit-graph.h:160-163 are not needed). k/k_w/k_out may be NULL (Q only);
+ * q_w/k_w NULL means no norm (plain rope). Same head size for q and k. */
+int mi_qk_norm_rope(const mi_tensor * q, const mi_tensor * q_w, const mi_tensor * q_out, const mi_tensor * k,
+                    const mi_tensor * k_w, const mi_tensor * k_out, const mi_tensor * pos, float eps, int n_dims,
+                    float freq_base, float freq_scale, float attn_factor, mi_stream stream);
+
+/* ggml_swiglu(gu) / ggml_glu(gu, SWIGLU, swapped): gu [2n, rows] -> y [n, rows],
+ * y = silu(gate) * up, gate = first half of ne0 (second half if swapped).
+ * Replaces qwen3-enc.h:217, dit-graph.h:259. */
+int mi_swiglu(const mi_tensor * gu, int swapped, const mi_tensor * y, mi_stream stream);
+
+/* ggml_swiglu_split(g, u): y = silu(g) * u. Replaces qwen3-enc.h:221,
+ * dit-graph.h:264. */
+int mi_swiglu_split(const mi_tensor * g, const mi_tensor * u, const mi_tensor * y, mi_stream stream);
+
+/* ggml_add(a, b): b same shape as a, or F32 [ne0] broadcast over rows, or
+ * any ggml_can_repeat(b, a) shape (slower path). Replaces the residual adds
+ * at qwen3-enc.h:238, 243, qwen3-lm.h:479, 487, 730, 738, dit-graph.h:432
+ * and the AdaLN vector build at dit-graph.h:391. */
+int mi_add(const mi_tensor * a, const mi_tensor * b, const mi_tensor * y, mi_stream stream);
+
+/* ggml_mul(a, b), same broadcast rules as mi_add. */
+int mi_mul(const mi_tensor * a, const mi_tensor * b, const mi_tensor * y, mi_stream stream);
+
+/* ggml_clamp(ggml_add(a, b), lo, hi); b may be NULL (clamp only).
+ * Replaces qwen3-lm.h:479-482, 487-490, 730-733, 738-741 and the V clamp at
+ * qwen3-lm.h:393, 676. */
+int mi_add_clamp(const mi_tensor * a, const mi_tensor * b, float lo, float hi, const mi_tensor * y,
+                 mi_stream stream);
+
+/* dit_ggml_gated_add (dit-graph.h:70-76): y = residual + (x * gate),
+ * gate F32 [ne0] (raw, no sigmoid). Used at dit-graph.h:420, 445. */
+int mi_gated_add(const mi_tensor * residual, const mi_tensor * x, const mi_tensor * gate, const mi_tensor * y,
+                 mi_stream stream);
+
+/* dit_ggml_adaln (dit-graph.h:54-64) alone: y = (x * (scale + 1)) + shift. */
+int mi_modulate(const mi_tensor * x, const mi_tensor * scale, const mi_tensor * shift, const mi_tensor * y,
+                mi_stream stream);
+
+/* ggml_get_rows(table, ids): table [n, n_rows] Q8_0/F16/BF16/F32, ids I32
+ * [n_ids] -> y [n, n_ids] F32 (or BF16). Replaces the embedding lookups at
+ * qwen3-enc.h:390, 465, qwen3-lm.h:464, 626. An id outside [0, n_rows)
+ * yields a zero row and, when d_err != NULL, increments *d_err (device
+ * int32) -- ggml-cpu aborts there instead. */
+int mi_get_rows(const mi_tensor * table, const mi_tensor * ids, const mi_tensor * y, int32_t * d_err,
+                mi_stream stream);
+
+/* ggml_cpy(src, dst): src F32/BF16/F16, dst F32/BF16/F16/Q8_0 view of the
+ * same shape (any strides; Q8_0 dst rows are whole blocks). Q8_0 uses the
+ * ggml-cpu x86 from_float rounding (MI_Q8_0_CPU_X86). Replaces the KV-cache
+ * writes at qwen3-lm.h:405-406, 701-702, songgen-lelm-gen.h:264-265,
+ * 559-560. */
+int mi_cpy(const mi_tensor * src, const mi_tensor * dst, mi_stream stream);
+
+/* mi_cpy with an explicit Q8_0 rounding variant (enum mi_q8_0_rounding). */
+int mi_cpy_q8_0(const mi_tensor * src, const mi_tensor * dst, int rounding, mi_stream stream);
+
+/* KV-cache store for a batch of sequences in one launch, replacing the N
+ * per-sequence ggml_cpy nodes per layer of qw3lm_forward_batch
+ * (qwen3-lm.h:682-703) and the prefill cpy (qwen3-lm.h:396-406,
+ * songgen-lelm-gen.h:254-265, 548-562).
+ *   k, v:       [D, Nkv, T, B]  F32/BF16/F16 (v may be NULL)
+ *   k/v_cache:  [D, max_seq, Nkv, n_sets] Q8_0/F16/BF16/F32
+ *   pos0:       I32 [B]   first slot written for sequence b
+ *   sets:       I32 [B] or NULL (set = b)
+ * cache[:, pos0[b] + t, h, sets[b]] = k[:, h, t, b]. Out-of-range slots or
+ * sets are skipped and counted in *d_err when d_err != NULL. */
+int mi_kv_store(const mi_tensor * k, const mi_tensor * k_cache, const mi_tensor * v, const mi_tensor * v_cache,
+                const mi_tensor * pos0, const mi_tensor * sets, int rounding, int32_t * d_err, mi_stream stream);
+
+/* ggml_timestep_embedding(t, dim, max_period): t F32 [n] -> y F32 [dim, n].
+ * Replaces dit-graph.h:90 (dim 256, max_period 10000). */
+int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi_tensor * y, mi_stream stream);
+
+/* ---------------------------------------------------------------------- */
+/* Layer-chain drivers: launch the fused-op sequence of one DiT block or   */
+/* one Qwen3 layer in the order of the reference's layer composers, taking */
+/* the GEMM / attention outputs (not computed by this library) as inputs.  */
+/* ---------------------------------------------------------------------- */
+
+/* One ACE-Step DiT block's non-GEMM ops, in dit_ggml_build_layer order
+ * (dit-graph.h:367-448). hidden is updated in place.
+ *   pre-SA:   norm_sa   = rms_norm_modulate(hidden, sa_norm_w, scale_sa, shift_sa)
+ *   SA:       q_out/k_out = qk_norm_rope(q, k)   [q, k: views of the QKV GEMM output]
+ *   post-SA:  hidden    = hidden + sa_out * gate_sa
+ *   CA:       norm_ca   = rms_norm(hidden) * ca_norm_w; ca_q_out = rms_norm(ca_q) * ca_q_w;
+ *             hidden    = hidden + ca_out          (skipped when ca_out is NULL)
+ *   pre-FFN:  norm_ffn  = rms_norm_modulate(hidden, ffn_norm_w, scale_ffn, shift_ffn)
+ *   FFN:      ff        = swiglu(gate_up)
+ *   post-FFN: hidden    = hidden + ffn_out * gate_ffn
+ * adaln: F32 [6H] = scale_shift_table + tproj (shift_sa, scale_sa, gate_sa,
+ * shift_ffn, scale_ffn, gate_ffn), as built at dit-graph.h:383-400. */
+typedef struct mi_dit_block_io {
+    mi_tensor hidden;                    /* [H, S, N] in/out */
+    mi_tensor adaln;                     /* F32 [6H] */
+    mi_tensor sa_norm_w, ffn_norm_w;     /* F32 [H] */
+    mi_tensor norm_sa;                   /* [H, S, N] out */
+    mi_tensor q, k, q_w, k_w, q_out, k_out, pos; /* self-attn QK-norm + rope */
+    mi_tensor sa_out;                    /* [H, S, N] O-projection output */
+    mi_tensor ca_norm_w, norm_ca;        /* cross-attn norm (optional) */
+    mi_tensor ca_q, ca_q_w, ca_q_out;    /* cross-attn Q-norm (optional) */
+    mi_tensor ca_out;                    /* cross-attn output (optional) */
+    mi_tensor norm_ffn;                  /* [H, S, N] out */
+    mi_tensor gate_up, ff;               /* [2I, S, N] -> [I, S, N] */
+    mi_tensor ffn_out;                   /* [H, S, N] down-projection output */
+    float     eps, rope_freq_base;
+    int       n_dims;
+    int       use_cross_attn;
+} mi_dit_block_io;
+
+int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream stream);
+
+/* One Qwen3 decoder layer's non-GEMM ops in qw3lm_forward_batch order
+ * (qwen3-lm.h:630-741):
+ *   norm   = rms_norm(hidden) * in_norm_w
+ *   q/k    = qk_norm_rope(q, k)                [views of the QKV GEMM output]
+ *   (clamp v when clamp_fp16), kv_store(k_out, v -> caches at pos0/sets)
+ *   hidden = hidden + attn_out   (clamped to +-65504 when clamp_fp16)
+ *   norm2  = rms_norm(hidden) * post_norm_w
+ *   ff     = swiglu(gate_up)
+ *   hidden = hidden + mlp_out    (clamped when clamp_fp16) */
+typedef struct mi_qwen3_layer_io {
+    mi_tensor hidden;                       /* [H, n_tok] in/out */
+    mi_tensor in_norm_w, post_norm_w;       /* F32 [H] */
+    mi_tensor norm, norm2;                  /* [H, n_tok] out */
+    mi_tensor q, k, v, q_w, k_w, q_out, k_out, pos;
+    mi_tensor k_cache, v_cache, pos0, sets; /* optional KV store (k_cache.data NULL = skip) */
+    mi_tensor attn_out;                     /* [H, n_tok] O-projection output */
+    mi_tensor gate_up, ff;                  /* [2I, n_tok] -> [I, n_tok] */
+    mi_tensor mlp_out;                      /* [H, n_tok] */
+    float     eps, rope_freq_base;
+    int       n_dims;
+    int       clamp_fp16;
+    int       kv_rounding;
+    int32_t * d_err;
+} mi_qwen3_layer_io;
+
+int mi_qwen3_layer_ops(const mi_qwen3_layer_io * io, mi_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_OPS_H */

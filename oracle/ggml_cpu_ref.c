@@ -1,0 +1,427 @@
+/*
+ * ggml_cpu_ref.c -- CPU oracle for the per-layer fused ops.
+ *
+ * TEST INFRASTRUCTURE ONLY (see ggml_cpu_ref.h). Not shipped, never on the
+ * product path.
+ *
+ * This restates, node by node, the ggml-cpu arithmetic behind the ops that
+ * acestep.cpp's graph builders emit. ggml is an empty submodule in the
+ * reference checkout (.gitmodules:1-3), so each function below follows the
+ * published ggml-cpu algorithm for that node; the reference call sites it
+ * serves are cited per function. Build with -ffp-contract=off and without
+ * -ffast-math so that every multiply/add rounds exactly as written.
+ */
+#include "ggml_cpu_ref.h"
+
+#include <math.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 1;
+
+void orc_set_threads(int n) {
+    g_threads = n < 1 ? 1 : n;
+}
+
+int orc_get_threads(void) {
+    return g_threads;
+}
+
+/* ------------------------------------------------------------------------ */
+/* number formats                                                           */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+static inline float u2f(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* IEEE binary16 -> binary32, exact (subnormals included). */
+float orc_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (uint32_t) (h & 0x8000u) << 16;
+    const uint32_t e    = (h >> 10) & 0x1fu;
+    const uint32_t m    = h & 0x3ffu;
+    if (e == 0) {
+        /* zero or subnormal: value = m * 2^-24 (exact in binary32) */
+        const float v = (float) m * 0x1p-24f;
+        return u2f(f2u(v) | sign);
+    }
+    if (e == 31) {
+        return u2f(sign | 0x7f800000u | (m << 13));
+    }
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* binary32 -> binary16, round to nearest even, overflow to inf, NaN kept quiet. */
+uint16_t orc_fp32_to_fp16(float f) {
+    const uint32_t x    = f2u(f);
+    const uint16_t sign = (uint16_t) ((x >> 16) & 0x8000u);
+    const uint32_t ax   = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) {
+        return (uint16_t) (sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    }
+    if (ax >= 0x477ff000u) { /* >= 65520: the halfway point to 2^16 rounds (to even) up to inf */
+        return (uint16_t) (sign | 0x7c00u);
+    }
+    if (ax >= 0x38800000u) { /* normal binary16 range, >= 2^-14 */
+        const uint32_t e   = (ax >> 23) - 112u;
+        const uint32_t m   = ax & 0x7fffffu;
+        uint32_t       h   = (e << 10) | (m >> 13);
+        const uint32_t rem = m & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) {
+            h++; /* a carry into the exponent is the correct result */
+        }
+        return (uint16_t) (sign | h);
+    }
+    if (ax <= 0x33000000u) { /* <= 2^-25: rounds to zero (2^-25 itself is a tie to even 0) */
+        return sign;
+    }
+    /* subnormal binary16: k = round(|f| * 2^24), k in [1, 1024] */
+    const uint32_t m   = (ax & 0x7fffffu) | 0x800000u;
+    const int      E   = (int) (ax >> 23) - 127;      /* -25 .. -15 */
+    const int      s   = -E - 1;                       /* 14 .. 24 */
+    uint32_t       k   = m >> s;
+    const uint32_t rem = m & ((1u << s) - 1u);
+    const uint32_t half = 1u << (s - 1);
+    if (rem > half || (rem == half && (k & 1u))) {
+        k++;
+    }
+    return (uint16_t) (sign | k);
+}
+
+float orc_bf16_to_fp32(uint16_t h) {
+    return u2f((uint32_t) h << 16);
+}
+
+/* binary32 -> bfloat16, round to nearest even; NaN is quieted. */
+uint16_t orc_fp32_to_bf16(float f) {
+    const uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return (uint16_t) ((u >> 16) | 64u);
+    }
+    return (uint16_t) ((u + (0x7fffu + ((u >> 16) & 1u))) >> 16);
+}
+
+void orc_fp16_to_fp32_n(const uint16_t * x, float * y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        y[i] = orc_fp16_to_fp32(x[i]);
+    }
+}
+
+void orc_fp32_to_fp16_n(const float * x, uint16_t * y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        y[i] = orc_fp32_to_fp16(x[i]);
+    }
+}
+
+void orc_bf16_to_fp32_n(const uint16_t * x, float * y, int64_t n) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        y[i] = orc_bf16_to_fp32(x[i]);
+    }
+}
+
+void orc_fp32_to_bf16_n(const float * x, uint16_t * y, int64_t n) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        y[i] = orc_fp32_to_bf16(x[i]);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml_rms_norm                                                            */
+/* Reference call sites: qwen3-enc.h:118 (qwen3_rms_norm), 165-168 (QK-norm),*/
+/* qwen3-lm.h:372-375, 660-663; dit-graph.h:28 (dit_ggml_rms_norm_weighted), */
+/* 183-186, 328-331.                                                         */
+/* Arithmetic (ggml-cpu rms_norm_f32): float square, double sequential sum,  */
+/* mean = (float)(sum/n), scale = 1.0f/sqrtf(mean + eps), y = x * scale.     */
+/* ------------------------------------------------------------------------ */
+void orc_rms_norm_f32(const float * x, int64_t rows, int64_t n, float eps, float * y) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const float * xr  = x + r * n;
+        float *       yr  = y + r * n;
+        double        sum = 0.0;
+        for (int64_t i = 0; i < n; i++) {
+            sum += (double) (xr[i] * xr[i]);
+        }
+        const float mean  = (float) (sum / (double) n);
+        const float scale = 1.0f / sqrtf(mean + eps);
+        for (int64_t i = 0; i < n; i++) {
+            yr[i] = xr[i] * scale;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml_add / ggml_mul with broadcast of b (ggml_can_repeat(b, a)).          */
+/* Call sites: qwen3-enc.h:119 (norm * w), 238, 243 (residual add);          */
+/* qwen3-lm.h:479, 487, 730, 738; dit-graph.h:29, 61-63 (AdaLN), 74-75       */
+/* (gated residual), 391 (AdaLN vectors), 432.                              */
+/* ------------------------------------------------------------------------ */
+void orc_add_f32(const float * a, const float * b, int64_t rows, int64_t n, int64_t brows, int64_t bn, float * y) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const float * br = b + (r % brows) * bn;
+        for (int64_t i = 0; i < n; i++) {
+            y[r * n + i] = a[r * n + i] + br[i % bn];
+        }
+    }
+}
+
+void orc_mul_f32(const float * a, const float * b, int64_t rows, int64_t n, int64_t brows, int64_t bn, float * y) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const float * br = b + (r % brows) * bn;
+        for (int64_t i = 0; i < n; i++) {
+            y[r * n + i] = a[r * n + i] * br[i % bn];
+        }
+    }
+}
+
+/* ggml_clamp (qwen3-lm.h:393, 481, 489, 676, 732, 740): MAX(MIN(x, hi), lo)
+ * with the C-macro comparisons, so a NaN input yields hi. */
+void orc_clamp_f32(const float * x, int64_t n, float lo, float hi, float * y) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        const float a = x[i] < hi ? x[i] : hi;
+        y[i]          = a > lo ? a : lo;
+    }
+}
+
+/* ggml_scale (dit-graph.h:87): y = x * s */
+void orc_scale_f32(const float * x, int64_t n, float s, float * y) {
+    for (int64_t i = 0; i < n; i++) {
+        y[i] = x[i] * s;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml_rope_ext, mode 2 (NEOX).                                             */
+/* Call sites: qwen3-enc.h:173-174, qwen3-lm.h:378-379, 666-667,             */
+/* dit-graph.h:194-196 (all: n_dims = D, n_ctx_orig = 0, freq_scale = 1,     */
+/* ext_factor = 0, attn_factor = 1, beta_fast = beta_slow = 0).              */
+/* Arithmetic (ggml-cpu rope): theta_scale = powf(base, -2/n_dims); per      */
+/* position the angle starts at (float)p and is multiplied by theta_scale    */
+/* once per pair (an iterative fp32 chain); cos/sin are libm cosf/sinf       */
+/* scaled by attn_factor; pair (i, i + n_dims/2) is rotated.                 */
+/* ------------------------------------------------------------------------ */
+float orc_rope_theta_scale(float freq_base, int n_dims) {
+    return powf(freq_base, -2.0f / (float) n_dims);
+}
+
+void orc_rope_neox_f32(const float * x, int64_t n_pos, int64_t heads, int64_t ne0, int n_dims, const int32_t * pos,
+                       float freq_base, float freq_scale, float attn_factor, float * y) {
+    const float   theta_scale = orc_rope_theta_scale(freq_base, n_dims);
+    const int64_t half        = n_dims / 2;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t t = 0; t < n_pos; t++) {
+        float cache[2 * 4096];
+        float theta = (float) pos[t];
+        for (int64_t i0 = 0; i0 < ne0 && i0 < 2 * 4096; i0 += 2) {
+            const float th = freq_scale * theta; /* rope_yarn with ext_factor == 0 */
+            cache[i0 + 0]  = cosf(th) * attn_factor;
+            cache[i0 + 1]  = sinf(th) * attn_factor;
+            theta *= theta_scale;
+        }
+        for (int64_t h = 0; h < heads; h++) {
+            const float * src = x + (t * heads + h) * ne0;
+            float *       dst = y + (t * heads + h) * ne0;
+            for (int64_t ic = 0; ic < half; ic++) {
+                const float c  = cache[2 * ic + 0];
+                const float s  = cache[2 * ic + 1];
+                const float x0 = src[ic];
+                const float x1 = src[ic + half];
+                dst[ic]        = x0 * c - x1 * s;
+                dst[ic + half] = x0 * s + x1 * c;
+            }
+            for (int64_t i0 = n_dims; i0 < ne0; i0++) {
+                dst[i0] = src[i0];
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml_swiglu (fused [2I] input, gate = first half) and ggml_swiglu_split.  */
+/* Call sites: qwen3-enc.h:217, 221; dit-graph.h:259, 264.                   */
+/* Arithmetic: ggml_silu_f32(g) * u with silu(x) = x/(1.0f + expf(-x)) (the  */
+/* scalar form; ggml's SIMD lanes use a polynomial expf -- see tests).       */
+/* ------------------------------------------------------------------------ */
+void orc_swiglu_f32(const float * g, int64_t gs, const float * u, int64_t us, int64_t rows, int64_t n, float * y) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const float * gr = g + r * gs;
+        const float * ur = u + r * us;
+        float *       yr = y + r * n;
+        for (int64_t i = 0; i < n; i++) {
+            const float xg = gr[i];
+            yr[i]          = (xg / (1.0f + expf(-xg))) * ur[i];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0. Block = { fp16 d; int8 qs[32] }, 34 bytes, no padding.              */
+/* Writers: the Q8_0 KV cache ggml_cpy at songgen-lelm-gen.h:254-265 and     */
+/* 548-562 (SG_KV_TYPE=q8_0, 53-61); the Q8_0 embedding tables written by    */
+/* tools/quantize.cpp (ggml_quantize_chunk -> quantize_row_q8_0_ref).        */
+/* ------------------------------------------------------------------------ */
+static inline float round_half_away(float v) {
+    return roundf(v);
+}
+
+static inline float round_half_even(float v) {
+    return rintf(v); /* default FE_TONEAREST */
+}
+
+void orc_quantize_row_q8_0_ref(const float * x, uint8_t * y, int64_t k) {
+    const int64_t nb = k / ORC_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const float * xb   = x + i * ORC_QK8_0;
+        uint8_t *     yb   = y + i * ORC_Q8_0_SIZE;
+        float         amax = 0.0f;
+        for (int j = 0; j < ORC_QK8_0; j++) {
+            const float v = fabsf(xb[j]);
+            amax          = amax > v ? amax : v;
+        }
+        const float    d   = amax / 127.0f;
+        const float    id  = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t d16 = orc_fp32_to_fp16(d);
+        memcpy(yb, &d16, 2);
+        for (int j = 0; j < ORC_QK8_0; j++) {
+            yb[2 + j] = (uint8_t) (int8_t) round_half_away(xb[j] * id);
+        }
+    }
+}
+
+void orc_quantize_row_q8_0_x86(const float * x, uint8_t * y, int64_t k) {
+    const int64_t nb = k / ORC_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const float * xb   = x + i * ORC_QK8_0;
+        uint8_t *     yb   = y + i * ORC_Q8_0_SIZE;
+        float         amax = 0.0f;
+        for (int j = 0; j < ORC_QK8_0; j++) {
+            const float v = fabsf(xb[j]);
+            amax          = amax > v ? amax : v;
+        }
+        const float    d   = amax / 127.0f;
+        const uint16_t d16 = orc_fp32_to_fp16(d);
+        const float    id  = amax != 0.0f ? 127.0f / amax : 0.0f;
+        memcpy(yb, &d16, 2);
+        for (int j = 0; j < ORC_QK8_0; j++) {
+            float q = round_half_even(xb[j] * id);
+            /* packs_epi32 / packs_epi16 saturate */
+            q         = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
+            yb[2 + j] = (uint8_t) (int8_t) q;
+        }
+    }
+}
+
+void orc_dequantize_row_q8_0(const uint8_t * x, float * y, int64_t k) {
+    const int64_t nb = k / ORC_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const uint8_t * xb = x + i * ORC_Q8_0_SIZE;
+        uint16_t        d16;
+        memcpy(&d16, xb, 2);
+        const float d = orc_fp16_to_fp32(d16);
+        for (int j = 0; j < ORC_QK8_0; j++) {
+            y[i * ORC_QK8_0 + j] = (float) (int8_t) xb[2 + j] * d;
+        }
+    }
+}
+
+void orc_quantize_rows_q8_0(const float * x, int64_t rows, int64_t n, int variant, uint8_t * y) {
+    const int64_t rb = n / ORC_QK8_0 * ORC_Q8_0_SIZE;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        if (variant == 0) {
+            orc_quantize_row_q8_0_ref(x + r * n, y + r * rb, n);
+        } else {
+            orc_quantize_row_q8_0_x86(x + r * n, y + r * rb, n);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml_get_rows (qwen3-enc.h:390, 465; qwen3-lm.h:464, 626): one table row  */
+/* per id, dequantized/converted to F32 (ggml-cpu get_rows_q / _f16 / _bf16).*/
+/* ------------------------------------------------------------------------ */
+int orc_get_rows(const void * table, int type, int64_t n_rows, int64_t n, const int32_t * ids, int64_t n_ids,
+                 float * y) {
+    int64_t row_size;
+    switch (type) {
+        case 0:
+            row_size = n * 4;
+            break;
+        case 1:
+        case 30:
+            row_size = n * 2;
+            break;
+        case 8:
+            row_size = n / ORC_QK8_0 * ORC_Q8_0_SIZE;
+            break;
+        default:
+            return -2;
+    }
+    int bad = 0;
+#pragma omp parallel for num_threads(g_threads) schedule(static) reduction(| : bad)
+    for (int64_t i = 0; i < n_ids; i++) {
+        const int64_t r = ids[i];
+        if (r < 0 || r >= n_rows) {
+            bad = 1;
+            continue;
+        }
+        const uint8_t * src = (const uint8_t *) table + r * row_size;
+        float *         dst = y + i * n;
+        switch (type) {
+            case 0:
+                memcpy(dst, src, (size_t) n * 4);
+                break;
+            case 1:
+                orc_fp16_to_fp32_n((const uint16_t *) src, dst, n);
+                break;
+            case 30:
+                for (int64_t j = 0; j < n; j++) {
+                    dst[j] = orc_bf16_to_fp32(((const uint16_t *) src)[j]);
+                }
+                break;
+            case 8:
+                orc_dequantize_row_q8_0(src, dst, n);
+                break;
+        }
+    }
+    return bad ? -1 : 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml_timestep_embedding (dit-graph.h:90, dim 256, max_period 10000):      */
+/* freq_j = expf(-logf(max_period) * j / half); out[j] = cosf(t*freq_j),     */
+/* out[j + half] = sinf(t*freq_j); an odd dim leaves a trailing 0.           */
+/* ------------------------------------------------------------------------ */
+void orc_timestep_embedding_f32(const float * t, int64_t n, int dim, int max_period, float * y) {
+    const int half = dim / 2;
+    for (int64_t i = 0; i < n; i++) {
+        float * e = y + i * dim;
+        for (int64_t j = 0; j < half; j++) {
+            const float timestep = t[i];
+            const float freq     = expf(-logf((float) max_period) * (float) j / (float) half);
+            const float arg      = timestep * freq;
+            e[j]                 = cosf(arg);
+            e[j + half]          = sinf(arg);
+        }
+        if (dim % 2 != 0) {
+            e[2 * half] = 0.0f;
+        }
+    }
+}

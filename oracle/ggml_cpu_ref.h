@@ -1,0 +1,95 @@
+/*
+ * ggml_cpu_ref.h -- CPU oracle for the per-layer fused ops.
+ *
+ * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the ggml-cpu
+ * arithmetic that acestep.cpp's graph builders invoke (ggml itself is an
+ * empty submodule in the reference checkout, so it cannot be built here).
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load this library, and only as the checker or the timed CPU baseline --
+ * never as part of the product path.
+ *
+ * Every function is one ggml graph node, computed the way ggml-cpu computes
+ * it; composite chains are built by calling these in the order the
+ * reference's graph builders emit them (see oracle/oracle.py).
+ *
+ * Layout convention: row-major, contiguous; "rows x n" means n is the
+ * innermost (ggml ne0) dimension.
+ */
+#ifndef ORC_GGML_CPU_REF_H
+#define ORC_GGML_CPU_REF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- threading (rows are independent; results do not depend on it) ---- */
+void orc_set_threads(int n);
+int  orc_get_threads(void);
+
+/* ---- number formats ---- */
+float    orc_fp16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_fp16(float f);
+float    orc_bf16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_bf16(float f);
+void     orc_fp16_to_fp32_n(const uint16_t * x, float * y, int64_t n);
+void     orc_fp32_to_fp16_n(const float * x, uint16_t * y, int64_t n);
+void     orc_bf16_to_fp32_n(const uint16_t * x, float * y, int64_t n);
+void     orc_fp32_to_bf16_n(const float * x, uint16_t * y, int64_t n);
+
+/* ---- ggml_rms_norm: y = x * (1/sqrtf(mean(x^2) + eps)), per row of n ---- */
+void orc_rms_norm_f32(const float * x, int64_t rows, int64_t n, float eps, float * y);
+
+/* ---- ggml binary ops with ggml_can_repeat broadcasting of b.
+ *      a: rows x n; b: brows x bn with rows % brows == 0, n % bn == 0;
+ *      b index = (r % brows, i % bn).  (ggml_add / ggml_mul) ---- */
+void orc_add_f32(const float * a, const float * b, int64_t rows, int64_t n, int64_t brows, int64_t bn, float * y);
+void orc_mul_f32(const float * a, const float * b, int64_t rows, int64_t n, int64_t brows, int64_t bn, float * y);
+
+/* ---- ggml_clamp: y = MAX(MIN(x, hi), lo) ---- */
+void orc_clamp_f32(const float * x, int64_t n, float lo, float hi, float * y);
+
+/* ---- ggml_scale: y = x * s ---- */
+void orc_scale_f32(const float * x, int64_t n, float s, float * y);
+
+/* ---- ggml_rope_ext, mode NEOX (2), no freq_factors.
+ *      x: n_pos x heads x ne0 (ggml [ne0, heads, n_pos]); rotates the first
+ *      n_dims of each head row, copies the rest.  pos[n_pos] int32.
+ *      ext_factor must be 0 (the only value the reference passes). ---- */
+void orc_rope_neox_f32(const float * x, int64_t n_pos, int64_t heads, int64_t ne0, int n_dims, const int32_t * pos,
+                       float freq_base, float freq_scale, float attn_factor, float * y);
+
+/* theta_scale exactly as ggml-cpu derives it: powf(freq_base, -2.0f/n_dims) */
+float orc_rope_theta_scale(float freq_base, int n_dims);
+
+/* ---- ggml_swiglu / ggml_swiglu_split: y = silu(g) * u, silu(x) = x/(1+expf(-x)).
+ *      g, u: rows x n with row strides gs, us (elements). ---- */
+void orc_swiglu_f32(const float * g, int64_t gs, const float * u, int64_t us, int64_t rows, int64_t n, float * y);
+
+/* ---- Q8_0 (block of 32: fp16 d, int8 qs[32]; 34 bytes) ---- */
+#define ORC_QK8_0     32
+#define ORC_Q8_0_SIZE 34
+/* quantize_row_q8_0_ref: d = amax/127, id = d ? 1/d : 0, q = roundf(x*id) */
+void orc_quantize_row_q8_0_ref(const float * x, uint8_t * y, int64_t k);
+/* x86 from_float (AVX2 path): d = amax/127, id = amax ? 127/amax : 0, q = rint(x*id) */
+void orc_quantize_row_q8_0_x86(const float * x, uint8_t * y, int64_t k);
+void orc_dequantize_row_q8_0(const uint8_t * x, float * y, int64_t k);
+/* rows x n floats -> rows x (n/32*34) bytes; variant 0 = ref, 1 = x86 */
+void orc_quantize_rows_q8_0(const float * x, int64_t rows, int64_t n, int variant, uint8_t * y);
+
+/* ---- ggml_get_rows: table n_rows x n (row bytes = row_size), ids[n_ids]
+ *      -> y n_ids x n floats.  type: 0 = F32, 1 = F16, 8 = Q8_0, 30 = BF16.
+ *      Returns -1 (and writes nothing for that row) on an out-of-range id. ---- */
+int orc_get_rows(const void * table, int type, int64_t n_rows, int64_t n, const int32_t * ids, int64_t n_ids,
+                 float * y);
+
+/* ---- ggml_timestep_embedding: t[n] -> y n x dim ---- */
+void orc_timestep_embedding_f32(const float * t, int64_t n, int dim, int max_period, float * y);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,83 @@
+"""Shared test helpers: tolerance checks, bf16 plumbing, seeded inputs."""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def rng(seed: int = 42):
+    return np.random.default_rng(seed)
+
+
+def randn(shape, seed=42, scale=1.0, mean=0.0):
+    return (rng(seed).standard_normal(shape) * scale + mean).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# tolerances (the bars stated for this path)
+#   fp32: max relative error <= 1e-5; where an output is a difference that can
+#         cancel (rope, modulate, gated add) the denominator is floored at the
+#         RMS of the reference row: |a-b| <= 1e-5 * max(|ref|, rms(ref row)).
+#   bf16: within 1 bf16 ulp of the oracle's RNE-rounded fp32 result.
+# ---------------------------------------------------------------------------
+def rel_err(a: np.ndarray, ref: np.ndarray, row_floor: bool = False, tiny: float = 1e-30) -> float:
+    a = np.asarray(a, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.abs(ref)
+    if row_floor:
+        rms = np.sqrt(np.mean(ref.reshape(-1, ref.shape[-1]) ** 2, axis=-1, keepdims=True))
+        den = np.maximum(den.reshape(-1, ref.shape[-1]), rms).reshape(ref.shape)
+    den = np.maximum(den, tiny)
+    both_nan = np.isnan(a) & np.isnan(ref)
+    same_inf = np.isinf(a) & np.isinf(ref) & (np.sign(a) == np.sign(ref))
+    with np.errstate(invalid="ignore"):
+        e = np.abs(a - ref) / den
+    e[both_nan | same_inf] = 0.0
+    return float(np.max(e)) if e.size else 0.0
+
+
+def assert_f32_close(a, ref, tol=1e-5, row_floor=False):
+    e = rel_err(a, ref, row_floor=row_floor)
+    assert e <= tol, f"max relative error {e:.3e} > {tol:.1e}"
+    return e
+
+
+def bf16_ordinal(h: np.ndarray) -> np.ndarray:
+    """Monotone integer index of bf16 bit patterns (adjacent values differ by 1)."""
+    h = np.asarray(h, np.uint16).astype(np.int64)
+    mag = h & 0x7FFF
+    return np.where(h & 0x8000, -mag, mag)
+
+
+def assert_bf16_ulp(a_bits, ref_bits, max_ulp=1):
+    d = np.abs(bf16_ordinal(a_bits) - bf16_ordinal(ref_bits))
+    worst = int(d.max()) if d.size else 0
+    assert worst <= max_ulp, f"max bf16 ulp distance {worst} > {max_ulp}"
+    return worst
+
+
+def frac_bitexact(a: np.ndarray, ref: np.ndarray) -> float:
+    a = np.ascontiguousarray(a)
+    ref = np.ascontiguousarray(ref)
+    eq = a.view(np.uint8).reshape(a.size, -1) == ref.view(np.uint8).reshape(ref.size, -1)
+    return float(np.mean(np.all(eq, axis=1)))
+
+
+# ---------------------------------------------------------------------------
+# host <-> device (acestep_ops.device; bf16/f16 travel as uint16 bit patterns)
+# ---------------------------------------------------------------------------
+def to_dev(a: np.ndarray, dev=None, bf16: bool = False, f16: bool = False):
+    from acestep_ops.device import DTensor
+
+    if bf16 or f16:
+        assert a.dtype in (np.uint16, np.int16)
+        return DTensor.from_numpy(a.view(np.uint16), "bf16" if bf16 else "f16")
+    return DTensor.from_numpy(np.ascontiguousarray(a))
+
+
+def to_np(t) -> np.ndarray:
+    return t.numpy()

