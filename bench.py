@@ -4,18 +4,22 @@
 Workload (the metric's configuration): DiT block, bf16 activations, hidden
 2048, T=6000 latent frames x batch 2 (CFG pair) = 12000 rows, 16 Q / 8 KV
 heads x 128 (NEOX rope, theta 1e4, frame-index positions), SwiGLU at
-intermediate 6144. One step = the block's six fused-op launches in
-dit_ggml_build_layer order (reference dit-graph.h:367-448):
-  norm_sa  = rms_norm*w -> AdaLN modulate (hidden)
-  q, k     = QK-norm -> rope on views of the fused QKV projection output
-  h1       = hidden + sa_out * gate_sa
-  norm_ffn = rms_norm*w -> AdaLN modulate (h1)
-  ff       = swiglu(gate_up)
-  h2       = h1 + ffn_out * gate_ffn
+intermediate 6144. One step = the block's fused-op launches in
+dit_ggml_build_layer order (reference dit-graph.h:367-448), captured once
+into a HIP graph and replayed:
+  norm_sa        = rms_norm*w -> AdaLN modulate (hidden)
+  q, k           = QK-norm -> rope on views of the fused QKV projection output
+  h1, norm_ffn   = hidden + sa_out * gate_sa, and rms_norm*w -> AdaLN of it
+                   (one pass: the gated residual fused into the FFN norm)
+  ff             = swiglu(gate_up)
+  h2             = h1 + ffn_out * gate_ffn
+The same block with the residual and the norm as separate launches (six
+launches, the op-per-node structure of the reference graph) is timed too and
+reported under "unfused".
 The GEMM / attention outputs between them (qkv, sa_out, gate_up, ffn_out)
 are synthetic N(0,1) bf16 tensors resident in HBM before timing starts.
 
-value = algorithmic bytes of the six launches / measured step time (GB/s);
+value = algorithmic bytes of the step's launches / measured step time (GB/s);
 algorithmic bytes count every input read once and every output written
 once at its storage type (bf16 activations, f32 vectors).
 
@@ -44,19 +48,24 @@ THETA, EPS = 1e4, 1e-6
 HBM_PEAK_GBS = 8000.0
 
 
-def block_bytes(rows: int, es: int = 2) -> dict:
+def block_bytes(rows: int, es: int = 2, fused: bool = True) -> dict:
     """Algorithmic bytes per launch (inputs read once + outputs written once)."""
     act = rows * H * es
     vec = H * 4
     qk = rows * (NH + NKV) * D * es
-    return {
+    b = {
         "rms_norm_modulate_sa": 2 * act + 3 * vec,
         "qk_norm_rope": 2 * qk + rows * 4 + 2 * D * 4,
-        "gated_add_sa": 3 * act + vec,
-        "rms_norm_modulate_ffn": 2 * act + 3 * vec,
-        "swiglu": rows * 2 * I_FF * es + rows * I_FF * es,
-        "gated_add_ffn": 3 * act + vec,
     }
+    if fused:
+        # h1 = h + sa_out * gate_sa and norm_ffn = AdaLN(rms_norm(h1) * w) in one pass
+        b["add_rms_norm_modulate_ffn"] = 4 * act + 4 * vec
+    else:
+        b["gated_add_sa"] = 3 * act + vec
+        b["rms_norm_modulate_ffn"] = 2 * act + 3 * vec
+    b["swiglu"] = rows * 2 * I_FF * es + rows * I_FF * es
+    b["gated_add_ffn"] = 3 * act + vec
+    return b
 
 
 def bf16_bits(a: np.ndarray) -> np.ndarray:
@@ -66,7 +75,7 @@ def bf16_bits(a: np.ndarray) -> np.ndarray:
 
 def gpu_bench(steps: int, warmup: int):
     from acestep_ops import device, ops
-    from acestep_ops.device import DTensor, Event
+    from acestep_ops.device import DTensor, Event, Graph, Stream
 
     rng = np.random.default_rng(42)
 
@@ -95,42 +104,73 @@ def gpu_bench(steps: int, warmup: int):
     q_out = DTensor.empty((ROWS, NH, D), "bf16")
     k_out = DTensor.empty((ROWS, NKV, D), "bf16")
     ff = DTensor.empty((BATCH, T_FRAMES, I_FF), "bf16")
+    stream = Stream()
+    sh = stream.handle
     device.synchronize()
 
-    names = list(block_bytes(ROWS).keys())
-    launches = [
-        lambda: ops.rms_norm_modulate(hidden, sa_w, scale_sa, shift_sa, EPS, out=norm_sa),
-        lambda: ops.qk_norm_rope(q, q_w, pos, EPS, D, THETA, k=k, k_w=k_w, q_out=q_out, k_out=k_out),
-        lambda: ops.gated_add(hidden, sa_out, gate_sa, out=h1),
-        lambda: ops.rms_norm_modulate(h1, ff_w, scale_ff, shift_ff, EPS, out=norm_ff),
-        lambda: ops.swiglu(gate_up, out=ff),
-        lambda: ops.gated_add(h1, ffn_out, gate_ff, out=h2),
+    fused = [
+        lambda: ops.rms_norm_modulate(hidden, sa_w, scale_sa, shift_sa, EPS, out=norm_sa, stream=sh),
+        lambda: ops.qk_norm_rope(q, q_w, pos, EPS, D, THETA, k=k, k_w=k_w, q_out=q_out, k_out=k_out, stream=sh),
+        lambda: ops.add_rms_norm(hidden, sa_out, EPS, gate=gate_sa, w=ff_w, scale=scale_ff, shift=shift_ff,
+                                 out_sum=h1, out_norm=norm_ff, stream=sh),
+        lambda: ops.swiglu(gate_up, out=ff, stream=sh),
+        lambda: ops.gated_add(h1, ffn_out, gate_ff, out=h2, stream=sh),
+    ]
+    unfused = [
+        fused[0], fused[1],
+        lambda: ops.gated_add(hidden, sa_out, gate_sa, out=h1, stream=sh),
+        lambda: ops.rms_norm_modulate(h1, ff_w, scale_ff, shift_ff, EPS, out=norm_ff, stream=sh),
+        fused[3], fused[4],
     ]
 
-    for _ in range(warmup):
-        for f in launches:
-            f()
-    device.synchronize()
+    def graph_of(launches):
+        g = Graph()
+        with g.capture(stream):
+            for f in launches:
+                f()
+        return g
 
-    # per-kernel HIP events on the launch stream (the null stream)
-    ev = [[(Event(), Event()) for _ in launches] for _ in range(steps)]
-    step_start, step_end = Event(), Event()
+    def time_graph(g, n):
+        a, b = Event(), Event()
+        stream.synchronize()
+        a.record(sh)
+        for _ in range(n):
+            g.launch()
+        b.record(sh)
+        b.synchronize()
+        return a.elapsed_ms(b) / n
+
+    def per_kernel(launches, n):
+        ev = [[(Event(), Event()) for _ in launches] for _ in range(n)]
+        stream.synchronize()
+        for i in range(n):
+            for j, f in enumerate(launches):
+                ev[i][j][0].record(sh)
+                f()
+                ev[i][j][1].record(sh)
+        stream.synchronize()
+        return [1000.0 * float(np.mean([ev[i][j][0].elapsed_ms(ev[i][j][1]) for i in range(n)]))
+                for j in range(len(launches))]
+
+    g_fused, g_unfused = graph_of(fused), graph_of(unfused)
+    for _ in range(warmup):
+        g_fused.launch()
+        g_unfused.launch()
+    stream.synchronize()
+
+    # timed region: K graph replays of the fused block
     device.synchronize()
     t0 = time.perf_counter()
-    step_start.record()
-    for s in range(steps):
-        for j, f in enumerate(launches):
-            ev[s][j][0].record()
-            f()
-            ev[s][j][1].record()
-    step_end.record()
-    step_end.synchronize()
+    ms_step = time_graph(g_fused, steps)
     device.synchronize()
     wall = time.perf_counter() - t0
-    total_ms = step_start.elapsed_ms(step_end)
-    per_kernel_us = {n: 1000.0 * float(np.mean([ev[s][j][0].elapsed_ms(ev[s][j][1]) for s in range(steps)]))
-                     for j, n in enumerate(names)}
-    return total_ms / steps, wall, per_kernel_us
+    ms_unfused = time_graph(g_unfused, steps)
+
+    names_f = list(block_bytes(ROWS, fused=True).keys())
+    names_u = list(block_bytes(ROWS, fused=False).keys())
+    pk_f = dict(zip(names_f, per_kernel(fused, steps)))
+    pk_u = dict(zip(names_u, per_kernel(unfused, steps)))
+    return ms_step, ms_unfused, wall, pk_f, pk_u
 
 
 def cpu_bench(rows: int, reps: int, threads: int):
@@ -191,9 +231,10 @@ def main():
         print("bench.py: one process / one GPU only", file=sys.stderr)
         sys.exit(2)
 
-    kb = block_bytes(ROWS)
+    kb = block_bytes(ROWS, fused=True)
+    kb_u = block_bytes(ROWS, fused=False)
     total_bytes = sum(kb.values())
-    ms_step, wall, per_k = gpu_bench(args.steps, args.warmup)
+    ms_step, ms_unfused, wall, per_k, per_k_u = gpu_bench(args.steps, args.warmup)
     value = total_bytes / (ms_step * 1e-3) / 1e9
     dom = "swiglu"
     dom_gbs = kb[dom] / (per_k[dom] * 1e-6) / 1e9
@@ -239,10 +280,14 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "ACE-Step DiT block fused ops, bf16, H=2048, T=6000 x N=2 (12000 rows), 16/8 heads "
-                               "x 128, SwiGLU I=6144, 6 launches/step",
+                               "x 128, SwiGLU I=6144; 5 launches/step (gated residual fused into the FFN norm), "
+                               "replayed as one HIP graph",
                    "rows": ROWS, "hidden": H, "intermediate": I_FF, "bytes_per_step": total_bytes},
         "per_kernel_us": {k: round(v, 2) for k, v in per_k.items()},
         "per_kernel_gbs": {k: round(kb[k] / (per_k[k] * 1e-6) / 1e9, 1) for k in kb},
+        "unfused": {"us_per_block": round(ms_unfused * 1e3, 2), "bytes_per_step": sum(kb_u.values()),
+                    "gbs": round(sum(kb_u.values()) / (ms_unfused * 1e-3) / 1e9, 1),
+                    "per_kernel_us": {k: round(v, 2) for k, v in per_k_u.items()}},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_swiglu (bf16)",
                      "bytes_per_launch": kb[dom]},

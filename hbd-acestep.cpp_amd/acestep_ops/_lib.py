@@ -71,6 +71,7 @@ PROTOTYPES = {
     "mi_status_str": [_I],
     "mi_rms_norm": [_TP, _TP, _F, _TP, _VP],
     "mi_rms_norm_modulate": [_TP, _TP, _TP, _TP, _F, _TP, _VP],
+    "mi_add_rms_norm": [_TP, _TP, _TP, _I, _F, _F, _TP, _TP, _TP, _F, _TP, _TP, _VP],
     "mi_rope_ext": [_TP, _TP, _I, _I, _F, _F, _F, _F, _TP, _VP],
     "mi_qk_norm_rope": [_TP, _TP, _TP, _TP, _TP, _TP, _TP, _F, _I, _F, _F, _F, _VP],
     "mi_swiglu": [_TP, _I, _TP, _VP],

@@ -71,6 +71,12 @@ def hip():
             "hipGetLastError": [],
             "hipRuntimeGetVersion": [ctypes.POINTER(i)],
             "hipDeviceGetAttribute": [ctypes.POINTER(i), i, i],
+            "hipStreamBeginCapture": [vp, i],
+            "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+            "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, ctypes.c_char_p, sz],
+            "hipGraphLaunch": [vp, vp],
+            "hipGraphExecDestroy": [vp],
+            "hipGraphDestroy": [vp],
         }
         for name, args in sig.items():
             f = getattr(h, name)
@@ -293,6 +299,66 @@ class DTensor:
 
     def item(self):
         return self.numpy().reshape(-1)[0].item()
+
+
+class Stream:
+    """A HIP stream at the default priority."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        check(hip().hipStreamCreate(ctypes.byref(h)), "hipStreamCreate")
+        self.handle = h.value
+
+    def synchronize(self):
+        check(hip().hipStreamSynchronize(self.handle), "hipStreamSynchronize")
+
+    def __del__(self):
+        if getattr(self, "handle", None) and _hip is not None:
+            _hip.hipStreamDestroy(self.handle)
+            self.handle = None
+
+
+class Graph:
+    """Stream-captured HIP graph: ``with g.capture(stream): <launches>``, then ``g.launch()``."""
+
+    RELAXED = 2  # hipStreamCaptureModeRelaxed
+
+    def __init__(self):
+        self.graph = None
+        self.exec = None
+        self.stream = None
+
+    def capture(self, stream: "Stream"):
+        g = self
+
+        class _Ctx:
+            def __enter__(self):
+                g.stream = stream
+                check(hip().hipStreamBeginCapture(stream.handle, Graph.RELAXED), "hipStreamBeginCapture")
+                return g
+
+            def __exit__(self, et, ev, tb):
+                graph = ctypes.c_void_p()
+                rc = hip().hipStreamEndCapture(stream.handle, ctypes.byref(graph))
+                if et is None:
+                    check(rc, "hipStreamEndCapture")
+                    g.graph = graph.value
+                    ex = ctypes.c_void_p()
+                    check(hip().hipGraphInstantiate(ctypes.byref(ex), g.graph, None, None, 0), "hipGraphInstantiate")
+                    g.exec = ex.value
+                return False
+
+        return _Ctx()
+
+    def launch(self):
+        check(hip().hipGraphLaunch(self.exec, self.stream.handle), "hipGraphLaunch")
+
+    def __del__(self):
+        if _hip is not None:
+            if getattr(self, "exec", None):
+                _hip.hipGraphExecDestroy(self.exec)
+            if getattr(self, "graph", None):
+                _hip.hipGraphDestroy(self.graph)
 
 
 class Event:

@@ -95,6 +95,18 @@ def rms_norm_modulate(x, w, scale, shift, eps: float, out=None, stream=None):
     return y
 
 
+def add_rms_norm(residual, x, eps: float, gate=None, w=None, scale=None, shift=None, clamp=None, out_sum=None,
+                 out_norm=None, stream=None):
+    """y_sum = residual + x [* gate] (clamped to `clamp`=(lo, hi) if given);
+    y_norm = rms_norm(y_sum) [* w] [* (scale + 1) + shift]. Returns (y_sum, y_norm)."""
+    ys = _out(out_sum, residual.shape, residual.dtype)
+    yn = _out(out_norm, residual.shape, residual.dtype)
+    lo, hi = clamp if clamp is not None else (0.0, 0.0)
+    _lib.call("mi_add_rms_norm", _p(residual), _p(x), _p(gate), int(clamp is not None), lo, hi, _p(w), _p(scale),
+              _p(shift), eps, _p(ys), _p(yn), _s(stream))
+    return ys, yn
+
+
 def rope_ext(x, pos, n_dims: int, mode: int = 2, freq_base: float = 10000.0, freq_scale: float = 1.0,
              ext_factor: float = 0.0, attn_factor: float = 1.0, out=None, stream=None):
     """ggml_rope_ext. x: (..., n_pos, heads, ne0); pos: i32 (n_pos,)."""

@@ -254,6 +254,52 @@ int mi_rms_norm_modulate(const mi_tensor * x, const mi_tensor * w, const mi_tens
                                   (const float *) shift->data, eps, *y, (hipStream_t) stream));
 }
 
+int mi_add_rms_norm(const mi_tensor * residual, const mi_tensor * x, const mi_tensor * gate, int clamp, float lo,
+                    float hi, const mi_tensor * w, const mi_tensor * scale, const mi_tensor * shift, float eps,
+                    const mi_tensor * y_sum, const mi_tensor * y_norm, mi_stream stream) {
+    MI_TRY(check_act(residual));
+    MI_TRY(check_act(x));
+    MI_TRY(check_act(y_sum));
+    MI_TRY(check_act(y_norm));
+    if (!same_shape(*residual, *x) || !same_shape(*residual, *y_sum) || !same_shape(*residual, *y_norm)) {
+        return MI_ERR_SHAPE;
+    }
+    if (x->type != residual->type || y_sum->type != residual->type || y_norm->type != residual->type) {
+        return MI_ERR_TYPE;
+    }
+    const int64_t n = residual->ne[0];
+    if (gate) {
+        MI_TRY(check_vec(gate, n));
+    }
+    if (w) {
+        MI_TRY(check_vec(w, n));
+    }
+    if ((scale == nullptr) != (shift == nullptr) || (scale && !w)) {
+        return MI_ERR_NULL;
+    }
+    if (scale) {
+        MI_TRY(check_vec(scale, n));
+        MI_TRY(check_vec(shift, n));
+    }
+    if (!(eps >= 0.0f) || std::isinf(eps) || (clamp && (std::isnan(lo) || std::isnan(hi)))) {
+        return MI_ERR_PARAM;
+    }
+    if (y_norm->data == residual->data || y_norm->data == x->data || y_norm->data == y_sum->data) {
+        return MI_ERR_PARAM;  // y_norm must not alias an input or y_sum
+    }
+    AddNorm add;
+    add.x2    = x;
+    add.gate  = gate ? (const float *) gate->data : nullptr;
+    add.clamp = clamp ? 1 : 0;
+    add.lo    = lo;
+    add.hi    = hi;
+    add.ysum  = y_sum;
+    return finish(launch_rms_norm(*residual, w ? (const float *) w->data : nullptr,
+                                  scale ? (const float *) scale->data : nullptr,
+                                  shift ? (const float *) shift->data : nullptr, eps, *y_norm, (hipStream_t) stream,
+                                  &add));
+}
+
 static int rope_common(const mi_tensor * q, const mi_tensor * q_w, const mi_tensor * q_out, const mi_tensor * k,
                        const mi_tensor * k_w, const mi_tensor * k_out, const mi_tensor * pos, float eps, int n_dims,
                        float freq_base, float freq_scale, float attn_factor, bool norm, bool rope,

@@ -9,9 +9,10 @@
 // (qwen3-lm.h:481, 732). Each result is rounded exactly as the separate
 // ggml nodes round it.
 //
-// Fast path: like the norm kernel, a workgroup spans whole rows and each
-// thread owns fixed 16-byte column vectors, so v0/v1 stay in registers;
-// R rows are loaded before any is computed.
+// Fast path: a flat one-shot grid, one (or MI_BIN_U) 16-byte vector per
+// thread, the F32 column vectors read through the caches. The row-stationary
+// kernel (a workgroup spans whole rows, each thread keeps its column vectors
+// in registers) remains for builds with MI_BIN_FLAT=0.
 #include "launch.h"
 
 namespace mi {
@@ -132,6 +133,79 @@ __global__ void __launch_bounds__(512) k_bin_rows(const BinArgs a) {
     }
 }
 
+#ifndef MI_BIN_FLAT
+#define MI_BIN_FLAT 1  // flat one-shot grid (U vectors per thread) instead of row-stationary
+#endif
+#ifndef MI_BIN_U
+#define MI_BIN_U 1
+#endif
+
+// Flat one-shot grid: thread (block b, lane t) handles vectors
+// v = b*256*U + k*256 + t of the [rows x nvr] vector grid; the F32 column
+// vectors are read through the caches (a few KB, shared by every row).
+template <int T_, int OP, bool BROW, int U>
+__global__ void __launch_bounds__(256) k_bin_flat(const BinArgs a, uint32_t nvr, FastDiv dnvr, uint32_t total) {
+    constexpr int  VI = TT<T_>::VEC;
+    constexpr int  ES = TT<T_>::ES;
+    constexpr bool V0 = (OP == OP_GATED || OP == OP_MOD || ((OP == OP_ADD || OP == OP_MUL) && !BROW));
+    constexpr bool V1 = (OP == OP_MOD);
+    constexpr bool LB = BROW || OP == OP_GATED;
+    const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
+    uint4          ra[U], rb[U];
+    uint32_t       row[U], col[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint32_t v = base + k * 256u;
+        if (v < total) {
+            row[k] = dnvr.div(v);
+            col[k] = v - row[k] * nvr;
+            ra[k]  = ld16(a.a + a.ar.off(row[k]) + (size_t) col[k] * 16);
+            if constexpr (LB) {
+                rb[k] = ld16(a.b + a.br.off(row[k]) + (size_t) col[k] * 16);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint32_t v = base + k * 256u;
+        if (v >= total) {
+            continue;
+        }
+        float fa[VI], fb[VI], fy[VI], c0[VI], c1[VI];
+        unpack16<T_>(ra[k], fa);
+        if constexpr (LB) {
+            unpack16<T_>(rb[k], fb);
+        }
+        const int c = (int) col[k] * VI;
+#pragma unroll
+        for (int e = 0; e < VI; e += 4) {
+            if constexpr (V0) {
+                const float4 q = *(const float4 *) (a.v0 + c + e);
+                c0[e + 0]      = OP == OP_MOD ? q.x + 1.0f : q.x;
+                c0[e + 1]      = OP == OP_MOD ? q.y + 1.0f : q.y;
+                c0[e + 2]      = OP == OP_MOD ? q.z + 1.0f : q.z;
+                c0[e + 3]      = OP == OP_MOD ? q.w + 1.0f : q.w;
+            }
+            if constexpr (V1) {
+                const float4 q = *(const float4 *) (a.v1 + c + e);
+                c1[e + 0]      = q.x;
+                c1[e + 1]      = q.y;
+                c1[e + 2]      = q.z;
+                c1[e + 3]      = q.w;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < VI; ++e) {
+            float v = bin_apply<OP, BROW>(fa[e], LB ? fb[e] : 0.0f, V0 ? c0[e] : 0.0f, V1 ? c1[e] : 0.0f);
+            if (a.clamp) {
+                v = clamp_ggml(v, a.lo, a.hi);
+            }
+            fy[e] = v;
+        }
+        st16(a.y + a.yr.off(row[k]) + (size_t) col[k] * VI * ES, pack16<T_>(fy));
+    }
+}
+
 // Generic path: any types, any strides, ggml_can_repeat broadcast of b.
 struct BinGenArgs {
     const char *  a;
@@ -243,6 +317,33 @@ static int launch_rows_c(const BinArgs & a, int T, int C, hipStream_t s) {
     }
 }
 
+template <int T_, int OP, bool BROW>
+static int launch_flat_op(const BinArgs & a, hipStream_t s) {
+    constexpr int  VI    = TT<T_>::VEC;
+    const uint32_t nvr   = (uint32_t) (a.n / VI);
+    const uint64_t total = (uint64_t) a.rows * nvr;
+    const uint32_t grid  = (uint32_t) ((total + 256u * MI_BIN_U - 1) / (256u * MI_BIN_U));
+    hipLaunchKernelGGL((k_bin_flat<T_, OP, BROW, MI_BIN_U>), dim3(grid), dim3(256), 0, s, a, nvr, FastDiv(nvr),
+                       (uint32_t) total);
+    return MI_OK;
+}
+
+template <int T_>
+static int launch_flat(int op, bool brow, const BinArgs & a, hipStream_t s) {
+    switch (op) {
+        case OP_ADD:
+            return brow ? launch_flat_op<T_, OP_ADD, true>(a, s) : launch_flat_op<T_, OP_ADD, false>(a, s);
+        case OP_MUL:
+            return brow ? launch_flat_op<T_, OP_MUL, true>(a, s) : launch_flat_op<T_, OP_MUL, false>(a, s);
+        case OP_GATED:
+            return launch_flat_op<T_, OP_GATED, true>(a, s);
+        case OP_MOD:
+            return launch_flat_op<T_, OP_MOD, false>(a, s);
+        default:
+            return launch_flat_op<T_, OP_NONE, false>(a, s);
+    }
+}
+
 template <int T_>
 static int launch_rows_op(int op, bool brow, const BinArgs & a, int T, int C, hipStream_t s) {
     switch (op) {
@@ -314,6 +415,23 @@ int launch_binary(int op, const mi_tensor & a, const mi_tensor * b, const float 
 
     bool      fast = a.type == y.type && (!b || b->type == a.type) && is_act(a.type);
     const int VI   = fast ? 16 / type_size(a.type) : 1;
+    // flat one-shot path: rows of whole 16-byte vectors, 16-byte aligned
+    bool flat = MI_BIN_FLAT && fast && k.n % VI == 0 && aligned(a.data, 16) && aligned(y.data, 16) &&
+                (!b || aligned(b->data, 16)) && (!v0 || aligned(v0, 16)) && (!v1 || aligned(v1, 16)) &&
+                (uint64_t) k.rows * (k.n / VI) < (1ull << 31);
+    for (int d = 1; d < 4 && flat; ++d) {
+        flat = a.nb[d] % 16 == 0 && y.nb[d] % 16 == 0 && (!b || b->nb[d] % 16 == 0);
+    }
+    if (flat) {
+        switch (a.type) {
+            case MI_TYPE_F32:
+                return launch_flat<MI_TYPE_F32>(op, b != nullptr, k, s);
+            case MI_TYPE_BF16:
+                return launch_flat<MI_TYPE_BF16>(op, b != nullptr, k, s);
+            default:
+                return launch_flat<MI_TYPE_F16>(op, b != nullptr, k, s);
+        }
+    }
     int       T = 0, C = 0;
     if (fast && k.n % (64 * VI) == 0) {
         const int kc = k.n / (64 * VI);

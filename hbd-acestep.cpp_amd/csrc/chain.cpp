@@ -57,18 +57,24 @@ extern "C" int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream s) {
     // [QKV GEMM] -> QK-norm -> rope (dit-graph.h:183-198)
     MI_TRY(mi_qk_norm_rope(&io->q, &io->q_w, &io->q_out, &io->k, &io->k_w, &io->k_out, &io->pos, io->eps,
                            io->n_dims, io->rope_freq_base, 1.0f, 1.0f, s));
-    // [FA, O-proj] -> gated residual (dit-graph.h:420)
-    MI_TRY(mi_gated_add(&io->hidden, &io->sa_out, &gate_sa, &io->hidden, s));
+    // [FA, O-proj] -> gated residual (dit-graph.h:420), fused with the norm
+    // that reads it: the cross-attention RMSNorm*w (429) or, without cross
+    // attention, the FFN RMSNorm*w -> AdaLN (442-443)
     if (io->use_cross_attn) {
-        // cross-attention norm and Q-norm (dit-graph.h:429, 328-329), residual add (432)
-        MI_TRY(mi_rms_norm(&io->hidden, &io->ca_norm_w, io->eps, &io->norm_ca, s));
+        MI_TRY(mi_add_rms_norm(&io->hidden, &io->sa_out, &gate_sa, 0, 0.0f, 0.0f, &io->ca_norm_w, nullptr, nullptr,
+                               io->eps, &io->hidden, &io->norm_ca, s));
+        // cross-attention Q-norm (328-329)
         if (io->ca_q.data) {
             MI_TRY(mi_rms_norm(&io->ca_q, &io->ca_q_w, io->eps, &io->ca_q_out, s));
         }
-        MI_TRY(mi_add(&io->hidden, &io->ca_out, &io->hidden, s));
+        // [CA, O-proj] -> residual add (432) fused with the FFN norm (442-443)
+        MI_TRY(mi_add_rms_norm(&io->hidden, &io->ca_out, nullptr, 0, 0.0f, 0.0f, &io->ffn_norm_w, &scale_ff,
+                               &shift_ff, io->eps, &io->hidden, &io->norm_ffn, s));
+    } else {
+        MI_TRY(mi_add_rms_norm(&io->hidden, &io->sa_out, &gate_sa, 0, 0.0f, 0.0f, &io->ffn_norm_w, &scale_ff,
+                               &shift_ff, io->eps, &io->hidden, &io->norm_ffn, s));
     }
-    // FFN: RMSNorm*w -> AdaLN (442-443) -> [gate_up GEMM] -> SwiGLU (259)
-    MI_TRY(mi_rms_norm_modulate(&io->hidden, &io->ffn_norm_w, &scale_ff, &shift_ff, io->eps, &io->norm_ffn, s));
+    // [gate_up GEMM] -> SwiGLU (259)
     MI_TRY(mi_swiglu(&io->gate_up, 0, &io->ff, s));
     // [down GEMM] -> gated residual (445)
     MI_TRY(mi_gated_add(&io->hidden, &io->ffn_out, &gate_ff, &io->hidden, s));
@@ -101,14 +107,11 @@ extern "C" int mi_qwen3_layer_ops(const mi_qwen3_layer_io * io, mi_stream s) {
         MI_TRY(mi_kv_store(&kk, &io->k_cache, io->v.data ? &vv : nullptr, io->v.data ? &io->v_cache : nullptr,
                            &io->pos0, io->sets.data ? &io->sets : nullptr, io->kv_rounding, io->d_err, s));
     }
-    // [FA, O-proj] -> residual add (+ clamp) (730-733)
-    if (io->clamp_fp16) {
-        MI_TRY(mi_add_clamp(&io->hidden, &io->attn_out, -lim, lim, &io->hidden, s));
-    } else {
-        MI_TRY(mi_add(&io->hidden, &io->attn_out, &io->hidden, s));
-    }
-    // post-attention RMSNorm (736) -> [gate_up GEMM] -> SwiGLU (737)
-    MI_TRY(mi_rms_norm(&io->hidden, &io->post_norm_w, io->eps, &io->norm2, s));
+    // [FA, O-proj] -> residual add (+ clamp) (730-733) fused with the
+    // post-attention RMSNorm (736)
+    MI_TRY(mi_add_rms_norm(&io->hidden, &io->attn_out, nullptr, io->clamp_fp16, -lim, lim, &io->post_norm_w, nullptr,
+                           nullptr, io->eps, &io->hidden, &io->norm2, s));
+    // [gate_up GEMM] -> SwiGLU (737)
     MI_TRY(mi_swiglu(&io->gate_up, 0, &io->ff, s));
     // [down GEMM] -> residual add (+ clamp) (738-741)
     if (io->clamp_fp16) {

@@ -185,12 +185,42 @@ template <> __device__ __forceinline__ void store_elem<MI_TYPE_F16>(char * p, fl
     *(uint16_t *) p = f32_to_f16_bits(v);
 }
 
+// Streaming (activation) loads/stores. MI_NT_LD / MI_NT_ST select the
+// non-temporal cache policy (each activation byte is touched once).
+#ifndef MI_NT_LD
+#define MI_NT_LD 1
+#endif
+#ifndef MI_NT_ST
+#define MI_NT_ST 1
+#endif
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint4 ld16(const char * p) {
+#if MI_NT_LD
+    const u32x4 v = __builtin_nontemporal_load((const u32x4 *) p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
     return *(const uint4 *) p;
+#endif
 }
 
 __device__ __forceinline__ void st16(char * p, const uint4 & v) {
+#if MI_NT_ST
+    const u32x4 w = { v.x, v.y, v.z, v.w };
+    __builtin_nontemporal_store(w, (u32x4 *) p);
+#else
     *(uint4 *) p = v;
+#endif
+}
+
+__device__ __forceinline__ void st8(char * p, const uint2 & v) {
+#if MI_NT_ST
+    const u32x2 w = { v.x, v.y };
+    __builtin_nontemporal_store(w, (u32x2 *) p);
+#else
+    *(uint2 *) p = v;
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -274,9 +304,12 @@ __device__ __forceinline__ float log_f32(float x) {
     return (float) log((double) x);
 }
 
-// ggml-cpu rms_norm scale from the double sum of float squares.
+// ggml-cpu rms_norm scale from the double sum of float squares:
+// mean = (float)(sum / n), scale = 1.0f / sqrtf(mean + eps). For n a power of
+// two, sum / n == sum * (1/n) exactly (a sum of float squares is never a
+// double subnormal), so the division becomes a multiply.
 __device__ __forceinline__ float rms_scale(double sum, int n, float eps) {
-    const float mean = (float) (sum / (double) n);
+    const float mean = (n & (n - 1)) == 0 ? (float) (sum * (1.0 / (double) n)) : (float) (sum / (double) n);
     return 1.0f / sqrtf(mean + eps);
 }
 
@@ -328,12 +361,18 @@ inline bool aligned(const void * p, size_t a) {
 }
 
 // Row addressing for [ne0, ne1, ne2, ne3] views: row r -> (i1, i2, i3).
+// When the rows are uniformly strided (nb2 == ne1*nb1, nb3 == ne2*nb2, the
+// usual case) the offset is one multiply.
 struct Rows3 {
     FastDiv  d1, d12;   // ne1, ne1*ne2
     uint32_t ne1, ne2;
     int64_t  s1, s2, s3; // byte strides
+    int      uni;       // rows uniformly strided by s1
 
     __device__ __forceinline__ int64_t off(uint32_t r) const {
+        if (uni) {
+            return (int64_t) r * s1;
+        }
         const uint32_t i3  = d12.div(r);
         const uint32_t rem = r - i3 * (ne1 * ne2);
         const uint32_t i2  = d1.div(rem);
@@ -351,6 +390,9 @@ inline Rows3 make_rows3(const mi_tensor & t) {
     r.s1  = (int64_t) t.nb[1];
     r.s2  = (int64_t) t.nb[2];
     r.s3  = (int64_t) t.nb[3];
+    // row r sits at r*nb1 iff every used outer stride is the packed one
+    r.uni = (t.ne[2] <= 1 || t.nb[2] == t.nb[1] * (uint64_t) t.ne[1]) &&
+            (t.ne[3] <= 1 || t.nb[3] == t.nb[1] * (uint64_t) (t.ne[1] * t.ne[2]));
     return r;
 }
 

@@ -90,10 +90,14 @@ __global__ void __launch_bounds__(256) k_swiglu_generic(const char * g, const ch
     }
 }
 
+#ifndef MI_GLU_U
+#define MI_GLU_U 2  // 16-byte vectors of g and u per thread
+#endif
+
 template <int TI, int TO>
 static int launch_t(const GluArgs & a, bool fast, int64_t rows, int64_t n, hipStream_t s) {
     if (fast) {
-        constexpr int  U    = 2;
+        constexpr int  U    = MI_GLU_U;
         const uint32_t grid = (a.total + 256u * U - 1) / (256u * U);
         hipLaunchKernelGGL((k_swiglu<TI, TO, U>), dim3(grid), dim3(256), 0, s, a);
         return MI_OK;

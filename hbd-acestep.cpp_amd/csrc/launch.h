@@ -23,21 +23,30 @@ template <int TO, int N> __device__ __forceinline__ void store_vec(char * p, con
         } else {
             v = make_uint2(pack_f16x2(f[0], f[1]), pack_f16x2(f[2], f[3]));
         }
-        *(uint2 *) p = v;
+        st8(p, v);
     }
 }
 
 // ---- norm.hip --------------------------------------------------------------
-// mode 0: rms_norm; 1: rms_norm * w; 2: (rms_norm * w) * (sc + 1) + sh
+// mode 0: rms_norm; 1: rms_norm * w; 2: (rms_norm * w) * (sc + 1) + sh.
+// With `add`, the normalized row is the residual sum x + x2 (* gate),
+// optionally clamped, which is also stored to add->ysum.
+struct AddNorm {
+    const mi_tensor * x2;
+    const float *     gate;
+    int               clamp;
+    float             lo, hi;
+    const mi_tensor * ysum;
+};
+
 int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, const float * sh, float eps,
-                    const mi_tensor & y, hipStream_t s);
+                    const mi_tensor & y, hipStream_t s, const AddNorm * add = nullptr);
 
 // ---- rope.hip --------------------------------------------------------------
 struct HeadSeg {
     const char * x;
     char *       y;
     uint32_t     heads;
-    FastDiv      hdiv;  // rows per WG -> (token, head) split
     int64_t      xs1, xs2, xs3, ys1, ys2, ys3;
     const float * w;
 };

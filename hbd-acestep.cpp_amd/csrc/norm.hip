@@ -30,9 +30,34 @@ struct NormArgs {
     const float * w;
     const float * sc;
     const float * sh;
+    // fused residual add in front of the norm (ADD != 0):
+    //   v = x + x2 (ADD 1) or x + x2 * gate (ADD 2), optionally clamped;
+    //   v is stored (ysum, rounded to the activation type) and normalized.
+    const char *  x2;
+    Rows3         x2r;
+    char *        ysum;
+    Rows3         ysr;
+    const float * gate;
+    int           clamp;
+    float         lo, hi;
 };
 
-template <int TI, int TO, int MODE, int C, int R>
+#ifndef MI_NORM_R
+#define MI_NORM_R 4  // rows per workgroup iteration when each thread owns one vector
+#endif
+
+// round an fp32 value to the storage type and back (identity for F32)
+template <int T> __device__ __forceinline__ float round_to(float v) {
+    if constexpr (T == MI_TYPE_BF16) {
+        return __uint_as_float((uint32_t) f32_to_bf16_bits(v) << 16);
+    } else if constexpr (T == MI_TYPE_F16) {
+        return (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(v));
+    } else {
+        return v;
+    }
+}
+
+template <int TI, int TO, int MODE, int ADD, int C, int R>
 __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
     constexpr int VI = TT<TI>::VEC;
     constexpr int EI = TT<TI>::ES;
@@ -45,7 +70,21 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
 
     __shared__ double part[2][R][8];
 
-    float wv[C][VI], sv[C][VI], hv[C][VI];
+    float wv[C][VI], sv[C][VI], hv[C][VI], gv[C][VI];
+    if constexpr (ADD == 2) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const int col = (j * T + tid) * VI;
+#pragma unroll
+            for (int e = 0; e < VI; e += 4) {
+                const float4 g4 = *(const float4 *) (a.gate + col + e);
+                gv[j][e + 0]    = g4.x;
+                gv[j][e + 1]    = g4.y;
+                gv[j][e + 2]    = g4.z;
+                gv[j][e + 3]    = g4.w;
+            }
+        }
+    }
     if constexpr (MODE >= 1) {
 #pragma unroll
         for (int j = 0; j < C; ++j) {
@@ -75,20 +114,70 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
 
     int it = 0;
     for (uint32_t rbase = blockIdx.x * R; rbase < a.rows; rbase += gridDim.x * R, ++it) {
-        uint4 raw[R][C];
+        uint4 raw[R][C], raw2[ADD ? R : 1][ADD ? C : 1];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t row = rbase + r;
             if (row < a.rows) {
-                const char * xp = a.x + a.xr.off(row);
+                const char * xp  = a.x + a.xr.off(row);
+                const char * x2p = ADD ? a.x2 + a.x2r.off(row) : nullptr;
 #pragma unroll
                 for (int j = 0; j < C; ++j) {
                     raw[r][j] = ld16(xp + (size_t) ((j * T + tid) * VI) * EI);
+                    if constexpr (ADD != 0) {
+                        raw2[r][j] = ld16(x2p + (size_t) ((j * T + tid) * VI) * EI);
+                    }
                 }
             } else {
 #pragma unroll
                 for (int j = 0; j < C; ++j) {
                     raw[r][j] = make_uint4(0, 0, 0, 0);
+                    if constexpr (ADD != 0) {
+                        raw2[r][j] = make_uint4(0, 0, 0, 0);
+                    }
+                }
+            }
+        }
+        // residual add (ggml_add / dit_ggml_gated_add, then ggml_clamp); the
+        // sum is rounded to the activation type first, exactly as the unfused
+        // add kernel would store it and the norm kernel read it back
+        float xin[R][C][VI];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int j = 0; j < C; ++j) {
+                unpack16<TI>(raw[r][j], xin[r][j]);
+                if constexpr (ADD != 0) {
+                    float f2[VI];
+                    unpack16<TI>(raw2[r][j], f2);
+#pragma unroll
+                    for (int e = 0; e < VI; ++e) {
+                        float v;
+                        if constexpr (ADD == 2) {
+                            const float gx = f2[e] * gv[j][e];
+                            v              = xin[r][j][e] + gx;
+                        } else {
+                            v = xin[r][j][e] + f2[e];
+                        }
+                        if (a.clamp) {
+                            const float c = v < a.hi ? v : a.hi;
+                            v             = c > a.lo ? c : a.lo;
+                        }
+                        xin[r][j][e] = round_to<TO>(v);
+                    }
+                }
+            }
+        }
+        if constexpr (ADD != 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t row = rbase + r;
+                if (row < a.rows) {
+                    char * sp = a.ysum + a.ysr.off(row);
+#pragma unroll
+                    for (int j = 0; j < C; ++j) {
+                        store_vec<TO, VI>(sp + (size_t) ((j * T + tid) * VI) * EO, xin[r][j]);
+                    }
                 }
             }
         }
@@ -98,11 +187,9 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
             s[r] = 0.0;
 #pragma unroll
             for (int j = 0; j < C; ++j) {
-                float f[VI];
-                unpack16<TI>(raw[r][j], f);
 #pragma unroll
                 for (int e = 0; e < VI; ++e) {
-                    s[r] += (double) (f[e] * f[e]);
+                    s[r] += (double) (xin[r][j][e] * xin[r][j][e]);
                 }
             }
             s[r] = group_sum<64>(s[r]);
@@ -129,10 +216,9 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
 #pragma unroll
             for (int j = 0; j < C; ++j) {
                 float f[VI];
-                unpack16<TI>(raw[r][j], f);
 #pragma unroll
                 for (int e = 0; e < VI; ++e) {
-                    float v = f[e] * scale;
+                    float v = xin[r][j][e] * scale;
                     if constexpr (MODE >= 1) {
                         v = v * wv[j][e];
                     }
@@ -148,7 +234,6 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
     }
 }
 
-// Any row length, element-aligned rows: one wave per row, scalar accesses.
 template <int TI, int TO, int MODE>
 __global__ void __launch_bounds__(256) k_rms_rows_generic(const NormArgs a) {
     constexpr int EI    = TT<TI>::ES;
@@ -156,17 +241,44 @@ __global__ void __launch_bounds__(256) k_rms_rows_generic(const NormArgs a) {
     const int     lane  = threadIdx.x & 63;
     const int     wpb   = blockDim.x >> 6;
     for (uint32_t row = blockIdx.x * wpb + (threadIdx.x >> 6); row < a.rows; row += gridDim.x * wpb) {
-        const char * xp = a.x + a.xr.off(row);
-        char *       yp = a.y + a.yr.off(row);
-        double       s  = 0.0;
+        const char * xp  = a.x + a.xr.off(row);
+        const char * x2p = a.x2 ? a.x2 + a.x2r.off(row) : nullptr;
+        char *       sp  = a.x2 ? a.ysum + a.ysr.off(row) : nullptr;
+        char *       yp  = a.y + a.yr.off(row);
+        // input of the norm: x, or the (clamped) residual sum rounded to the
+        // activation type as it is stored
+        auto xval = [&](int i) {
+            float v = load_elem<TI>(xp + (size_t) i * EI);
+            if (x2p) {
+                const float f2 = load_elem<TI>(x2p + (size_t) i * EI);
+                if (a.gate) {
+                    const float gx = f2 * a.gate[i];
+                    v              = v + gx;
+                } else {
+                    v = v + f2;
+                }
+                if (a.clamp) {
+                    const float c = v < a.hi ? v : a.hi;
+                    v             = c > a.lo ? c : a.lo;
+                }
+                v = round_to<TO>(v);
+            }
+            return v;
+        };
+        double s = 0.0;
         for (int i = lane; i < a.n; i += 64) {
-            const float f = load_elem<TI>(xp + (size_t) i * EI);
+            const float f = xval(i);
+            if (sp) {
+                store_elem<TO>(sp + (size_t) i * EO, f);
+            }
             s += (double) (f * f);
         }
         s                 = group_sum<64>(s);
         const float scale = rms_scale(s, a.n, a.eps);
         for (int i = lane; i < a.n; i += 64) {
-            float v = load_elem<TI>(xp + (size_t) i * EI) * scale;
+            // with a fused add, read back this lane's stored sum (ysum may
+            // alias the residual input, so the sum is not recomputed)
+            float v = (sp ? load_elem<TO>(sp + (size_t) i * EO) : load_elem<TI>(xp + (size_t) i * EI)) * scale;
             if constexpr (MODE >= 1) {
                 v = v * a.w[i];
             }
@@ -189,30 +301,41 @@ static uint32_t balanced_grid(uint32_t rows, int R, int nw) {
     return (iters + per - 1) / per;
 }
 
-template <int TI, int TO, int MODE>
-static int dispatch_fast(const NormArgs & a, int T, int C, hipStream_t s) {
+template <int TI, int TO, int MODE, int ADD>
+static int dispatch_fast_add(const NormArgs & a, int T, int C, hipStream_t s) {
     const int nw = T / 64;
     switch (C) {
         case 1:
-            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, 1, 4>), dim3(balanced_grid(a.rows, 4, nw)), dim3(T), 0, s,
-                               a);
+            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, ADD, 1, MI_NORM_R>),
+                               dim3(balanced_grid(a.rows, MI_NORM_R, nw)), dim3(T), 0, s, a);
             break;
         case 2:
-            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, 2, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0, s,
-                               a);
+            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, ADD, 2, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
+                               s, a);
             break;
         case 3:
-            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, 3, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0, s,
-                               a);
+            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, ADD, 3, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
+                               s, a);
             break;
         case 4:
-            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, 4, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0, s,
-                               a);
+            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, ADD, 4, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
+                               s, a);
             break;
         default:
             return MI_ERR_UNSUPPORTED;
     }
     return MI_OK;
+}
+
+template <int TI, int TO, int MODE>
+static int dispatch_fast(const NormArgs & a, int T, int C, hipStream_t s) {
+    if (a.x2 == nullptr) {
+        return dispatch_fast_add<TI, TO, MODE, 0>(a, T, C, s);
+    }
+    if (a.gate == nullptr) {
+        return dispatch_fast_add<TI, TO, MODE, 1>(a, T, C, s);
+    }
+    return dispatch_fast_add<TI, TO, MODE, 2>(a, T, C, s);
 }
 
 template <int TI, int TO>
@@ -246,8 +369,8 @@ static int dispatch_types(const NormArgs & a, int mode, bool fast, int T, int C,
 }
 
 int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, const float * sh, float eps,
-                    const mi_tensor & y, hipStream_t s) {
-    NormArgs a;
+                    const mi_tensor & y, hipStream_t s, const AddNorm * add) {
+    NormArgs a{};
     a.x    = (const char *) x.data;
     a.y    = (char *) y.data;
     a.xr   = make_rows3(x);
@@ -258,6 +381,16 @@ int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, cons
     a.w    = w;
     a.sc   = sc;
     a.sh   = sh;
+    if (add) {
+        a.x2    = (const char *) add->x2->data;
+        a.x2r   = make_rows3(*add->x2);
+        a.ysum  = (char *) add->ysum->data;
+        a.ysr   = make_rows3(*add->ysum);
+        a.gate  = add->gate;
+        a.clamp = add->clamp;
+        a.lo    = add->lo;
+        a.hi    = add->hi;
+    }
     if (a.rows == 0 || a.n == 0) {
         return MI_OK;
     }
@@ -287,6 +420,13 @@ int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, cons
     }
     fast = fast && aligned(x.data, 16) && aligned(y.data, 16) && (!w || aligned(w, 16)) &&
            (!sc || aligned(sc, 16)) && (!sh || aligned(sh, 16));
+    if (add) {
+        fast = fast && add->x2->type == x.type && add->ysum->type == x.type && aligned(add->x2->data, 16) &&
+               aligned(add->ysum->data, 16) && (!add->gate || aligned(add->gate, 16));
+        for (int d = 1; d < 4 && fast; ++d) {
+            fast = add->x2->nb[d] % 16 == 0 && add->ysum->nb[d] % 16 == 0;
+        }
+    }
 
     switch (x.type) {
         case MI_TYPE_F32:

@@ -6,133 +6,197 @@
 //   ggml_rope_ext mode 2 (NEOX): for pair i < n_dims/2
 //     theta_0 = (float)pos, theta_{i+1} = theta_i * theta_scale   (fp32 chain)
 //     c = cosf(freq_scale*theta_i)*attn_factor, s = sinf(...)*attn_factor
-//     (cos/sin evaluated in double, rounded once to fp32)
+//     (cos/sin from sincos_rot, trig.h: |error| < 1e-7 against exact sin/cos)
 //     y_i = n_i*c - n_{i+h}*s ;  y_{i+h} = n_i*s + n_{i+h}*c     (h = n_dims/2)
 // theta_scale = powf(freq_base, -2/n_dims) is computed on the host, with the
 // host libm, as ggml-cpu does.
 //
-// Fast path (n_dims == ne0 == D in {64, 128, 256}): a lane holds 16 bytes of
-// the first half of a head row and the matching 16 bytes of the second
-// half, so both members of every rotated pair are in the same lane (no
-// cross-lane exchange for the rotation). A head row is spread over
-// L = D/2/VEC lanes and reduced with DPP. Each workgroup covers TPB tokens;
-// their cos/sin tables (one (pos, pair) per thread) are built once in LDS and
-// shared by all Q and K heads of those tokens. Inputs may be strided views of
-// the fused QKV projection output, so no separate contiguous copy is needed.
+// Fast path (n_dims == ne0 == D in {64, 128, 256}): one wave per token. A
+// lane holds 16 bytes of the first half of a head row and the matching 16
+// bytes of the second half, so both members of every rotated pair are in the
+// same lane (no cross-lane exchange for the rotation). A head row is spread
+// over L = D/2/VEC lanes and reduced with DPP. The token's cos/sin table is
+// built once per token in LDS and reused for all its Q and K head rows.
+// Inputs may be strided views of the fused QKV projection output, so no
+// separate contiguous copy is needed.
 #include "launch.h"
+#include "trig.h"
 
 namespace mi {
 
+#ifndef MI_ROPE_PF
+#define MI_ROPE_PF 3  // row batches (64/L head rows each) loaded ahead per wave
+#endif
+
+// One wave per token (grid-stride over tokens). Lane 0 runs the token's fp32
+// theta chain into LDS, lane l turns theta_l into cos/sin (sincos_rot) and
+// stores them back, and every lane then reads the VEC pairs it rotates. The
+// wave streams the token's head rows in batches of R = 64/L rows, Q rows
+// first, then K rows; a batch never mixes Q and K, so the segment (pointers,
+// strides, weights) is wave-uniform and its addressing stays scalar. Loads of
+// the first PF batches are issued before the trig so their latency hides
+// behind it. Lanes whose row lies past the segment end load nothing and
+// store nothing (whole L-lane groups, so the DPP row sums stay per group).
+// The Q/K norm weights are staged once per workgroup in LDS.
 template <int TI, int TO, int D, bool NORM, bool ROPE>
-__global__ void __launch_bounds__(256) k_heads(const HeadArgs a) {
+__global__ void __launch_bounds__(256) k_heads(const HeadArgs a, uint32_t nb0, uint32_t nb) {
     constexpr int VI   = TT<TI>::VEC;
     constexpr int EI   = TT<TI>::ES;
     constexpr int EO   = TT<TO>::ES;
     constexpr int HALF = D / 2;
-    constexpr int L    = HALF / VI;   // lanes per head row
-    constexpr int TPB  = 256 / HALF;  // tokens per workgroup
-    constexpr int G    = 256 / L;     // head rows in flight per workgroup
+    constexpr int L    = HALF / VI;  // lanes per head row
+    constexpr int R    = 64 / L;     // head rows per batch
+    constexpr int PF   = MI_ROPE_PF;
+    constexpr int PL   = (HALF + 63) / 64;  // cos/sin pairs per lane
 
-    __shared__ f32x2 cs[ROPE ? TPB : 1][ROPE ? HALF : 1];
+    __shared__ float tab[4][2][HALF];  // per wave: cos | sin (theta staged in the cos half)
+    __shared__ float wt[2][D];         // Q and K norm weights
 
-    const int      tid  = threadIdx.x;
-    const uint32_t tok0 = blockIdx.x * TPB;
+    const int      lane = threadIdx.x & 63;
+    const uint32_t wv   = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int      j    = lane % L;
+    const int      g    = lane / L;
 
-    if constexpr (ROPE) {
-        const int      tt = tid / HALF;
-        const int      i  = tid % HALF;
-        const uint32_t t  = tok0 + tt;
-        float          c = 1.0f, sn = 0.0f;
-        if (t < a.ntok) {
-            const uint32_t i3    = a.dne2.div(t);
-            const uint32_t i2    = t - i3 * a.ne2;
-            float          theta = (float) a.pos[i2];
-            // theta_i after i sequential fp32 multiplies (the ggml cache chain)
-#pragma unroll 8
-            for (int k = 0; k < HALF - 1; ++k) {
-                const float nt = theta * a.theta_scale;
-                theta          = k < i ? nt : theta;
-            }
-            const float th = a.freq_scale * theta;
-            float       sv, cv;
-            sincos_f32(th, &sv, &cv);
-            c  = cv * a.mscale;
-            sn = sv * a.mscale;
+    if constexpr (NORM) {
+        for (int i = threadIdx.x; i < 2 * D; i += 256) {
+            const float * w = i < D ? a.seg[0].w : (a.nseg > 1 ? a.seg[1].w : nullptr);
+            wt[i / D][i % D] = w ? w[i % D] : 1.0f;
         }
-        cs[tt][i] = f32x2{ c, sn };
         __syncthreads();
     }
 
-    const int g = tid / L;
-    const int j = tid % L;
+    // per-lane byte offsets inside a batch, per segment
+    int64_t lx[2], ly[2];
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+        lx[sg] = (int64_t) g * a.seg[sg].xs1 + (int64_t) (j * VI) * EI;
+        ly[sg] = (int64_t) g * a.seg[sg].ys1 + (int64_t) (j * VI) * EO;
+    }
 
-    for (int sgi = 0; sgi < a.nseg; ++sgi) {
-        const HeadSeg & S = a.seg[sgi];
-        float           w0[VI], w1[VI];
-        if constexpr (NORM) {
+    for (uint32_t t = blockIdx.x * 4 + wv; t < a.ntok; t += gridDim.x * 4) {
+        const uint32_t i3 = a.dne2.div(t);
+        const uint32_t i2 = t - i3 * a.ne2;
+
+        // batch b: segment and first head row (both wave-uniform)
+        auto seg_of = [&](uint32_t b, int & sg, uint32_t & h0) {
+            sg = b >= nb0 ? 1 : 0;
+            h0 = (b - (sg ? nb0 : 0u)) * R;
+        };
+        auto load_batch = [&](uint32_t b0, uint4 * v0, uint4 * v1) {
 #pragma unroll
-            for (int e = 0; e < VI; ++e) {
-                w0[e] = S.w ? S.w[j * VI + e] : 1.0f;
-                w1[e] = S.w ? S.w[HALF + j * VI + e] : 1.0f;
-            }
-        }
-        const bool     has_w = S.w != nullptr;
-        const uint32_t nrows = TPB * S.heads;
-        for (uint32_t r = g; r < nrows; r += G) {
-            const uint32_t tt = S.hdiv.div(r);
-            const uint32_t h  = r - tt * S.heads;
-            const uint32_t t  = tok0 + tt;
-            if (t >= a.ntok) {
-                continue;
-            }
-            const uint32_t i3 = a.dne2.div(t);
-            const uint32_t i2 = t - i3 * a.ne2;
-            const char *   xp = S.x + (int64_t) i3 * S.xs3 + (int64_t) i2 * S.xs2 + (int64_t) h * S.xs1;
-            char *         yp = S.y + (int64_t) i3 * S.ys3 + (int64_t) i2 * S.ys2 + (int64_t) h * S.ys1;
-            const uint4    v0 = ld16(xp + (size_t) (j * VI) * EI);
-            const uint4    v1 = ld16(xp + (size_t) (HALF + j * VI) * EI);
-            float          x0[VI], x1[VI];
-            unpack16<TI>(v0, x0);
-            unpack16<TI>(v1, x1);
-            if constexpr (NORM) {
-                double s = 0.0;
-#pragma unroll
-                for (int e = 0; e < VI; ++e) {
-                    s += (double) (x0[e] * x0[e]);
-                }
-#pragma unroll
-                for (int e = 0; e < VI; ++e) {
-                    s += (double) (x1[e] * x1[e]);
-                }
-                s                 = group_sum<L>(s);
-                const float scale = rms_scale(s, D, a.eps);
-#pragma unroll
-                for (int e = 0; e < VI; ++e) {
-                    x0[e] = x0[e] * scale;
-                    x1[e] = x1[e] * scale;
-                }
-                if (has_w) {
-#pragma unroll
-                    for (int e = 0; e < VI; ++e) {
-                        x0[e] = x0[e] * w0[e];
-                        x1[e] = x1[e] * w1[e];
+            for (int k = 0; k < PF; ++k) {
+                if (b0 + k < nb) {
+                    int      sg;
+                    uint32_t h0;
+                    seg_of(b0 + k, sg, h0);
+                    const HeadSeg & S  = a.seg[sg];
+                    const char *    xp = S.x + (int64_t) i3 * S.xs3 + (int64_t) i2 * S.xs2 + (int64_t) h0 * S.xs1 + lx[sg];
+                    v0[k] = make_uint4(0, 0, 0, 0);
+                    v1[k] = make_uint4(0, 0, 0, 0);
+                    if (h0 + g < S.heads) {
+                        v0[k] = ld16(xp);
+                        v1[k] = ld16(xp + (size_t) HALF * EI);
                     }
                 }
             }
-            if constexpr (ROPE) {
-#pragma unroll
-                for (int e = 0; e < VI; ++e) {
-                    const f32x2 q  = cs[tt][j * VI + e];
-                    const float a0 = x0[e] * q.x;
-                    const float b0 = x1[e] * q.y;
-                    const float a1 = x0[e] * q.y;
-                    const float b1 = x1[e] * q.x;
-                    x0[e]          = a0 - b0;
-                    x1[e]          = a1 + b1;
+        };
+
+        uint4 v0[PF], v1[PF];
+        load_batch(0, v0, v1);
+
+        float cv[VI], sv[VI];
+        if constexpr (ROPE) {
+            float * ct = tab[wv][0];
+            float * st = tab[wv][1];
+            if (lane == 0) {
+                float th = (float) a.pos[i2];
+                ct[0]    = th;
+                for (int i = 1; i < HALF; ++i) {
+                    th    = th * a.theta_scale;
+                    ct[i] = th;
                 }
             }
-            store_vec<TO, VI>(yp + (size_t) (j * VI) * EO, x0);
-            store_vec<TO, VI>(yp + (size_t) (HALF + j * VI) * EO, x1);
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            float th[PL];
+#pragma unroll
+            for (int q = 0; q < PL; ++q) {
+                th[q] = lane + 64 * q < HALF ? ct[lane + 64 * q] : 0.0f;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int q = 0; q < PL; ++q) {
+                if (lane + 64 * q < HALF) {
+                    float sn, cs;
+                    sincos_rot(a.freq_scale * th[q], &sn, &cs);
+                    ct[lane + 64 * q] = cs * a.mscale;
+                    st[lane + 64 * q] = sn * a.mscale;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int e = 0; e < VI; ++e) {
+                cv[e] = ct[j * VI + e];
+                sv[e] = st[j * VI + e];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+
+        for (uint32_t b0 = 0; b0 < nb; b0 += PF) {
+            if (b0 > 0) {
+                load_batch(b0, v0, v1);
+            }
+#pragma unroll
+            for (int k = 0; k < PF; ++k) {
+                if (b0 + k >= nb) {
+                    continue;
+                }
+                int      sg;
+                uint32_t h0;
+                seg_of(b0 + k, sg, h0);
+                float x0[VI], x1[VI];
+                unpack16<TI>(v0[k], x0);
+                unpack16<TI>(v1[k], x1);
+                if constexpr (NORM) {
+                    double ss = 0.0;
+#pragma unroll
+                    for (int e = 0; e < VI; ++e) {
+                        ss += (double) (x0[e] * x0[e]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < VI; ++e) {
+                        ss += (double) (x1[e] * x1[e]);
+                    }
+                    ss                = group_sum<L>(ss);
+                    const float scale = rms_scale(ss, D, a.eps);
+                    const float * w   = wt[sg];
+#pragma unroll
+                    for (int e = 0; e < VI; ++e) {
+                        x0[e] = x0[e] * scale * w[j * VI + e];
+                        x1[e] = x1[e] * scale * w[HALF + j * VI + e];
+                    }
+                }
+                if constexpr (ROPE) {
+#pragma unroll
+                    for (int e = 0; e < VI; ++e) {
+                        const float a0 = x0[e] * cv[e];
+                        const float b0_ = x1[e] * sv[e];
+                        const float a1 = x0[e] * sv[e];
+                        const float b1 = x1[e] * cv[e];
+                        x0[e]          = a0 - b0_;
+                        x1[e]          = a1 + b1;
+                    }
+                }
+                const HeadSeg & S = a.seg[sg];
+                if (h0 + g < S.heads) {
+                    char * yp = S.y + (int64_t) i3 * S.ys3 + (int64_t) i2 * S.ys2 + (int64_t) h0 * S.ys1 + ly[sg];
+                    store_vec<TO, VI>(yp, x0);
+                    store_vec<TO, VI>(yp + (size_t) HALF * EO, x1);
+                }
+            }
         }
     }
 }
@@ -185,7 +249,7 @@ __global__ void __launch_bounds__(256) k_heads_generic(const HeadArgs a) {
                     }
                     const float th = a.freq_scale * theta;
                     float       sv, cv;
-                    sincos_f32(th, &sv, &cv);
+                    sincos_rot(th, &sv, &cv);
                     const float c  = cv * a.mscale;
                     const float sn = sv * a.mscale;
                     const float x0 = nval(ic);
@@ -211,24 +275,28 @@ __global__ void __launch_bounds__(256) k_heads_generic(const HeadArgs a) {
 
 template <int TI, int TO, int D>
 static void launch_fast(const HeadArgs & a, hipStream_t s) {
-    constexpr int  TPB  = 256 / (D / 2);
-    const uint32_t grid = (a.ntok + TPB - 1) / TPB;
-    const bool     rope = a.pos != nullptr;
+    constexpr int  L   = D / 2 / TT<TI>::VEC;
+    constexpr int  R   = 64 / L;
+    const uint32_t h0  = a.seg[0].heads;
+    const uint32_t h1  = a.nseg > 1 ? a.seg[1].heads : 0u;
+    const uint32_t nb0 = (h0 + R - 1) / R;
+    const uint32_t nb  = nb0 + (h1 + R - 1) / R;
+    uint64_t       grid = ((uint64_t) a.ntok + 3) / 4;  // 4 waves (tokens) per workgroup
+    const uint64_t cap  = (uint64_t) num_cus() * 64;
+    grid                = grid > cap ? cap : grid;
+    const bool rope     = a.pos != nullptr;
     if (a.norm && rope) {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, true, true>), dim3(grid), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_heads<TI, TO, D, true, true>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb);
     } else if (a.norm) {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, true, false>), dim3(grid), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_heads<TI, TO, D, true, false>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb);
     } else {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, false, true>), dim3(grid), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_heads<TI, TO, D, false, true>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb);
     }
 }
 
 template <int TI, int TO>
 static int launch_t(HeadArgs & a, bool fast, hipStream_t s) {
     if (fast) {
-        for (int i = 0; i < a.nseg; ++i) {
-            a.seg[i].hdiv = FastDiv(a.seg[i].heads);
-        }
         switch (a.ne0) {
             case 64:
                 launch_fast<TI, TO, 64>(a, s);
@@ -261,8 +329,9 @@ int launch_heads(HeadArgs & a, int tin, int tout, hipStream_t s) {
     a.dne2 = FastDiv(a.ne2);
     // fast path preconditions: full-width rotation (or none), D in {64,128,256},
     // 16-byte aligned rows, same in/out type
+    const uint64_t hall = (uint64_t) a.seg[0].heads + (a.nseg > 1 ? a.seg[1].heads : 0u);
     bool fast = (a.pos == nullptr || a.n_dims == a.ne0) && (a.ne0 == 64 || a.ne0 == 128 || a.ne0 == 256) &&
-                tin == tout && (a.norm || a.pos);
+                tin == tout && (a.norm || a.pos) && (uint64_t) a.ntok * hall < (1ull << 31);
     for (int i = 0; i < a.nseg && fast; ++i) {
         const HeadSeg & S = a.seg[i];
         fast = aligned(S.x, 16) && aligned(S.y, 16) && S.xs1 % 16 == 0 && S.xs2 % 16 == 0 && S.xs3 % 16 == 0 &&

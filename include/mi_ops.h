@@ -90,6 +90,23 @@ int mi_rms_norm(const mi_tensor * x, const mi_tensor * w, float eps, const mi_te
 int mi_rms_norm_modulate(const mi_tensor * x, const mi_tensor * w, const mi_tensor * scale, const mi_tensor * shift,
                          float eps, const mi_tensor * y, mi_stream stream);
 
+/* Residual add fused with the RMSNorm that consumes it:
+ *   y_sum  = residual + x            (gate == NULL; ggml_add)
+ *          = residual + x * gate     (dit_ggml_gated_add, dit-graph.h:70-76)
+ *   y_sum  = clamp(y_sum, lo, hi)    when clamp != 0 (ggml_clamp)
+ *   y_norm = rms_norm(y_sum) [* w] [* (scale + 1) + shift]
+ * Replaces, in one pass over the activations, the add -> norm node pairs at
+ * dit-graph.h:420 -> 429/442-443, dit-graph.h:432 -> 442-443 and
+ * qwen3-lm.h:730-736 (residual add + clamp -> post-attention norm),
+ * 738-741 -> 632 of the next layer. y_sum is stored in the activation type
+ * and y_norm is computed from that stored value, so the results equal the
+ * unfused kernels'. All four activations share one type and shape; y_sum may
+ * alias residual; y_norm must not alias any input or y_sum. scale/shift need
+ * w (as dit_ggml_adaln follows dit_ggml_rms_norm_weighted). */
+int mi_add_rms_norm(const mi_tensor * residual, const mi_tensor * x, const mi_tensor * gate, int clamp, float lo,
+                    float hi, const mi_tensor * w, const mi_tensor * scale, const mi_tensor * shift, float eps,
+                    const mi_tensor * y_sum, const mi_tensor * y_norm, mi_stream stream);
+
 /* ggml_rope_ext(x, pos, NULL, n_dims, mode, n_ctx_orig=0, freq_base, freq_scale,
  * ext_factor, attn_factor, beta_fast, beta_slow) for mode 2 (NEOX).
  * Replaces the rope nodes at qwen3-enc.h:173-174, qwen3-lm.h:378-379,

@@ -75,6 +75,18 @@ def test_rms_norm_validation():
     assert L.mi_rms_norm_modulate(R(x), R(w), R(_t([1023])), R(w), 1e-6, R(y), NULL_S) == -3
 
 
+def test_add_rms_norm_validation():
+    a, x, ys, yn, w = _t([2048, 8]), _t([2048, 8], data=8192), _t([2048, 8], data=16384), _t([2048, 8], data=32768), _t([2048])
+    f = L.mi_add_rms_norm
+    assert f(R(a), R(x), None, 0, 0.0, 0.0, R(w), None, None, 1e-6, R(ys), R(_t([2048, 9])), NULL_S) == -3
+    assert f(R(a), R(_t([2048, 8], BF16)), None, 0, 0.0, 0.0, R(w), None, None, 1e-6, R(ys), R(yn), NULL_S) == -2
+    assert f(R(a), R(x), R(_t([2047])), 0, 0.0, 0.0, R(w), None, None, 1e-6, R(ys), R(yn), NULL_S) == -3
+    assert f(R(a), R(x), None, 0, 0.0, 0.0, None, R(w), R(w), 1e-6, R(ys), R(yn), NULL_S) == -1    # modulate needs w
+    assert f(R(a), R(x), None, 0, 0.0, 0.0, R(w), R(w), None, 1e-6, R(ys), R(yn), NULL_S) == -1    # scale without shift
+    assert f(R(a), R(x), None, 1, float("nan"), 1.0, R(w), None, None, 1e-6, R(ys), R(yn), NULL_S) == -6
+    assert f(R(a), R(x), None, 0, 0.0, 0.0, R(w), None, None, 1e-6, R(ys), R(a), NULL_S) == -6     # y_norm aliases
+
+
 def test_rope_validation():
     x, y = _t([128, 16, 32]), _t([128, 16, 32])
     pos = _t([32], I32)

@@ -126,3 +126,27 @@ def test_in_place_gated_add(dev):
     rd = to_dev(res, dev)
     ops.gated_add(rd, to_dev(x, dev), to_dev(g, dev), out=rd)
     assert _bits_equal(to_np(rd), orc.gated_add(res, x, g))
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_views_with_packed_inner_rows(dev, T):
+    """[D, nkv, T, B] views of a fused QKV buffer (the decode-time V view):
+    rows inside a token are packed but tokens sit a whole QKV row apart, so
+    row addressing must not treat them as uniformly strided, also when T = 1."""
+    B, nh, nkv, D = 4, 4, 2, 128
+    W = (nh + 2 * nkv) * D
+    qkv = randn((B, T, W), seed=21)
+    qkv[0, 0, (nh + nkv) * D + 5] = 7e4
+    qd = to_dev(qkv, dev)
+    vd = qd[:, :, (nh + nkv) * D:].unflatten(2, (nkv, D))
+    v = qkv[:, :, (nh + nkv) * D:].reshape(B, T, nkv, D)
+    other = randn((B, T, nkv, D), seed=22)
+    y = to_np(ops.add(vd, to_dev(other, dev)))
+    assert _bits_equal(y, v + other)
+    y = to_np(ops.rms_norm(vd, 1e-6))
+    assert_f32_close(y, orc.rms_norm(v, 1e-6))
+    ops.clamp(vd, -65504.0, 65504.0, out=vd)  # in place, as the layer driver does
+    got = to_np(qd)
+    ref = qkv.copy()
+    ref[:, :, (nh + nkv) * D:] = orc.clamp(qkv[:, :, (nh + nkv) * D:], -65504.0, 65504.0)
+    assert _bits_equal(got, ref)

@@ -103,3 +103,49 @@ def test_rms_norm_special_rows(dev):
     x[3, ::7] = -3.0
     y = to_np(ops.rms_norm(to_dev(x, dev), EPS))
     assert_f32_close(y, orc.rms_norm(x, EPS))
+
+
+@pytest.mark.parametrize("rows,n", [(600, 2048), (33, 2560), (50, 1024), (7, 3000), (9, 128)])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_add_rms_norm_gated_modulate(dev, rows, n, dt):
+    """DiT: h1 = h + sa_out * gate_sa; norm_ffn = rms_norm(h1) * w -> AdaLN (dit-graph.h:420, 442-443)."""
+    print(f"add_rms_norm gated+mod rows={rows} n={n} {dt}", flush=True)
+    bf16 = dt == "bf16"
+    h = randn((rows, n), seed=21)
+    x = randn((rows, n), seed=22)
+    gate, w = randn((n,), seed=23, scale=0.1), randn((n,), seed=24, scale=0.1, mean=1.0)
+    sc, sh = randn((n,), seed=25, scale=0.1), randn((n,), seed=26, scale=0.1)
+    hh = orc.f32_to_bf16(h) if bf16 else h
+    xh = orc.f32_to_bf16(x) if bf16 else x
+    vd = [to_dev(v, dev) for v in (gate, w, sc, sh)]
+    ys, yn = ops.add_rms_norm(to_dev(hh, dev, bf16=bf16), to_dev(xh, dev, bf16=bf16), EPS, gate=vd[0], w=vd[1],
+                              scale=vd[2], shift=vd[3])
+    f = orc.bf16_to_f32 if bf16 else (lambda a: a)
+    s_ref = orc.gated_add(f(hh), f(xh), gate)
+    if bf16:
+        s_ref = orc.f32_to_bf16(s_ref)
+        assert np.array_equal(to_np(ys), s_ref)
+        assert_bf16_ulp(to_np(yn), orc.bf16_chain(lambda a: orc.rms_norm_modulate(a, w, sc, sh, EPS), s_ref))
+    else:
+        assert np.array_equal(to_np(ys), s_ref)
+        ref = orc.rms_norm_modulate(s_ref, w, sc, sh, EPS)
+        assert_f32_close(to_np(yn), ref, row_floor=True)
+        assert frac_bitexact(to_np(yn), ref) >= 0.999
+
+
+@pytest.mark.parametrize("n", [2560, 2048, 96])
+def test_add_clamp_rms_norm_in_place(dev, n):
+    """Qwen3: hidden = clamp(hidden + attn_out); norm2 = rms_norm(hidden) * w (qwen3-lm.h:730-736),
+    with y_sum written in place over the residual."""
+    rows = 40
+    h = randn((rows, n), seed=31)
+    h[0, :3] = [7e4, -7e4, 6e4]
+    a = randn((rows, n), seed=32)
+    w = randn((n,), seed=33, scale=0.1, mean=1.0)
+    hd = to_dev(h, dev)
+    ys, yn = ops.add_rms_norm(hd, to_dev(a, dev), EPS, w=to_dev(w, dev), clamp=(-65504.0, 65504.0), out_sum=hd)
+    s_ref = orc.add_clamp(h, a)
+    assert np.array_equal(to_np(hd), s_ref)
+    ref = orc.rms_norm_mul(s_ref, w, EPS)
+    assert_f32_close(to_np(yn), ref)
+    assert frac_bitexact(to_np(yn), ref) >= 0.999
