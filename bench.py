@@ -73,9 +73,10 @@ def bf16_bits(a: np.ndarray) -> np.ndarray:
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
-def gpu_bench(steps: int, warmup: int):
+def _setup():
+    """Synthetic block inputs resident in HBM, and the fused / unfused launch lists."""
     from acestep_ops import device, ops
-    from acestep_ops.device import DTensor, Event, Graph, Stream
+    from acestep_ops.device import DTensor, Stream
 
     rng = np.random.default_rng(42)
 
@@ -122,6 +123,35 @@ def gpu_bench(steps: int, warmup: int):
         lambda: ops.rms_norm_modulate(h1, ff_w, scale_ff, shift_ff, EPS, out=norm_ff, stream=sh),
         fused[3], fused[4],
     ]
+    # plain bf16 copy of a known size (the SwiGLU output, 147.456 MB each way):
+    # the reference point for scaling the FETCH_SIZE / WRITE_SIZE counters
+    ff_copy = DTensor.empty((BATCH, T_FRAMES, I_FF), "bf16")
+    calib = lambda: ops.cpy(ff, ff_copy, stream=sh)  # noqa: E731
+    keep = (hidden, qkv, sa_out, gate_up, ffn_out, adaln, sa_w, ff_w, q_w, k_w, pos, norm_sa, norm_ff, h1, h2, q_out,
+            k_out, ff, ff_copy)
+    return fused, unfused, calib, stream, keep
+
+
+def pmc_pass():
+    """Each fused launch once, then the calibration copy, eagerly (for rocprofv3 --pmc)."""
+    from acestep_ops import device
+
+    fused, _, calib, stream, _keep = _setup()
+    for f in fused:
+        f()
+    calib()
+    stream.synchronize()
+    device.synchronize()
+    print("pmc pass: 5 block launches + 1 calibration copy (bf16, 147456000 B read, 147456000 B written)",
+          flush=True)
+
+
+def gpu_bench(steps: int, warmup: int):
+    from acestep_ops import device
+    from acestep_ops.device import Event, Graph
+
+    fused, unfused, _calib, stream, _keep = _setup()
+    sh = stream.handle
 
     def graph_of(launches):
         g = Graph()
@@ -140,16 +170,22 @@ def gpu_bench(steps: int, warmup: int):
         b.synchronize()
         return a.elapsed_ms(b) / n
 
-    def per_kernel(launches, n):
-        ev = [[(Event(), Event()) for _ in launches] for _ in range(n)]
+    def per_kernel(launches, n, g_ahead):
+        """Per-launch device time inside the block sequence. Each sample first
+        queues 8 replays of the block graph (about 1.6 ms of device work) so the
+        host has enqueued every event and launch of the sample before the
+        device reaches them: the event pairs then bracket only the kernel."""
+        ev = [[Event() for _ in range(len(launches) + 1)] for _ in range(n)]
         stream.synchronize()
         for i in range(n):
+            for _ in range(8):
+                g_ahead.launch()
+            ev[i][0].record(sh)
             for j, f in enumerate(launches):
-                ev[i][j][0].record(sh)
                 f()
-                ev[i][j][1].record(sh)
+                ev[i][j + 1].record(sh)
         stream.synchronize()
-        return [1000.0 * float(np.mean([ev[i][j][0].elapsed_ms(ev[i][j][1]) for i in range(n)]))
+        return [1000.0 * float(np.mean([ev[i][j].elapsed_ms(ev[i][j + 1]) for i in range(n)]))
                 for j in range(len(launches))]
 
     g_fused, g_unfused = graph_of(fused), graph_of(unfused)
@@ -168,8 +204,8 @@ def gpu_bench(steps: int, warmup: int):
 
     names_f = list(block_bytes(ROWS, fused=True).keys())
     names_u = list(block_bytes(ROWS, fused=False).keys())
-    pk_f = dict(zip(names_f, per_kernel(fused, steps)))
-    pk_u = dict(zip(names_u, per_kernel(unfused, steps)))
+    pk_f = dict(zip(names_f, per_kernel(fused, steps, g_fused)))
+    pk_u = dict(zip(names_u, per_kernel(unfused, steps, g_unfused)))
     return ms_step, ms_unfused, wall, pk_f, pk_u
 
 
@@ -221,6 +257,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=1500, help="row sample for the CPU baseline")
     ap.add_argument("--cpu-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="launch each block kernel once plus a copy of known size, for counter collection")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); every op of the path is "
@@ -231,6 +269,9 @@ def main():
         print("bench.py: one process / one GPU only", file=sys.stderr)
         sys.exit(2)
 
+    if args.pmc_pass:
+        pmc_pass()
+        return
     kb = block_bytes(ROWS, fused=True)
     kb_u = block_bytes(ROWS, fused=False)
     total_bytes = sum(kb.values())
@@ -239,11 +280,13 @@ def main():
     dom = "swiglu"
     dom_gbs = kb[dom] / (per_k[dom] * 1e-6) / 1e9
 
+    # HBM bytes per launch of the dominant kernel from the committed counter
+    # summary (FETCH_SIZE and WRITE_SIZE, each scaled by a copy of known size)
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "swiglu_dit_T6000_traffic.md")
+    tpath = os.path.join(ROOT, "profiles", "dit_block_T6000_traffic.md")
     if os.path.exists(tpath):
         for line in open(tpath):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith("traffic_bytes_per_launch k_swiglu:"):
                 traffic = int(line.split(":", 1)[1].strip())
 
     cpu = None

@@ -203,13 +203,16 @@ int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi
 /* ---------------------------------------------------------------------- */
 
 /* One ACE-Step DiT block's non-GEMM ops, in dit_ggml_build_layer order
- * (dit-graph.h:367-448). hidden is updated in place.
+ * (dit-graph.h:367-448). hidden is updated in place. Each residual add is
+ * fused with the RMSNorm that reads it (mi_add_rms_norm), so the block runs
+ * as 5 launches without cross attention (8 with):
  *   pre-SA:   norm_sa   = rms_norm_modulate(hidden, sa_norm_w, scale_sa, shift_sa)
  *   SA:       q_out/k_out = qk_norm_rope(q, k)   [q, k: views of the QKV GEMM output]
- *   post-SA:  hidden    = hidden + sa_out * gate_sa
- *   CA:       norm_ca   = rms_norm(hidden) * ca_norm_w; ca_q_out = rms_norm(ca_q) * ca_q_w;
- *             hidden    = hidden + ca_out          (skipped when ca_out is NULL)
- *   pre-FFN:  norm_ffn  = rms_norm_modulate(hidden, ffn_norm_w, scale_ffn, shift_ffn)
+ *   post-SA:  hidden    = hidden + sa_out * gate_sa, fused with
+ *               norm_ca  = rms_norm(hidden) * ca_norm_w            (cross attention), or
+ *               norm_ffn = rms_norm_modulate(hidden, ffn_norm_w, scale_ffn, shift_ffn)
+ *   CA:       ca_q_out  = rms_norm(ca_q) * ca_q_w   (when ca_q.data != NULL)
+ *             hidden    = hidden + ca_out, fused with norm_ffn as above
  *   FFN:      ff        = swiglu(gate_up)
  *   post-FFN: hidden    = hidden + ffn_out * gate_ffn
  * adaln: F32 [6H] = scale_shift_table + tproj (shift_sa, scale_sa, gate_sa,
@@ -238,8 +241,8 @@ int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream stream);
  * (qwen3-lm.h:630-741):
  *   norm   = rms_norm(hidden) * in_norm_w
  *   q/k    = qk_norm_rope(q, k)                [views of the QKV GEMM output]
- *   (clamp v when clamp_fp16), kv_store(k_out, v -> caches at pos0/sets)
- *   hidden = hidden + attn_out   (clamped to +-65504 when clamp_fp16)
+ *   (clamp v in place when clamp_fp16), kv_store(k_out, v -> caches at pos0/sets)
+ *   hidden = hidden + attn_out   (clamped to +-65504 when clamp_fp16), fused with
  *   norm2  = rms_norm(hidden) * post_norm_w
  *   ff     = swiglu(gate_up)
  *   hidden = hidden + mlp_out    (clamped when clamp_fp16) */
