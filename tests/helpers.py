@@ -67,6 +67,22 @@ def frac_bitexact(a: np.ndarray, ref: np.ndarray) -> float:
     return float(np.mean(np.all(eq, axis=1)))
 
 
+def tsembd_bar(y, ref, t, dim, max_period):
+    """1e-5 relative (row-RMS floor) plus the conditioning of cos/sin(t*freq):
+    a 1-ulp difference between device and glibc exp in freq moves the angle by
+    |t*freq| * 2^-23, which no implementation can avoid at t ~ 1000."""
+    half = dim // 2
+    freq = np.exp(-np.log(max_period) * np.arange(half) / half)
+    arg = np.abs(t.astype(np.float64)[:, None] * freq[None, :])
+    slack = np.concatenate([arg, arg], axis=1) * 2.0 ** -23
+    if dim % 2:
+        slack = np.concatenate([slack, np.zeros((t.size, 1))], axis=1)
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2, axis=1, keepdims=True))
+    bound = 1e-5 * np.maximum(np.abs(ref), rms) + slack
+    worst = np.max(np.abs(y.astype(np.float64) - ref) - bound)
+    assert worst <= 0, f"timestep embedding exceeds bound by {worst:.3e}"
+
+
 # ---------------------------------------------------------------------------
 # host <-> device (acestep_ops.device; bf16/f16 travel as uint16 bit patterns)
 # ---------------------------------------------------------------------------

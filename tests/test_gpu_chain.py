@@ -6,7 +6,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from helpers import assert_bf16_ulp, assert_f32_close, randn, rng, to_dev, to_np
+from helpers import assert_bf16_ulp, assert_f32_close, randn, rng, to_dev, to_np, tsembd_bar
 from oracle import oracle as orc
 
 from acestep_ops import _lib, device, ops
@@ -16,29 +16,13 @@ pytestmark = pytest.mark.gpu
 EPS = 1e-6
 
 
-def _tsembd_bar(y, ref, t, dim, max_period):
-    """1e-5 relative (row-RMS floor) plus the conditioning of cos/sin(t*freq):
-    a 1-ulp difference between device and glibc exp in freq moves the angle by
-    |t*freq| * 2^-23, which no implementation can avoid at t ~ 1000."""
-    half = dim // 2
-    freq = np.exp(-np.log(max_period) * np.arange(half) / half)
-    arg = np.abs(t.astype(np.float64)[:, None] * freq[None, :])
-    slack = np.concatenate([arg, arg], axis=1) * 2.0 ** -23
-    if dim % 2:
-        slack = np.concatenate([slack, np.zeros((t.size, 1))], axis=1)
-    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2, axis=1, keepdims=True))
-    bound = 1e-5 * np.maximum(np.abs(ref), rms) + slack
-    worst = np.max(np.abs(y.astype(np.float64) - ref) - bound)
-    assert worst <= 0, f"timestep embedding exceeds bound by {worst:.3e}"
-
-
 def test_timestep_embedding(dev):
     t = (rng(1).uniform(0, 1, 64) * 1000).astype(np.float32)
     t[:3] = [0.0, 1000.0, 0.5]
     y = to_np(ops.timestep_embedding(to_dev(t, dev), 256, 10000))
-    _tsembd_bar(y, orc.timestep_embedding(t, 256, 10000), t, 256, 10000)
+    tsembd_bar(y, orc.timestep_embedding(t, 256, 10000), t, 256, 10000)
     y = to_np(ops.timestep_embedding(to_dev(t, dev), 7, 100))
-    _tsembd_bar(y, orc.timestep_embedding(t, 7, 100), t, 7, 100)
+    tsembd_bar(y, orc.timestep_embedding(t, 7, 100), t, 7, 100)
     assert not y[:, 6].any()
 
 
