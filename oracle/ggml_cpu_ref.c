@@ -256,7 +256,8 @@ void orc_rope_neox_f32(const float * x, int64_t n_pos, int64_t heads, int64_t ne
 /* ggml_swiglu (fused [2I] input, gate = first half) and ggml_swiglu_split.  */
 /* Call sites: qwen3-enc.h:217, 221; dit-graph.h:259, 264.                   */
 /* Arithmetic: ggml_silu_f32(g) * u with silu(x) = x/(1.0f + expf(-x)) (the  */
-/* scalar form; ggml's SIMD lanes use a polynomial expf -- see tests).       */
+/* scalar form; ggml's SIMD lanes use a polynomial expf whose lane results   */
+/* cannot be reproduced without the ggml source: within ~1e-7 relative).     */
 /* ------------------------------------------------------------------------ */
 void orc_swiglu_f32(const float * g, int64_t gs, const float * u, int64_t us, int64_t rows, int64_t n, float * y) {
 #pragma omp parallel for num_threads(g_threads) schedule(static)

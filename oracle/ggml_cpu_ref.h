@@ -14,6 +14,21 @@
  *
  * Layout convention: row-major, contiguous; "rows x n" means n is the
  * innermost (ggml ne0) dimension.
+ *
+ * Pinning (tests/test_oracle_pinning.py; each check is independent of the
+ * formula restated here and fails on a planted mistake): fp16/bf16
+ * conversions against numpy float16 and a nearest-neighbour search;
+ * rms_norm against float64, exact rational arithmetic on tiny rows and
+ * bit-exact power-of-two scaling; add/mul/clamp against single IEEE ops and
+ * the NaN -> hi clamp semantics; rope by position-0 identity, pair norms,
+ * the fp32 theta chain (and its divergence from the closed form at p = 8191),
+ * partial n_dims, attn/freq scale; swiglu against float64 and IEEE special
+ * values; Q8_0 by brute-force dequant, quantizer invariants and tie blocks
+ * that separate the two variants; timestep embedding against float64 with a
+ * derived bound. Parity unpinned (needs the absent ggml source): which Q8_0
+ * variant ggml-cpu's ggml_cpy uses on x86 (both are implemented; X86 is the
+ * default), the lane results of ggml's SIMD expf in swiglu, whether the
+ * fork's CPU backend fuses nodes, and its FP-contraction flags.
  */
 #ifndef ORC_GGML_CPU_REF_H
 #define ORC_GGML_CPU_REF_H
