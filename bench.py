@@ -249,6 +249,188 @@ def cpu_bench(rows: int, reps: int, threads: int):
     return float(np.median(ts)), float(np.sum(ts))
 
 
+# ---------------------------------------------------------------------------
+# The Qwen3 configurations (reported with --configs; the JSON line above stays
+# the DiT block metric). Each is one layer's fused-op chain in
+# qw3lm_forward_batch order (reference qwen3-lm.h:626-741), synthetic N(0,1)
+# inputs resident in HBM, replayed as one HIP graph.
+# ---------------------------------------------------------------------------
+Q8_ROW = lambda n: n // 32 * 34  # noqa: E731
+
+
+def _qwen3_configs():
+    from acestep_ops import device, ops
+    from acestep_ops.device import DTensor
+
+    rng = np.random.default_rng(42)
+    H2D = 3  # hipMemcpyDeviceToDevice
+
+    def dev(shape, dt="f32", scale=1.0, mean=0.0):
+        a = (rng.standard_normal(shape, dtype=np.float32) * scale + mean).astype(np.float32)
+        return DTensor.from_numpy(bf16_bits(a), "bf16") if dt == "bf16" else DTensor.from_numpy(a)
+
+    def q8_table(n_rows, n, stream):
+        """Q8_0 table of N(0, 0.02) rows: a 4096-row block quantized on the device
+        with the REF quantizer (as GGUF tables are made), repeated to n_rows."""
+        seed_rows = min(4096, n_rows)
+        src = dev((seed_rows, n), scale=0.02)
+        tab = DTensor.empty((n_rows, Q8_ROW(n)), "u8")
+        ops.cpy(src, ops.Q8(tab[:seed_rows]), rounding=1, stream=stream.handle)
+        for r0 in range(seed_rows, n_rows, seed_rows):
+            nb = min(seed_rows, n_rows - r0) * Q8_ROW(n)
+            device.check(device.hip().hipMemcpyAsync(tab.ptr + r0 * Q8_ROW(n), tab.ptr, nb, H2D, stream.handle),
+                         "hipMemcpyAsync")
+        stream.synchronize()
+        return tab
+
+    def layer(name, dt, T, H, NH_, NKV_, I, *, clamp=False, emb_rows=0, kv=None, split_glu=False, theta=1e6,
+              pos=None):
+        """Launch list + algorithmic bytes for one Qwen3 layer at one shape."""
+        from acestep_ops.device import Stream
+
+        st = Stream()
+        sh = st.handle
+        es = 2 if dt == "bf16" else 4
+        W = (NH_ + 2 * NKV_) * D
+        if clamp:
+            # 0.1 % outliers ~ N(0, 1000) and 16 values at +-1e5, so the FP16 clamp fires
+            a = rng.standard_normal((T, H), dtype=np.float32)
+            o = rng.choice(a.size, a.size // 1000, replace=False)
+            a.reshape(-1)[o] = rng.standard_normal(o.size, dtype=np.float32) * 1000
+            a.reshape(-1)[rng.choice(a.size, 16, replace=False)] = 1e5
+            h = DTensor.from_numpy(a)
+        else:
+            h = dev((T, H), dt)
+        attn, mlp = dev((T, H), dt), dev((T, H), dt)
+        w_in, w_post = dev((H,), scale=0.1, mean=1.0), dev((H,), scale=0.1, mean=1.0)
+        qw, kw = dev((D,), scale=0.1, mean=1.0), dev((D,), scale=0.1, mean=1.0)
+        qkv = dev((T, W), dt)
+        q = qkv[:, :NH_ * D].unflatten(1, (NH_, D))
+        k = qkv[:, NH_ * D:(NH_ + NKV_) * D].unflatten(1, (NKV_, D))
+        p = DTensor.from_numpy(np.asarray(pos if pos is not None else np.arange(T), np.int32))
+        norm, norm2, h1, h2 = (DTensor.empty((T, H), dt) for _ in range(4))
+        q_out, k_out = DTensor.empty((T, NH_, D), dt), DTensor.empty((T, NKV_, D), dt)
+        if split_glu:
+            g_, u_ = dev((T, I), dt), dev((T, I), dt)
+        else:
+            gu = dev((T, 2 * I), dt)
+        ff = DTensor.empty((T, I), dt)
+        act = T * H * es
+        L, B = [], {}
+
+        def add(label, fn, nbytes):
+            L.append((label, fn))
+            B[label] = nbytes
+
+        keep = [h, attn, mlp, w_in, w_post, qw, kw, qkv, p, norm, norm2, h1, h2, q_out, k_out, ff, st]
+        if emb_rows:
+            tab = q8_table(emb_rows, H, st)
+            ids = DTensor.from_numpy(rng.integers(0, emb_rows, T).astype(np.int32))
+            emb = DTensor.empty((T, H), "f32")
+            keep += [tab, ids, emb]
+            add("get_rows_q8_0", lambda: ops.get_rows(ops.Q8(tab), ids, out=emb, stream=sh),
+                T * Q8_ROW(H) + T * 4 + T * H * 4)
+        add("rms_norm", lambda: ops.rms_norm(h, EPS, w_in, out=norm, stream=sh), 2 * act + H * 4)
+        add("qk_norm_rope", lambda: ops.qk_norm_rope(q, qw, p, EPS, D, theta, k=k, k_w=kw, q_out=q_out, k_out=k_out,
+                                                     stream=sh),
+            2 * T * (NH_ + NKV_) * D * es + T * 4 + 2 * D * 4)
+        if kv is not None:
+            n_seq, T_seq, max_seq, s0 = kv
+            kc = DTensor.zeros((n_seq, NKV_, max_seq, Q8_ROW(D)), "u8")
+            vc = DTensor.zeros((n_seq, NKV_, max_seq, Q8_ROW(D)), "u8")
+            kk = k_out.view(n_seq, T_seq, NKV_, D)
+            vv = qkv.view(n_seq, T_seq, W)[:, :, (NH_ + NKV_) * D:].unflatten(2, (NKV_, D))
+            p0 = DTensor.from_numpy(np.asarray(s0, np.int32))
+            keep += [kc, vc, p0]
+            n_kv = n_seq * T_seq * NKV_ * D
+            add("kv_store_q8_0", lambda: ops.kv_store(kk, ops.Q8(kc), p0, v=vv, v_cache=ops.Q8(vc), stream=sh),
+                2 * (n_kv * es + n_kv // 32 * 34) + n_seq * 4)
+            if T_seq > 1:
+                # dequantize the written K and V rows back (get_rows on the caches viewed as row tables)
+                rows = (np.arange(n_seq)[:, None, None] * NKV_ + np.arange(NKV_)[None, None, :]) * max_seq + \
+                    (np.asarray(s0)[:, None, None] + np.arange(T_seq)[None, :, None])
+                rid = DTensor.from_numpy(rows.reshape(-1).astype(np.int32))
+                kt, vt = kc.view(n_seq * NKV_ * max_seq, Q8_ROW(D)), vc.view(n_seq * NKV_ * max_seq, Q8_ROW(D))
+                kb, vb = DTensor.empty((rows.size, D), "f32"), DTensor.empty((rows.size, D), "f32")
+                keep += [rid, kb, vb]
+                add("get_rows_kv_back", lambda: (ops.get_rows(ops.Q8(kt), rid, out=kb, stream=sh),
+                                                 ops.get_rows(ops.Q8(vt), rid, out=vb, stream=sh)),
+                    2 * (rows.size * Q8_ROW(D) + rows.size * 4 + rows.size * D * 4))
+        clamp_lim = (-65504.0, 65504.0) if clamp else None
+        add("add_rms_norm", lambda: ops.add_rms_norm(h, attn, EPS, w=w_post, clamp=clamp_lim, out_sum=h1,
+                                                     out_norm=norm2, stream=sh), 4 * act + H * 4)
+        if split_glu:
+            keep += [g_, u_]
+            add("swiglu", lambda: ops.swiglu_split(g_, u_, out=ff, stream=sh), 3 * T * I * es)
+        else:
+            keep += [gu]
+            add("swiglu", lambda: ops.swiglu(gu, out=ff, stream=sh), 3 * T * I * es)
+        if clamp:
+            add("add_clamp", lambda: ops.add_clamp(h1, mlp, out=h2, stream=sh), 3 * act)
+        else:
+            add("add", lambda: ops.add(h1, mlp, out=h2, stream=sh), 3 * act)
+        return dict(name=name, launches=L, bytes=B, stream=st, keep=keep)
+
+    r = np.random.default_rng(7)
+    yield lambda: layer("C1 Qwen3-0.6B layer, fp32, T=512 (split SwiGLU, Q8_0 embedding 151669x1024)", "f32", 512,
+                        1024, 16, 8, 3072, emb_rows=151669, split_glu=True)
+    dpos = r.integers(0, 8192, 8)
+    yield lambda: layer("C2 Qwen3-4B decode layer, bf16, batch 8 (Q8_0 KV store, 8192 slots)", "bf16", 8, 2560, 32,
+                        8, 9728, kv=(8, 1, 8192, dpos), pos=dpos)
+    yield lambda: layer("C4 Qwen3-1.7B prefill layer, fp32, 4x4096 (clamp, Q8_0 embedding 151669x2048)", "f32",
+                        16384, 2048, 16, 8, 6144, clamp=True, emb_rows=151669)
+    s0 = r.integers(0, 6144, 8)
+    ppos = (s0[:, None] + np.arange(2048)[None, :]).reshape(-1)
+    yield lambda: layer("C5 Qwen3-4B prefill layer, fp32, 8x2048 (Q8_0 KV store at slots U[0,6144), dequant back)",
+                        "f32", 16384, 2560, 32, 8, 9728, kv=(8, 2048, 8192, s0), pos=ppos)
+
+
+def configs_bench(steps: int, warmup: int):
+    """One JSON line per Qwen3 configuration: µs per layer and GB/s per op."""
+    from acestep_ops import device
+    from acestep_ops.device import Event, Graph
+
+    for make in _qwen3_configs():
+        c = make()
+        st, sh = c["stream"], c["stream"].handle
+        fns = [f for _, f in c["launches"]]
+        g = Graph()
+        with g.capture(st):
+            for f in fns:
+                f()
+        for _ in range(warmup):
+            g.launch()
+        st.synchronize()
+        a, b = Event(), Event()
+        a.record(sh)
+        for _ in range(steps):
+            g.launch()
+        b.record(sh)
+        b.synchronize()
+        us_layer = 1000.0 * a.elapsed_ms(b) / steps
+        ev = [[Event() for _ in range(len(fns) + 1)] for _ in range(steps)]
+        for i in range(steps):
+            for _ in range(4):
+                g.launch()
+            ev[i][0].record(sh)
+            for j, f in enumerate(fns):
+                f()
+                ev[i][j + 1].record(sh)
+        st.synchronize()
+        per = {}
+        for j, (label, _) in enumerate(c["launches"]):
+            us = 1000.0 * float(np.mean([ev[i][j].elapsed_ms(ev[i][j + 1]) for i in range(steps)]))
+            gbs = c["bytes"][label] / (us * 1e-6) / 1e9
+            per[label] = {"us": round(us, 2), "MB": round(c["bytes"][label] / 1e6, 3), "GB/s": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 3)}
+        tot = sum(c["bytes"].values())
+        print(json.dumps({"config": c["name"], "us_per_layer": round(us_layer, 2), "launches": len(fns),
+                          "bytes_per_layer": tot, "GB/s": round(tot / (us_layer * 1e-6) / 1e9, 1),
+                          "per_op": per}), flush=True)
+        del c, g
+        device.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -259,6 +441,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="launch each block kernel once plus a copy of known size, for counter collection")
+    ap.add_argument("--configs", action="store_true",
+                    help="time the Qwen3 layer op chains at the C1/C2/C4/C5 shapes instead (one JSON line each)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); every op of the path is "
@@ -271,6 +455,9 @@ def main():
 
     if args.pmc_pass:
         pmc_pass()
+        return
+    if args.configs:
+        configs_bench(args.steps, args.warmup)
         return
     kb = block_bytes(ROWS, fused=True)
     kb_u = block_bytes(ROWS, fused=False)

@@ -554,7 +554,7 @@ static int kv_desc(const mi_tensor * x, const mi_tensor * cache, const mi_tensor
     r.ne1  = (uint32_t) x->ne[1];
     r.ne2  = (uint32_t) x->ne[2];
     r.d1   = FastDiv(r.ne1);
-    r.d12  = FastDiv(r.ne1 * r.ne2);
+    r.d2   = FastDiv(r.ne2);
     r.pos0 = (const int32_t *) pos0->data;
     r.sets = sets ? (const int32_t *) sets->data : nullptr;
     r.cnb1 = (int64_t) cache->nb[1];

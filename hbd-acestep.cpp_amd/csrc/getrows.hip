@@ -7,9 +7,11 @@
 // result is exact: the output is bit-identical to ggml-cpu.
 //
 // Q8_0 path: one wave per id; each lane produces 8 consecutive outputs (two
-// 16-byte stores, so the wave's stores are fully coalesced). Its 8 quants sit
-// at byte 34b + 2 + 8k of the row, which is only 2-byte aligned, so they are
-// read as four 16-bit loads (always in bounds: no over-read past a block).
+// 16-byte stores, so the wave's stores are fully coalesced). When the row is
+// a whole number of 16-byte chunks (ne0 % 256 == 0: every Qwen3 hidden size)
+// the wave first stages the row in LDS with coalesced 16-byte loads, so a row
+// costs one memory round trip; otherwise its 8 quants, at byte 34b + 2 + 8k
+// (only 2-byte aligned), are read as four 16-bit loads.
 // F16/BF16/F32 tables: 16-byte row vectors converted to f32.
 // An id outside [0, n_rows) writes a zero row and bumps *d_err.
 #include "launch.h"
@@ -36,9 +38,9 @@ __device__ __forceinline__ float i8f(uint32_t w, int k) {
 template <int TO>
 __global__ void __launch_bounds__(256) k_get_rows_q8_0(const GetRowsArgs a) {
     constexpr int EO   = TT<TO>::ES;
+    constexpr int OPS  = 16 / EO;  // outputs per 16-byte store: wave-contiguous store instructions
     const int     lane = threadIdx.x & 63;
     const int     wpb  = blockDim.x >> 6;
-    const int     n8   = a.n >> 3;  // groups of 8 outputs
     for (uint32_t i = blockIdx.x * wpb + (threadIdx.x >> 6); i < a.n_ids; i += gridDim.x * wpb) {
         const int64_t r   = a.ids[(int64_t) i * a.ids_stride];
         char *        yp  = a.y + (int64_t) i * a.ynb1;
@@ -47,39 +49,107 @@ __global__ void __launch_bounds__(256) k_get_rows_q8_0(const GetRowsArgs a) {
             atomicAdd(a.d_err, 1);
         }
         const char * row = a.table + (bad ? 0 : r) * a.tnb1;
-        for (int m = lane; m < n8; m += 64) {
-            float f[8];
+        for (int o = lane * OPS; o < a.n; o += 64 * OPS) {
+            float f[OPS];
             if (!bad) {
-                const int       b  = m >> 2;
-                const char *    bp = row + (size_t) b * 34;
-                const uint16_t  dh = *(const uint16_t *) bp;
-                const uint16_t * qp = (const uint16_t *) (bp + 2 + (m & 3) * 8);
-                const uint32_t  w0 = (uint32_t) qp[0] | ((uint32_t) qp[1] << 16);
-                const uint32_t  w1 = (uint32_t) qp[2] | ((uint32_t) qp[3] << 16);
-                const float     d  = (float) __builtin_bit_cast(_Float16, dh);
+                const char *     bp = row + (size_t) (o >> 5) * 34;
+                const uint16_t * qp = (const uint16_t *) (bp + 2 + (o & 31));
+                const float      d  = (float) __builtin_bit_cast(_Float16, *(const uint16_t *) bp);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    f[k]     = i8f(w0, k) * d;
-                    f[k + 4] = i8f(w1, k) * d;
+                for (int h = 0; h < OPS / 4; ++h) {
+                    const uint32_t w = (uint32_t) qp[2 * h] | ((uint32_t) qp[2 * h + 1] << 16);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        f[4 * h + k] = i8f(w, k) * d;
+                    }
                 }
             } else {
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
+                for (int k = 0; k < OPS; ++k) {
                     f[k] = 0.0f;
                 }
             }
-            store_vec<TO, 8>(yp + (size_t) m * 8 * EO, f);
+            store_vec<TO, OPS>(yp + (size_t) o * EO, f);
         }
+    }
+}
+
+// Q8_0 rows whose byte length is a multiple of 16 (ne0 % 256 == 0) in a
+// 16-byte aligned table: the wave copies its row into LDS with coalesced
+// 16-byte loads, all issued at once (one memory round trip per id), then each
+// lane decodes groups of 8 outputs from LDS and writes them with 16-byte
+// stores. LDS per wave: the row's nc 16-byte chunks (nc <= 9*64, ne0 <= 8192).
+template <int TO>
+__global__ void __launch_bounds__(256) k_get_rows_q8_0_lds(const GetRowsArgs a, int nc) {
+    extern __shared__ uint4 stage_all[];
+    constexpr int    EO   = TT<TO>::ES;
+    constexpr int    OPS  = 16 / EO;  // outputs per 16-byte store: 4 (F32) or 8 (BF16)
+    constexpr int    MAXC = 9;
+    const int        lane = threadIdx.x & 63;
+    const uint32_t   wv   = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint4 *          stage = stage_all + wv * nc;
+    const uint16_t * s16   = (const uint16_t *) stage;
+    for (uint32_t i = blockIdx.x * 4 + wv; i < a.n_ids; i += gridDim.x * 4) {
+        const int64_t r   = a.ids[(int64_t) i * a.ids_stride];
+        char *        yp  = a.y + (int64_t) i * a.ynb1;
+        if (r < 0 || r >= a.n_rows) {
+            if (lane == 0 && a.d_err) {
+                atomicAdd(a.d_err, 1);
+            }
+            float z[OPS] = {};
+            for (int o = lane * OPS; o < a.n; o += 64 * OPS) {
+                store_vec<TO, OPS>(yp + (size_t) o * EO, z);
+            }
+            continue;
+        }
+        const char * row = a.table + r * a.tnb1;
+        uint4         v[MAXC];
+#pragma unroll
+        for (int k = 0; k < MAXC; ++k) {
+            const int c = lane + 64 * k;
+            if (c < nc) {
+                v[k] = ld16(row + (size_t) c * 16);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < MAXC; ++k) {
+            const int c = lane + 64 * k;
+            if (c < nc) {
+                stage[c] = v[k];
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        // OPS outputs (one 16-byte store) per lane per step: each store
+        // instruction writes 1 KB contiguous, whole cache lines
+        for (int o = lane * OPS; o < a.n; o += 64 * OPS) {
+            const uint16_t * bp = s16 + (o >> 5) * 17;  // a 34-byte block is 17 halfwords
+            const uint16_t * qp = bp + 1 + ((o & 31) >> 1);
+            const float      d  = (float) __builtin_bit_cast(_Float16, bp[0]);
+            float            f[OPS];
+#pragma unroll
+            for (int h = 0; h < OPS / 4; ++h) {
+                const uint32_t w = (uint32_t) qp[2 * h] | ((uint32_t) qp[2 * h + 1] << 16);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    f[4 * h + k] = i8f(w, k) * d;
+                }
+            }
+            store_vec<TO, OPS>(yp + (size_t) o * EO, f);
+        }
+        // the next id overwrites this wave's LDS rows
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
 template <int TT_, int TO>
 __global__ void __launch_bounds__(256) k_get_rows_vec(const GetRowsArgs a) {
-    constexpr int VI   = TT<TT_>::VEC;
+    constexpr int ET   = TT<TT_>::ES;
     constexpr int EO   = TT<TO>::ES;
+    constexpr int OPS  = 16 / (ET > EO ? ET : EO);  // elements per lane step: 16-byte loads or stores
     const int     lane = threadIdx.x & 63;
     const int     wpb  = blockDim.x >> 6;
-    const int     nv   = a.n / VI;
     for (uint32_t i = blockIdx.x * wpb + (threadIdx.x >> 6); i < a.n_ids; i += gridDim.x * wpb) {
         const int64_t r   = a.ids[(int64_t) i * a.ids_stride];
         char *        yp  = a.y + (int64_t) i * a.ynb1;
@@ -88,17 +158,23 @@ __global__ void __launch_bounds__(256) k_get_rows_vec(const GetRowsArgs a) {
             atomicAdd(a.d_err, 1);
         }
         const char * row = a.table + (bad ? 0 : r) * a.tnb1;
-        for (int m = lane; m < nv; m += 64) {
-            float f[VI];
-            if (!bad) {
-                unpack16<TT_>(ld16(row + (size_t) m * 16), f);
-            } else {
+        for (int o = lane * OPS; o < a.n; o += 64 * OPS) {
+            float f[OPS];
+            if (bad) {
 #pragma unroll
-                for (int k = 0; k < VI; ++k) {
+                for (int k = 0; k < OPS; ++k) {
                     f[k] = 0.0f;
                 }
+            } else if constexpr (OPS * ET == 16) {
+                unpack16<TT_>(ld16(row + (size_t) o * ET), f);
+            } else {  // 4 half-width elements widened to F32
+                const uint2 w = *(const uint2 *) (row + (size_t) o * ET);
+                f[0]          = TT_ == MI_TYPE_BF16 ? bf16_lo(w.x) : f16_lo(w.x);
+                f[1]          = TT_ == MI_TYPE_BF16 ? bf16_hi(w.x) : f16_hi(w.x);
+                f[2]          = TT_ == MI_TYPE_BF16 ? bf16_lo(w.y) : f16_lo(w.y);
+                f[3]          = TT_ == MI_TYPE_BF16 ? bf16_hi(w.y) : f16_hi(w.y);
             }
-            store_vec<TO, VI>(yp + (size_t) m * VI * EO, f);
+            store_vec<TO, OPS>(yp + (size_t) o * EO, f);
         }
     }
 }
@@ -144,14 +220,20 @@ __global__ void __launch_bounds__(256) k_get_rows_generic(const GetRowsArgs a, i
 }
 
 template <int TO>
-static int launch_to(const GetRowsArgs & a, int ttype, bool fast, hipStream_t s) {
+static int launch_to(const GetRowsArgs & a, int ttype, bool fast, bool lds, hipStream_t s) {
     uint32_t       grid = (a.n_ids + 3) / 4;
     const uint32_t cap  = (uint32_t) num_cus() * 16;
     grid                = grid > cap ? cap : grid;
     if (fast) {
         switch (ttype) {
             case MI_TYPE_Q8_0:
-                hipLaunchKernelGGL((k_get_rows_q8_0<TO>), dim3(grid), dim3(256), 0, s, a);
+                if (lds) {
+                    const int nc = a.n / 32 * 34 / 16;
+                    hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO>), dim3(grid), dim3(256), (size_t) 4 * nc * 16, s, a,
+                                       nc);
+                } else {
+                    hipLaunchKernelGGL((k_get_rows_q8_0<TO>), dim3(grid), dim3(256), 0, s, a);
+                }
                 return MI_OK;
             case MI_TYPE_F32:
                 hipLaunchKernelGGL((k_get_rows_vec<MI_TYPE_F32, TO>), dim3(grid), dim3(256), 0, s, a);
@@ -186,20 +268,22 @@ int launch_get_rows(const mi_tensor & table, const int32_t * ids, int64_t n_ids,
     a.d_err      = d_err;
 
     const int es_out = type_size(y.type);
-    bool      fast;
+    bool      fast, lds = false;
     if (table.type == MI_TYPE_Q8_0) {
         // 8 outputs per lane; 16-bit aligned quants; output 16-byte stores
         fast = a.n % 8 == 0 && aligned(table.data, 2) && a.tnb1 % 2 == 0 && aligned(y.data, 16) &&
                (a.ynb1 % 16 == 0) && (8 * es_out) % 16 == 0;
+        // whole rows through LDS: rows of 16-byte multiples (ne0 % 256 == 0), 16-byte aligned
+        lds = fast && a.n % 256 == 0 && a.n <= 8192 && aligned(table.data, 16) && a.tnb1 % 16 == 0;
     } else {
         const int VI = 16 / type_size(table.type);
         fast         = a.n % VI == 0 && aligned(table.data, 16) && a.tnb1 % 16 == 0 && aligned(y.data, 16) &&
                a.ynb1 % 16 == 0 && (VI * es_out) % 8 == 0;
     }
     if (y.type == MI_TYPE_F32) {
-        return launch_to<MI_TYPE_F32>(a, table.type, fast, s);
+        return launch_to<MI_TYPE_F32>(a, table.type, fast, lds, s);
     }
-    return launch_to<MI_TYPE_BF16>(a, table.type, fast, s);
+    return launch_to<MI_TYPE_BF16>(a, table.type, fast, lds, s);
 }
 
 }  // namespace mi

@@ -101,7 +101,7 @@ struct RowCopy {
     // kv store
     int             kv;
     uint32_t        ne1, ne2;   // src heads, tokens per sequence
-    FastDiv         d1, d12;
+    FastDiv         d1, d2;
     const int32_t * pos0;
     const int32_t * sets;
     int64_t         cnb1, cnb2, cnb3;

@@ -292,11 +292,15 @@ __global__ void __launch_bounds__(256) k_rms_rows_generic(const NormArgs a) {
 }
 
 // Workgroups for a grid-stride loop over ceil(rows/R) row groups, capped at
-// about 16 resident waves per CU, with the groups spread evenly (every
+// about MI_NORM_WPC resident waves per CU, with the groups spread evenly (every
 // workgroup runs the same number of iterations, +-1).
+#ifndef MI_NORM_WPC
+#define MI_NORM_WPC 16  // resident waves per CU the grid is sized for
+#endif
+
 static uint32_t balanced_grid(uint32_t rows, int R, int nw) {
     const uint32_t iters  = (rows + R - 1) / R;
-    const uint32_t max_wg = (uint32_t) num_cus() * (uint32_t) (16 / nw > 0 ? 16 / nw : 1);
+    const uint32_t max_wg = (uint32_t) num_cus() * (uint32_t) (MI_NORM_WPC / nw > 0 ? MI_NORM_WPC / nw : 1);
     const uint32_t per    = (iters + max_wg - 1) / max_wg;
     return (iters + per - 1) / per;
 }

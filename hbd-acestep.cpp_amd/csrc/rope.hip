@@ -38,8 +38,17 @@ namespace mi {
 // behind it. Lanes whose row lies past the segment end load nothing and
 // store nothing (whole L-lane groups, so the DPP row sums stay per group).
 // The Q/K norm weights are staged once per workgroup in LDS.
+#ifndef MI_ROPE_WPE
+#define MI_ROPE_WPE 0  // > 0: ask the compiler for at least this many waves per SIMD
+#endif
+#if MI_ROPE_WPE > 0
+#define MI_ROPE_OCC __attribute__((amdgpu_waves_per_eu(MI_ROPE_WPE, 8)))
+#else
+#define MI_ROPE_OCC
+#endif
+
 template <int TI, int TO, int D, bool NORM, bool ROPE>
-__global__ void __launch_bounds__(256) k_heads(const HeadArgs a, uint32_t nb0, uint32_t nb) {
+__global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uint32_t nb0, uint32_t nb) {
     constexpr int VI   = TT<TI>::VEC;
     constexpr int EI   = TT<TI>::ES;
     constexpr int EO   = TT<TO>::ES;

@@ -17,7 +17,8 @@ def _q8_table(n_rows, n, seed):
     return orc.quantize_q8_0(randn((n_rows, n), seed=seed, scale=0.02), "ref")
 
 
-@pytest.mark.parametrize("n_rows,n,n_ids", [(4096, 1024, 512), (2048, 2048, 1000), (300, 2560, 64), (50, 96, 7)])
+@pytest.mark.parametrize("n_rows,n,n_ids", [(4096, 1024, 512), (2048, 2048, 1000), (300, 2560, 64), (40, 8192, 33),
+                                           (50, 96, 7)])
 @pytest.mark.parametrize("out", ["f32", "bf16"])
 def test_get_rows_q8_0(dev, n_rows, n, n_ids, out):
     print(f"get_rows q8_0 {n_rows}x{n} ids={n_ids} out={out}", flush=True)
