@@ -5,8 +5,9 @@ Workload (the metric's configuration): DiT block, bf16 activations, hidden
 2048, T=6000 latent frames x batch 2 (CFG pair) = 12000 rows, 16 Q / 8 KV
 heads x 128 (NEOX rope, theta 1e4, frame-index positions), SwiGLU at
 intermediate 6144. One step = the block's fused-op launches in
-dit_ggml_build_layer order (reference dit-graph.h:367-448), captured once
-into a HIP graph and replayed:
+dit_ggml_build_layer order (reference dit-graph.h:367-448). K steps are timed
+as one replay of a HIP graph holding K consecutive blocks, as a DiT step runs
+its blocks back to back in one graph:
   norm_sa        = rms_norm*w -> AdaLN modulate (hidden)
   q, k           = QK-norm -> rope on views of the fused QKV projection output
   h1, norm_ffn   = hidden + sa_out * gate_sa, and rms_norm*w -> AdaLN of it
@@ -153,19 +154,25 @@ def gpu_bench(steps: int, warmup: int):
     fused, unfused, _calib, stream, _keep = _setup()
     sh = stream.handle
 
-    def graph_of(launches):
+    def graph_of(launches, copies=1):
+        """One HIP graph holding `copies` consecutive blocks (a DiT step runs its
+        blocks back to back in one graph, so the ~11 us cost of launching a
+        graph is paid once per graph, not once per block)."""
         g = Graph()
         with g.capture(stream):
-            for f in launches:
-                f()
+            for _ in range(copies):
+                for f in launches:
+                    f()
         return g
 
-    def time_graph(g, n):
-        a, b = Event(), Event()
+    def time_steps(launches, n):
+        """Device time of exactly n blocks: one replay of an n-block graph."""
+        g = graph_of(launches, n)
+        g.launch()  # first replay pays one-time costs
         stream.synchronize()
+        a, b = Event(), Event()
         a.record(sh)
-        for _ in range(n):
-            g.launch()
+        g.launch()
         b.record(sh)
         b.synchronize()
         return a.elapsed_ms(b) / n
@@ -189,18 +196,18 @@ def gpu_bench(steps: int, warmup: int):
                 for j in range(len(launches))]
 
     g_fused, g_unfused = graph_of(fused), graph_of(unfused)
-    for _ in range(warmup):
-        g_fused.launch()
-        g_unfused.launch()
+    if warmup:
+        graph_of(fused, warmup).launch()
+        graph_of(unfused, warmup).launch()
     stream.synchronize()
 
-    # timed region: K graph replays of the fused block
+    # timed region: K blocks, one replay of a K-block graph
     device.synchronize()
     t0 = time.perf_counter()
-    ms_step = time_graph(g_fused, steps)
+    ms_step = time_steps(fused, steps)
     device.synchronize()
     wall = time.perf_counter() - t0
-    ms_unfused = time_graph(g_unfused, steps)
+    ms_unfused = time_steps(unfused, steps)
 
     names_f = list(block_bytes(ROWS, fused=True).keys())
     names_u = list(block_bytes(ROWS, fused=False).keys())
@@ -253,7 +260,8 @@ def cpu_bench(rows: int, reps: int, threads: int):
 # The Qwen3 configurations (reported with --configs; the JSON line above stays
 # the DiT block metric). Each is one layer's fused-op chain in
 # qw3lm_forward_batch order (reference qwen3-lm.h:626-741), synthetic N(0,1)
-# inputs resident in HBM, replayed as one HIP graph.
+# inputs resident in HBM; `steps` consecutive layers are captured in one HIP
+# graph and timed as one replay.
 # ---------------------------------------------------------------------------
 Q8_ROW = lambda n: n // 32 * 34  # noqa: E731
 
@@ -394,24 +402,29 @@ def configs_bench(steps: int, warmup: int):
         c = make()
         st, sh = c["stream"], c["stream"].handle
         fns = [f for _, f in c["launches"]]
+        # `steps` consecutive layers in one graph (a model runs its layers back
+        # to back), replayed once after a warm-up replay
         g = Graph()
         with g.capture(st):
-            for f in fns:
-                f()
-        for _ in range(warmup):
-            g.launch()
+            for _ in range(steps):
+                for f in fns:
+                    f()
+        g.launch()
         st.synchronize()
         a, b = Event(), Event()
         a.record(sh)
-        for _ in range(steps):
-            g.launch()
+        g.launch()
         b.record(sh)
         b.synchronize()
         us_layer = 1000.0 * a.elapsed_ms(b) / steps
+        g1 = Graph()
+        with g1.capture(st):
+            for f in fns:
+                f()
         ev = [[Event() for _ in range(len(fns) + 1)] for _ in range(steps)]
         for i in range(steps):
             for _ in range(4):
-                g.launch()
+                g1.launch()
             ev[i][0].record(sh)
             for j, f in enumerate(fns):
                 f()
@@ -427,7 +440,7 @@ def configs_bench(steps: int, warmup: int):
         print(json.dumps({"config": c["name"], "us_per_layer": round(us_layer, 2), "launches": len(fns),
                           "bytes_per_layer": tot, "GB/s": round(tot / (us_layer * 1e-6) / 1e9, 1),
                           "per_op": per}), flush=True)
-        del c, g
+        del c, g, g1
         device.synchronize()
 
 
@@ -510,8 +523,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "ACE-Step DiT block fused ops, bf16, H=2048, T=6000 x N=2 (12000 rows), 16/8 heads "
-                               "x 128, SwiGLU I=6144; 5 launches/step (gated residual fused into the FFN norm), "
-                               "replayed as one HIP graph",
+                               "x 128, SwiGLU I=6144; 5 launches/step (gated residual fused into the FFN norm); "
+                               "K steps timed as one replay of a HIP graph of K consecutive blocks",
                    "rows": ROWS, "hidden": H, "intermediate": I_FF, "bytes_per_step": total_bytes},
         "per_kernel_us": {k: round(v, 2) for k, v in per_k.items()},
         "per_kernel_gbs": {k: round(kb[k] / (per_k[k] * 1e-6) / 1e9, 1) for k in kb},

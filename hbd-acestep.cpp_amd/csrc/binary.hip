@@ -141,9 +141,11 @@ __global__ void __launch_bounds__(512) k_bin_rows(const BinArgs a) {
 #endif
 
 // Flat one-shot grid: thread (block b, lane t) handles vectors
-// v = b*256*U + k*256 + t of the [rows x nvr] vector grid; the F32 column
+// v = b*256*U + k*256 + t of the [rows x nvr] vector grid. Rows are uniformly
+// strided (row r at r * nb1 for every operand); the clamp is a template
+// parameter, so neither costs instructions when unused. The F32 column
 // vectors are read through the caches (a few KB, shared by every row).
-template <int T_, int OP, bool BROW, int U>
+template <int T_, int OP, bool BROW, int U, bool CLAMP>
 __global__ void __launch_bounds__(256) k_bin_flat(const BinArgs a, uint32_t nvr, FastDiv dnvr, uint32_t total) {
     constexpr int  VI = TT<T_>::VEC;
     constexpr int  ES = TT<T_>::ES;
@@ -159,9 +161,9 @@ __global__ void __launch_bounds__(256) k_bin_flat(const BinArgs a, uint32_t nvr,
         if (v < total) {
             row[k] = dnvr.div(v);
             col[k] = v - row[k] * nvr;
-            ra[k]  = ld16(a.a + a.ar.off(row[k]) + (size_t) col[k] * 16);
+            ra[k]  = ld16(a.a + (int64_t) row[k] * a.ar.s1 + (size_t) col[k] * 16);
             if constexpr (LB) {
-                rb[k] = ld16(a.b + a.br.off(row[k]) + (size_t) col[k] * 16);
+                rb[k] = ld16(a.b + (int64_t) row[k] * a.br.s1 + (size_t) col[k] * 16);
             }
         }
     }
@@ -197,12 +199,12 @@ __global__ void __launch_bounds__(256) k_bin_flat(const BinArgs a, uint32_t nvr,
 #pragma unroll
         for (int e = 0; e < VI; ++e) {
             float v = bin_apply<OP, BROW>(fa[e], LB ? fb[e] : 0.0f, V0 ? c0[e] : 0.0f, V1 ? c1[e] : 0.0f);
-            if (a.clamp) {
+            if constexpr (CLAMP) {
                 v = clamp_ggml(v, a.lo, a.hi);
             }
             fy[e] = v;
         }
-        st16(a.y + a.yr.off(row[k]) + (size_t) col[k] * VI * ES, pack16<T_>(fy));
+        st16(a.y + (int64_t) row[k] * a.yr.s1 + (size_t) col[k] * VI * ES, pack16<T_>(fy));
     }
 }
 
@@ -323,8 +325,15 @@ static int launch_flat_op(const BinArgs & a, hipStream_t s) {
     const uint32_t nvr   = (uint32_t) (a.n / VI);
     const uint64_t total = (uint64_t) a.rows * nvr;
     const uint32_t grid  = (uint32_t) ((total + 256u * MI_BIN_U - 1) / (256u * MI_BIN_U));
-    hipLaunchKernelGGL((k_bin_flat<T_, OP, BROW, MI_BIN_U>), dim3(grid), dim3(256), 0, s, a, nvr, FastDiv(nvr),
-                       (uint32_t) total);
+    if constexpr (OP == OP_ADD || OP == OP_NONE) {
+        if (a.clamp) {
+            hipLaunchKernelGGL((k_bin_flat<T_, OP, BROW, MI_BIN_U, true>), dim3(grid), dim3(256), 0, s, a, nvr,
+                               FastDiv(nvr), (uint32_t) total);
+            return MI_OK;
+        }
+    }
+    hipLaunchKernelGGL((k_bin_flat<T_, OP, BROW, MI_BIN_U, false>), dim3(grid), dim3(256), 0, s, a, nvr,
+                       FastDiv(nvr), (uint32_t) total);
     return MI_OK;
 }
 
@@ -422,6 +431,8 @@ int launch_binary(int op, const mi_tensor & a, const mi_tensor * b, const float 
     for (int d = 1; d < 4 && flat; ++d) {
         flat = a.nb[d] % 16 == 0 && y.nb[d] % 16 == 0 && (!b || b->nb[d] % 16 == 0);
     }
+    // rows at r * nb1 in every operand (the flat kernel's addressing)
+    flat = flat && k.ar.uni && k.yr.uni && (!b || k.br.uni);
     if (flat) {
         switch (a.type) {
             case MI_TYPE_F32:

@@ -31,7 +31,7 @@ struct NormArgs {
     const float * sc;
     const float * sh;
     // fused residual add in front of the norm (ADD != 0):
-    //   v = x + x2 (ADD 1) or x + x2 * gate (ADD 2), optionally clamped;
+    //   v = x + x2 (ADD 1), x + x2 * gate (ADD 2), clamp(x + x2) (ADD 3);
     //   v is stored (ysum, rounded to the activation type) and normalized.
     const char *  x2;
     Rows3         x2r;
@@ -119,8 +119,8 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
         for (int r = 0; r < R; ++r) {
             const uint32_t row = rbase + r;
             if (row < a.rows) {
-                const char * xp  = a.x + a.xr.off(row);
-                const char * x2p = ADD ? a.x2 + a.x2r.off(row) : nullptr;
+                const char * xp  = a.x + (int64_t) row * a.xr.s1;
+                const char * x2p = ADD ? a.x2 + (int64_t) row * a.x2r.s1 : nullptr;
 #pragma unroll
                 for (int j = 0; j < C; ++j) {
                     raw[r][j] = ld16(xp + (size_t) ((j * T + tid) * VI) * EI);
@@ -159,7 +159,7 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
                         } else {
                             v = xin[r][j][e] + f2[e];
                         }
-                        if (a.clamp) {
+                        if constexpr (ADD == 3) {
                             const float c = v < a.hi ? v : a.hi;
                             v             = c > a.lo ? c : a.lo;
                         }
@@ -173,7 +173,7 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
             for (int r = 0; r < R; ++r) {
                 const uint32_t row = rbase + r;
                 if (row < a.rows) {
-                    char * sp = a.ysum + a.ysr.off(row);
+                    char * sp = a.ysum + (int64_t) row * a.ysr.s1;
 #pragma unroll
                     for (int j = 0; j < C; ++j) {
                         store_vec<TO, VI>(sp + (size_t) ((j * T + tid) * VI) * EO, xin[r][j]);
@@ -212,7 +212,7 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
                 tot += part[it & 1][r][q];
             }
             const float scale = rms_scale(tot, a.n, a.eps);
-            char *      yp    = a.y + a.yr.off(row);
+            char *      yp    = a.y + (int64_t) row * a.yr.s1;
 #pragma unroll
             for (int j = 0; j < C; ++j) {
                 float f[VI];
@@ -294,6 +294,10 @@ __global__ void __launch_bounds__(256) k_rms_rows_generic(const NormArgs a) {
 // Workgroups for a grid-stride loop over ceil(rows/R) row groups, capped at
 // about MI_NORM_WPC resident waves per CU, with the groups spread evenly (every
 // workgroup runs the same number of iterations, +-1).
+#ifndef MI_NORM_MAXW
+#define MI_NORM_MAXW 8  // most waves sharing one row (more waves: fewer columns per lane)
+#endif
+
 #ifndef MI_NORM_WPC
 #define MI_NORM_WPC 16  // resident waves per CU the grid is sized for
 #endif
@@ -336,10 +340,13 @@ static int dispatch_fast(const NormArgs & a, int T, int C, hipStream_t s) {
     if (a.x2 == nullptr) {
         return dispatch_fast_add<TI, TO, MODE, 0>(a, T, C, s);
     }
-    if (a.gate == nullptr) {
-        return dispatch_fast_add<TI, TO, MODE, 1>(a, T, C, s);
+    if (a.gate != nullptr) {
+        return dispatch_fast_add<TI, TO, MODE, 2>(a, T, C, s);
     }
-    return dispatch_fast_add<TI, TO, MODE, 2>(a, T, C, s);
+    if (a.clamp) {
+        return dispatch_fast_add<TI, TO, MODE, 3>(a, T, C, s);
+    }
+    return dispatch_fast_add<TI, TO, MODE, 1>(a, T, C, s);
 }
 
 template <int TI, int TO>
@@ -407,7 +414,7 @@ int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, cons
     if (fast && a.n % (64 * VI) == 0) {
         const int k = a.n / (64 * VI);
         int       nw = 1;
-        for (int d = 8; d >= 1; --d) {
+        for (int d = MI_NORM_MAXW; d >= 1; --d) {
             if (k % d == 0) {
                 nw = d;
                 break;
@@ -424,6 +431,10 @@ int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, cons
     }
     fast = fast && aligned(x.data, 16) && aligned(y.data, 16) && (!w || aligned(w, 16)) &&
            (!sc || aligned(sc, 16)) && (!sh || aligned(sh, 16));
+    // the fast kernel addresses row r at r * nb1 in every operand
+    fast = fast && a.xr.uni && a.yr.uni && (!add || (a.x2r.uni && a.ysr.uni));
+    // its fused add is either gated or clamped, not both
+    fast = fast && (!add || !(add->gate && add->clamp));
     if (add) {
         fast = fast && add->x2->type == x.type && add->ysum->type == x.type && aligned(add->x2->data, 16) &&
                aligned(add->ysum->data, 16) && (!add->gate || aligned(add->gate, 16));

@@ -16,23 +16,40 @@
 #pragma once
 
 #if defined(__HIPCC__)
-#define MI_HD __host__ __device__ __forceinline__
+#define MI_HD    __host__ __device__ __forceinline__
+#define MI_HD_NI static __host__ __device__ __attribute__((noinline))
 #else
 #include <math.h>
-#define MI_HD static inline
+#define MI_HD    static inline
+#define MI_HD_NI static
 #endif
 
 namespace mi {
 
+struct float2_t {
+    float s, c;
+};
+
+// |x| >= 2^20 or non-finite: the math library. Kept out of line so that the
+// fast path does not carry (or speculatively execute) its large-argument
+// reduction; it returns by value (no pointer into private memory).
+MI_HD_NI float2_t sincos_rot_big(float x) {
+    float2_t r;
+#if defined(__HIP_DEVICE_COMPILE__)
+    sincosf(x, &r.s, &r.c);
+#else
+    r.s = sinf(x);
+    r.c = cosf(x);
+#endif
+    return r;
+}
+
 MI_HD void sincos_rot(float x, float * sp, float * cp) {
     const float ax = __builtin_fabsf(x);
     if (!(ax < 1048576.0f)) {  // |x| >= 2^20 or NaN
-#if defined(__HIP_DEVICE_COMPILE__)
-        sincosf(x, sp, cp);
-#else
-        *sp = sinf(x);
-        *cp = cosf(x);
-#endif
+        const float2_t r = sincos_rot_big(x);
+        *sp              = r.s;
+        *cp              = r.c;
         return;
     }
     const float TWO_OVER_PI = 0.636619746685028076171875f;           // fp32(2/pi)

@@ -94,6 +94,18 @@ def test_rope_position_zero_is_identity(dev):
     assert np.array_equal(y, x)
 
 
+@pytest.mark.parametrize("ne0,n_dims", [(128, 128), (96, 64)])
+def test_rope_huge_positions_take_library_path(dev, ne0, n_dims):
+    """Angles |x| >= 2^20 (positions past 2^20) use the math library's sincosf;
+    positions below stay on the in-kernel reduction. Both against glibc."""
+    x = randn((6, 4, ne0), seed=9)
+    pos = np.array([3, 1048575, 1048576, 3000017, 123456789, 2147483000], np.int32)
+    y = to_np(ops.qk_norm_rope(to_dev(x, dev), to_dev(randn((ne0,), seed=10, scale=0.1, mean=1.0), dev),
+                               to_dev(pos, dev), EPS, n_dims, 1e6)[0])
+    ref = orc.qk_norm_rope(x, randn((ne0,), seed=10, scale=0.1, mean=1.0), pos, EPS, n_dims, 1e6)
+    assert_f32_close(y, ref, row_floor=True)
+
+
 def test_qk_norm_no_rope_cross_attn(dev):
     """Cross-attention QK-norm: rms_norm(x) * w on [D, S, H, N] permuted views."""
     N, S, H, D = 2, 30, 8, 128
