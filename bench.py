@@ -449,8 +449,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-rows", type=int, default=1500, help="row sample for the CPU baseline")
-    ap.add_argument("--cpu-reps", type=int, default=20)
+    ap.add_argument("--cpu-rows", type=int, default=ROWS, help="rows of the block the CPU baseline runs")
+    ap.add_argument("--cpu-reps", type=int, default=64, help="timed CPU repetitions (about 10 s on 8 threads)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="launch each block kernel once plus a copy of known size, for counter collection")
@@ -502,9 +502,10 @@ def main():
             "kind": "port",
             "us_per_block": round(cpu_block_s * 1e6, 1),
             "sample": (f"reference's unfused F32 ggml node graph of one DiT block (rms_norm, mul, add, rope, swiglu "
-                       f"nodes) on {args.cpu_rows} of {ROWS} rows, median of {args.cpu_reps} reps after 3 warm-ups "
-                       f"({spent:.1f} s of CPU work), scaled x{scale:.1f} to the full block; GB/s uses the same "
-                       f"bf16 byte accounting as value"),
+                       f"nodes, ggml-cpu arithmetic restated in C, OpenMP over rows) on {args.cpu_rows} of {ROWS} "
+                       f"rows, median of {args.cpu_reps} reps after 3 warm-ups ({spent:.1f} s of CPU work)"
+                       + (f", scaled x{scale:.2f} to the full block" if args.cpu_rows != ROWS else "")
+                       + "; GB/s uses the same bf16 byte accounting as value"),
         }
 
     line = {
