@@ -22,7 +22,11 @@ def randn(shape, seed=42, scale=1.0, mean=0.0):
 #   fp32: max relative error <= 1e-5; where an output is a difference that can
 #         cancel (rope, modulate, gated add) the denominator is floored at the
 #         RMS of the reference row: |a-b| <= 1e-5 * max(|ref|, rms(ref row)).
-#   bf16: within 1 bf16 ulp of the oracle's RNE-rounded fp32 result.
+#   bf16: within 1 bf16 ulp of the oracle's RNE-rounded fp32 result; for
+#         outputs that are differences that can cancel (rope, modulate), an
+#         element beyond 1 ulp must still meet the fp32 bar with the row floor,
+#         |a-b| <= 1e-5 * rms(ref row): near zero a bf16 ulp is far below the
+#         fp32 rounding of the terms that cancelled.
 # ---------------------------------------------------------------------------
 def rel_err(a: np.ndarray, ref: np.ndarray, row_floor: bool = False, tiny: float = 1e-30) -> float:
     a = np.asarray(a, np.float64)
@@ -53,11 +57,19 @@ def bf16_ordinal(h: np.ndarray) -> np.ndarray:
     return np.where(h & 0x8000, -mag, mag)
 
 
-def assert_bf16_ulp(a_bits, ref_bits, max_ulp=1):
+def assert_bf16_ulp(a_bits, ref_bits, max_ulp=1, row_floor=False, tol=1e-5):
     d = np.abs(bf16_ordinal(a_bits) - bf16_ordinal(ref_bits))
-    worst = int(d.max()) if d.size else 0
-    assert worst <= max_ulp, f"max bf16 ulp distance {worst} > {max_ulp}"
-    return worst
+    bad = d > max_ulp
+    if row_floor and bad.any():
+        a = (np.asarray(a_bits, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        r = (np.asarray(ref_bits, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        n = r.shape[-1]
+        rms = np.sqrt(np.mean(r.reshape(-1, n) ** 2, axis=1, keepdims=True))
+        floor = (tol * rms * np.ones((1, n))).reshape(r.shape)
+        bad &= ~(np.abs(a - r) <= floor)
+    worst = int(d[bad].max()) if bad.any() else 0
+    assert not bad.any(), f"{int(bad.sum())} elements beyond {max_ulp} bf16 ulp (worst {worst})"
+    return int(d.max()) if d.size else 0
 
 
 def frac_bitexact(a: np.ndarray, ref: np.ndarray) -> float:

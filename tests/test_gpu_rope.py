@@ -30,7 +30,7 @@ def _fused_qkv(T, nh, nkv, D, seed, bf16, dev):
 
 def _check(out, ref_f32_fn, host_in, bf16):
     if bf16:
-        assert_bf16_ulp(to_np(out), orc.bf16_chain(ref_f32_fn, host_in))
+        assert_bf16_ulp(to_np(out), orc.bf16_chain(ref_f32_fn, host_in), row_floor=True)
     else:
         assert_f32_close(to_np(out), ref_f32_fn(host_in), row_floor=True)
 
