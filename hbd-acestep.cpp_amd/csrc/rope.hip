@@ -28,7 +28,9 @@ namespace mi {
 #define MI_ROPE_PF 3  // row batches (64/L head rows each) loaded ahead per wave
 #endif
 
-// One wave per token (grid-stride over tokens). Lane 0 runs the token's fp32
+// One wave per (token, group of head batches): a whole token per wave when
+// there are enough tokens to fill the chip, a few batches per wave otherwise
+// (decode), grid-stride over those items. Lane 0 runs the token's fp32
 // theta chain into LDS, lane l turns theta_l into cos/sin (sincos_rot) and
 // stores them back, and every lane then reads the VEC pairs it rotates. The
 // wave streams the token's head rows in batches of R = 64/L rows, Q rows
@@ -48,7 +50,8 @@ namespace mi {
 #endif
 
 template <int TI, int TO, int D, bool NORM, bool ROPE>
-__global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uint32_t nb0, uint32_t nb) {
+__global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uint32_t nb0, uint32_t nb, uint32_t bpw,
+                                                           FastDiv dgroups) {
     constexpr int VI   = TT<TI>::VEC;
     constexpr int EI   = TT<TI>::ES;
     constexpr int EO   = TT<TO>::ES;
@@ -82,9 +85,15 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
         ly[sg] = (int64_t) g * a.seg[sg].ys1 + (int64_t) (j * VI) * EO;
     }
 
-    for (uint32_t t = blockIdx.x * 4 + wv; t < a.ntok; t += gridDim.x * 4) {
-        const uint32_t i3 = a.dne2.div(t);
-        const uint32_t i2 = t - i3 * a.ne2;
+    // work item = (token, group of bpw batches); few tokens -> several waves per token
+    const uint32_t ngroups = dgroups.d;
+    const uint32_t nitems  = a.ntok * ngroups;
+    for (uint32_t item = blockIdx.x * 4 + wv; item < nitems; item += gridDim.x * 4) {
+        const uint32_t t     = dgroups.div(item);
+        const uint32_t bbeg  = (item - t * ngroups) * bpw;
+        const uint32_t bend  = bbeg + bpw < nb ? bbeg + bpw : nb;
+        const uint32_t i3    = a.dne2.div(t);
+        const uint32_t i2    = t - i3 * a.ne2;
 
         // batch b: segment and first head row (both wave-uniform)
         auto seg_of = [&](uint32_t b, int & sg, uint32_t & h0) {
@@ -94,7 +103,7 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
         auto load_batch = [&](uint32_t b0, uint4 * v0, uint4 * v1) {
 #pragma unroll
             for (int k = 0; k < PF; ++k) {
-                if (b0 + k < nb) {
+                if (b0 + k < bend) {
                     int      sg;
                     uint32_t h0;
                     seg_of(b0 + k, sg, h0);
@@ -111,7 +120,7 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
         };
 
         uint4 v0[PF], v1[PF];
-        load_batch(0, v0, v1);
+        load_batch(bbeg, v0, v1);
 
         float cv[VI], sv[VI];
         if constexpr (ROPE) {
@@ -154,13 +163,13 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
             __builtin_amdgcn_wave_barrier();
         }
 
-        for (uint32_t b0 = 0; b0 < nb; b0 += PF) {
-            if (b0 > 0) {
+        for (uint32_t b0 = bbeg; b0 < bend; b0 += PF) {
+            if (b0 > bbeg) {
                 load_batch(b0, v0, v1);
             }
 #pragma unroll
             for (int k = 0; k < PF; ++k) {
-                if (b0 + k >= nb) {
+                if (b0 + k >= bend) {
                     continue;
                 }
                 int      sg;
@@ -290,16 +299,28 @@ static void launch_fast(const HeadArgs & a, hipStream_t s) {
     const uint32_t h1  = a.nseg > 1 ? a.seg[1].heads : 0u;
     const uint32_t nb0 = (h0 + R - 1) / R;
     const uint32_t nb  = nb0 + (h1 + R - 1) / R;
-    uint64_t       grid = ((uint64_t) a.ntok + 3) / 4;  // 4 waves (tokens) per workgroup
+    // one wave per token when there are enough tokens to fill the chip (cos/sin
+    // computed once per token); otherwise split each token's batches over up to
+    // nb waves so that every wave makes a single memory round trip
+    const uint64_t want = (uint64_t) num_cus() * 8;
+    uint32_t       grp  = (uint32_t) ((want + a.ntok - 1) / a.ntok);
+    grp                 = grp < 1 ? 1 : (grp > nb ? nb : grp);
+    const uint32_t bpw  = (nb + grp - 1) / grp;
+    grp                 = (nb + bpw - 1) / bpw;
+    uint64_t       grid = ((uint64_t) a.ntok * grp + 3) / 4;  // 4 waves per workgroup
     const uint64_t cap  = (uint64_t) num_cus() * 64;
     grid                = grid > cap ? cap : grid;
-    const bool rope     = a.pos != nullptr;
+    const FastDiv dg(grp);
+    const bool    rope = a.pos != nullptr;
     if (a.norm && rope) {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, true, true>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb);
+        hipLaunchKernelGGL((k_heads<TI, TO, D, true, true>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb, bpw,
+                           dg);
     } else if (a.norm) {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, true, false>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb);
+        hipLaunchKernelGGL((k_heads<TI, TO, D, true, false>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb,
+                           bpw, dg);
     } else {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, false, true>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb);
+        hipLaunchKernelGGL((k_heads<TI, TO, D, false, true>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb,
+                           bpw, dg);
     }
 }
 
