@@ -10,6 +10,8 @@
 //    shuffles across rows.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -263,6 +265,28 @@ template <int L> __device__ __forceinline__ double group_sum(double v) {
     return v;
 }
 
+template <int L> __device__ __forceinline__ float group_sum(float v) {
+    if constexpr (L >= 2) {
+        v += dpp_f<0xB1>(v);
+    }
+    if constexpr (L >= 4) {
+        v += dpp_f<0x4E>(v);
+    }
+    if constexpr (L >= 8) {
+        v += dpp_f<0x141>(v);
+    }
+    if constexpr (L >= 16) {
+        v += dpp_f<0x140>(v);
+    }
+    if constexpr (L >= 32) {
+        v += __shfl_xor(v, 16, 64);
+    }
+    if constexpr (L >= 64) {
+        v += __shfl_xor(v, 32, 64);
+    }
+    return v;
+}
+
 template <int L> __device__ __forceinline__ float group_max(float v) {
     if constexpr (L >= 2) {
         v = fmaxf(v, dpp_f<0xB1>(v));
@@ -308,6 +332,25 @@ __device__ __forceinline__ float log_f32(float x) {
 // mean = (float)(sum / n), scale = 1.0f / sqrtf(mean + eps). For n a power of
 // two, sum / n == sum * (1/n) exactly (a sum of float squares is never a
 // double subnormal), so the division becomes a multiply.
+// RMSNorm sum of squares. F32 activations: ggml's arithmetic, the float
+// square summed in double. BF16/F16 activations: fp32 accumulation (one fma
+// per element), the arithmetic the bf16 bar is stated for; it keeps the
+// row scale within a few fp32 ulp of the double sum.
+template <int TI> using sq_t = typename std::conditional<TI == MI_TYPE_F32, double, float>::type;
+
+template <int TI> __device__ __forceinline__ sq_t<TI> sq_acc(sq_t<TI> acc, float x) {
+    if constexpr (TI == MI_TYPE_F32) {
+        return acc + (double) (x * x);
+    } else {
+        return __builtin_fmaf(x, x, acc);
+    }
+}
+
+__device__ __forceinline__ float rms_scale(float sum, int n, float eps) {
+    const float mean = (n & (n - 1)) == 0 ? sum * (1.0f / (float) n) : sum / (float) n;
+    return 1.0f / sqrtf(mean + eps);
+}
+
 __device__ __forceinline__ float rms_scale(double sum, int n, float eps) {
     const float mean = (n & (n - 1)) == 0 ? (float) (sum * (1.0 / (double) n)) : (float) (sum / (double) n);
     return 1.0f / sqrtf(mean + eps);

@@ -68,7 +68,8 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
     const int     lane = tid & 63;
     const int     nw   = T >> 6;
 
-    __shared__ double part[2][R][8];
+    using acc_t = sq_t<TI>;
+    __shared__ acc_t part[2][R][8];
 
     float wv[C][VI], sv[C][VI], hv[C][VI], gv[C][VI];
     if constexpr (ADD == 2) {
@@ -181,15 +182,15 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
                 }
             }
         }
-        double s[R];
+        acc_t s[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            s[r] = 0.0;
+            s[r] = 0;
 #pragma unroll
             for (int j = 0; j < C; ++j) {
 #pragma unroll
                 for (int e = 0; e < VI; ++e) {
-                    s[r] += (double) (xin[r][j][e] * xin[r][j][e]);
+                    s[r] = sq_acc<TI>(s[r], xin[r][j][e]);
                 }
             }
             s[r] = group_sum<64>(s[r]);
@@ -207,7 +208,7 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
             if (row >= a.rows) {
                 continue;
             }
-            double tot = 0.0;
+            acc_t tot = 0;
             for (int q = 0; q < nw; ++q) {
                 tot += part[it & 1][r][q];
             }

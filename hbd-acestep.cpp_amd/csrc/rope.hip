@@ -40,6 +40,9 @@ namespace mi {
 // behind it. Lanes whose row lies past the segment end load nothing and
 // store nothing (whole L-lane groups, so the DPP row sums stay per group).
 // The Q/K norm weights are staged once per workgroup in LDS.
+#ifndef MI_ROPE_WG_PER_CU
+#define MI_ROPE_WG_PER_CU 64  // grid cap (workgroups per CU); fewer: each wave walks more tokens
+#endif
 #ifndef MI_ROPE_WPE
 #define MI_ROPE_WPE 0  // > 0: ask the compiler for at least this many waves per SIMD
 #endif
@@ -179,14 +182,14 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
                 unpack16<TI>(v0[k], x0);
                 unpack16<TI>(v1[k], x1);
                 if constexpr (NORM) {
-                    double ss = 0.0;
+                    sq_t<TI> ss = 0;
 #pragma unroll
                     for (int e = 0; e < VI; ++e) {
-                        ss += (double) (x0[e] * x0[e]);
+                        ss = sq_acc<TI>(ss, x0[e]);
                     }
 #pragma unroll
                     for (int e = 0; e < VI; ++e) {
-                        ss += (double) (x1[e] * x1[e]);
+                        ss = sq_acc<TI>(ss, x1[e]);
                     }
                     ss                = group_sum<L>(ss);
                     const float scale = rms_scale(ss, D, a.eps);
@@ -308,7 +311,7 @@ static void launch_fast(const HeadArgs & a, hipStream_t s) {
     const uint32_t bpw  = (nb + grp - 1) / grp;
     grp                 = (nb + bpw - 1) / bpw;
     uint64_t       grid = ((uint64_t) a.ntok * grp + 3) / 4;  // 4 waves per workgroup
-    const uint64_t cap  = (uint64_t) num_cus() * 64;
+    const uint64_t cap  = (uint64_t) num_cus() * MI_ROPE_WG_PER_CU;
     grid                = grid > cap ? cap : grid;
     const FastDiv dg(grp);
     const bool    rope = a.pos != nullptr;

@@ -79,8 +79,9 @@ const char * mi_status_str(int status);
  * 429 cross-attn norm) and the QK-norm without rope of the DiT cross
  * attention (dit-graph.h:328-331).
  * x, y: [n, ...] F32/BF16, rows may be strided (nb[0] = element size);
- * w: F32 [n] or NULL. Reduction: float squares summed in double,
- * mean = (float)(sum/n), scale = 1.0f/sqrtf(mean + eps). */
+ * w: F32 [n] or NULL. Reduction: float squares summed in double for F32
+ * rows (ggml-cpu's order of operations), in fp32 for BF16 rows;
+ * mean = sum/n, scale = 1.0f/sqrtf(mean + eps). */
 int mi_rms_norm(const mi_tensor * x, const mi_tensor * w, float eps, const mi_tensor * y, mi_stream stream);
 
 /* RMSNorm * w then AdaLN modulate, fused:

@@ -3,7 +3,9 @@
 fp32: <= 1e-5 relative and, since the kernels sum float squares in double
 like ggml-cpu, >= 99.9% of outputs bit-identical (a different summation order
 can flip the final float rounding of the mean in rare rows).
-bf16: within 1 ulp of the oracle's RNE-rounded fp32 chain.
+bf16: within 1 ulp of the oracle's RNE-rounded fp32 chain. The kernels sum
+bf16 squares in fp32 (the oracle in double); the two sums differ by ~2^-18
+relative, far inside half a bf16 ulp.
 """
 import numpy as np
 import pytest
