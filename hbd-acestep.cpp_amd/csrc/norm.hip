@@ -5,6 +5,7 @@
 // dit-graph.h:24-30 and 54-64):
 //   n = rms_norm(x, eps)          sum_i (double)(x_i*x_i); mean = (float)(sum/ne0);
 //                                 scale = 1.0f/sqrtf(mean + eps); n_i = x_i*scale
+//                                 (F32 rows; BF16/F16 rows sum the squares in fp32)
 //   n = n * w                     (ggml_mul, [ne0] broadcast)
 //   m = (n * (scale_v + 1)) + shift_v   (dit_ggml_adaln)
 // Every intermediate stays fp32 in registers, rounded exactly as the ggml
@@ -14,8 +15,9 @@
 // same C 16-byte column vectors, so the F32 weight / (scale+1) / shift
 // vectors are loaded once into registers and reused for every row the
 // workgroup processes. R rows are loaded before any is reduced so each lane
-// keeps R*C 128-bit loads in flight; per-row partial sums (double) are
-// reduced in-wave with DPP, then across waves through LDS in a fixed order.
+// keeps R*C 128-bit loads in flight; per-row partial sums (double for F32
+// rows, fp32 for 16-bit rows) are reduced in-wave with DPP, then across waves
+// through LDS in a fixed order.
 #include "launch.h"
 
 namespace mi {

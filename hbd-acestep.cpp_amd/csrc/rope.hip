@@ -11,7 +11,8 @@
 // theta_scale = powf(freq_base, -2/n_dims) is computed on the host, with the
 // host libm, as ggml-cpu does.
 //
-// Fast path (n_dims == ne0 == D in {64, 128, 256}): one wave per token. A
+// Fast path (n_dims == ne0 == D in {64, 128, 256}): a wave handles one token
+// at a time and walks its tokens with the next one's loads in flight. A
 // lane holds 16 bytes of the first half of a head row and the matching 16
 // bytes of the second half, so both members of every rotated pair are in the
 // same lane (no cross-lane exchange for the rotation). A head row is spread
@@ -28,20 +29,27 @@ namespace mi {
 #define MI_ROPE_PF 3  // row batches (64/L head rows each) loaded ahead per wave
 #endif
 
-// One wave per (token, group of head batches): a whole token per wave when
-// there are enough tokens to fill the chip, a few batches per wave otherwise
-// (decode), grid-stride over those items. Lane 0 runs the token's fp32
-// theta chain into LDS, lane l turns theta_l into cos/sin (sincos_rot) and
-// stores them back, and every lane then reads the VEC pairs it rotates. The
-// wave streams the token's head rows in batches of R = 64/L rows, Q rows
-// first, then K rows; a batch never mixes Q and K, so the segment (pointers,
-// strides, weights) is wave-uniform and its addressing stays scalar. Loads of
-// the first PF batches are issued before the trig so their latency hides
-// behind it. Lanes whose row lies past the segment end load nothing and
-// store nothing (whole L-lane groups, so the DPP row sums stay per group).
-// The Q/K norm weights are staged once per workgroup in LDS.
+// One wave per (token, group of head batches) work item: a whole token per
+// item when there are enough tokens to fill the chip, a few batches per item
+// otherwise (decode). The grid is persistent (the workgroups that fit on the
+// chip at once) and each wave walks its items with a stride, software
+// pipelined: the loads of the next item's first PF batches are issued before
+// the current item is computed, so every wave keeps a token's rows in flight
+// while it computes and stores the previous one. The two register sets
+// alternate between even and odd steps (no copies, which would wait for the
+// loads). The first item's loads are issued before anything else, the Q/K
+// norm weights are then staged once per workgroup in LDS.
+//
+// Per item, lane 0 runs the token's fp32 theta chain into LDS, lane l turns
+// theta_l into cos/sin (sincos_rot) and stores them back, and every lane then
+// reads the VEC pairs it rotates. The wave streams the token's head rows in
+// batches of R = 64/L rows, Q rows first, then K rows; a batch never mixes Q
+// and K, so the segment (pointers, strides, weights) is wave-uniform and its
+// addressing stays scalar. Lanes whose row lies past the segment end load
+// nothing and store nothing (whole L-lane groups, so the DPP row sums stay per
+// group).
 #ifndef MI_ROPE_WG_PER_CU
-#define MI_ROPE_WG_PER_CU 64  // grid cap (workgroups per CU); fewer: each wave walks more tokens
+#define MI_ROPE_WG_PER_CU 0  // grid cap in workgroups per CU; 0: as many as fit at once
 #endif
 #ifndef MI_ROPE_WPE
 #define MI_ROPE_WPE 0  // > 0: ask the compiler for at least this many waves per SIMD
@@ -51,6 +59,11 @@ namespace mi {
 #else
 #define MI_ROPE_OCC
 #endif
+
+struct HeadItem {
+    uint32_t bbeg, bend;  // batch range
+    uint32_t i2, i3;      // token coordinates
+};
 
 template <int TI, int TO, int D, bool NORM, bool ROPE>
 __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uint32_t nb0, uint32_t nb, uint32_t bpw,
@@ -72,14 +85,6 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
     const int      j    = lane % L;
     const int      g    = lane / L;
 
-    if constexpr (NORM) {
-        for (int i = threadIdx.x; i < 2 * D; i += 256) {
-            const float * w = i < D ? a.seg[0].w : (a.nseg > 1 ? a.seg[1].w : nullptr);
-            wt[i / D][i % D] = w ? w[i % D] : 1.0f;
-        }
-        __syncthreads();
-    }
-
     // per-lane byte offsets inside a batch, per segment
     int64_t lx[2], ly[2];
 #pragma unroll
@@ -88,49 +93,66 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
         ly[sg] = (int64_t) g * a.seg[sg].ys1 + (int64_t) (j * VI) * EO;
     }
 
-    // work item = (token, group of bpw batches); few tokens -> several waves per token
     const uint32_t ngroups = dgroups.d;
     const uint32_t nitems  = a.ntok * ngroups;
-    for (uint32_t item = blockIdx.x * 4 + wv; item < nitems; item += gridDim.x * 4) {
-        const uint32_t t     = dgroups.div(item);
-        const uint32_t bbeg  = (item - t * ngroups) * bpw;
-        const uint32_t bend  = bbeg + bpw < nb ? bbeg + bpw : nb;
-        const uint32_t i3    = a.dne2.div(t);
-        const uint32_t i2    = t - i3 * a.ne2;
+    const uint32_t stride  = gridDim.x * 4;
 
-        // batch b: segment and first head row (both wave-uniform)
-        auto seg_of = [&](uint32_t b, int & sg, uint32_t & h0) {
-            sg = b >= nb0 ? 1 : 0;
-            h0 = (b - (sg ? nb0 : 0u)) * R;
-        };
-        auto load_batch = [&](uint32_t b0, uint4 * v0, uint4 * v1) {
+    auto decode = [&](uint32_t item) {
+        HeadItem       it;
+        const uint32_t t = dgroups.div(item);
+        it.bbeg          = (item - t * ngroups) * bpw;
+        it.bend          = it.bbeg + bpw < nb ? it.bbeg + bpw : nb;
+        it.i3            = a.dne2.div(t);
+        it.i2            = t - it.i3 * a.ne2;
+        return it;
+    };
+    // batch b: segment and first head row (both wave-uniform)
+    auto seg_of = [&](uint32_t b, int & sg, uint32_t & h0) {
+        sg = b >= nb0 ? 1 : 0;
+        h0 = (b - (sg ? nb0 : 0u)) * R;
+    };
+    auto load_batch = [&](const HeadItem & it, uint32_t b0, uint4 * v0, uint4 * v1) {
 #pragma unroll
-            for (int k = 0; k < PF; ++k) {
-                if (b0 + k < bend) {
-                    int      sg;
-                    uint32_t h0;
-                    seg_of(b0 + k, sg, h0);
-                    const HeadSeg & S  = a.seg[sg];
-                    const char *    xp = S.x + (int64_t) i3 * S.xs3 + (int64_t) i2 * S.xs2 + (int64_t) h0 * S.xs1 + lx[sg];
-                    v0[k] = make_uint4(0, 0, 0, 0);
-                    v1[k] = make_uint4(0, 0, 0, 0);
-                    if (h0 + g < S.heads) {
-                        v0[k] = ld16(xp);
-                        v1[k] = ld16(xp + (size_t) HALF * EI);
-                    }
+        for (int k = 0; k < PF; ++k) {
+            if (b0 + k < it.bend) {
+                int      sg;
+                uint32_t h0;
+                seg_of(b0 + k, sg, h0);
+                const HeadSeg & S  = a.seg[sg];
+                const char *    xp = S.x + (int64_t) it.i3 * S.xs3 + (int64_t) it.i2 * S.xs2 + (int64_t) h0 * S.xs1 + lx[sg];
+                v0[k]              = make_uint4(0, 0, 0, 0);
+                v1[k]              = make_uint4(0, 0, 0, 0);
+                if (h0 + g < S.heads) {
+                    v0[k] = ld16(xp);
+                    v1[k] = ld16(xp + (size_t) HALF * EI);
                 }
             }
-        };
+        }
+    };
 
-        uint4 v0[PF], v1[PF];
-        load_batch(bbeg, v0, v1);
+    // one item: rows of `it` arrive in c0/c1 (first PF batches already
+    // issued); the next item's first batches are issued into n0/n1
+    auto step = [&](uint32_t item, HeadItem & it, uint4 * c0, uint4 * c1, uint4 * n0, uint4 * n1) {
+        const uint32_t nxt    = item + stride;
+        const bool     one    = it.bend - it.bbeg <= (uint32_t) PF;  // a single load round
+        HeadItem       nx     = it;
+        auto           ahead  = [&]() {
+            if (nxt < nitems) {
+                nx = decode(nxt);
+                load_batch(nx, nx.bbeg, n0, n1);
+            }
+        };
+        if (one) {
+            ahead();
+        }
 
         float cv[VI], sv[VI];
         if constexpr (ROPE) {
-            float * ct = tab[wv][0];
-            float * st = tab[wv][1];
+            float *     ct = tab[wv][0];
+            float *     st = tab[wv][1];
+            const float p  = (float) a.pos[it.i2];  // wave-uniform: scalar load
             if (lane == 0) {
-                float th = (float) a.pos[i2];
+                float th = p;
                 ct[0]    = th;
                 for (int i = 1; i < HALF; ++i) {
                     th    = th * a.theta_scale;
@@ -166,21 +188,24 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
             __builtin_amdgcn_wave_barrier();
         }
 
-        for (uint32_t b0 = bbeg; b0 < bend; b0 += PF) {
-            if (b0 > bbeg) {
-                load_batch(b0, v0, v1);
+        for (uint32_t b0 = it.bbeg; b0 < it.bend; b0 += PF) {
+            if (b0 > it.bbeg) {
+                load_batch(it, b0, c0, c1);
+                if (b0 + PF >= it.bend) {
+                    ahead();
+                }
             }
 #pragma unroll
             for (int k = 0; k < PF; ++k) {
-                if (b0 + k >= bend) {
+                if (b0 + k >= it.bend) {
                     continue;
                 }
                 int      sg;
                 uint32_t h0;
                 seg_of(b0 + k, sg, h0);
                 float x0[VI], x1[VI];
-                unpack16<TI>(v0[k], x0);
-                unpack16<TI>(v1[k], x1);
+                unpack16<TI>(c0[k], x0);
+                unpack16<TI>(c1[k], x1);
                 if constexpr (NORM) {
                     sq_t<TI> ss = 0;
 #pragma unroll
@@ -203,27 +228,50 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
                 if constexpr (ROPE) {
 #pragma unroll
                     for (int e = 0; e < VI; ++e) {
-                        const float a0 = x0[e] * cv[e];
+                        const float a0  = x0[e] * cv[e];
                         const float b0_ = x1[e] * sv[e];
-                        const float a1 = x0[e] * sv[e];
-                        const float b1 = x1[e] * cv[e];
-                        x0[e]          = a0 - b0_;
-                        x1[e]          = a1 + b1;
+                        const float a1  = x0[e] * sv[e];
+                        const float b1  = x1[e] * cv[e];
+                        x0[e]           = a0 - b0_;
+                        x1[e]           = a1 + b1;
                     }
                 }
                 const HeadSeg & S = a.seg[sg];
                 if (h0 + g < S.heads) {
-                    char * yp = S.y + (int64_t) i3 * S.ys3 + (int64_t) i2 * S.ys2 + (int64_t) h0 * S.ys1 + ly[sg];
+                    char * yp = S.y + (int64_t) it.i3 * S.ys3 + (int64_t) it.i2 * S.ys2 + (int64_t) h0 * S.ys1 + ly[sg];
                     store_vec<TO, VI>(yp, x0);
                     store_vec<TO, VI>(yp + (size_t) HALF * EO, x1);
                 }
             }
         }
+        it = nx;
+    };
+
+    uint4    va0[PF], va1[PF], vb0[PF], vb1[PF];
+    uint32_t item = blockIdx.x * 4 + wv;
+    HeadItem it{};
+    if (item < nitems) {
+        it = decode(item);
+        load_batch(it, it.bbeg, va0, va1);
+    }
+    if constexpr (NORM) {
+        for (int i = threadIdx.x; i < 2 * D; i += 256) {
+            const float * w = i < D ? a.seg[0].w : (a.nseg > 1 ? a.seg[1].w : nullptr);
+            wt[i / D][i % D] = w ? w[i % D] : 1.0f;
+        }
+        __syncthreads();
+    }
+    while (item < nitems) {
+        step(item, it, va0, va1, vb0, vb1);
+        item += stride;
+        if (item >= nitems) {
+            break;
+        }
+        step(item, it, vb0, vb1, va0, va1);
+        item += stride;
     }
 }
 
-// Generic path: any ne0 / n_dims (even, <= ne0), element-aligned rows.
-// One wave per head row; each lane derives the theta chain of its own pairs.
 template <int TI, int TO>
 __global__ void __launch_bounds__(256) k_heads_generic(const HeadArgs a) {
     constexpr int EI   = TT<TI>::ES;
@@ -294,6 +342,27 @@ __global__ void __launch_bounds__(256) k_heads_generic(const HeadArgs a) {
     }
 }
 
+// Grid of the workgroups (4 waves, one item each at a time) that fit on the
+// chip at once, or fewer when there are fewer items; each kernel's
+// occupancy is queried once.
+template <auto kernel, typename... Args>
+static void launch_persistent(uint64_t items, hipStream_t s, Args... args) {
+    static const int per_cu = [&]() {
+        int n = 0;
+        if (MI_ROPE_WG_PER_CU > 0 ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(kernel), 256, 0) !=
+                hipSuccess ||
+            n < 1) {
+            n = MI_ROPE_WG_PER_CU > 0 ? MI_ROPE_WG_PER_CU : 4;
+        }
+        return n;
+    }();
+    uint64_t       grid = (items + 3) / 4;
+    const uint64_t cap  = (uint64_t) num_cus() * (uint64_t) per_cu;
+    grid                = grid > cap ? cap : grid;
+    hipLaunchKernelGGL(kernel, dim3((uint32_t) grid), dim3(256), 0, s, args...);
+}
+
 template <int TI, int TO, int D>
 static void launch_fast(const HeadArgs & a, hipStream_t s) {
     constexpr int  L   = D / 2 / TT<TI>::VEC;
@@ -310,20 +379,15 @@ static void launch_fast(const HeadArgs & a, hipStream_t s) {
     grp                 = grp < 1 ? 1 : (grp > nb ? nb : grp);
     const uint32_t bpw  = (nb + grp - 1) / grp;
     grp                 = (nb + bpw - 1) / bpw;
-    uint64_t       grid = ((uint64_t) a.ntok * grp + 3) / 4;  // 4 waves per workgroup
-    const uint64_t cap  = (uint64_t) num_cus() * MI_ROPE_WG_PER_CU;
-    grid                = grid > cap ? cap : grid;
-    const FastDiv dg(grp);
-    const bool    rope = a.pos != nullptr;
+    const uint64_t items = (uint64_t) a.ntok * grp;
+    const FastDiv  dg(grp);
+    const bool     rope = a.pos != nullptr;
     if (a.norm && rope) {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, true, true>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb, bpw,
-                           dg);
+        launch_persistent<k_heads<TI, TO, D, true, true>>(items, s, a, nb0, nb, bpw, dg);
     } else if (a.norm) {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, true, false>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb,
-                           bpw, dg);
+        launch_persistent<k_heads<TI, TO, D, true, false>>(items, s, a, nb0, nb, bpw, dg);
     } else {
-        hipLaunchKernelGGL((k_heads<TI, TO, D, false, true>), dim3((uint32_t) grid), dim3(256), 0, s, a, nb0, nb,
-                           bpw, dg);
+        launch_persistent<k_heads<TI, TO, D, false, true>>(items, s, a, nb0, nb, bpw, dg);
     }
 }
 
