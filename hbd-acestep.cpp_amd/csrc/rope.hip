@@ -28,6 +28,9 @@ namespace mi {
 #ifndef MI_ROPE_PF
 #define MI_ROPE_PF 3  // row batches (64/L head rows each) loaded ahead per wave
 #endif
+#ifndef MI_ROPE_ONE_ROUND
+#define MI_ROPE_ONE_ROUND 1  // split tokens with more than PF batches over several work items
+#endif
 
 // One wave per (token, group of head batches) work item: a whole token per
 // item when there are enough tokens to fill the chip, a few batches per item
@@ -376,6 +379,12 @@ static void launch_fast(const HeadArgs & a, hipStream_t s) {
     // nb waves so that every wave makes a single memory round trip
     const uint64_t want = (uint64_t) num_cus() * 8;
     uint32_t       grp  = (uint32_t) ((want + a.ntok - 1) / a.ntok);
+#if MI_ROPE_ONE_ROUND
+    // at most PF batches per item: one load round, which the item before it
+    // already issued (the cos/sin table is then built once per item)
+    const uint32_t rounds = (nb + MI_ROPE_PF - 1) / MI_ROPE_PF;
+    grp                   = grp < rounds ? rounds : grp;
+#endif
     grp                 = grp < 1 ? 1 : (grp > nb ? nb : grp);
     const uint32_t bpw  = (nb + grp - 1) / grp;
     grp                 = (nb + bpw - 1) / bpw;
