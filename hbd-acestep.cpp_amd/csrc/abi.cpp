@@ -481,7 +481,7 @@ int mi_modulate(const mi_tensor * x, const mi_tensor * scale, const mi_tensor * 
 int mi_get_rows(const mi_tensor * table, const mi_tensor * ids, const mi_tensor * y, int32_t * d_err,
                 mi_stream stream) {
     MI_TRY(check(table));
-    MI_TRY(check(ids));
+    MI_TRY(check(ids, false));
     MI_TRY(check(y));
     if (table->type != MI_TYPE_Q8_0 && !is_act(table->type)) {
         return MI_ERR_TYPE;
@@ -495,10 +495,11 @@ int mi_get_rows(const mi_tensor * table, const mi_tensor * ids, const mi_tensor 
     if (y->ne[0] != table->ne[0] || y->ne[1] != ids->ne[0] || y->ne[2] != 1 || y->ne[3] != 1) {
         return MI_ERR_SHAPE;
     }
-    if (!aligned(d_err, 4)) {
+    if (!aligned(d_err, 4) || ids->nb[0] % 4 != 0) {
         return MI_ERR_ALIGN;
     }
-    return finish(launch_get_rows(*table, (const int32_t *) ids->data, ids->ne[0], 1, *y, d_err,
+    const int64_t ids_stride = ids->ne[0] > 1 ? (int64_t) (ids->nb[0] / 4) : 1;
+    return finish(launch_get_rows(*table, (const int32_t *) ids->data, ids->ne[0], ids_stride, *y, d_err,
                                   (hipStream_t) stream));
 }
 

@@ -6,12 +6,14 @@
 // The int8 x fp16 product has at most 8 + 11 significant bits, so the fp32
 // result is exact: the output is bit-identical to ggml-cpu.
 //
-// Q8_0 path: one wave per id; each lane produces 8 consecutive outputs (two
-// 16-byte stores, so the wave's stores are fully coalesced). When the row is
-// a whole number of 16-byte chunks (ne0 % 256 == 0: every Qwen3 hidden size)
-// the wave first stages the row in LDS with coalesced 16-byte loads, so a row
-// costs one memory round trip; otherwise its 8 quants, at byte 34b + 2 + 8k
-// (only 2-byte aligned), are read as four 16-bit loads.
+// Q8_0 path: rows shorter than 64 16-byte output vectors (KV-cache heads) go
+// through a flat kernel, one output vector per thread-step. Longer rows: one
+// wave per id; each lane produces one 16-byte output vector (4 F32 or 8 BF16
+// outputs) per step, so every store instruction writes 1 KB contiguous. When
+// the row is a whole number of 16-byte chunks (ne0 % 256 == 0: every Qwen3
+// hidden size) the wave first stages the row in LDS with coalesced 16-byte
+// loads, so a row costs one memory round trip; otherwise a lane's quants,
+// only 2-byte aligned (block b starts at byte 34b), are read as 16-bit loads.
 // F16/BF16/F32 tables: 16-byte row vectors converted to f32.
 // An id outside [0, n_rows) writes a zero row and bumps *d_err.
 #include "launch.h"
@@ -179,6 +181,77 @@ __global__ void __launch_bounds__(256) k_get_rows_vec(const GetRowsArgs a) {
     }
 }
 
+// Flat Q8_0 path, for rows shorter than one wave-wide store (KV-cache heads):
+// the output is a stream of 16-byte chunks (OPS outputs of one row) and each
+// thread produces U of them, 256 chunks apart, so every store instruction
+// still writes 1 KB contiguous. A thread finds each chunk's id and column by
+// division, reads the id (shared by the row's threads, a cache hit after the
+// first), then the block scale and its OPS quants (16-bit loads: a block is
+// 34 bytes, so quants are only 2-byte aligned), and writes one 16-byte
+// vector. All U chunks' loads are issued before the first store. A wave per
+// row would leave most lanes idle on such rows. An invalid id writes zeros
+// (its loads read row 0, which the host guarantees exists); its first
+// chunk's thread bumps *d_err.
+template <int TO, int U>
+__global__ void __launch_bounds__(256) k_get_rows_q8_0_flat(const GetRowsArgs a, FastDiv per_row, uint32_t nchunks) {
+    constexpr int  EO  = TT<TO>::ES;
+    constexpr int  OPS = 16 / EO;
+    const uint32_t c0  = blockIdx.x * (256 * U) + threadIdx.x;
+    uint32_t       i[U];
+    int            o[U];
+    int64_t        r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t c = c0 + 256 * u < nchunks ? c0 + 256 * u : nchunks - 1;  // clamped: loads stay in bounds
+        i[u]             = per_row.div(c);
+        o[u]             = (int) (c - i[u] * per_row.d) * OPS;
+        r[u]             = a.ids[(int64_t) i[u] * a.ids_stride];
+    }
+    uint16_t dh[U], q[U][OPS / 2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const bool       ok = r[u] >= 0 && r[u] < a.n_rows;
+        const char *     bp = a.table + (ok ? r[u] : 0) * a.tnb1 + (int64_t) (o[u] >> 5) * 34;
+        const uint16_t * qp = (const uint16_t *) (bp + 2 + (o[u] & 31));
+        dh[u]               = *(const uint16_t *) bp;
+#pragma unroll
+        for (int h = 0; h < OPS / 2; ++h) {
+            q[u][h] = qp[h];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (c0 + 256 * u >= nchunks) {
+            break;
+        }
+        float f[OPS];
+        if (r[u] < 0 || r[u] >= a.n_rows) {
+            if (o[u] == 0 && a.d_err) {
+                atomicAdd(a.d_err, 1);
+            }
+#pragma unroll
+            for (int k = 0; k < OPS; ++k) {
+                f[k] = 0.0f;
+            }
+        } else {
+            const float d = (float) __builtin_bit_cast(_Float16, dh[u]);
+#pragma unroll
+            for (int h = 0; h < OPS / 4; ++h) {
+                const uint32_t w = (uint32_t) q[u][2 * h] | ((uint32_t) q[u][2 * h + 1] << 16);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    f[4 * h + k] = i8f(w, k) * d;
+                }
+            }
+        }
+        store_vec<TO, OPS>(a.y + (int64_t) i[u] * a.ynb1 + (int64_t) o[u] * EO, f);
+    }
+}
+
+#ifndef MI_GR_FLAT_U
+#define MI_GR_FLAT_U 4  // output chunks per thread in the flat kernel
+#endif
+
 // Generic: any n, element-aligned table rows, scalar.
 template <int TO>
 __global__ void __launch_bounds__(256) k_get_rows_generic(const GetRowsArgs a, int ttype) {
@@ -226,7 +299,17 @@ static int launch_to(const GetRowsArgs & a, int ttype, bool fast, bool lds, hipS
     grid                = grid > cap ? cap : grid;
     if (fast) {
         switch (ttype) {
-            case MI_TYPE_Q8_0:
+            case MI_TYPE_Q8_0: {
+                constexpr int  OPS     = 16 / TT<TO>::ES;
+                const uint64_t nchunks = (uint64_t) a.n_ids * (uint64_t) (a.n / OPS);
+                // rows shorter than one wave-wide store; an invalid id loads from row 0
+                if (a.n / OPS < 64 && a.n_rows > 0 && nchunks < (1ull << 31)) {
+                    constexpr uint32_t per_wg = 256 * MI_GR_FLAT_U;
+                    hipLaunchKernelGGL((k_get_rows_q8_0_flat<TO, MI_GR_FLAT_U>),
+                                       dim3((uint32_t) ((nchunks + per_wg - 1) / per_wg)), dim3(256), 0, s, a,
+                                       FastDiv((uint32_t) (a.n / OPS)), (uint32_t) nchunks);
+                    return MI_OK;
+                }
                 if (lds) {
                     const int nc = a.n / 32 * 34 / 16;
                     hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO>), dim3(grid), dim3(256), (size_t) 4 * nc * 16, s, a,
@@ -235,6 +318,7 @@ static int launch_to(const GetRowsArgs & a, int ttype, bool fast, bool lds, hipS
                     hipLaunchKernelGGL((k_get_rows_q8_0<TO>), dim3(grid), dim3(256), 0, s, a);
                 }
                 return MI_OK;
+            }
             case MI_TYPE_F32:
                 hipLaunchKernelGGL((k_get_rows_vec<MI_TYPE_F32, TO>), dim3(grid), dim3(256), 0, s, a);
                 return MI_OK;

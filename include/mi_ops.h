@@ -164,7 +164,8 @@ int mi_modulate(const mi_tensor * x, const mi_tensor * scale, const mi_tensor * 
 
 /* ggml_get_rows(table, ids): table [n, n_rows] Q8_0/F16/BF16/F32, ids I32
  * [n_ids] -> y [n, n_ids] F32 (or BF16). Replaces the embedding lookups at
- * qwen3-enc.h:390, 465, qwen3-lm.h:464, 626. An id outside [0, n_rows)
+ * qwen3-enc.h:390, 465, qwen3-lm.h:464, 626. ids may be strided (nb[0] any
+ * multiple of 4, as ggml reads src1 through nb10). An id outside [0, n_rows)
  * yields a zero row and, when d_err != NULL, increments *d_err (device
  * int32) -- ggml-cpu aborts there instead. */
 int mi_get_rows(const mi_tensor * table, const mi_tensor * ids, const mi_tensor * y, int32_t * d_err,

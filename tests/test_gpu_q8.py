@@ -81,6 +81,35 @@ def test_get_rows_out_of_range_ids(dev):
     assert not y[[1, 2, 4]].any()
 
 
+@pytest.mark.parametrize("n,n_ids", [(32, 1), (64, 77), (128, 1025), (128, 4099), (160, 333)])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_get_rows_q8_0_short_rows(dev, n, n_ids, out):
+    """Rows shorter than one wave-wide store (KV-cache heads) take the flat
+    chunk-per-thread kernel: chunk counts that end mid-workgroup, strided ids,
+    padded output rows, and invalid ids (zeros, counted once per row)."""
+    print(f"get_rows q8_0 short rows n={n} ids={n_ids} out={out}", flush=True)
+    n_rows = 700
+    tab = _q8_table(n_rows, n, seed=n + n_ids)
+    ids2 = rng(n_ids).integers(0, n_rows, (n_ids, 2)).astype(np.int32)
+    bad = np.arange(n_ids) % 97 == 5
+    ids2[bad, 0] = np.where(np.arange(bad.sum()) % 2 == 0, -3, n_rows)
+    d_ids = to_dev(ids2, dev)[:, 0]  # ids with a stride of 2 elements
+    pad = 8 if out == "f32" else 16
+    yfull = DTensor.full_byte((n_ids, n + pad), 0x7F, "f32" if out == "f32" else "bf16")
+    y = yfull[:, :n]
+    err = DTensor.zeros((1,), "i32")
+    ops.get_rows(ops.Q8(to_dev(tab, dev)), d_ids, out=y, out_dtype=out, err=err)
+    got = to_np(yfull)
+    ids = ids2[:, 0]
+    ref = np.zeros((n_ids, n), np.float32)
+    ref[~bad] = orc.get_rows(tab, orc.Q8_0, n, ids[~bad])
+    if out == "bf16":
+        ref = orc.f32_to_bf16(ref)
+    assert np.array_equal(got[:, :n].view(np.uint8), ref.view(np.uint8))
+    assert (got[:, n:].view(np.uint8) == 0x7F).all()  # padding untouched
+    assert int(err.item()) == int(bad.sum())
+
+
 def _tie_blocks():
     """Blocks separating the two quantizers: exact .5 ties under both id
     formulas, amax values where 127/amax != 1/(amax/127) in fp32, zero blocks,
