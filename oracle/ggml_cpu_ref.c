@@ -426,3 +426,91 @@ void orc_timestep_embedding_f32(const float * t, int64_t n, int dim, int max_per
         }
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* ggml_flash_attn_ext (dit-graph.h:227-231, 348-349; qwen3-lm.h:718-723),  */
+/* GGML_PREC_F32, max_bias = 0, logit_softcap = 0. ggml-cpu converts each q  */
+/* row to K's vec_dot type before the dot products (fp16 for F16 K, bf16 for */
+/* BF16 K, Q8_0 -- the arch from_float -- for Q8_0 K), skips keys whose mask */
+/* is -inf, and runs an online softmax over the rest. This states the exact  */
+/* value of that definition: products and sums in double, one softmax.      */
+/* ------------------------------------------------------------------------ */
+static void fa_convert_q(const float * q, int64_t D, int qconv, double * qc) {
+    if (qconv == 3) {
+        uint8_t blk[ORC_Q8_0_SIZE];
+        float   deq[ORC_QK8_0];
+        for (int64_t b = 0; b < D / ORC_QK8_0; b++) {
+            orc_quantize_row_q8_0_x86(q + b * ORC_QK8_0, blk, ORC_QK8_0);
+            orc_dequantize_row_q8_0(blk, deq, ORC_QK8_0);
+            for (int j = 0; j < ORC_QK8_0; j++) {
+                qc[b * ORC_QK8_0 + j] = deq[j];
+            }
+        }
+        return;
+    }
+    for (int64_t d = 0; d < D; d++) {
+        float x = q[d];
+        if (qconv == 1) {
+            x = orc_fp16_to_fp32(orc_fp32_to_fp16(x));
+        } else if (qconv == 2) {
+            x = orc_bf16_to_fp32(orc_fp32_to_bf16(x));
+        }
+        qc[d] = x;
+    }
+}
+
+void orc_flash_attn_ext(const float * q, const float * k, const float * v, const float * mask, int64_t N, int64_t Nh,
+                        int64_t Nkv, int64_t n_q, int64_t n_kv, int64_t D, int64_t mN, int64_t mH, int64_t mQ,
+                        float scale, int qconv, float * y) {
+    const int64_t rk = Nh / Nkv;
+#pragma omp parallel for collapse(3) num_threads(g_threads) schedule(static)
+    for (int64_t b = 0; b < N; b++) {
+        for (int64_t h = 0; h < Nh; h++) {
+            for (int64_t iq = 0; iq < n_q; iq++) {
+                double        qc[1024];
+                double        acc[1024];
+                const int64_t g  = h / rk;
+                const float * kk = k + (b * Nkv + g) * n_kv * D;
+                const float * vv = v + (b * Nkv + g) * n_kv * D;
+                const float * mm = mask ? mask + (((b % mN) * mH + (h % mH)) * mQ + iq) * n_kv : NULL;
+                fa_convert_q(q + ((b * Nh + h) * n_q + iq) * D, D, qconv, qc);
+                double smax = -INFINITY;
+                for (int64_t j = 0; j < n_kv; j++) {
+                    const double mv = mm ? (double) mm[j] : 0.0;
+                    if (mv == -INFINITY) {
+                        continue;
+                    }
+                    double dot = 0.0;
+                    for (int64_t d = 0; d < D; d++) {
+                        dot += qc[d] * (double) kk[j * D + d];
+                    }
+                    const double s = (double) scale * dot + mv;
+                    smax           = s > smax ? s : smax;
+                }
+                double sum = 0.0;
+                for (int64_t d = 0; d < D; d++) {
+                    acc[d] = 0.0;
+                }
+                for (int64_t j = 0; j < n_kv; j++) {
+                    const double mv = mm ? (double) mm[j] : 0.0;
+                    if (mv == -INFINITY) {
+                        continue;
+                    }
+                    double dot = 0.0;
+                    for (int64_t d = 0; d < D; d++) {
+                        dot += qc[d] * (double) kk[j * D + d];
+                    }
+                    const double p = exp((double) scale * dot + mv - smax);
+                    sum += p;
+                    for (int64_t d = 0; d < D; d++) {
+                        acc[d] += p * (double) vv[j * D + d];
+                    }
+                }
+                float * yo = y + ((b * n_q + iq) * Nh + h) * D;
+                for (int64_t d = 0; d < D; d++) {
+                    yo[d] = (float) (acc[d] * (1.0 / sum)); /* all masked: 0 * inf = NaN, as ggml */
+                }
+            }
+        }
+    }
+}

@@ -25,10 +25,15 @@
  * partial n_dims, attn/freq scale; swiglu against float64 and IEEE special
  * values; Q8_0 by brute-force dequant, quantizer invariants and tie blocks
  * that separate the two variants; timestep embedding against float64 with a
- * derived bound. Parity unpinned (needs the absent ggml source): which Q8_0
- * variant ggml-cpu's ggml_cpy uses on x86 (both are implemented; X86 is the
- * default), the lane results of ggml's SIMD expf in swiglu, whether the
- * fork's CPU backend fuses nodes, and its FP-contraction flags.
+ * derived bound; flash attention by one-key, equal-score and scale-0 closed
+ * forms, key-permutation and GQA-mapping invariants, mask exclusion and the
+ * q-conversion idempotence. Parity unpinned (needs the absent ggml source):
+ * which Q8_0 variant ggml-cpu's ggml_cpy uses on x86 (both are implemented;
+ * X86 is the default), the lane results of ggml's SIMD expf in swiglu,
+ * whether the fork's CPU backend fuses nodes, and its FP-contraction flags;
+ * for flash attention, ggml-cpu's own rounding (its SIMD dot products, and
+ * the fp16 accumulation of the output when V is F16): orc_flash_attn_ext
+ * states the exact value those roundings approximate.
  */
 #ifndef ORC_GGML_CPU_REF_H
 #define ORC_GGML_CPU_REF_H
@@ -102,6 +107,22 @@ int orc_get_rows(const void * table, int type, int64_t n_rows, int64_t n, const 
 
 /* ---- ggml_timestep_embedding: t[n] -> y n x dim ---- */
 void orc_timestep_embedding_f32(const float * t, int64_t n, int dim, int max_period, float * y);
+
+/* ---- ggml_flash_attn_ext(q, k, v, mask, scale, max_bias = 0, logit_softcap = 0)
+ *      (dit-graph.h:227-231, 348-349; qwen3-lm.h:718-723), the exact
+ *      mathematics of ggml-cpu's definition, in double:
+ *        qc = q converted to K's vec_dot type: qconv 0 none (F32 K), 1 fp16
+ *             (F16 K), 2 bf16 (BF16 K), 3 Q8_0 x86 quantize+dequantize (Q8_0 K)
+ *        s_j = scale * dot(qc, k_j) + mask_j ; keys with mask_j == -inf skipped
+ *        y   = sum_j exp(s_j - max) v_j / sum_j exp(s_j - max)
+ *      A row whose keys are all masked gives NaN (ggml: 0 * (1/0)).
+ *      q: [N][Nh][n_q][D], k, v: [N][Nkv][n_kv][D] (already dequantized to
+ *      F32), mask: [mN][mH][mQ][n_kv] (F32 values of the F16 mask; index
+ *      (b % mN, h % mH, iq)) or NULL, y: [N][n_q][Nh][D] (ggml's permuted
+ *      result [D, Nh, n_q, N]). Head h reads KV head h / (Nh / Nkv). D <= 1024. ---- */
+void orc_flash_attn_ext(const float * q, const float * k, const float * v, const float * mask, int64_t N, int64_t Nh,
+                        int64_t Nkv, int64_t n_q, int64_t n_kv, int64_t D, int64_t mN, int64_t mH, int64_t mQ,
+                        float scale, int qconv, float * y);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,8 @@ def lib():
         L.orc_fp16_to_fp32_n.argtypes = [_u16p, _fp, _i64]
         L.orc_fp32_to_bf16_n.argtypes = [_fp, _u16p, _i64]
         L.orc_bf16_to_fp32_n.argtypes = [_u16p, _fp, _i64]
+        L.orc_flash_attn_ext.argtypes = [_fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                         ctypes.c_float, ctypes.c_int, _fp]
         L.orc_set_threads.argtypes = [ctypes.c_int]
         L.orc_get_threads.restype = ctypes.c_int
         _lib = L
@@ -254,6 +256,33 @@ def timestep_embedding(t, dim: int, max_period: int = 10000) -> np.ndarray:
     t = _c32(t).reshape(-1)
     y = np.empty((t.size, dim), np.float32)
     lib().orc_timestep_embedding_f32(_f(t), t.size, dim, max_period, _f(y))
+    return y
+
+
+QCONV = {"f32": 0, "f16": 1, "bf16": 2, "q8_0": 3}
+
+
+def flash_attn_ext(q, k, v, mask, scale: float, k_type: str = "f16") -> np.ndarray:
+    """ggml_flash_attn_ext (max_bias 0, softcap 0), exact value in double.
+    q (N, Nh, n_q, D); k, v (N, Nkv, n_kv, D) as F32 values (dequantized);
+    mask (mN, mH, mQ, n_kv) F32 values of the F16 mask, or None.
+    k_type names K's storage type: q is converted as ggml-cpu converts it.
+    Returns (N, n_q, Nh, D), ggml's [D, Nh, n_q, N] result."""
+    q, k, v = _c32(q), _c32(k), _c32(v)
+    N, Nh, n_q, D = q.shape
+    _, Nkv, n_kv, _ = k.shape
+    assert k.shape == v.shape == (N, Nkv, n_kv, D) and Nh % Nkv == 0 and D <= 1024
+    if mask is not None:
+        mask = _c32(mask)
+        mN, mH, mQ, mk = mask.shape
+        assert mk == n_kv and mQ >= n_q
+        mp = _f(mask)
+    else:
+        mN = mH = mQ = 1
+        mp = None
+    y = np.empty((N, n_q, Nh, D), np.float32)
+    lib().orc_flash_attn_ext(_f(q), _f(k), _f(v), mp, N, Nh, Nkv, n_q, n_kv, D, mN, mH, mQ, scale, QCONV[k_type],
+                             _f(y))
     return y
 
 
