@@ -86,6 +86,8 @@ PROTOTYPES = {
     "mi_cpy_q8_0": [_TP, _TP, _I, _VP],
     "mi_kv_store": [_TP, _TP, _TP, _TP, _TP, _TP, _I, _VP, _VP],
     "mi_timestep_embedding": [_TP, _I, _I, _TP, _VP],
+    "mi_flash_attn_ext_workspace": [_TP, _TP, _TP, ctypes.POINTER(ctypes.c_size_t)],
+    "mi_flash_attn_ext": [_TP, _TP, _TP, _TP, _F, _F, _F, _TP, _VP, ctypes.c_size_t, _VP],
     "mi_dit_block_ops": [ctypes.POINTER(MiDitBlockIO), _VP],
     "mi_qwen3_layer_ops": [ctypes.POINTER(MiQwen3LayerIO), _VP],
 }

@@ -202,3 +202,29 @@ def timestep_embedding(t, dim: int, max_period: int = 10000, out=None, stream=No
     y = _out(out, (t.shape[0], dim), "f32")
     _lib.call("mi_timestep_embedding", _p(t), dim, max_period, _p(y), _s(stream))
     return y
+
+
+def flash_attn_workspace(q, k, v) -> int:
+    """Bytes of device workspace mi_flash_attn_ext needs for these operands."""
+    n = ctypes.c_size_t(0)
+    _lib.call("mi_flash_attn_ext_workspace", _p(q), _p(k), _p(v), ctypes.byref(n))
+    return int(n.value)
+
+
+def flash_attn_ext(q, k, v, mask, scale: float, out=None, workspace=None, max_bias: float = 0.0,
+                   logit_softcap: float = 0.0, stream=None):
+    """ggml_flash_attn_ext (GGML_PREC_F32). Shapes outermost first:
+    q (N, Nh, n_q, D); k, v (Nk3, Nkv, n_kv, D) [or Q8]; mask F16 (mne3, mne2, >= n_q, n_kv) or None;
+    returns F32 (N, n_q, Nh, D) -- ggml's [D, Nh, n_q, N]. A workspace of the required size is
+    allocated when none is passed."""
+    N, Nh, n_q, D = q.shape
+    y = _out(out, (N, n_q, Nh, D), "f32")
+    need = flash_attn_workspace(q, k, v)
+    ws = workspace
+    if need and ws is None:
+        ws = DTensor.empty((need,), "u8")
+    wp = ctypes.c_void_p(ws.ptr) if ws is not None else None
+    wn = ws.numel() * ws.es if ws is not None else 0
+    _lib.call("mi_flash_attn_ext", _p(q), _p(k), _p(v), _p(mask), scale, max_bias, logit_softcap, _p(y), wp, wn,
+              _s(stream))
+    return y

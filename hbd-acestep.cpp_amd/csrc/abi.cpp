@@ -609,6 +609,137 @@ int mi_kv_store(const mi_tensor * k, const mi_tensor * k_cache, const mi_tensor 
     return finish(launch_row_copy(rk, v ? &rv : nullptr, k->type, k_cache->type, rounding, (hipStream_t) stream));
 }
 
+// ggml_flash_attn_ext shape rules; fills the launcher's descriptor (without data pointers' workspace)
+static int fa_desc(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v, const mi_tensor * mask,
+                   const mi_tensor * y, FaArgs & a) {
+    MI_TRY(check(q));
+    MI_TRY(check(k));
+    MI_TRY(check(v));
+    if (!is_act(q->type)) {
+        return MI_ERR_TYPE;
+    }
+    const int kt = k->type;
+    if (kt != v->type || (kt != MI_TYPE_F16 && kt != MI_TYPE_BF16 && kt != MI_TYPE_Q8_0 && kt != MI_TYPE_F32)) {
+        return MI_ERR_TYPE;
+    }
+    const int64_t D = q->ne[0];
+    if (k->ne[0] != D || v->ne[0] != D || k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[3] != v->ne[3]) {
+        return MI_ERR_SHAPE;
+    }
+    if (k->ne[2] == 0 || k->ne[3] == 0 || q->ne[2] % k->ne[2] != 0 || q->ne[3] % k->ne[3] != 0) {
+        return MI_ERR_SHAPE;
+    }
+    if (D != 64 && D != 128 && D != 256) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    if (kt == MI_TYPE_F32 && D > 128) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    // K/V rows are read in 16-byte chunks (Q8_0, 34-byte blocks: 8-byte when D is a
+    // multiple of 128, else 4-byte)
+    const size_t cb = kt == MI_TYPE_Q8_0 ? (D % 128 == 0 ? 8 : 4) : 16;
+    for (const mi_tensor * t : { k, v }) {
+        if (!aligned(t->data, cb) || t->nb[1] % cb != 0 || t->nb[2] % cb != 0 || t->nb[3] % cb != 0) {
+            return MI_ERR_ALIGN;
+        }
+    }
+    if (q->nb[1] % type_size(q->type) != 0 || q->nb[2] % type_size(q->type) != 0) {
+        return MI_ERR_ALIGN;
+    }
+    a      = FaArgs{};
+    a.q    = (const char *) q->data;
+    a.q1   = (int64_t) q->nb[1];
+    a.q2   = (int64_t) q->nb[2];
+    a.q3   = (int64_t) q->nb[3];
+    a.tq   = q->type;
+    a.k    = (const char *) k->data;
+    a.k1   = (int64_t) k->nb[1];
+    a.k2   = (int64_t) k->nb[2];
+    a.k3   = (int64_t) k->nb[3];
+    a.v    = (const char *) v->data;
+    a.v1   = (int64_t) v->nb[1];
+    a.v2   = (int64_t) v->nb[2];
+    a.v3   = (int64_t) v->nb[3];
+    a.n_q  = (int) q->ne[1];
+    a.n_kv = (int) k->ne[1];
+    a.nh   = (int) q->ne[2];
+    a.nkv  = (int) k->ne[2];
+    a.nb   = (int) q->ne[3];
+    a.rk   = (int) (q->ne[2] / k->ne[2]);
+    a.rk3  = (int) (q->ne[3] / k->ne[3]);
+    a.kt   = kt;
+    if (mask) {
+        MI_TRY(check(mask));
+        if (mask->type != MI_TYPE_F16) {
+            return MI_ERR_TYPE;
+        }
+        if (mask->ne[0] != k->ne[1] || mask->ne[1] < q->ne[1] || mask->ne[2] == 0 || mask->ne[3] == 0 ||
+            q->ne[2] % mask->ne[2] != 0 || q->ne[3] % mask->ne[3] != 0) {
+            return MI_ERR_SHAPE;
+        }
+        a.mask = (const char *) mask->data;
+        a.m1   = (int64_t) mask->nb[1];
+        a.m2   = (int64_t) mask->nb[2];
+        a.m3   = (int64_t) mask->nb[3];
+        a.mne2 = (int) mask->ne[2];
+        a.mne3 = (int) mask->ne[3];
+    } else {
+        a.mne2 = 1;
+        a.mne3 = 1;
+    }
+    if (y) {
+        MI_TRY(check(y));
+        if (y->type != MI_TYPE_F32) {
+            return MI_ERR_TYPE;
+        }
+        if (y->ne[0] != D || y->ne[1] != q->ne[2] || y->ne[2] != q->ne[1] || y->ne[3] != q->ne[3]) {
+            return MI_ERR_SHAPE;
+        }
+        a.y  = (char *) y->data;
+        a.y1 = (int64_t) y->nb[1];
+        a.y2 = (int64_t) y->nb[2];
+        a.y3 = (int64_t) y->nb[3];
+    }
+    flash_attn_plan(a, (int) D);
+    return MI_OK;
+}
+
+int mi_flash_attn_ext_workspace(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v, size_t * bytes) {
+    if (!bytes) {
+        return MI_ERR_NULL;
+    }
+    FaArgs a;
+    MI_TRY(fa_desc(q, k, v, nullptr, nullptr, a));
+    *bytes = flash_attn_workspace(a, (int) q->ne[0]);
+    return MI_OK;
+}
+
+int mi_flash_attn_ext(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v, const mi_tensor * mask,
+                      float scale, float max_bias, float logit_softcap, const mi_tensor * y, void * workspace,
+                      size_t workspace_bytes, mi_stream stream) {
+    if (!y) {
+        return MI_ERR_NULL;
+    }
+    if (max_bias != 0.0f || logit_softcap != 0.0f) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    if (!std::isfinite(scale)) {
+        return MI_ERR_PARAM;
+    }
+    FaArgs a;
+    MI_TRY(fa_desc(q, k, v, mask, y, a));
+    a.scale         = scale;
+    const size_t need = flash_attn_workspace(a, (int) q->ne[0]);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(workspace, 16)) {
+        return MI_ERR_ALIGN;
+    }
+    a.ws = (float *) workspace;
+    return finish(launch_flash_attn(a, k->type, (int) q->ne[0], (hipStream_t) stream));
+}
+
 int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi_tensor * y, mi_stream stream) {
     MI_TRY(check(t));
     MI_TRY(check(y));

@@ -1,0 +1,532 @@
+// fattn.hip -- ggml_flash_attn_ext(q, k, v, mask, scale, max_bias = 0,
+// logit_softcap = 0) with GGML_PREC_F32: the DiT self/cross attention
+// (dit-graph.h:227-231, 348-349) and the batched LM decode over the KV cache
+// (qwen3-lm.h:706-723, reading a 256-bucketed length, qwen3-lm.h:582-596).
+//
+// Semantics kept from ggml-cpu's flash attention:
+//   - each q row is first converted to K's vec_dot type: fp16 for F16 K, bf16
+//     for BF16 K, Q8_0 (the x86 from_float: id = 127/amax, round half to even,
+//     saturate; fp16 scale) for Q8_0 K; the Q8_0 dot product is then an exact
+//     integer sum per block scaled by d_k*d_q;
+//   - s = dot * scale + mask; a key whose mask is -inf is skipped, and one
+//     masked for every row of a workgroup is not even read (its K/V bytes may
+//     hold anything);
+//   - online softmax; a row whose keys are all masked ends as 0 * (1/0) = NaN;
+//   - the result is F32 [D, Nh, n_q, N] (heads of a token adjacent).
+// Arithmetic is fp32 throughout (dot products via v_dot2 / v_dot4, exp,
+// accumulation of the output), closer to the exact value than ggml-cpu's
+// fp16 output accumulation for F16 V.
+//
+// Decomposition (flash-decoding): a wave owns (KV range split, sequence b,
+// KV head g, block of RB query rows), where the query rows of a KV head are
+// its n_q x (Nh/Nkv) (query position, head) pairs, so a K/V tile is loaded
+// once for every query head that shares it (GQA). The wave walks its range
+// in tiles of 32 keys: the mask values first (keys masked for all rows are
+// neither loaded nor counted), then all of the tile's K and V bytes with
+// coalesced loads into LDS, then q.k with lane = (key, half of D) and one
+// cross-half exchange, the softmax update, and p.V with lane = output
+// columns. With several splits, each writes (max, sum, unnormalized output)
+// to the caller's workspace and k_fa_combine merges them.
+#include "launch.h"
+
+namespace mi {
+
+#ifndef MI_FA_WAVES_PER_CU
+#define MI_FA_WAVES_PER_CU 16  // splits are chosen so the grid holds about this many waves per CU
+#endif
+
+constexpr int FA_TILE = 32;  // keys per tile
+
+template <int KT> struct FaT;
+template <> struct FaT<MI_TYPE_F32> {
+    static constexpr int row(int D) { return 4 * D; }
+    static constexpr int cb(int) { return 16; }  // load chunk bytes
+};
+template <> struct FaT<MI_TYPE_F16> {
+    static constexpr int row(int D) { return 2 * D; }
+    static constexpr int cb(int) { return 16; }
+};
+template <> struct FaT<MI_TYPE_BF16> {
+    static constexpr int row(int D) { return 2 * D; }
+    static constexpr int cb(int) { return 16; }
+};
+template <> struct FaT<MI_TYPE_Q8_0> {
+    static constexpr int row(int D) { return D / 32 * 34; }
+    // 34-byte blocks: a row of 4k blocks is a multiple of 8 bytes (136 = 8 * 17), else of 4
+    static constexpr int cb(int D) { return D % 128 == 0 ? 8 : 4; }
+};
+
+typedef _Float16 fa_f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16   fa_bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float fa_load_q(const char * p, int tq) {
+    if (tq == MI_TYPE_F32) {
+        return load_elem<MI_TYPE_F32>(p);
+    }
+    if (tq == MI_TYPE_BF16) {
+        return load_elem<MI_TYPE_BF16>(p);
+    }
+    return load_elem<MI_TYPE_F16>(p);
+}
+
+// x86 from_float for one 32-element block: quants into q (8 words), scale (fp16 value)
+__device__ __forceinline__ float fa_q8_block(const float * x, uint32_t * qw) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        amax = fmaxf(amax, fabsf(x[j]));
+    }
+    constexpr float C  = 1.0f / 127.0f;
+    const float     q0 = amax * C;
+    const float     d  = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, amax), C, q0);  // IEEE amax / 127
+    const float     id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    for (int w = 0; w < 8; ++w) {
+        uint32_t acc = 0;
+        for (int e = 0; e < 4; ++e) {
+            const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(x[4 * w + e] * id), -128.0f, 127.0f);
+            acc |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
+        }
+        qw[w] = acc;
+    }
+    return (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
+}
+
+template <int KT, int D, int RB>
+__global__ void __launch_bounds__(64) k_fa_split(const FaArgs a) {
+    constexpr int RBYTES = FaT<KT>::row(D);
+    constexpr int CB     = FaT<KT>::cb(D);
+    constexpr int CPR    = RBYTES / CB;                                    // load chunks per row
+    constexpr int NCH    = (FA_TILE * CPR + 63) / 64;                      // chunks per lane per tile
+    constexpr int RSTR   = KT == MI_TYPE_Q8_0 ? RBYTES : RBYTES + 16;      // LDS row stride (bank spread)
+    constexpr int DPL    = D / 64;                                         // output columns per lane
+    constexpr int QW     = KT == MI_TYPE_Q8_0 ? D / 4 : (KT == MI_TYPE_F32 ? D : D / 2);  // q words per row
+    using chunk_t        = typename std::conditional<CB == 16, uint4,
+                                              typename std::conditional<CB == 8, uint2, uint32_t>::type>::type;
+
+    __shared__ __align__(16) char     kt[FA_TILE * RSTR];
+    __shared__ __align__(16) char     vt[FA_TILE * RSTR];
+    __shared__ __align__(16) uint32_t qs[RB][QW];       // q converted to K's dot type
+    __shared__ float                  qd[RB][D / 32];    // Q8_0: per-block q scales
+    __shared__ __align__(16) float    pt[FA_TILE][RB];   // the tile's probabilities
+
+    const int      lane  = threadIdx.x;
+    const uint32_t split = blockIdx.x;
+    const uint32_t bg    = blockIdx.y;  // b * nkv + g
+    const uint32_t b     = bg / (uint32_t) a.nkv;
+    const uint32_t g     = bg - b * (uint32_t) a.nkv;
+    const int      r0    = blockIdx.z * RB;
+
+    // rows of this block: (query position iq, head h); invalid rows are masked out entirely
+    int  iq_of[RB], h_of[RB];
+    bool rv[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const int gr = r0 + r;
+        rv[r]        = gr < a.rows;
+        const int gc = rv[r] ? gr : 0;
+        iq_of[r]     = gc / a.rk;
+        h_of[r]      = (int) g * a.rk + (gc - iq_of[r] * a.rk);
+    }
+
+    // 1. q rows, converted to K's dot type, into LDS
+    if constexpr (KT == MI_TYPE_Q8_0) {
+        // one lane per (row, 32-block)
+        for (int t = lane; t < RB * (D / 32); t += 64) {
+            const int r  = t / (D / 32);
+            const int bk = t - r * (D / 32);
+            float     x[32];
+            const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h_of[r] * a.q2 + (int64_t) iq_of[r] * a.q1;
+            const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
+            for (int j = 0; j < 32; ++j) {
+                x[j] = rv[r] ? fa_load_q(qp + (size_t) (bk * 32 + j) * es, a.tq) : 0.0f;
+            }
+            qd[r][bk] = fa_q8_block(x, &qs[r][bk * 8]);
+        }
+    } else {
+        constexpr int EPW = KT == MI_TYPE_F32 ? 1 : 2;  // elements per word
+        for (int t = lane; t < RB * QW; t += 64) {
+            const int    r  = t / QW;
+            const int    w  = t - r * QW;
+            const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h_of[r] * a.q2 + (int64_t) iq_of[r] * a.q1;
+            const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
+            float        x0 = rv[r] ? fa_load_q(qp + (size_t) (w * EPW) * es, a.tq) : 0.0f;
+            if constexpr (KT == MI_TYPE_F32) {
+                qs[r][w] = __float_as_uint(x0);
+            } else {
+                const float x1 = rv[r] ? fa_load_q(qp + (size_t) (w * EPW + 1) * es, a.tq) : 0.0f;
+                qs[r][w]       = KT == MI_TYPE_F16 ? pack_f16x2(x0, x1) : pack_bf16x2(x0, x1);
+            }
+        }
+    }
+
+    // mask rows (per row: its query position and head)
+    const char * mrow[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        mrow[r] = a.mask ? a.mask + (int64_t) (b % (uint32_t) a.mne3) * a.m3 + (int64_t) (h_of[r] % a.mne2) * a.m2 +
+                               (int64_t) iq_of[r] * a.m1
+                         : nullptr;
+    }
+    const uint32_t kb = b / (uint32_t) a.rk3;  // K/V batch index (broadcast over ne3)
+    const char *   kg = a.k + (int64_t) kb * a.k3 + (int64_t) g * a.k2;
+    const char *   vg = a.v + (int64_t) kb * a.v3 + (int64_t) g * a.v2;
+
+    float m[RB], l[RB], o[RB][DPL];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+            o[r][j] = 0.0f;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+
+    const int key  = lane & 31;
+    const int half = lane >> 5;
+    const int kbeg = (int) split * a.chunk;
+    const int kend = kbeg + a.chunk < a.n_kv ? kbeg + a.chunk : a.n_kv;
+    for (int t0 = kbeg; t0 < kend; t0 += FA_TILE) {
+        const int nk = kend - t0 < FA_TILE ? kend - t0 : FA_TILE;
+        // 2. mask values of this lane's key for every row
+        float mv[RB];
+        bool  any = false;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            float x = -INFINITY;
+            if (rv[r] && key < nk) {
+                x = mrow[r] ? load_elem<MI_TYPE_F16>(mrow[r] + (size_t) (t0 + key) * 2) : 0.0f;
+            }
+            mv[r] = x;
+            any   = any || x != -INFINITY;
+        }
+        const uint64_t live = __builtin_amdgcn_ballot_w64(any && half == 0);  // bit k: key k is read
+        if (live == 0) {
+            continue;
+        }
+        // 3. K and V bytes of the live keys, all loads issued before any is used
+        chunk_t kc[NCH], vc[NCH];
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c  = lane + 64 * i;
+            const int kk = c / CPR;
+            const int pp = c - kk * CPR;
+            if (c < FA_TILE * CPR && ((live >> kk) & 1)) {
+                const int64_t ko = (int64_t) (t0 + kk) * a.k1 + pp * CB;
+                const int64_t vo = (int64_t) (t0 + kk) * a.v1 + pp * CB;
+                if constexpr (CB == 16) {
+                    kc[i] = ld16(kg + ko);
+                    vc[i] = ld16(vg + vo);
+                } else {
+                    kc[i] = *(const chunk_t *) (kg + ko);
+                    vc[i] = *(const chunk_t *) (vg + vo);
+                }
+            } else {
+                kc[i] = chunk_t{};
+                vc[i] = chunk_t{};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = lane + 64 * i;
+            if (c < FA_TILE * CPR) {
+                const int kk = c / CPR;
+                const int pp = c - kk * CPR;
+                *(chunk_t *) (kt + kk * RSTR + pp * CB) = kc[i];
+                *(chunk_t *) (vt + kk * RSTR + pp * CB) = vc[i];
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+
+        // 4. s = q.k for (row, key): lane = (key, half of D)
+        float s[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            s[r] = 0.0f;
+        }
+        const char * kr = kt + key * RSTR;
+        if constexpr (KT == MI_TYPE_Q8_0) {
+            constexpr int NBH = D / 64;  // blocks per half
+#pragma unroll
+            for (int bb = 0; bb < NBH; ++bb) {
+                const int        bk = half * NBH + bb;
+                const uint16_t * bp = (const uint16_t *) (kr + 34 * bk);
+                const float      dk = (float) __builtin_bit_cast(_Float16, bp[0]);
+                uint32_t         kw[8];
+#pragma unroll
+                for (int w = 0; w < 8; ++w) {
+                    kw[w] = (uint32_t) bp[1 + 2 * w] | ((uint32_t) bp[2 + 2 * w] << 16);
+                }
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    int sumi = 0;
+#pragma unroll
+                    for (int w = 0; w < 8; ++w) {
+                        sumi = __builtin_amdgcn_sdot4((int) kw[w], (int) qs[r][bk * 8 + w], sumi, false);
+                    }
+                    s[r] = __builtin_fmaf(dk * qd[r][bk], (float) sumi, s[r]);
+                }
+            }
+        } else {
+            constexpr int WH = QW / 2;  // words per half
+            const uint4 * k4 = (const uint4 *) (kr + half * (RBYTES / 2));
+#pragma unroll
+            for (int c4 = 0; c4 < WH / 4; ++c4) {
+                const uint4 kv = k4[c4];
+                const uint32_t kw[4] = { kv.x, kv.y, kv.z, kv.w };
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    const uint4    qv   = *(const uint4 *) &qs[r][half * WH + 4 * c4];
+                    const uint32_t qw[4] = { qv.x, qv.y, qv.z, qv.w };
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (KT == MI_TYPE_F16) {
+                            s[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(fa_f16x2, kw[e]),
+                                                          __builtin_bit_cast(fa_f16x2, qw[e]), s[r], false);
+                        } else if constexpr (KT == MI_TYPE_BF16) {
+                            s[r] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(fa_bf16x2, kw[e]),
+                                                                   __builtin_bit_cast(fa_bf16x2, qw[e]), s[r], false);
+                        } else {
+                            s[r] = __builtin_fmaf(__uint_as_float(kw[e]), __uint_as_float(qw[e]), s[r]);
+                        }
+                    }
+                }
+            }
+        }
+        // 5. full dot (both halves), scale, mask; online softmax update per row
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const float full = s[r] + __shfl_xor(s[r], 32, 64);
+            float       x    = mv[r] == -INFINITY ? -INFINITY : full * a.scale + mv[r];
+            const float tmax = group_max<32>(x);
+            const float mn   = fmaxf(m[r], tmax);
+            float       alpha = 1.0f, p = 0.0f;
+            if (mn != -INFINITY) {
+                alpha = __expf(m[r] - mn);  // exp(-inf) = 0 on the first live tile
+                p     = x == -INFINITY ? 0.0f : __expf(x - mn);
+            }
+            m[r] = mn;
+            l[r] = l[r] * alpha + (half == 0 ? p : 0.0f);
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) {
+                o[r][j] *= alpha;
+            }
+            if (half == 0) {
+                pt[key][r] = p;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+
+        // 6. o += p.V, lane = output columns [lane*DPL, +DPL)
+        for (int kk = 0; kk < nk; ++kk) {
+            if (!((live >> kk) & 1)) {
+                continue;  // never read: its K/V bytes were not loaded
+            }
+            float pr[RB];
+#pragma unroll
+            for (int r4 = 0; r4 < RB; r4 += 4) {
+                const float4 p4 = *(const float4 *) &pt[kk][r4];
+                pr[r4]          = p4.x;
+                pr[r4 + 1]      = p4.y;
+                pr[r4 + 2]      = p4.z;
+                pr[r4 + 3]      = p4.w;
+            }
+            float       vv[DPL];
+            const char * vr = vt + kk * RSTR;
+            if constexpr (KT == MI_TYPE_Q8_0) {
+                const int      c0 = lane * DPL;
+                const char *   bp = vr + 34 * (c0 / 32);
+                const float    dv = (float) __builtin_bit_cast(_Float16, *(const uint16_t *) bp);
+                const int8_t * qp = (const int8_t *) (bp + 2 + (c0 % 32));
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) {
+                    vv[j] = (float) qp[j] * dv;
+                }
+            } else if constexpr (KT == MI_TYPE_F32) {
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) {
+                    vv[j] = ((const float *) vr)[lane * DPL + j];
+                }
+            } else {
+                const uint16_t * hp = (const uint16_t *) vr + lane * DPL;
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) {
+                    vv[j] = KT == MI_TYPE_F16 ? (float) __builtin_bit_cast(_Float16, hp[j])
+                                              : __uint_as_float((uint32_t) hp[j] << 16);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) {
+                    o[r][j] = __builtin_fmaf(pr[r], vv[j], o[r][j]);
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // the next tile overwrites kt, vt, pt
+    }
+
+    // 7. row sums across lanes; the final output or this split's partial
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        l[r] = group_sum<64>(l[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        if (!rv[r]) {
+            continue;
+        }
+        if (a.splits == 1) {
+            const float inv = 1.0f / l[r];  // all keys masked: 0 * inf = NaN, as ggml
+            float *     yp  = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) iq_of[r] * a.y2 + (int64_t) h_of[r] * a.y1);
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) {
+                yp[lane * DPL + j] = o[r][j] * inv;
+            }
+        } else {
+            float * wp = a.ws + (((int64_t) split * a.nb * a.nkv + bg) * a.rows + r0 + r) * (D + 2);
+            if (lane == 0) {
+                wp[0] = m[r];
+                wp[1] = l[r];
+            }
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) {
+                wp[2 + lane * DPL + j] = o[r][j];
+            }
+        }
+    }
+}
+
+// Merge the splits of one (sequence, KV head, row): y = sum_s w_s o_s / sum_s w_s l_s,
+// w_s = exp(m_s - max_s m_s) (0 for a split whose keys were all masked).
+template <int D>
+__global__ void __launch_bounds__(64) k_fa_combine(const FaArgs a) {
+    constexpr int  DPL  = D / 64;
+    const int      lane = threadIdx.x;
+    const uint32_t rec  = blockIdx.x;  // bg * rows + row
+    const uint32_t bg   = rec / (uint32_t) a.rows;
+    const int      row  = (int) (rec - bg * (uint32_t) a.rows);
+    const uint32_t b    = bg / (uint32_t) a.nkv;
+    const uint32_t g    = bg - b * (uint32_t) a.nkv;
+    const int      iq   = row / a.rk;
+    const int      h    = (int) g * a.rk + (row - iq * a.rk);
+    const int64_t  sstr = (int64_t) a.nb * a.nkv * a.rows * (D + 2);  // one split's records
+    const float *  w0   = a.ws + (int64_t) rec * (D + 2);
+    float          mx   = -INFINITY;
+    for (int s = 0; s < a.splits; ++s) {
+        mx = fmaxf(mx, w0[s * sstr]);
+    }
+    float L = 0.0f, acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+        acc[j] = 0.0f;
+    }
+    for (int s = 0; s < a.splits; ++s) {
+        const float * wp = w0 + s * sstr;
+        const float   ms = wp[0];
+        const float   w  = ms == -INFINITY ? 0.0f : __expf(ms - mx);
+        L                = __builtin_fmaf(w, wp[1], L);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+            acc[j] = __builtin_fmaf(w, wp[2 + lane * DPL + j], acc[j]);
+        }
+    }
+    const float inv = 1.0f / L;  // all keys masked: 0 * inf = NaN, as ggml
+    float *     yp  = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) iq * a.y2 + (int64_t) h * a.y1);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+        yp[lane * DPL + j] = acc[j] * inv;
+    }
+}
+
+// query rows per wave: 4, or 8 for 16-bit and Q8_0 K/V at D = 64 (more would
+// spill registers: each row keeps its output columns and scores in registers)
+static int fa_rb(int rows, int D, int kt) {
+    return D == 64 && kt != MI_TYPE_F32 && rows > 4 ? 8 : 4;
+}
+
+// rows per wave and KV splits for a problem; the workspace holds one
+// (max, sum, D outputs) record per split and row when there is more than one split
+void flash_attn_plan(FaArgs & a, int D) {
+    a.rows          = a.n_q * a.rk;
+    const int rb    = fa_rb(a.rows, D, a.kt);
+    a.rblocks       = (a.rows + rb - 1) / rb;
+    if (a.n_kv == 0 || a.rows == 0 || a.nb == 0) {  // no keys: one pass that writes NaN rows (0 * (1/0), as ggml)
+        a.chunk  = FA_TILE;
+        a.splits = 1;
+        return;
+    }
+    const int64_t pairs  = (int64_t) a.nb * a.nkv * a.rblocks;
+    const int64_t want   = (int64_t) num_cus() * MI_FA_WAVES_PER_CU;
+    const int64_t tiles  = (a.n_kv + FA_TILE - 1) / FA_TILE;
+    int64_t       splits = (want + pairs - 1) / pairs;
+    splits               = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
+    const int64_t per    = (tiles + splits - 1) / splits;  // tiles per split
+    a.chunk              = (int) (per * FA_TILE);
+    a.splits             = (int) ((a.n_kv + a.chunk - 1) / a.chunk);
+}
+
+size_t flash_attn_workspace(const FaArgs & a, int D) {
+    return a.splits > 1 ? (size_t) a.splits * a.nb * a.nkv * a.rows * (D + 2) * sizeof(float) : 0;
+}
+
+template <int KT, int D>
+static void launch_kd(const FaArgs & a, hipStream_t s) {
+    const dim3 grid((uint32_t) a.splits, (uint32_t) (a.nb * a.nkv), (uint32_t) a.rblocks);
+    if constexpr (D == 64 && KT != MI_TYPE_F32) {
+        if (fa_rb(a.rows, D, KT) == 8) {
+            hipLaunchKernelGGL((k_fa_split<KT, D, 8>), grid, dim3(64), 0, s, a);
+        } else {
+            hipLaunchKernelGGL((k_fa_split<KT, D, 4>), grid, dim3(64), 0, s, a);
+        }
+    } else {
+        hipLaunchKernelGGL((k_fa_split<KT, D, 4>), grid, dim3(64), 0, s, a);
+    }
+    if (a.splits > 1) {
+        hipLaunchKernelGGL((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(64), 0, s, a);
+    }
+}
+
+template <int KT>
+static int launch_k(const FaArgs & a, int D, hipStream_t s) {
+    switch (D) {
+        case 64:
+            launch_kd<KT, 64>(a, s);
+            return MI_OK;
+        case 128:
+            launch_kd<KT, 128>(a, s);
+            return MI_OK;
+        case 256:
+            if constexpr (KT != MI_TYPE_F32) {
+                launch_kd<KT, 256>(a, s);
+                return MI_OK;
+            }
+            return MI_ERR_UNSUPPORTED;
+        default:
+            return MI_ERR_UNSUPPORTED;
+    }
+}
+
+int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
+    if (a.rows == 0 || a.nb == 0 || a.nkv == 0) {
+        return MI_OK;
+    }
+    switch (kt) {
+        case MI_TYPE_F16:
+            return launch_k<MI_TYPE_F16>(a, D, s);
+        case MI_TYPE_BF16:
+            return launch_k<MI_TYPE_BF16>(a, D, s);
+        case MI_TYPE_Q8_0:
+            return launch_k<MI_TYPE_Q8_0>(a, D, s);
+        case MI_TYPE_F32:
+            return launch_k<MI_TYPE_F32>(a, D, s);
+        default:
+            return MI_ERR_TYPE;
+    }
+}
+
+}  // namespace mi

@@ -111,6 +111,32 @@ struct RowCopy {
 
 int launch_row_copy(const RowCopy & k, const RowCopy * v, int tin, int tout, int rounding, hipStream_t s);
 
+// ---- fattn.hip -------------------------------------------------------------
+// ggml_flash_attn_ext operands (byte strides; ne0 = D contiguous everywhere)
+struct FaArgs {
+    const char * q;  // [D, n_q, Nh, N]: q1 = position, q2 = head, q3 = batch
+    int64_t      q1, q2, q3;
+    int          tq;
+    const char * k;  // [D, n_kv, Nkv, N / rk3]
+    int64_t      k1, k2, k3;
+    const char * v;
+    int64_t      v1, v2, v3;
+    const char * mask;  // F16 [n_kv, >= n_q, mne2, mne3] or nullptr
+    int64_t      m1, m2, m3;
+    int          mne2, mne3;
+    char *       y;  // F32 [D, Nh, n_q, N]: y1 = head, y2 = position, y3 = batch
+    int64_t      y1, y2, y3;
+    int          n_q, n_kv, nh, nkv, nb, rk, rk3;
+    int          kt;  // K and V type
+    float        scale;
+    int          rows, rblocks, chunk, splits;  // from flash_attn_plan
+    float *      ws;                            // split partials (flash_attn_workspace bytes)
+};
+
+void   flash_attn_plan(FaArgs & a, int D);
+size_t flash_attn_workspace(const FaArgs & a, int D);
+int    launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s);
+
 // ---- tsembd.hip ------------------------------------------------------------
 int launch_timestep_embedding(const float * t, int64_t n, int64_t ts, int dim, int max_period, char * y,
                               int64_t ys, hipStream_t s);

@@ -198,6 +198,31 @@ int mi_kv_store(const mi_tensor * k, const mi_tensor * k_cache, const mi_tensor 
  * Replaces dit-graph.h:90 (dim 256, max_period 10000). */
 int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi_tensor * y, mi_stream stream);
 
+/* ggml_flash_attn_ext(q, k, v, mask, scale, max_bias, logit_softcap) with
+ * GGML_PREC_F32. Replaces the DiT self and cross attention
+ * (dit-graph.h:227-231, 348-349) and the batched decode attention over the KV
+ * cache (qwen3-lm.h:718-723, 256-bucketed read length at 582-596).
+ *   q:    [D, n_q, Nh, N]      F32/BF16/F16
+ *   k, v: [D, n_kv, Nkv, Nk3]  both F16, both BF16, both Q8_0 or both F32
+ *         (F32 only for D <= 128); Nh % Nkv == 0, N % Nk3 == 0; rows at a
+ *         16-byte aligned stride (Q8_0: 8-byte when D % 128 == 0, else
+ *         4-byte), e.g. cache views
+ *   mask: F16 [n_kv, >= n_q, mne2, mne3] (head h uses h % mne2, batch b uses
+ *         b % mne3) or NULL
+ *   y:    F32 [D, Nh, n_q, N]  (ggml's permuted result)
+ * D (= ne0 of q, k and v) is 64, 128 or 256. max_bias and logit_softcap must
+ * be 0 (the only values the reference passes); others return
+ * MI_ERR_UNSUPPORTED. q is converted to K's dot type as ggml-cpu converts it
+ * (fp16, bf16, or Q8_0 with the x86 rounding); keys whose mask is -inf are
+ * skipped and never read; a row whose keys are all masked is NaN.
+ * workspace: device memory of at least mi_flash_attn_ext_workspace() bytes
+ * (for the partial results of a split key range; NULL when that is 0). The
+ * size depends on the shapes and on the current device's CU count. */
+int mi_flash_attn_ext_workspace(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v, size_t * bytes);
+int mi_flash_attn_ext(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v, const mi_tensor * mask,
+                      float scale, float max_bias, float logit_softcap, const mi_tensor * y, void * workspace,
+                      size_t workspace_bytes, mi_stream stream);
+
 /* ---------------------------------------------------------------------- */
 /* Layer-chain drivers: launch the fused-op sequence of one DiT block or   */
 /* one Qwen3 layer in the order of the reference's layer composers, taking */

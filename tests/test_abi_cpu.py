@@ -150,6 +150,43 @@ def test_q8_get_rows_kv_validation():
     assert L.mi_timestep_embedding(R(_t([4])), 256, 10000, R(_t([256, 5])), NULL_S) == -3
 
 
+def test_flash_attn_validation():
+    D, n_q, Nh, N, n_kv, Nkv = 128, 1, 32, 8, 256, 8
+    q = _t([D, n_q, Nh, N])
+    k = _t([D, n_kv, Nkv, N], 1)     # F16
+    v = _t([D, n_kv, Nkv, N], 1)
+    y = _t([D, Nh, n_q, N])
+    mask = _t([n_kv, 1, 1, N], 1)
+    ws = ctypes.c_size_t(0)
+    fa = L.mi_flash_attn_ext
+    assert fa(R(q), R(k), R(v), R(mask), 0.1, 0.0, 0.0, None, None, 0, NULL_S) == -1
+    assert fa(R(q), R(k), R(v), R(mask), 0.1, 0.5, 0.0, R(y), None, 0, NULL_S) == -7      # max_bias (ALiBi)
+    assert fa(R(q), R(k), R(v), R(mask), 0.1, 0.0, 30.0, R(y), None, 0, NULL_S) == -7     # logit softcap
+    assert fa(R(q), R(k), R(v), R(mask), float("nan"), 0.0, 0.0, R(y), None, 0, NULL_S) == -6
+    assert fa(R(q), R(k), R(_t([D, n_kv, Nkv, N], Q8_0)), R(mask), 0.1, 0.0, 0.0, R(y), None, 0, NULL_S) == -2
+    assert fa(R(_t([D, n_q, Nh, N], I32)), R(k), R(v), R(mask), 0.1, 0.0, 0.0, R(y), None, 0, NULL_S) == -2
+    assert fa(R(q), R(k), R(v), R(mask), 0.1, 0.0, 0.0, R(_t([D, Nh, n_q, N], BF16)), None, 0, NULL_S) == -2
+    assert fa(R(q), R(_t([D, n_kv, 5, N], 1)), R(_t([D, n_kv, 5, N], 1)), None, 0.1, 0.0, 0.0, R(y), None, 0,
+              NULL_S) == -3                                                                 # Nh % Nkv
+    assert fa(R(q), R(k), R(v), R(_t([n_kv + 1, 1, 1, N], 1)), 0.1, 0.0, 0.0, R(y), None, 0, NULL_S) == -3
+    assert fa(R(q), R(k), R(v), R(_t([n_kv, 1, 1, N])), 0.1, 0.0, 0.0, R(y), None, 0, NULL_S) == -2  # F32 mask
+    assert fa(R(q), R(k), R(v), R(mask), 0.1, 0.0, 0.0, R(_t([D, Nh, n_q + 1, N])), None, 0, NULL_S) == -3
+    q96, k96 = _t([96, n_q, Nh, N]), _t([96, n_kv, Nkv, N], 1)
+    assert fa(R(q96), R(k96), R(k96), None, 0.1, 0.0, 0.0, R(_t([96, Nh, n_q, N])), None, 0, NULL_S) == -7
+    kodd = _t([D, n_kv, Nkv, N], 1, nb=[2, 264, 264 * n_kv, 264 * n_kv * Nkv])  # rows 8-byte aligned only
+    assert fa(R(q), R(kodd), R(kodd), None, 0.1, 0.0, 0.0, R(y), None, 0, NULL_S) == -5
+    # a split key range needs the workspace the query reports
+    assert L.mi_flash_attn_ext_workspace(R(q), R(k), R(v), ctypes.byref(ws)) == 0
+    big = _t([D, 8192, Nkv, N], Q8_0)
+    assert L.mi_flash_attn_ext_workspace(R(q), R(big), R(big), ctypes.byref(ws)) == 0 and ws.value > 0
+    assert fa(R(q), R(big), R(big), None, 0.1, 0.0, 0.0, R(y), None, 0, NULL_S) == -6
+    assert fa(R(q), R(big), R(big), None, 0.1, 0.0, 0.0, R(y), ctypes.c_void_p(4096), ws.value - 1, NULL_S) == -6
+    assert L.mi_flash_attn_ext_workspace(R(q), R(k), R(v), None) == -1
+    for qs in ([64, 1, 2, 0], [64, 0, 2, 1], [64, 1, 2, 1]):  # empty batch, no queries, no keys
+        k0 = _t([64, 0, 2, 1], 1)
+        assert L.mi_flash_attn_ext_workspace(R(_t(qs)), R(k0), R(k0), ctypes.byref(ws)) == 0 and ws.value == 0
+
+
 def test_chain_validation():
     io = _lib.MiDitBlockIO()
     io.hidden = _t([2048, 4])

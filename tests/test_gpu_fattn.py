@@ -1,0 +1,180 @@
+"""GPU parity: ggml_flash_attn_ext (mi_flash_attn_ext) against the oracle.
+
+The oracle is the exact value of ggml-cpu's definition in double: q converted
+to K's dot type (fp16 / bf16 / Q8_0 x86), s = scale * q.k + mask with -inf keys
+skipped, softmax, p.V. The kernels compute in fp32, so the bar is a
+tolerance, written here: |y - ref| <= 1e-4 * max|V| over the KV head the row
+reads (fp32 rounding of the dot products, exp and the accumulation over up to
+8192 keys is ~1e-6 of that scale; 1e-4 leaves room, and is far below the
+difference a wrong key, head, mask row or scale would make). Rows whose keys
+are all masked must be NaN, as ggml's 0 * (1/0) makes them.
+"""
+import numpy as np
+import pytest
+from helpers import to_dev, to_np
+from oracle import oracle as orc
+
+from acestep_ops import ops
+from acestep_ops.device import DTensor
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _kv(x, kt):
+    """host float array (..., D) -> (device operand, float values the oracle sees)"""
+    if kt == "q8_0":
+        qb = orc.quantize_q8_0(x, "x86")
+        return ops.Q8(to_dev(qb)), orc.dequantize_q8_0(qb)
+    if kt == "f16":
+        h = orc.f32_to_f16(x)
+        return to_dev(h, f16=True), orc.f16_to_f32(h)
+    if kt == "bf16":
+        h = orc.f32_to_bf16(x)
+        return to_dev(h, bf16=True), orc.bf16_to_f32(h)
+    return to_dev(x), x
+
+
+def _q(x, qt):
+    if qt == "bf16":
+        h = orc.f32_to_bf16(x)
+        return to_dev(h, bf16=True), orc.bf16_to_f32(h)
+    return to_dev(x), x
+
+
+def _mask_dev(m):
+    """float mask (values exactly representable in fp16) -> device F16, oracle floats"""
+    h = orc.f32_to_f16(m)
+    return to_dev(h, f16=True), orc.f16_to_f32(h)
+
+
+def _check(y, ref, vf, rk):
+    """y, ref (N, n_q, Nh, D); vf (Nk3, Nkv, n_kv, D) values; row (b, h) reads KV head h // rk"""
+    N, n_q, Nh, D = ref.shape
+    nan_ref = np.isnan(ref)
+    assert np.array_equal(np.isnan(y), nan_ref), "NaN rows differ"
+    rk3 = N // vf.shape[0]
+    for b in range(N):
+        for h in range(Nh):
+            vmax = float(np.abs(vf[b // rk3, h // rk]).max())
+            d = np.abs(y[b, :, h] - ref[b, :, h])[~nan_ref[b, :, h]]
+            if d.size:
+                assert d.max() <= TOL * vmax, f"b={b} h={h}: {d.max()} > {TOL} * {vmax}"
+
+
+def _run(N, Nh, Nkv, n_q, n_kv, D, kt, qt="f32", mask=None, scale=None, seed=0, Nk3=None, kview=None):
+    Nk3 = Nk3 or N
+    r = _rng(seed)
+    q = r.standard_normal((N, Nh, n_q, D)).astype(np.float32)
+    k = r.standard_normal((Nk3, Nkv, n_kv, D)).astype(np.float32)
+    v = r.standard_normal((Nk3, Nkv, n_kv, D)).astype(np.float32)
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    dq, qf = _q(q, qt)
+    if kview is None:
+        dk, kf = _kv(k, kt)
+        dv, vf = _kv(v, kt)
+    else:  # views of the first n_kv slots of larger caches
+        pad = np.zeros((Nk3, Nkv, kview - n_kv, D), np.float32)
+        dk_full, kf_full = _kv(np.concatenate([k, pad + 7.0], axis=2), kt)
+        dv_full, vf_full = _kv(np.concatenate([v, pad - 7.0], axis=2), kt)
+        sl = (slice(None), slice(None), slice(0, n_kv))
+        dk = ops.Q8(dk_full.data[sl]) if kt == "q8_0" else dk_full[sl]
+        dv = ops.Q8(dv_full.data[sl]) if kt == "q8_0" else dv_full[sl]
+        kf, vf = kf_full[:, :, :n_kv], vf_full[:, :, :n_kv]
+    dm, mf = (None, None) if mask is None else _mask_dev(mask)
+    y = to_np(ops.flash_attn_ext(dq, dk, dv, dm, float(scale)))
+    rep = N // Nk3  # the oracle takes one KV batch per q batch (ggml: KV batch b // rep)
+    ref = orc.flash_attn_ext(qf, np.repeat(kf, rep, axis=0), np.repeat(vf, rep, axis=0), mf, float(scale), kt)
+    _check(y, ref, vf, Nh // Nkv)
+    return y, ref
+
+
+def _decode_mask(N, n_kv, lens):
+    m = np.zeros((N, 1, 1, n_kv), np.float32)
+    for b, L in enumerate(lens):
+        m[b, 0, 0, L:] = -np.inf
+    return m
+
+
+@pytest.mark.parametrize("kt", ["q8_0", "f16", "bf16", "f32"])
+@pytest.mark.parametrize("qt", ["f32", "bf16"])
+def test_decode_gqa_per_sequence_lengths(dev, kt, qt):
+    """Qwen3-4B decode shape (32/8 heads x 128), 4 sequences of different lengths over a
+    1280-slot read (the 256-bucketed length), cache views of a 2048-slot cache."""
+    N, n_kv = 4, 1280
+    print(f"fa decode kt={kt} qt={qt}", flush=True)
+    lens = [1, 300, 1025, 1280]
+    _run(N, 32, 8, 1, n_kv, 128, kt, qt, mask=_decode_mask(N, n_kv, lens), seed=1, kview=2048)
+
+
+@pytest.mark.parametrize("kt", ["q8_0", "f16"])
+def test_decode_long_kv_splits(dev, kt):
+    """8192 keys: the key range is split over many waves and merged."""
+    print(f"fa long kv kt={kt}", flush=True)
+    N, n_kv = 2, 8192
+    _run(N, 8, 2, 1, n_kv, 128, kt, "bf16", mask=_decode_mask(N, n_kv, [8192, 5000]), seed=2)
+
+
+@pytest.mark.parametrize("D,kt", [(64, "f16"), (64, "q8_0"), (64, "f32"), (128, "bf16"), (256, "f16"),
+                                  (256, "q8_0")])
+def test_prefill_window_mask_ragged(dev, D, kt):
+    """DiT-style self attention: 37 queries x 300 keys (ragged tiles), a sliding-window +
+    padding mask, 16/8 heads, 2 batch elements sharing the mask."""
+    print(f"fa prefill D={D} kt={kt}", flush=True)
+    n_q, n_kv, win, real = 37, 300, 64, 290
+    m = np.zeros((1, 1, 40, n_kv), np.float32)  # padded to 40 query rows, as ggml pads the mask
+    for i in range(n_q):
+        for j in range(n_kv):
+            if abs(i * 8 - j) > win or j >= real:
+                m[0, 0, i, j] = -np.inf
+    _run(2, 16, 8, n_q, n_kv, D, kt, "f32", mask=m, seed=3)
+
+
+def test_finite_mask_values_per_head(dev):
+    """A mask with finite biases, one per (head, query): mne2 = Nh, mne3 = 1."""
+    print("fa finite per-head mask", flush=True)
+    r = _rng(4)
+    m = np.round(r.uniform(-3, 3, (1, 4, 5, 200)) * 64) / 64  # exact in fp16
+    _run(3, 4, 2, 5, 200, 128, "f16", mask=m.astype(np.float32), seed=4)
+
+
+def test_no_mask_and_kv_batch_broadcast(dev):
+    """No mask; K/V shared by pairs of batch elements (ne3 broadcast, rk3 = 2)."""
+    print("fa no mask, rk3 = 2", flush=True)
+    _run(4, 8, 8, 3, 100, 128, "q8_0", "f32", mask=None, seed=5, Nk3=2)
+
+
+def test_fully_masked_rows_and_poisoned_masked_keys(dev):
+    """Rows with every key masked are NaN; keys masked for every row are never read, so
+    NaN bytes there do not reach the output."""
+    print("fa fully masked rows / poisoned keys", flush=True)
+    N, Nh, Nkv, n_q, n_kv, D = 2, 4, 4, 2, 96, 128
+    r = _rng(6)
+    q = r.standard_normal((N, Nh, n_q, D)).astype(np.float32)
+    k = r.standard_normal((N, Nkv, n_kv, D)).astype(np.float32)
+    v = r.standard_normal((N, Nkv, n_kv, D)).astype(np.float32)
+    m = np.zeros((N, 1, n_q, n_kv), np.float32)
+    m[0, 0, 1, :] = -np.inf               # b=0, query 1: all keys masked
+    m[1, 0, :, 40:70] = -np.inf           # b=1: keys 40..69 masked for both queries
+    kh, vh = orc.f32_to_f16(k), orc.f32_to_f16(v)
+    kh[1, :, 40:70] = 0x7E00              # NaN bytes in the masked keys
+    vh[1, :, 40:70] = 0x7E00
+    dm, mf = _mask_dev(m)
+    y = to_np(ops.flash_attn_ext(to_dev(q), to_dev(kh, f16=True), to_dev(vh, f16=True), dm, 0.125))
+    kf, vf = orc.f16_to_f32(kh), orc.f16_to_f32(vh)
+    ref = orc.flash_attn_ext(q, kf, vf, mf, 0.125, "f16")
+    assert np.isnan(y[0, 1]).all() and np.isnan(ref[0, 1]).all()
+    assert np.isfinite(y[1]).all()
+    _check(y, ref, np.nan_to_num(vf), 1)
+
+
+def test_empty_key_range_is_nan(dev):
+    print("fa n_kv = 0", flush=True)
+    q = DTensor.from_numpy(np.ones((1, 2, 1, 64), np.float32))
+    k = DTensor.empty((1, 2, 0, 64), "f16")
+    y = to_np(ops.flash_attn_ext(q, k, k, None, 1.0))
+    assert np.isnan(y).all()
