@@ -444,6 +444,76 @@ def configs_bench(steps: int, warmup: int):
         device.synchronize()
 
 
+# ---------------------------------------------------------------------------
+# Attention (reported with --attention): ggml_flash_attn_ext over the KV cache
+# at the Qwen3-4B batch-8 decode shape (reference qwen3-lm.h:706-723): one
+# query row per sequence, 32/8 heads x 128, an 8192-slot cache per sequence,
+# sequence lengths U[1, 8192], the read length rounded up to 256 and the
+# tail masked (qwen3-lm.h:582-596).
+# ---------------------------------------------------------------------------
+def attention_bench(steps: int):
+    from acestep_ops import device, ops
+    from acestep_ops.device import DTensor, Event, Graph, Stream
+
+    N, NH_, NKV_, Dh, SLOTS = 8, 32, 8, 128, 8192
+    rng = np.random.default_rng(11)
+    lens = rng.integers(1, SLOTS + 1, N)
+    read = min(SLOTS, int((lens.max() + 255) // 256 * 256))
+    st = Stream()
+    sh = st.handle
+    q = DTensor.from_numpy(bf16_bits(rng.standard_normal((N, NH_, 1, Dh), dtype=np.float32)), "bf16")
+    m = np.zeros((N, 1, 1, read), np.float32)
+    for b, L in enumerate(lens):
+        m[b, 0, 0, L:] = -np.inf
+    mask = DTensor.from_numpy(m.astype(np.float16).view(np.uint16), "f16")
+    y = DTensor.empty((N, 1, NH_, Dh), "f32")
+    for kt in ("q8_0", "f16"):
+        caches = []
+        for _ in range(2):  # K, V
+            src = DTensor.from_numpy(rng.standard_normal((N, NKV_, SLOTS, Dh), dtype=np.float32))
+            if kt == "q8_0":
+                c = DTensor.empty((N, NKV_, SLOTS, Q8_ROW(Dh)), "u8")
+                ops.cpy(src, ops.Q8(c), stream=sh)
+                caches.append(ops.Q8(c[:, :, :read]))
+            else:
+                c = DTensor.empty((N, NKV_, SLOTS, Dh), "f16")
+                ops.cpy(src, c, stream=sh)
+                caches.append(c[:, :, :read])
+            st.synchronize()
+            del src
+        kc, vc = caches
+        need = ops.flash_attn_workspace(q, kc, vc)
+        ws = DTensor.empty((max(need, 1),), "u8")
+        call = lambda: ops.flash_attn_ext(q, kc, vc, mask, 1.0 / float(np.sqrt(Dh)), out=y, workspace=ws,  # noqa
+                                          stream=sh)
+        call()
+        st.synchronize()
+        g = Graph()
+        with g.capture(st):
+            for _ in range(steps):
+                call()
+        g.launch()
+        st.synchronize()
+        a, b_ = Event(), Event()
+        a.record(sh)
+        g.launch()
+        b_.record(sh)
+        b_.synchronize()
+        us = 1000.0 * a.elapsed_ms(b_) / steps
+        row = Q8_ROW(Dh) if kt == "q8_0" else 2 * Dh
+        kv_bytes = int(lens.sum()) * NKV_ * 2 * row
+        alg = kv_bytes + N * read * 2 + N * NH_ * Dh * 2 + N * NH_ * Dh * 4
+        gbs = alg / (us * 1e-6) / 1e9
+        print(json.dumps({"config": f"C2 decode attention, Qwen3-4B batch 8, 32/8 heads x 128, {kt} KV cache of "
+                                    f"{SLOTS} slots, lengths U[1,{SLOTS}] (sum {int(lens.sum())}), read length "
+                                    f"{read}",
+                          "us_per_call": round(us, 2), "launches": 2 if need else 1, "bytes_per_call": alg,
+                          "kv_bytes": kv_bytes, "workspace_bytes": need, "GB/s": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 3)}), flush=True)
+        del g, caches, kc, vc, ws
+        device.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -456,6 +526,8 @@ def main():
                     help="launch each block kernel once plus a copy of known size, for counter collection")
     ap.add_argument("--configs", action="store_true",
                     help="time the Qwen3 layer op chains at the C1/C2/C4/C5 shapes instead (one JSON line each)")
+    ap.add_argument("--attention", action="store_true",
+                    help="time flash attention over the KV cache at the C2 decode shape (one JSON line per cache type)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); every op of the path is "
@@ -471,6 +543,9 @@ def main():
         return
     if args.configs:
         configs_bench(args.steps, args.warmup)
+        return
+    if args.attention:
+        attention_bench(args.steps)
         return
     kb = block_bytes(ROWS, fused=True)
     kb_u = block_bytes(ROWS, fused=False)

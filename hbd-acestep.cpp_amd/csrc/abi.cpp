@@ -652,6 +652,7 @@ static int fa_desc(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v
     a.q2   = (int64_t) q->nb[2];
     a.q3   = (int64_t) q->nb[3];
     a.tq   = q->type;
+    a.qvec = aligned(q->data, 16) && q->nb[1] % 16 == 0 && q->nb[2] % 16 == 0 && q->nb[3] % 16 == 0;
     a.k    = (const char *) k->data;
     a.k1   = (int64_t) k->nb[1];
     a.k2   = (int64_t) k->nb[2];
@@ -701,6 +702,9 @@ static int fa_desc(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v
         a.y3 = (int64_t) y->nb[3];
     }
     flash_attn_plan(a, (int) D);
+    if (a.splits == 0) {
+        return MI_ERR_UNSUPPORTED;  // a key range beyond 1024 splits of 256 keys
+    }
     return MI_OK;
 }
 

@@ -8,9 +8,9 @@
 //     for BF16 K, Q8_0 (the x86 from_float: id = 127/amax, round half to even,
 //     saturate; fp16 scale) for Q8_0 K; the Q8_0 dot product is then an exact
 //     integer sum per block scaled by d_k*d_q;
-//   - s = dot * scale + mask; a key whose mask is -inf is skipped, and one
-//     masked for every row of a workgroup is not even read (its K/V bytes may
-//     hold anything);
+//   - s = dot * scale + mask; a key whose mask is -inf is skipped, and the
+//     bytes of one masked for every row of the wave are discarded (replaced by
+//     zeros before any arithmetic), so they may hold anything, NaN included;
 //   - online softmax; a row whose keys are all masked ends as 0 * (1/0) = NaN;
 //   - the result is F32 [D, Nh, n_q, N] (heads of a token adjacent).
 // Arithmetic is fp32 throughout (dot products via v_dot2 / v_dot4, exp,
@@ -21,8 +21,8 @@
 // KV head g, block of RB query rows), where the query rows of a KV head are
 // its n_q x (Nh/Nkv) (query position, head) pairs, so a K/V tile is loaded
 // once for every query head that shares it (GQA). The wave walks its range
-// in tiles of 32 keys: the mask values first (keys masked for all rows are
-// neither loaded nor counted), then all of the tile's K and V bytes with
+// in tiles of 32 keys: the mask values first (tiles masked for all rows are
+// skipped), then all of the tile's K and V bytes with
 // coalesced loads into LDS, then q.k with lane = (key, half of D) and one
 // cross-half exchange, the softmax update, and p.V with lane = output
 // columns. With several splits, each writes (max, sum, unnormalized output)
@@ -32,10 +32,12 @@
 namespace mi {
 
 #ifndef MI_FA_WAVES_PER_CU
-#define MI_FA_WAVES_PER_CU 16  // splits are chosen so the grid holds about this many waves per CU
+#define MI_FA_WAVES_PER_CU 8  // splits are chosen so the grid holds about this many waves per CU
 #endif
 
 constexpr int FA_TILE = 32;  // keys per tile
+constexpr int FA_MAXT = 16;  // tiles per split at most (the split's mask is staged in LDS)
+constexpr int FA_MAX_SPLITS = 1024;  // splits of one key range at most (the merge keeps their weights in LDS)
 
 template <int KT> struct FaT;
 template <> struct FaT<MI_TYPE_F32> {
@@ -59,16 +61,6 @@ template <> struct FaT<MI_TYPE_Q8_0> {
 typedef _Float16 fa_f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16   fa_bf16x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ float fa_load_q(const char * p, int tq) {
-    if (tq == MI_TYPE_F32) {
-        return load_elem<MI_TYPE_F32>(p);
-    }
-    if (tq == MI_TYPE_BF16) {
-        return load_elem<MI_TYPE_BF16>(p);
-    }
-    return load_elem<MI_TYPE_F16>(p);
-}
-
 // x86 from_float for one 32-element block: quants into q (8 words), scale (fp16 value)
 __device__ __forceinline__ float fa_q8_block(const float * x, uint32_t * qw) {
     float amax = 0.0f;
@@ -90,8 +82,17 @@ __device__ __forceinline__ float fa_q8_block(const float * x, uint32_t * qw) {
     return (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
 }
 
+#ifndef MI_FA_WPE
+#define MI_FA_WPE 0  // > 0: ask the compiler for at least this many waves per SIMD
+#endif
+#if MI_FA_WPE > 0
+#define MI_FA_OCC __attribute__((amdgpu_waves_per_eu(MI_FA_WPE, 8)))
+#else
+#define MI_FA_OCC
+#endif
+
 template <int KT, int D, int RB>
-__global__ void __launch_bounds__(64) k_fa_split(const FaArgs a) {
+__global__ void __launch_bounds__(64) MI_FA_OCC k_fa_split(const FaArgs a) {
     constexpr int RBYTES = FaT<KT>::row(D);
     constexpr int CB     = FaT<KT>::cb(D);
     constexpr int CPR    = RBYTES / CB;                                    // load chunks per row
@@ -104,9 +105,12 @@ __global__ void __launch_bounds__(64) k_fa_split(const FaArgs a) {
 
     __shared__ __align__(16) char     kt[FA_TILE * RSTR];
     __shared__ __align__(16) char     vt[FA_TILE * RSTR];
+    __shared__ __align__(16) float    qf[RB][D];        // q rows as floats
     __shared__ __align__(16) uint32_t qs[RB][QW];       // q converted to K's dot type
     __shared__ float                  qd[RB][D / 32];    // Q8_0: per-block q scales
     __shared__ __align__(16) float    pt[FA_TILE][RB];   // the tile's probabilities
+    __shared__ float                  mt[FA_MAXT * FA_TILE][RB];  // the split's mask values
+    __shared__ uint64_t               lt[FA_MAXT];       // per tile: keys some row reads
 
     const int      lane  = threadIdx.x;
     const uint32_t split = blockIdx.x;
@@ -127,37 +131,6 @@ __global__ void __launch_bounds__(64) k_fa_split(const FaArgs a) {
         h_of[r]      = (int) g * a.rk + (gc - iq_of[r] * a.rk);
     }
 
-    // 1. q rows, converted to K's dot type, into LDS
-    if constexpr (KT == MI_TYPE_Q8_0) {
-        // one lane per (row, 32-block)
-        for (int t = lane; t < RB * (D / 32); t += 64) {
-            const int r  = t / (D / 32);
-            const int bk = t - r * (D / 32);
-            float     x[32];
-            const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h_of[r] * a.q2 + (int64_t) iq_of[r] * a.q1;
-            const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
-            for (int j = 0; j < 32; ++j) {
-                x[j] = rv[r] ? fa_load_q(qp + (size_t) (bk * 32 + j) * es, a.tq) : 0.0f;
-            }
-            qd[r][bk] = fa_q8_block(x, &qs[r][bk * 8]);
-        }
-    } else {
-        constexpr int EPW = KT == MI_TYPE_F32 ? 1 : 2;  // elements per word
-        for (int t = lane; t < RB * QW; t += 64) {
-            const int    r  = t / QW;
-            const int    w  = t - r * QW;
-            const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h_of[r] * a.q2 + (int64_t) iq_of[r] * a.q1;
-            const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
-            float        x0 = rv[r] ? fa_load_q(qp + (size_t) (w * EPW) * es, a.tq) : 0.0f;
-            if constexpr (KT == MI_TYPE_F32) {
-                qs[r][w] = __float_as_uint(x0);
-            } else {
-                const float x1 = rv[r] ? fa_load_q(qp + (size_t) (w * EPW + 1) * es, a.tq) : 0.0f;
-                qs[r][w]       = KT == MI_TYPE_F16 ? pack_f16x2(x0, x1) : pack_bf16x2(x0, x1);
-            }
-        }
-    }
-
     // mask rows (per row: its query position and head)
     const char * mrow[RB];
 #pragma unroll
@@ -170,6 +143,93 @@ __global__ void __launch_bounds__(64) k_fa_split(const FaArgs a) {
     const char *   kg = a.k + (int64_t) kb * a.k3 + (int64_t) g * a.k2;
     const char *   vg = a.v + (int64_t) kb * a.v3 + (int64_t) g * a.v2;
 
+    const int key  = lane & 31;
+    const int half = lane >> 5;
+    const int kbeg = (int) split * a.chunk;
+    const int kend = kbeg + a.chunk < a.n_kv ? kbeg + a.chunk : a.n_kv;
+    const int nt   = (kend - kbeg + FA_TILE - 1) / FA_TILE;  // tiles of this split (<= FA_MAXT)
+
+    // the shared mask row's values for every tile of the split, issued first
+    float ms[FA_MAXT];
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        const int t0 = kbeg + t * FA_TILE;
+        const int kc = t0 + key < kend ? t0 + key : kend - 1;
+        ms[t]        = a.mask != nullptr && a.mshared && t < nt ? load_elem<MI_TYPE_F16>(mrow[0] + (size_t) kc * 2)
+                                                              : 0.0f;
+    }
+
+    // 1. q rows into LDS as floats: 16-byte loads when q's rows are 16-byte
+    //    aligned (elementwise otherwise), all issued before any is used; then
+    //    converted to K's dot type from LDS
+    {
+        constexpr int NQC = (RB * D * 4 / 16 + 63) / 64;  // 16-byte chunks per lane at most (F32 q)
+        const int     es  = a.tq == MI_TYPE_F32 ? 4 : 2;
+        const int     epc = 16 / es;    // elements per chunk
+        const int     cpr = D / epc;    // chunks per row
+        uint4         qv[NQC];
+#pragma unroll
+        for (int i = 0; i < NQC; ++i) {
+            const int c  = lane + 64 * i;
+            const int cc = c < RB * cpr ? c : RB * cpr - 1;
+            const int r  = cc / cpr;
+            const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h_of[r] * a.q2 + (int64_t) iq_of[r] * a.q1 +
+                              (int64_t) (cc - r * cpr) * 16;
+            if (a.qvec) {
+                qv[i] = ld16(qp);
+            } else if (es == 4) {
+                const uint32_t * w = (const uint32_t *) qp;
+                qv[i]              = make_uint4(w[0], w[1], w[2], w[3]);
+            } else {
+                const uint16_t * h = (const uint16_t *) qp;
+                qv[i]              = make_uint4((uint32_t) h[0] | ((uint32_t) h[1] << 16),
+                                                (uint32_t) h[2] | ((uint32_t) h[3] << 16),
+                                                (uint32_t) h[4] | ((uint32_t) h[5] << 16),
+                                                (uint32_t) h[6] | ((uint32_t) h[7] << 16));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NQC; ++i) {
+            const int c = lane + 64 * i;
+            if (c < RB * cpr) {
+                const int r  = c / cpr;
+                const int e0 = (c - r * cpr) * epc;
+                float     f[8];
+                if (a.tq == MI_TYPE_F32) {
+                    unpack16<MI_TYPE_F32>(qv[i], f);
+                } else if (a.tq == MI_TYPE_BF16) {
+                    unpack16<MI_TYPE_BF16>(qv[i], f);
+                } else {
+                    unpack16<MI_TYPE_F16>(qv[i], f);
+                }
+                for (int e = 0; e < epc; ++e) {
+                    qf[r][e0 + e] = rv[r] ? f[e] : 0.0f;
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if constexpr (KT == MI_TYPE_Q8_0) {
+        // one lane per (row, 32-block): the x86 from_float
+        for (int t = lane; t < RB * (D / 32); t += 64) {
+            const int r  = t / (D / 32);
+            const int bk = t - r * (D / 32);
+            qd[r][bk]    = fa_q8_block(&qf[r][bk * 32], &qs[r][bk * 8]);
+        }
+    } else {
+        for (int t = lane; t < RB * QW; t += 64) {
+            const int r = t / QW;
+            const int w = t - r * QW;
+            if constexpr (KT == MI_TYPE_F32) {
+                qs[r][w] = __float_as_uint(qf[r][w]);
+            } else {
+                const float x0 = qf[r][2 * w], x1 = qf[r][2 * w + 1];
+                qs[r][w]       = KT == MI_TYPE_F16 ? pack_f16x2(x0, x1) : pack_bf16x2(x0, x1);
+            }
+        }
+    }
+
     float m[RB], l[RB], o[RB][DPL];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
@@ -180,194 +240,240 @@ __global__ void __launch_bounds__(64) k_fa_split(const FaArgs a) {
             o[r][j] = 0.0f;
         }
     }
+
+    // 2. the split's mask values into LDS, and per tile the set of keys some
+    //    row reads (a tile no row reads is skipped). When every row of the wave
+    //    uses one mask row (decode: one query position, the heads of one KV
+    //    head), one value per key is loaded, for all tiles at once, before the
+    //    q conversion above so that the two round trips overlap.
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        if (t < nt) {
+            const int  t0  = kbeg + t * FA_TILE;
+            const int  kc  = t0 + key < kend ? t0 + key : kend - 1;  // clamped: every load is in bounds
+            const bool ok  = t0 + key < kend;
+            bool       any = false;
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                float x = 0.0f;
+                if (a.mask != nullptr) {
+                    x = a.mshared ? ms[t] : load_elem<MI_TYPE_F16>(mrow[r] + (size_t) kc * 2);
+                }
+                x = ok && rv[r] ? x : -INFINITY;
+                if (half == 0) {
+                    mt[t * FA_TILE + key][r] = x;
+                }
+                any = any || x != -INFINITY;
+            }
+            const uint64_t lv = __builtin_amdgcn_ballot_w64(any && half == 0);  // bit k: key k is read
+            if (lane == 0) {
+                lt[t] = lv;
+            }
+        }
+    }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 
-    const int key  = lane & 31;
-    const int half = lane >> 5;
-    const int kbeg = (int) split * a.chunk;
-    const int kend = kbeg + a.chunk < a.n_kv ? kbeg + a.chunk : a.n_kv;
-    for (int t0 = kbeg; t0 < kend; t0 += FA_TILE) {
-        const int nk = kend - t0 < FA_TILE ? kend - t0 : FA_TILE;
-        // 2. mask values of this lane's key for every row
-        float mv[RB];
-        bool  any = false;
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            float x = -INFINITY;
-            if (rv[r] && key < nk) {
-                x = mrow[r] ? load_elem<MI_TYPE_F16>(mrow[r] + (size_t) (t0 + key) * 2) : 0.0f;
-            }
-            mv[r] = x;
-            any   = any || x != -INFINITY;
-        }
-        const uint64_t live = __builtin_amdgcn_ballot_w64(any && half == 0);  // bit k: key k is read
-        if (live == 0) {
-            continue;
-        }
-        // 3. K and V bytes of the live keys, all loads issued before any is used
-        chunk_t kc[NCH], vc[NCH];
+    // 3. K/V tiles, software pipelined: the registers of tile t are staged in
+    //    LDS, then receive tile t+1's loads while tile t is computed
+    chunk_t kc[NCH], vc[NCH];
+    // Every lane loads all of its chunks from a row clamped into the tile (no
+    // branches); in a tile with unread keys (masked for every row, or past the
+    // end) their chunks are then replaced by zeros, so their bytes never reach
+    // the sums. Offsets within a tile fit 32 bits; the tile base is uniform.
+    auto load_kv = [&](int t0, uint64_t live) {
+        const int    nk  = kend - t0 < FA_TILE ? kend - t0 : FA_TILE;
+        const char * kgt = kg + (int64_t) t0 * a.k1;
+        const char * vgt = vg + (int64_t) t0 * a.v1;
 #pragma unroll
         for (int i = 0; i < NCH; ++i) {
-            const int c  = lane + 64 * i;
-            const int kk = c / CPR;
-            const int pp = c - kk * CPR;
-            if (c < FA_TILE * CPR && ((live >> kk) & 1)) {
-                const int64_t ko = (int64_t) (t0 + kk) * a.k1 + pp * CB;
-                const int64_t vo = (int64_t) (t0 + kk) * a.v1 + pp * CB;
-                if constexpr (CB == 16) {
-                    kc[i] = ld16(kg + ko);
-                    vc[i] = ld16(vg + vo);
-                } else {
-                    kc[i] = *(const chunk_t *) (kg + ko);
-                    vc[i] = *(const chunk_t *) (vg + vo);
-                }
+            const int      c  = lane + 64 * i < FA_TILE * CPR ? lane + 64 * i : FA_TILE * CPR - 1;
+            const int      kk = c / CPR < nk ? c / CPR : nk - 1;
+            const uint32_t pp = (uint32_t) (c % CPR) * CB;
+            const uint32_t ko = (uint32_t) kk * (uint32_t) a.k1 + pp;
+            const uint32_t vo = (uint32_t) kk * (uint32_t) a.v1 + pp;
+            if constexpr (CB == 16) {
+                kc[i] = ld16(kgt + ko);
+                vc[i] = ld16(vgt + vo);
             } else {
-                kc[i] = chunk_t{};
-                vc[i] = chunk_t{};
+                kc[i] = *(const chunk_t *) (kgt + ko);
+                vc[i] = *(const chunk_t *) (vgt + vo);
             }
         }
+        if (live != 0xffffffffull) {
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const int c = lane + 64 * i;
-            if (c < FA_TILE * CPR) {
-                const int kk = c / CPR;
-                const int pp = c - kk * CPR;
-                *(chunk_t *) (kt + kk * RSTR + pp * CB) = kc[i];
-                *(chunk_t *) (vt + kk * RSTR + pp * CB) = vc[i];
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-
-        // 4. s = q.k for (row, key): lane = (key, half of D)
-        float s[RB];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            s[r] = 0.0f;
-        }
-        const char * kr = kt + key * RSTR;
-        if constexpr (KT == MI_TYPE_Q8_0) {
-            constexpr int NBH = D / 64;  // blocks per half
-#pragma unroll
-            for (int bb = 0; bb < NBH; ++bb) {
-                const int        bk = half * NBH + bb;
-                const uint16_t * bp = (const uint16_t *) (kr + 34 * bk);
-                const float      dk = (float) __builtin_bit_cast(_Float16, bp[0]);
-                uint32_t         kw[8];
-#pragma unroll
-                for (int w = 0; w < 8; ++w) {
-                    kw[w] = (uint32_t) bp[1 + 2 * w] | ((uint32_t) bp[2 + 2 * w] << 16);
-                }
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    int sumi = 0;
-#pragma unroll
-                    for (int w = 0; w < 8; ++w) {
-                        sumi = __builtin_amdgcn_sdot4((int) kw[w], (int) qs[r][bk * 8 + w], sumi, false);
-                    }
-                    s[r] = __builtin_fmaf(dk * qd[r][bk], (float) sumi, s[r]);
-                }
-            }
-        } else {
-            constexpr int WH = QW / 2;  // words per half
-            const uint4 * k4 = (const uint4 *) (kr + half * (RBYTES / 2));
-#pragma unroll
-            for (int c4 = 0; c4 < WH / 4; ++c4) {
-                const uint4 kv = k4[c4];
-                const uint32_t kw[4] = { kv.x, kv.y, kv.z, kv.w };
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    const uint4    qv   = *(const uint4 *) &qs[r][half * WH + 4 * c4];
-                    const uint32_t qw[4] = { qv.x, qv.y, qv.z, qv.w };
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if constexpr (KT == MI_TYPE_F16) {
-                            s[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(fa_f16x2, kw[e]),
-                                                          __builtin_bit_cast(fa_f16x2, qw[e]), s[r], false);
-                        } else if constexpr (KT == MI_TYPE_BF16) {
-                            s[r] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(fa_bf16x2, kw[e]),
-                                                                   __builtin_bit_cast(fa_bf16x2, qw[e]), s[r], false);
-                        } else {
-                            s[r] = __builtin_fmaf(__uint_as_float(kw[e]), __uint_as_float(qw[e]), s[r]);
-                        }
-                    }
+            for (int i = 0; i < NCH; ++i) {
+                const int  c    = lane + 64 * i;
+                const bool keep = c < FA_TILE * CPR && ((live >> (c / CPR)) & 1);
+                if (!keep) {
+                    kc[i] = chunk_t{};
+                    vc[i] = chunk_t{};
                 }
             }
         }
-        // 5. full dot (both halves), scale, mask; online softmax update per row
+    };
+    uint64_t live = nt > 0 ? lt[0] : 0;
+    if (live) {
+        load_kv(kbeg, live);
+    }
+    for (int t = 0; t < nt; ++t) {
+        const int t0 = kbeg + t * FA_TILE;
+        const uint64_t next = t + 1 < nt ? lt[t + 1] : 0;
+        if (live) {
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            const float full = s[r] + __shfl_xor(s[r], 32, 64);
-            float       x    = mv[r] == -INFINITY ? -INFINITY : full * a.scale + mv[r];
-            const float tmax = group_max<32>(x);
-            const float mn   = fmaxf(m[r], tmax);
-            float       alpha = 1.0f, p = 0.0f;
-            if (mn != -INFINITY) {
-                alpha = __expf(m[r] - mn);  // exp(-inf) = 0 on the first live tile
-                p     = x == -INFINITY ? 0.0f : __expf(x - mn);
+            for (int i = 0; i < NCH; ++i) {
+                const int c = lane + 64 * i;
+                if (c < FA_TILE * CPR) {
+                    const int kk = c / CPR;
+                    const int pp = c - kk * CPR;
+                    *(chunk_t *) (kt + kk * RSTR + pp * CB) = kc[i];
+                    *(chunk_t *) (vt + kk * RSTR + pp * CB) = vc[i];
+                }
             }
-            m[r] = mn;
-            l[r] = l[r] * alpha + (half == 0 ? p : 0.0f);
-#pragma unroll
-            for (int j = 0; j < DPL; ++j) {
-                o[r][j] *= alpha;
-            }
-            if (half == 0) {
-                pt[key][r] = p;
-            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-
-        // 6. o += p.V, lane = output columns [lane*DPL, +DPL)
-        for (int kk = 0; kk < nk; ++kk) {
-            if (!((live >> kk) & 1)) {
-                continue;  // never read: its K/V bytes were not loaded
-            }
-            float pr[RB];
-#pragma unroll
-            for (int r4 = 0; r4 < RB; r4 += 4) {
-                const float4 p4 = *(const float4 *) &pt[kk][r4];
-                pr[r4]          = p4.x;
-                pr[r4 + 1]      = p4.y;
-                pr[r4 + 2]      = p4.z;
-                pr[r4 + 3]      = p4.w;
-            }
-            float       vv[DPL];
-            const char * vr = vt + kk * RSTR;
-            if constexpr (KT == MI_TYPE_Q8_0) {
-                const int      c0 = lane * DPL;
-                const char *   bp = vr + 34 * (c0 / 32);
-                const float    dv = (float) __builtin_bit_cast(_Float16, *(const uint16_t *) bp);
-                const int8_t * qp = (const int8_t *) (bp + 2 + (c0 % 32));
-#pragma unroll
-                for (int j = 0; j < DPL; ++j) {
-                    vv[j] = (float) qp[j] * dv;
-                }
-            } else if constexpr (KT == MI_TYPE_F32) {
-#pragma unroll
-                for (int j = 0; j < DPL; ++j) {
-                    vv[j] = ((const float *) vr)[lane * DPL + j];
-                }
-            } else {
-                const uint16_t * hp = (const uint16_t *) vr + lane * DPL;
-#pragma unroll
-                for (int j = 0; j < DPL; ++j) {
-                    vv[j] = KT == MI_TYPE_F16 ? (float) __builtin_bit_cast(_Float16, hp[j])
-                                              : __uint_as_float((uint32_t) hp[j] << 16);
-                }
-            }
+        if (next) {
+            load_kv(t0 + FA_TILE, next);  // in flight during this tile's math
+        }
+        if (live) {
+            // 4. s = q.k for (row, key): lane = (key, half of D)
+            float s[RB];
 #pragma unroll
             for (int r = 0; r < RB; ++r) {
+                s[r] = 0.0f;
+            }
+            const char * kr = kt + key * RSTR;
+            if constexpr (KT == MI_TYPE_Q8_0) {
+                constexpr int NBH = D / 64;  // blocks per half
 #pragma unroll
-                for (int j = 0; j < DPL; ++j) {
-                    o[r][j] = __builtin_fmaf(pr[r], vv[j], o[r][j]);
+                for (int bb = 0; bb < NBH; ++bb) {
+                    const int        bk = half * NBH + bb;
+                    const uint16_t * bp = (const uint16_t *) (kr + 34 * bk);
+                    const float      dk = (float) __builtin_bit_cast(_Float16, bp[0]);
+                    uint32_t         kw[8];
+#pragma unroll
+                    for (int w = 0; w < 8; ++w) {
+                        kw[w] = (uint32_t) bp[1 + 2 * w] | ((uint32_t) bp[2 + 2 * w] << 16);
+                    }
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        int sumi = 0;
+#pragma unroll
+                        for (int w = 0; w < 8; ++w) {
+                            sumi = __builtin_amdgcn_sdot4((int) kw[w], (int) qs[r][bk * 8 + w], sumi, false);
+                        }
+                        s[r] = __builtin_fmaf(dk * qd[r][bk], (float) sumi, s[r]);
+                    }
+                }
+            } else {
+                constexpr int WH = QW / 2;  // words per half
+                const uint4 * k4 = (const uint4 *) (kr + half * (RBYTES / 2));
+#pragma unroll
+                for (int c4 = 0; c4 < WH / 4; ++c4) {
+                    const uint4    kv    = k4[c4];
+                    const uint32_t kw[4] = { kv.x, kv.y, kv.z, kv.w };
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        const uint4    qv    = *(const uint4 *) &qs[r][half * WH + 4 * c4];
+                        const uint32_t qw[4] = { qv.x, qv.y, qv.z, qv.w };
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if constexpr (KT == MI_TYPE_F16) {
+                                s[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(fa_f16x2, kw[e]),
+                                                              __builtin_bit_cast(fa_f16x2, qw[e]), s[r], false);
+                            } else if constexpr (KT == MI_TYPE_BF16) {
+                                s[r] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(fa_bf16x2, kw[e]),
+                                                                       __builtin_bit_cast(fa_bf16x2, qw[e]), s[r],
+                                                                       false);
+                            } else {
+                                s[r] = __builtin_fmaf(__uint_as_float(kw[e]), __uint_as_float(qw[e]), s[r]);
+                            }
+                        }
+                    }
+                    // bound the scheduler's look-ahead: hoisting every row's q words
+                    // for the whole dot product would cost 4 x D/4 registers
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
+            // 5. full dot (both halves), scale, mask; online softmax update per row
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const float full  = s[r] + __shfl_xor(s[r], 32, 64);
+                const float mvr   = mt[t * FA_TILE + key][r];
+                const float x     = mvr == -INFINITY ? -INFINITY : full * a.scale + mvr;
+                const float tmax  = group_max<32>(x);
+                const float mn    = fmaxf(m[r], tmax);
+                float       alpha = 1.0f, p = 0.0f;
+                if (mn != -INFINITY) {
+                    alpha = __expf(m[r] - mn);  // exp(-inf) = 0 on the first live tile
+                    p     = x == -INFINITY ? 0.0f : __expf(x - mn);
+                }
+                m[r] = mn;
+                l[r] = l[r] * alpha + (half == 0 ? p : 0.0f);
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) {
+                    o[r][j] *= alpha;
+                }
+                if (half == 0) {
+                    pt[key][r] = p;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+
+            // 6. o += p.V, lane = output columns [lane*DPL, +DPL). Keys no row reads
+            //    (and keys past the end) have p = 0 and zero V bytes in LDS, so the
+            //    loop runs over the whole tile without a branch.
+#pragma unroll 8
+            for (int kk = 0; kk < FA_TILE; ++kk) {
+                float pr[RB];
+#pragma unroll
+                for (int r4 = 0; r4 < RB; r4 += 4) {
+                    const float4 p4 = *(const float4 *) &pt[kk][r4];
+                    pr[r4]          = p4.x;
+                    pr[r4 + 1]      = p4.y;
+                    pr[r4 + 2]      = p4.z;
+                    pr[r4 + 3]      = p4.w;
+                }
+                float        vv[DPL];
+                const char * vr = vt + kk * RSTR;
+                if constexpr (KT == MI_TYPE_Q8_0) {
+                    const int      c0 = lane * DPL;
+                    const char *   bp = vr + 34 * (c0 / 32);
+                    const float    dv = (float) __builtin_bit_cast(_Float16, *(const uint16_t *) bp);
+                    const int8_t * qp = (const int8_t *) (bp + 2 + (c0 % 32));
+#pragma unroll
+                    for (int j = 0; j < DPL; ++j) {
+                        vv[j] = (float) qp[j] * dv;
+                    }
+                } else if constexpr (KT == MI_TYPE_F32) {
+#pragma unroll
+                    for (int j = 0; j < DPL; ++j) {
+                        vv[j] = ((const float *) vr)[lane * DPL + j];
+                    }
+                } else {
+                    const uint16_t * hp = (const uint16_t *) vr + lane * DPL;
+#pragma unroll
+                    for (int j = 0; j < DPL; ++j) {
+                        vv[j] = KT == MI_TYPE_F16 ? (float) __builtin_bit_cast(_Float16, hp[j])
+                                                  : __uint_as_float((uint32_t) hp[j] << 16);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+#pragma unroll
+                    for (int j = 0; j < DPL; ++j) {
+                        o[r][j] = __builtin_fmaf(pr[r], vv[j], o[r][j]);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();  // the next tile overwrites kt, vt, pt
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();  // the next tile overwrites kt, vt, pt
+        live = next;
     }
 
     // 7. row sums across lanes; the final output or this split's partial
@@ -402,11 +508,20 @@ __global__ void __launch_bounds__(64) k_fa_split(const FaArgs a) {
 }
 
 // Merge the splits of one (sequence, KV head, row): y = sum_s w_s o_s / sum_s w_s l_s,
-// w_s = exp(m_s - max_s m_s) (0 for a split whose keys were all masked).
+// w_s = exp(m_s - max_s m_s) (0 for a split whose keys were all masked). A
+// workgroup of 256 threads per row: every split's (m, l) loaded at once, the
+// weights in LDS; then thread t accumulates one 16-byte column chunk over the
+// splits s = t / (D/4) (mod 256 / (D/4)), and the partial sums are added
+// through LDS. Every load of a pass is independent of the others.
 template <int D>
-__global__ void __launch_bounds__(64) k_fa_combine(const FaArgs a) {
-    constexpr int  DPL  = D / 64;
-    const int      lane = threadIdx.x;
+__global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
+    constexpr int  C4  = D / 4;    // float4 chunks per output row
+    constexpr int  SG  = 256 / C4; // split groups
+    __shared__ float wsh[FA_MAX_SPLITS];
+    __shared__ float red[8];
+    __shared__ __align__(16) float4 part[SG][C4];
+
+    const int      tid  = threadIdx.x;
     const uint32_t rec  = blockIdx.x;  // bg * rows + row
     const uint32_t bg   = rec / (uint32_t) a.rows;
     const int      row  = (int) (rec - bg * (uint32_t) a.rows);
@@ -416,30 +531,71 @@ __global__ void __launch_bounds__(64) k_fa_combine(const FaArgs a) {
     const int      h    = (int) g * a.rk + (row - iq * a.rk);
     const int64_t  sstr = (int64_t) a.nb * a.nkv * a.rows * (D + 2);  // one split's records
     const float *  w0   = a.ws + (int64_t) rec * (D + 2);
-    float          mx   = -INFINITY;
-    for (int s = 0; s < a.splits; ++s) {
-        mx = fmaxf(mx, w0[s * sstr]);
-    }
-    float L = 0.0f, acc[DPL];
+
+    // pass 1: max over the splits, weights, weighted sum of the row sums
+    float ml[FA_MAX_SPLITS / 256], ll[FA_MAX_SPLITS / 256];
+    float mloc = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-        acc[j] = 0.0f;
+    for (int i = 0; i < FA_MAX_SPLITS / 256; ++i) {
+        const int s = tid + 256 * i;
+        ml[i]       = s < a.splits ? w0[s * sstr] : -INFINITY;
+        ll[i]       = s < a.splits ? w0[s * sstr + 1] : 0.0f;
+        mloc        = fmaxf(mloc, ml[i]);
     }
-    for (int s = 0; s < a.splits; ++s) {
-        const float * wp = w0 + s * sstr;
-        const float   ms = wp[0];
-        const float   w  = ms == -INFINITY ? 0.0f : __expf(ms - mx);
-        L                = __builtin_fmaf(w, wp[1], L);
+    mloc = group_max<64>(mloc);
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = mloc;
+    }
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float       lw = 0.0f;
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-            acc[j] = __builtin_fmaf(w, wp[2 + lane * DPL + j], acc[j]);
+    for (int i = 0; i < FA_MAX_SPLITS / 256; ++i) {
+        const int   s = tid + 256 * i;
+        const float w = ml[i] == -INFINITY ? 0.0f : __expf(ml[i] - mx);
+        if (s < a.splits) {
+            wsh[s] = w;
         }
+        lw = __builtin_fmaf(w, ll[i], lw);
     }
-    const float inv = 1.0f / L;  // all keys masked: 0 * inf = NaN, as ggml
-    float *     yp  = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) iq * a.y2 + (int64_t) h * a.y1);
+    lw = group_sum<64>(lw);
+    if ((tid & 63) == 0) {
+        red[4 + (tid >> 6)] = lw;
+    }
+    __syncthreads();
+    const float L = (red[4] + red[5]) + (red[6] + red[7]);
+
+    // pass 2: weighted outputs
+    const int c  = tid % C4;
+    const int sg = tid / C4;
+    float4    acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+    for (int s = sg; s < a.splits; s += SG) {
+        const float  w = wsh[s];
+        const float4 v = *(const float4 *) (w0 + s * sstr + 2 + 4 * c);
+        acc.x          = __builtin_fmaf(w, v.x, acc.x);
+        acc.y          = __builtin_fmaf(w, v.y, acc.y);
+        acc.z          = __builtin_fmaf(w, v.z, acc.z);
+        acc.w          = __builtin_fmaf(w, v.w, acc.w);
+    }
+    part[sg][c] = acc;
+    __syncthreads();
+    if (tid < C4) {
+        float4 t = part[0][tid];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-        yp[lane * DPL + j] = acc[j] * inv;
+        for (int q = 1; q < SG; ++q) {
+            const float4 u = part[q][tid];
+            t.x += u.x;
+            t.y += u.y;
+            t.z += u.z;
+            t.w += u.w;
+        }
+        const float inv = 1.0f / L;  // all keys masked: 0 * inf = NaN, as ggml
+        float *     yp  = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) iq * a.y2 + (int64_t) h * a.y1);
+        yp[4 * tid]     = t.x * inv;
+        yp[4 * tid + 1] = t.y * inv;
+        yp[4 * tid + 2] = t.z * inv;
+        yp[4 * tid + 3] = t.w * inv;
     }
 }
 
@@ -455,6 +611,9 @@ void flash_attn_plan(FaArgs & a, int D) {
     a.rows          = a.n_q * a.rk;
     const int rb    = fa_rb(a.rows, D, a.kt);
     a.rblocks       = (a.rows + rb - 1) / rb;
+    // rows r0..r0+rb-1 of a wave share one query position when n_q == 1 or rb
+    // divides Nh/Nkv, and one mask head when the mask does not vary by head
+    a.mshared = a.mask != nullptr && a.mne2 == 1 && (a.n_q == 1 || a.rk % rb == 0);
     if (a.n_kv == 0 || a.rows == 0 || a.nb == 0) {  // no keys: one pass that writes NaN rows (0 * (1/0), as ggml)
         a.chunk  = FA_TILE;
         a.splits = 1;
@@ -465,7 +624,11 @@ void flash_attn_plan(FaArgs & a, int D) {
     const int64_t tiles  = (a.n_kv + FA_TILE - 1) / FA_TILE;
     int64_t       splits = (want + pairs - 1) / pairs;
     splits               = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
-    const int64_t per    = (tiles + splits - 1) / splits;  // tiles per split
+    int64_t       per    = (tiles + splits - 1) / splits;  // tiles per split
+    per                  = per > FA_MAXT ? FA_MAXT : per;
+    if ((tiles + per - 1) / per > FA_MAX_SPLITS) {
+        return;  // more than FA_MAX_SPLITS * FA_MAXT * FA_TILE keys: rejected by the caller (splits = 0)
+    }
     a.chunk              = (int) (per * FA_TILE);
     a.splits             = (int) ((a.n_kv + a.chunk - 1) / a.chunk);
 }
@@ -487,7 +650,7 @@ static void launch_kd(const FaArgs & a, hipStream_t s) {
         hipLaunchKernelGGL((k_fa_split<KT, D, 4>), grid, dim3(64), 0, s, a);
     }
     if (a.splits > 1) {
-        hipLaunchKernelGGL((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(64), 0, s, a);
+        hipLaunchKernelGGL((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(256), 0, s, a);
     }
 }
 

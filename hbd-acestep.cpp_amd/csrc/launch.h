@@ -117,6 +117,7 @@ struct FaArgs {
     const char * q;  // [D, n_q, Nh, N]: q1 = position, q2 = head, q3 = batch
     int64_t      q1, q2, q3;
     int          tq;
+    int          qvec;  // q rows 16-byte aligned (base and q1/q2/q3 strides)
     const char * k;  // [D, n_kv, Nkv, N / rk3]
     int64_t      k1, k2, k3;
     const char * v;
@@ -124,6 +125,7 @@ struct FaArgs {
     const char * mask;  // F16 [n_kv, >= n_q, mne2, mne3] or nullptr
     int64_t      m1, m2, m3;
     int          mne2, mne3;
+    int          mshared;  // every row of a wave uses one mask row (set by flash_attn_plan)
     char *       y;  // F32 [D, Nh, n_q, N]: y1 = head, y2 = position, y3 = batch
     int64_t      y1, y2, y3;
     int          n_q, n_kv, nh, nkv, nb, rk, rk3;
