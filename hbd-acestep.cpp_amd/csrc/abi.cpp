@@ -684,6 +684,7 @@ static int fa_desc(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v
         a.m3   = (int64_t) mask->nb[3];
         a.mne2 = (int) mask->ne[2];
         a.mne3 = (int) mask->ne[3];
+        a.mvec = aligned(mask->data, 8) && a.m1 % 8 == 0 && a.m2 % 8 == 0 && a.m3 % 8 == 0;
     } else {
         a.mne2 = 1;
         a.mne3 = 1;
@@ -696,10 +697,11 @@ static int fa_desc(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v
         if (y->ne[0] != D || y->ne[1] != q->ne[2] || y->ne[2] != q->ne[1] || y->ne[3] != q->ne[3]) {
             return MI_ERR_SHAPE;
         }
-        a.y  = (char *) y->data;
-        a.y1 = (int64_t) y->nb[1];
-        a.y2 = (int64_t) y->nb[2];
-        a.y3 = (int64_t) y->nb[3];
+        a.y    = (char *) y->data;
+        a.y1   = (int64_t) y->nb[1];
+        a.y2   = (int64_t) y->nb[2];
+        a.y3   = (int64_t) y->nb[3];
+        a.yvec = aligned(y->data, 16) && a.y1 % 16 == 0 && a.y2 % 16 == 0 && a.y3 % 16 == 0;
     }
     flash_attn_plan(a, (int) D);
     if (a.splits == 0) {

@@ -599,6 +599,338 @@ __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core path (prefill: many query rows; F16/BF16 K and V; D = 128).
+// A workgroup of 4 waves owns 128 query rows of one (sequence, KV head) -- the
+// rows are (query position, head) pairs, so the query heads sharing the KV
+// head share the workgroup -- and walks all keys in tiles of 64, K and V
+// double-buffered in LDS (V transposed on the way in). Per wave and tile:
+//   S^T = K Q^T   (v_mfma_f32_32x32x16: keys x 32 rows, q converted to K's
+//                  type as ggml converts it; products exact, fp32 sums)
+//   softmax       (lane-local: a lane holds 32 keys of one row, the other
+//                  half-wave the other 32; one exchange per tile)
+//   O^T += V^T P^T with P split into a high and a low 16-bit part (two
+//                  MFMAs), so P keeps ~16 (BF16) / ~22 (F16) significant bits
+// S^T and O^T put a query row in one lane column, so every row statistic
+// (max, sum, rescale) stays in the lane. Lane layout of the 32x32x16 MFMA
+// (checked on the device): A lane l = row l%32, k = 8*(l/32)+i; B lane l =
+// column l%32, same k; D lane l = column l%32, row 8j + 4*(l/32) + i at 4j+i.
+// Keys whose mask is -inf get p = 0 (their K/V bytes are multiplied, so they
+// must be finite, as every activation the reference feeds here is).
+// ---------------------------------------------------------------------------
+#ifndef MI_FA_MFMA_MIN_ROWS
+#define MI_FA_MFMA_MIN_ROWS 64  // (query position, head) rows per KV head from which the MFMA path is used
+#endif
+
+template <int KT> struct FaM;
+template <> struct FaM<MI_TYPE_BF16> {
+    typedef __bf16 e;
+    typedef __bf16 x8 __attribute__((ext_vector_type(8)));
+    static __device__ __forceinline__ uint16_t bits(float v) { return f32_to_bf16_bits(v); }
+    static __device__ __forceinline__ float    val(uint16_t h) { return __uint_as_float((uint32_t) h << 16); }
+};
+template <> struct FaM<MI_TYPE_F16> {
+    typedef _Float16 e;
+    typedef _Float16 x8 __attribute__((ext_vector_type(8)));
+    static __device__ __forceinline__ uint16_t bits(float v) { return f32_to_f16_bits(v); }
+    static __device__ __forceinline__ float    val(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
+};
+typedef float fa_f32x16 __attribute__((ext_vector_type(16)));
+
+template <int KT>
+__device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, const typename FaM<KT>::x8 & b,
+                                            const fa_f32x16 & c) {
+    if constexpr (KT == MI_TYPE_BF16) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+}
+
+template <int KT, int D>
+__global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
+    using M          = FaM<KT>;
+    using x8         = typename M::x8;
+    constexpr int BQ = 128, BK = 64;
+    constexpr int KS = D * 2 + 16;   // K row stride in LDS (bytes): 16-byte bank spread
+    constexpr int VS = BK * 2 + 16;  // V^T row stride (bytes)
+    constexpr int KC = D * 2 / 16;   // 16-byte chunks per K/V row
+    constexpr int NC = BK * KC / 256;  // chunks per thread per tile (K and V each; even)
+    constexpr int NKS = D / 16;      // k-steps of the S MFMA
+    constexpr int NDB = D / 32;      // 32-row blocks of O^T
+    static_assert(NC * 256 == BK * KC, "tile chunks");
+
+    __shared__ __align__(16) char kt[2][BK * KS];
+    __shared__ __align__(16) char vt[2][D * VS];
+
+    const int      tid  = threadIdx.x;
+    const int      wave = tid >> 6;
+    const int      lane = tid & 63;
+    const int      n    = lane & 31;  // this lane's query row within the wave
+    const int      hh   = lane >> 5;
+    const uint32_t bg   = blockIdx.y;
+    const uint32_t b    = bg / (uint32_t) a.nkv;
+    const uint32_t g    = bg - b * (uint32_t) a.nkv;
+    const int      r    = blockIdx.x * BQ + wave * 32 + n;
+    const bool     rvld = r < a.rows;
+    const int      rc   = rvld ? r : a.rows - 1;
+    const int      iq   = rc / a.rk;
+    const int      h    = (int) g * a.rk + (rc - iq * a.rk);
+    const uint32_t kb   = b / (uint32_t) a.rk3;
+    const char *   kg   = a.k + (int64_t) kb * a.k3 + (int64_t) g * a.k2;
+    const char *   vg   = a.v + (int64_t) kb * a.v3 + (int64_t) g * a.v2;
+    const char *   mrow = a.mask ? a.mask + (int64_t) (b % (uint32_t) a.mne3) * a.m3 + (int64_t) (h % a.mne2) * a.m2 +
+                                      (int64_t) iq * a.m1
+                                 : nullptr;
+
+    // Q^T operands: k-step ks needs q[row][16 ks + 8 hh + i], converted to K's type (RNE)
+    x8 qb[NKS];
+    {
+        const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2 + (int64_t) iq * a.q1;
+        const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const char * p = qp + (size_t) (16 * ks + 8 * hh) * es;
+            float        f[8];
+            if (a.tq == MI_TYPE_F32) {
+                if (a.qvec) {
+                    unpack16<MI_TYPE_F32>(ld16(p), f);
+                    unpack16<MI_TYPE_F32>(ld16(p + 16), f + 4);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        f[e] = ((const float *) p)[e];
+                    }
+                }
+            } else {
+                uint4 v;
+                if (a.qvec) {
+                    v = ld16(p);
+                } else {
+                    const uint16_t * q16 = (const uint16_t *) p;
+                    v = make_uint4((uint32_t) q16[0] | ((uint32_t) q16[1] << 16), (uint32_t) q16[2] | ((uint32_t) q16[3] << 16),
+                                   (uint32_t) q16[4] | ((uint32_t) q16[5] << 16), (uint32_t) q16[6] | ((uint32_t) q16[7] << 16));
+                }
+                if (a.tq == MI_TYPE_BF16) {
+                    unpack16<MI_TYPE_BF16>(v, f);
+                } else {
+                    unpack16<MI_TYPE_F16>(v, f);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                qb[ks][e] = __builtin_bit_cast(typename M::e, M::bits(rvld ? f[e] : 0.0f));
+            }
+        }
+    }
+
+    // K tile loads: chunk c = tid + 256 i -> key c / KC, 16-byte part c % KC (a row
+    // is read by KC consecutive threads). V: thread t loads the same 16-byte part
+    // of two consecutive keys, c = tid + 256 i -> key pair c % 32, part c / 32, and
+    // writes V^T[d][2m..2m+1] as 4-byte words: a wave writes two 128-byte runs of
+    // V^T rows, conflict-free. Keys past the end re-read the last key.
+    uint4 kr[NC], vr[NC];
+    auto load_tile = [&](int t0) {
+        const int nk = a.n_kv - t0 < BK ? a.n_kv - t0 : BK;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c  = tid + 256 * i;
+            const int kk = c / KC < nk ? c / KC : nk - 1;
+            kr[i]        = ld16(kg + (int64_t) (t0 + kk) * a.k1 + (c % KC) * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < NC / 2; ++i) {
+            const int c  = tid + 256 * i;
+            const int m2 = c % 32, pp = c / 32;
+            const int k0 = 2 * m2 < nk ? 2 * m2 : nk - 1;
+            const int k1 = 2 * m2 + 1 < nk ? 2 * m2 + 1 : nk - 1;
+            vr[2 * i]     = ld16(vg + (int64_t) (t0 + k0) * a.v1 + pp * 16);
+            vr[2 * i + 1] = ld16(vg + (int64_t) (t0 + k1) * a.v1 + pp * 16);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = tid + 256 * i;
+            *(uint4 *) (kt[buf] + (c / KC) * KS + (c % KC) * 16) = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NC / 2; ++i) {
+            const int      c  = tid + 256 * i;
+            const int      m2 = c % 32, pp = c / 32;
+            const uint32_t a0[4] = { vr[2 * i].x, vr[2 * i].y, vr[2 * i].z, vr[2 * i].w };
+            const uint32_t a1[4] = { vr[2 * i + 1].x, vr[2 * i + 1].y, vr[2 * i + 1].z, vr[2 * i + 1].w };
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {  // V^T[8 pp + e][2 m2], [2 m2 + 1]
+                const uint32_t lo = (a0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                const uint32_t hi = (a1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                *(uint32_t *) (vt[buf] + (pp * 8 + e) * VS + m2 * 4) = lo | (hi << 16);
+            }
+        }
+    };
+    // mask values of this lane's 32 keys (key 32 bk + 8 j + 4 hh + i: groups of 4),
+    // as 4 fp16 per 8-byte load when the mask rows allow it
+    uint2 mr[2][4];
+    auto load_mask = [&](int t0) {
+#pragma unroll
+        for (int bk = 0; bk < 2; ++bk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k4 = t0 + 32 * bk + 8 * j + 4 * hh;
+                if (a.mvec && k4 + 3 < a.n_kv) {
+                    mr[bk][j] = *(const uint2 *) (mrow + (size_t) k4 * 2);
+                } else {
+                    uint16_t hv[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int kc = k4 + i < a.n_kv ? k4 + i : a.n_kv - 1;
+                        hv[i]        = *(const uint16_t *) (mrow + (size_t) kc * 2);
+                    }
+                    mr[bk][j] = make_uint2((uint32_t) hv[0] | ((uint32_t) hv[1] << 16),
+                                           (uint32_t) hv[2] | ((uint32_t) hv[3] << 16));
+                }
+            }
+        }
+    };
+
+    fa_f32x16 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+        o[db] = fa_f32x16{};
+    }
+    float       mrun = -INFINITY, lrun = 0.0f;
+    const float sl2  = a.scale * 1.4426950408889634f;  // scale * log2(e)
+    const int   ntl  = (a.n_kv + BK - 1) / BK;
+    const bool  hasm = mrow != nullptr;
+    load_tile(0);
+    if (hasm) {
+        load_mask(0);
+    }
+    store_tile(0);
+    __syncthreads();
+    for (int t = 0; t < ntl; ++t) {
+        const int cur = t & 1;
+        const int t0  = t * BK;
+        uint2     mc[2][4];
+#pragma unroll
+        for (int bk = 0; bk < 2; ++bk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                mc[bk][j] = hasm ? mr[bk][j] : make_uint2(0, 0);
+            }
+        }
+        if (t + 1 < ntl) {
+            load_tile(t0 + BK);  // in flight during this tile's math
+            if (hasm) {
+                load_mask(t0 + BK);
+            }
+        }
+        // S^T for keys [32 bk, 32 bk + 32) x this wave's 32 rows (two independent chains)
+        fa_f32x16 sacc[2] = { fa_f32x16{}, fa_f32x16{} };
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+            for (int bk = 0; bk < 2; ++bk) {
+                const x8 kv = *(const x8 *) (kt[cur] + (32 * bk + n) * KS + (16 * ks + 8 * hh) * 2);
+                sacc[bk]    = fa_mma<KT>(kv, qb[ks], sacc[bk]);
+            }
+        }
+        // softmax update (base 2: x = (dot * scale + mask) * log2 e), in place
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int bk = 0; bk < 2; ++bk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int      key = t0 + 32 * bk + 8 * j + 4 * hh + i;
+                    const uint32_t w   = i < 2 ? mc[bk][j].x : mc[bk][j].y;
+                    const float    m   = (float) __builtin_bit_cast(_Float16, (uint16_t) (w >> (16 * (i & 1))));
+                    const bool     off = m == -INFINITY || key >= a.n_kv || !rvld;
+                    const float    v   = off ? -INFINITY : sacc[bk][4 * j + i] * sl2 + m * 1.4426950408889634f;
+                    sacc[bk][4 * j + i] = v;
+                    tmax                = fmaxf(tmax, v);
+                }
+            }
+        }
+        tmax            = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mn  = fmaxf(mrun, tmax);
+        const float alp = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mrun - mn);
+        mrun            = mn;
+        float psum      = 0.0f;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                o[db][q] *= alp;
+            }
+        }
+        // O^T += V^T P^T. MFMA (bk, jj) covers keys 32 bk + 16 jj + [0, 16): k-slot
+        // 8 hh + 4 jh + i is key 32 bk + 16 jj + 8 jh + 4 hh + i (S^T accumulator
+        // 8 jj + 4 jh + i); A lane = V^T row 32 db + n at those keys
+#pragma unroll
+        for (int bk = 0; bk < 2; ++bk) {
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                x8 phi, plo;
+#pragma unroll
+                for (int slot = 0; slot < 8; ++slot) {
+                    const float    v  = sacc[bk][8 * jj + slot];
+                    const float    p  = v == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(v - mn);
+                    const uint16_t hb = M::bits(p);
+                    psum += p;
+                    phi[slot] = __builtin_bit_cast(typename M::e, hb);
+                    plo[slot] = __builtin_bit_cast(typename M::e, M::bits(p - M::val(hb)));
+                }
+                x8 va[NDB];
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const char * vp = vt[cur] + (32 * db + n) * VS + (32 * bk + 16 * jj + 4 * hh) * 2;
+                    const uint2  v0 = *(const uint2 *) vp;         // keys +0..3
+                    const uint2  v1 = *(const uint2 *) (vp + 16);  // keys +8..11
+                    va[db]          = __builtin_bit_cast(x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+                }
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    o[db] = fa_mma<KT>(va[db], phi, o[db]);
+                }
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    o[db] = fa_mma<KT>(va[db], plo, o[db]);
+                }
+            }
+        }
+        lrun = lrun * alp + psum;
+        if (t + 1 < ntl) {
+            store_tile(cur ^ 1);
+        }
+        __syncthreads();
+    }
+    // rows: sum over both half-waves' keys; y[b][iq][h][d], d = 32 db + 8 j + 4 hh + i
+    lrun = lrun + __shfl_xor(lrun, 32, 64);
+    if (rvld) {
+        const float inv = 1.0f / lrun;  // all keys masked: 0 * inf = NaN, as ggml
+        float *     yp  = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) iq * a.y2 + (int64_t) h * a.y1);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = make_float4(o[db][4 * j] * inv, o[db][4 * j + 1] * inv, o[db][4 * j + 2] * inv,
+                                             o[db][4 * j + 3] * inv);
+                float *      d = yp + 32 * db + 8 * j + 4 * hh;
+                if (a.yvec) {
+                    *(float4 *) d = v;
+                } else {
+                    d[0] = v.x;
+                    d[1] = v.y;
+                    d[2] = v.z;
+                    d[3] = v.w;
+                }
+            }
+        }
+    }
+}
+
 // query rows per wave: 4, or 8 for 16-bit and Q8_0 K/V at D = 64 (more would
 // spill registers: each row keeps its output columns and scores in registers)
 static int fa_rb(int rows, int D, int kt) {
@@ -614,6 +946,13 @@ void flash_attn_plan(FaArgs & a, int D) {
     // rows r0..r0+rb-1 of a wave share one query position when n_q == 1 or rb
     // divides Nh/Nkv, and one mask head when the mask does not vary by head
     a.mshared = a.mask != nullptr && a.mne2 == 1 && (a.n_q == 1 || a.rk % rb == 0);
+    a.mfma    = (a.kt == MI_TYPE_F16 || a.kt == MI_TYPE_BF16) && D == 128 && a.rows >= MI_FA_MFMA_MIN_ROWS &&
+             a.n_kv > 0;
+    if (a.mfma) {
+        a.chunk  = a.n_kv;
+        a.splits = 1;  // no workspace
+        return;
+    }
     if (a.n_kv == 0 || a.rows == 0 || a.nb == 0) {  // no keys: one pass that writes NaN rows (0 * (1/0), as ggml)
         a.chunk  = FA_TILE;
         a.splits = 1;
@@ -676,6 +1015,15 @@ static int launch_k(const FaArgs & a, int D, hipStream_t s) {
 
 int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
     if (a.rows == 0 || a.nb == 0 || a.nkv == 0) {
+        return MI_OK;
+    }
+    if (a.mfma) {
+        const dim3 grid((uint32_t) ((a.rows + 127) / 128), (uint32_t) (a.nb * a.nkv));
+        if (kt == MI_TYPE_BF16) {
+            hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_BF16, 128>), grid, dim3(256), 0, s, a);
+        } else {
+            hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_F16, 128>), grid, dim3(256), 0, s, a);
+        }
         return MI_OK;
     }
     switch (kt) {

@@ -126,6 +126,9 @@ struct FaArgs {
     int64_t      m1, m2, m3;
     int          mne2, mne3;
     int          mshared;  // every row of a wave uses one mask row (set by flash_attn_plan)
+    int          mfma;     // the matrix-core prefill path (set by flash_attn_plan)
+    int          yvec;     // y rows 16-byte aligned
+    int          mvec;     // mask rows 8-byte aligned (4 fp16 per load)
     char *       y;  // F32 [D, Nh, n_q, N]: y1 = head, y2 = position, y3 = batch
     int64_t      y1, y2, y3;
     int          n_q, n_kv, nh, nkv, nb, rk, rk3;
