@@ -513,38 +513,44 @@ def attention_bench(steps: int):
         del g, caches, kc, vc, ws
         device.synchronize()
 
-    # DiT self-attention (dit-graph.h:227-231) at the C3 shape: T=6000 frames x 2,
-    # 16/8 heads x 128, bf16 operands read as the block produces them (q, k from
-    # the QK-norm/rope outputs, v a view of the QKV projection rows), the F16
-    # padding mask (all zero: no padding, the full-attention layers) or none
-    S, NB, NHD, NKVD = 6000, 2, 16, 8
-    qd = DTensor.from_numpy(bf16_bits(rng.standard_normal((NB * S, NHD, Dh), dtype=np.float32)), "bf16")
-    kd = DTensor.from_numpy(bf16_bits(rng.standard_normal((NB * S, NKVD, Dh), dtype=np.float32)), "bf16")
-    qkv = DTensor.from_numpy(bf16_bits(rng.standard_normal((NB * S, (NHD + 2 * NKVD) * Dh), dtype=np.float32)),
-                             "bf16")
-    qv = qd.view(NB, S, NHD, Dh).permute(0, 2, 1, 3)
-    kv = kd.view(NB, S, NKVD, Dh).permute(0, 2, 1, 3)
-    vv = qkv.view(NB, S, NHD + 2 * NKVD, Dh)[:, :, NHD + NKVD:].permute(0, 2, 1, 3)
-    yd = DTensor.empty((NB, S, NHD, Dh), "f32")
-    zmask = DTensor.zeros((NB, 1, S, S), "f16")
-    flops = 4.0 * S * S * Dh * NHD * NB
-    for label, mk in (("F16 padding mask (all zero)", zmask), ("no mask", None)):
-        call = lambda: ops.flash_attn_ext(qv, kv, vv, mk, 1.0 / float(np.sqrt(Dh)), out=yd, stream=sh)  # noqa
-        call()
-        st.synchronize()
-        ev = [Event() for _ in range(steps + 1)]
-        ev[0].record(sh)
-        for i in range(steps):
+    # DiT self-attention (dit-graph.h:227-231): S = T / patch_size rows per CFG
+    # element (dit-graph.h:475; S=3000 for T=6000 frames at patch size 2, and
+    # S=6000), x 2, 16/8 heads x 128, bf16 operands read as the block produces
+    # them (q, k from the QK-norm/rope outputs, v a view of the QKV projection
+    # rows), the F16 padding mask (all zero: no padding, the full-attention
+    # layers) or none
+    NB, NHD, NKVD = 2, 16, 8
+    for S in (3000, 6000):
+        qd = DTensor.from_numpy(bf16_bits(rng.standard_normal((NB * S, NHD, Dh), dtype=np.float32)), "bf16")
+        kd = DTensor.from_numpy(bf16_bits(rng.standard_normal((NB * S, NKVD, Dh), dtype=np.float32)), "bf16")
+        qkv = DTensor.from_numpy(bf16_bits(rng.standard_normal((NB * S, (NHD + 2 * NKVD) * Dh), dtype=np.float32)),
+                                 "bf16")
+        qv = qd.view(NB, S, NHD, Dh).permute(0, 2, 1, 3)
+        kv = kd.view(NB, S, NKVD, Dh).permute(0, 2, 1, 3)
+        vv = qkv.view(NB, S, NHD + 2 * NKVD, Dh)[:, :, NHD + NKVD:].permute(0, 2, 1, 3)
+        yd = DTensor.empty((NB, S, NHD, Dh), "f32")
+        zmask = DTensor.zeros((NB, 1, S, S), "f16")
+        flops = 4.0 * S * S * Dh * NHD * NB
+        wsd = DTensor.empty((max(ops.flash_attn_workspace(qv, kv, vv), 1),), "u8")
+        for label, mk in (("F16 padding mask (all zero)", zmask), ("no mask", None)):
+            call = lambda: ops.flash_attn_ext(qv, kv, vv, mk, 1.0 / float(np.sqrt(Dh)), out=yd,  # noqa
+                                              workspace=wsd, stream=sh)
             call()
-            ev[i + 1].record(sh)
-        st.synchronize()
-        us = 1000.0 * ev[0].elapsed_ms(ev[steps]) / steps
-        tf = flops / (us * 1e-6) / 1e12
-        print(json.dumps({"config": f"C3 DiT self-attention, bf16 q/k/v views, T={S} x {NB}, {NHD}/{NKVD} heads x "
-                                    f"{Dh}, {label}",
-                          "us_per_call": round(us, 2), "TFLOP/s": round(tf, 1), "flop_per_call": flops,
-                          "frac_of_bf16_dense": round(tf / 2500.0, 3)}), flush=True)
-
+            st.synchronize()
+            ev = [Event() for _ in range(steps + 1)]
+            ev[0].record(sh)
+            for i in range(steps):
+                call()
+                ev[i + 1].record(sh)
+            st.synchronize()
+            us = 1000.0 * ev[0].elapsed_ms(ev[steps]) / steps
+            tf = flops / (us * 1e-6) / 1e12
+            print(json.dumps({"config": f"DiT self-attention, bf16 q/k/v views, S={S} x {NB}, {NHD}/{NKVD} heads "
+                                        f"x {Dh}, {label}",
+                              "us_per_call": round(us, 2), "TFLOP/s": round(tf, 1), "flop_per_call": flops,
+                              "frac_of_bf16_dense": round(tf / 2500.0, 3)}), flush=True)
+        del qd, kd, qkv, qv, kv, vv, yd, zmask, wsd
+        device.synchronize()
 
 def main():
     ap = argparse.ArgumentParser()

@@ -742,7 +742,8 @@ int mi_flash_attn_ext(const mi_tensor * q, const mi_tensor * k, const mi_tensor 
     if (!aligned(workspace, 16)) {
         return MI_ERR_ALIGN;
     }
-    a.ws = (float *) workspace;
+    a.ws   = (float *) workspace;
+    a.msum = a.mfma && a.mask ? (uint8_t *) workspace : nullptr;
     return finish(launch_flash_attn(a, k->type, (int) q->ne[0], (hipStream_t) stream));
 }
 

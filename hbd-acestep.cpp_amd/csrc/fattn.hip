@@ -647,6 +647,36 @@ __device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, cons
     }
 }
 
+// Mask summary for the matrix-core path, one wave per (mask batch and head,
+// group of 16 query positions, 64-key tile): lane = key, 16 coalesced rows.
+// The attention kernel then loads no mask values for a tile whose values are
+// all 0 and skips the math of a tile whose keys are all -inf for its rows.
+__global__ void __launch_bounds__(64) k_fa_mask_summary(const FaArgs a) {
+    const int      lane = threadIdx.x;
+    const uint32_t tile = blockIdx.x, grp = blockIdx.y, mh = blockIdx.z;
+    const uint32_t m3 = mh / (uint32_t) a.mne2, m2 = mh - m3 * (uint32_t) a.mne2;
+    const int      key  = (int) tile * 64 + lane;
+    const char *   mp   = a.mask + (int64_t) m3 * a.m3 + (int64_t) m2 * a.m2 + (int64_t) (key < a.n_kv ? key : 0) * 2;
+    uint16_t       hv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int iq = (int) grp * 16 + r;
+        hv[r]        = *(const uint16_t *) (mp + (int64_t) (iq < a.n_q ? iq : 0) * a.m1);
+    }
+    bool live = false, nz = false;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const bool ok = key < a.n_kv && (int) grp * 16 + r < a.n_q;
+        live          = live || (ok && hv[r] != 0xFC00u);    // not -inf
+        nz            = nz || (ok && (hv[r] & 0x7FFFu) != 0);  // not +-0
+    }
+    const uint64_t lv = __builtin_amdgcn_ballot_w64(live), nv = __builtin_amdgcn_ballot_w64(nz);
+    if (lane == 0) {
+        const int ntl = (a.n_kv + 63) / 64;
+        a.msum[((int64_t) mh * a.ngq + grp) * ntl + tile] = (uint8_t) ((lv ? 1 : 0) | (nv ? 2 : 0));
+    }
+}
+
 template <int KT, int D>
 __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
     using M          = FaM<KT>;
@@ -801,9 +831,18 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
     float       mrun = -INFINITY, lrun = 0.0f;
     const float sl2  = a.scale * 1.4426950408889634f;  // scale * log2(e)
     const int   ntl  = (a.n_kv + BK - 1) / BK;
-    const bool  hasm = mrow != nullptr;
+    // per tile, from the mask summary of this lane's row (two tiles ahead):
+    // does the wave read the tile's mask values, does it have a live key at all
+    const uint8_t * sp =
+        a.msum ? a.msum + (((int64_t) (b % (uint32_t) a.mne3) * a.mne2 + h % a.mne2) * a.ngq + iq / 16) * ntl
+               : nullptr;
+    auto flag = [&](int t) -> int { return t < ntl ? (sp ? (int) sp[t] : 1) : 0; };
+    auto wave_mask = [&](int f) { return __builtin_amdgcn_ballot_w64(rvld && (f & 2)) != 0; };
+    auto wave_live = [&](int f) { return __builtin_amdgcn_ballot_w64(rvld && (f & 1)) != 0; };
+    int  fcur = flag(0), fnext = flag(1);
+    bool mcur = wave_mask(fcur);
     load_tile(0);
-    if (hasm) {
+    if (mcur) {
         load_mask(0);
     }
     store_tile(0);
@@ -816,15 +855,18 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
         for (int bk = 0; bk < 2; ++bk) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                mc[bk][j] = hasm ? mr[bk][j] : make_uint2(0, 0);
+                mc[bk][j] = mcur ? mr[bk][j] : make_uint2(0, 0);
             }
         }
+        const int  fnn   = flag(t + 2);
+        const bool mnext = wave_mask(fnext);
         if (t + 1 < ntl) {
             load_tile(t0 + BK);  // in flight during this tile's math
-            if (hasm) {
+            if (mnext) {
                 load_mask(t0 + BK);
             }
         }
+        if (wave_live(fcur)) {
         // S^T for keys [32 bk, 32 bk + 32) x this wave's 32 rows (two independent chains)
         fa_f32x16 sacc[2] = { fa_f32x16{}, fa_f32x16{} };
 #pragma unroll
@@ -835,36 +877,56 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
                 sacc[bk]    = fa_mma<KT>(kv, qb[ks], sacc[bk]);
             }
         }
-        // softmax update (base 2: x = (dot * scale + mask) * log2 e), in place
-        float tmax = -INFINITY;
+        // softmax update (base 2: x = (dot * scale + mask) * log2 e), in place. A
+        // full tile with no mask values and every row valid takes the short form.
+        float      tmax  = -INFINITY;
+        const bool clean = !mcur && t0 + BK <= a.n_kv && blockIdx.x * BQ + BQ <= a.rows;
+        if (clean) {
 #pragma unroll
-        for (int bk = 0; bk < 2; ++bk) {
+            for (int bk = 0; bk < 2; ++bk) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+                for (int q = 0; q < 16; ++q) {
+                    sacc[bk][q] *= sl2;
+                    tmax = fmaxf(tmax, sacc[bk][q]);
+                }
+            }
+        } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int      key = t0 + 32 * bk + 8 * j + 4 * hh + i;
-                    const uint32_t w   = i < 2 ? mc[bk][j].x : mc[bk][j].y;
-                    const float    m   = (float) __builtin_bit_cast(_Float16, (uint16_t) (w >> (16 * (i & 1))));
-                    const bool     off = m == -INFINITY || key >= a.n_kv || !rvld;
-                    const float    v   = off ? -INFINITY : sacc[bk][4 * j + i] * sl2 + m * 1.4426950408889634f;
-                    sacc[bk][4 * j + i] = v;
-                    tmax                = fmaxf(tmax, v);
+            for (int bk = 0; bk < 2; ++bk) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int      key = t0 + 32 * bk + 8 * j + 4 * hh + i;
+                        const uint32_t w   = i < 2 ? mc[bk][j].x : mc[bk][j].y;
+                        const float    m = (float) __builtin_bit_cast(_Float16, (uint16_t) (w >> (16 * (i & 1))));
+                        const bool     off = m == -INFINITY || key >= a.n_kv || !rvld;
+                        const float    v = off ? -INFINITY : sacc[bk][4 * j + i] * sl2 + m * 1.4426950408889634f;
+                        sacc[bk][4 * j + i] = v;
+                        tmax                = fmaxf(tmax, v);
+                    }
                 }
             }
         }
-        tmax            = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mn  = fmaxf(mrun, tmax);
-        const float alp = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mrun - mn);
-        mrun            = mn;
-        float psum      = 0.0f;
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        // Lazy rescale: p = exp2(x - mrun) against a reference max that moves only
+        // when some row's max grows past it by more than 8 (p <= 2^8 stays exact
+        // enough in fp32 and in the 16-bit parts); O and l are rescaled then only.
+        if (__builtin_amdgcn_ballot_w64(tmax > mrun + 8.0f) != 0) {
+            const float mn  = fmaxf(mrun, tmax);
+            const float alp = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mrun - mn);
+            mrun            = mn;
+            lrun *= alp;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
+            for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                o[db][q] *= alp;
+                for (int q = 0; q < 16; ++q) {
+                    o[db][q] *= alp;
+                }
             }
         }
+        const float mn   = mrun;
+        float       psum = 0.0f;
         // O^T += V^T P^T. MFMA (bk, jj) covers keys 32 bk + 16 jj + [0, 16): k-slot
         // 8 hh + 4 jh + i is key 32 bk + 16 jj + 8 jh + 4 hh + i (S^T accumulator
         // 8 jj + 4 jh + i); A lane = V^T row 32 db + n at those keys
@@ -900,10 +962,14 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
                 }
             }
         }
-        lrun = lrun * alp + psum;
+        lrun += psum;
+        }  // wave_live
         if (t + 1 < ntl) {
             store_tile(cur ^ 1);
         }
+        fcur  = fnext;
+        fnext = fnn;
+        mcur  = mnext;
         __syncthreads();
     }
     // rows: sum over both half-waves' keys; y[b][iq][h][d], d = 32 db + 8 j + 4 hh + i
@@ -950,7 +1016,8 @@ void flash_attn_plan(FaArgs & a, int D) {
              a.n_kv > 0;
     if (a.mfma) {
         a.chunk  = a.n_kv;
-        a.splits = 1;  // no workspace
+        a.splits = 1;
+        a.ngq    = (a.n_q + 15) / 16;
         return;
     }
     if (a.n_kv == 0 || a.rows == 0 || a.nb == 0) {  // no keys: one pass that writes NaN rows (0 * (1/0), as ggml)
@@ -973,6 +1040,9 @@ void flash_attn_plan(FaArgs & a, int D) {
 }
 
 size_t flash_attn_workspace(const FaArgs & a, int D) {
+    if (a.mfma) {  // the mask summary, sized for the largest mask a call may pass (one per batch and head)
+        return (size_t) a.nb * a.nh * a.ngq * ((a.n_kv + 63) / 64);
+    }
     return a.splits > 1 ? (size_t) a.splits * a.nb * a.nkv * a.rows * (D + 2) * sizeof(float) : 0;
 }
 
@@ -1018,6 +1088,11 @@ int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
         return MI_OK;
     }
     if (a.mfma) {
+        if (a.msum != nullptr) {
+            hipLaunchKernelGGL(k_fa_mask_summary, dim3((uint32_t) ((a.n_kv + 63) / 64), (uint32_t) a.ngq,
+                                                       (uint32_t) (a.mne3 * a.mne2)),
+                               dim3(64), 0, s, a);
+        }
         const dim3 grid((uint32_t) ((a.rows + 127) / 128), (uint32_t) (a.nb * a.nkv));
         if (kt == MI_TYPE_BF16) {
             hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_BF16, 128>), grid, dim3(256), 0, s, a);

@@ -129,6 +129,9 @@ struct FaArgs {
     int          mfma;     // the matrix-core prefill path (set by flash_attn_plan)
     int          yvec;     // y rows 16-byte aligned
     int          mvec;     // mask rows 8-byte aligned (4 fp16 per load)
+    int          ngq;      // matrix-core path: groups of 16 query positions in the mask summary
+    uint8_t *    msum;     // matrix-core path with a mask: per (mask batch, mask head, group, key tile)
+                           // bit 0 = some key not -inf, bit 1 = some value not 0 (in the workspace)
     char *       y;  // F32 [D, Nh, n_q, N]: y1 = head, y2 = position, y3 = batch
     int64_t      y1, y2, y3;
     int          n_q, n_kv, nh, nkv, nb, rk, rk3;
