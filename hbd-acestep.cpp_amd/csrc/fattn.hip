@@ -677,8 +677,22 @@ __global__ void __launch_bounds__(64) k_fa_mask_summary(const FaArgs a) {
     }
 }
 
+// raw buffer loads (32-bit offsets, range-checked: reads past the end return 0)
+typedef __amdgpu_buffer_rsrc_t fa_rsrc;
+__device__ __forceinline__ fa_rsrc fa_make_rsrc(const char * base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *) base, (short) 0, (int) bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 fa_bld16(fa_rsrc r, uint32_t voff, uint32_t soff) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int) voff, (int) soff, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+#ifndef MI_FA_MFMA_WPE
+#define MI_FA_MFMA_WPE 2  // waves per SIMD: 2 caps registers at 256 (two workgroups per CU, 144 KB of LDS)
+#endif
 template <int KT, int D>
-__global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MI_FA_MFMA_WPE, MI_FA_MFMA_WPE)))
+k_fa_mfma(const FaArgs a) {
     using M          = FaM<KT>;
     using x8         = typename M::x8;
     constexpr int BQ = 128, BK = 64;
@@ -758,24 +772,28 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
     // is read by KC consecutive threads). V: thread t loads the same 16-byte part
     // of two consecutive keys, c = tid + 256 i -> key pair c % 32, part c / 32, and
     // writes V^T[d][2m..2m+1] as 4-byte words: a wave writes two 128-byte runs of
-    // V^T rows, conflict-free. Keys past the end re-read the last key.
-    uint4 kr[NC], vr[NC];
+    // V^T rows, conflict-free. Buffer loads: a fixed 32-bit offset per thread plus
+    // the tile's uniform offset (the planner keeps the key range below 4 GB).
+    constexpr int KR = 256 / KC;  // K rows per load round
+    static_assert(KC <= 32 && 256 % KC == 0, "tile chunks");
+    uint4          kr[NC], vr[NC];
+    const uint32_t ko0 = (uint32_t) (tid / KC) * (uint32_t) a.k1 + (uint32_t) (tid % KC) * 16;
+    const uint32_t vo0 = (uint32_t) (2 * (tid % 32)) * (uint32_t) a.v1 + (uint32_t) (tid / 32) * 16;
+    const uint32_t vo1 = vo0 + (uint32_t) a.v1;
+    // buffers end at the last key's row: keys past the end read as zeros
+    const fa_rsrc  krs = fa_make_rsrc(kg, (uint32_t) ((int64_t) (a.n_kv - 1) * a.k1 + D * 2));
+    const fa_rsrc  vrs = fa_make_rsrc(vg, (uint32_t) ((int64_t) (a.n_kv - 1) * a.v1 + D * 2));
     auto load_tile = [&](int t0) {
-        const int nk = a.n_kv - t0 < BK ? a.n_kv - t0 : BK;
+        const uint32_t ks0 = (uint32_t) t0 * (uint32_t) a.k1;
+        const uint32_t vs0 = (uint32_t) t0 * (uint32_t) a.v1;
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
-            const int c  = tid + 256 * i;
-            const int kk = c / KC < nk ? c / KC : nk - 1;
-            kr[i]        = ld16(kg + (int64_t) (t0 + kk) * a.k1 + (c % KC) * 16);
+            kr[i] = fa_bld16(krs, ko0, ks0 + (uint32_t) (KR * i) * (uint32_t) a.k1);
         }
 #pragma unroll
-        for (int i = 0; i < NC / 2; ++i) {
-            const int c  = tid + 256 * i;
-            const int m2 = c % 32, pp = c / 32;
-            const int k0 = 2 * m2 < nk ? 2 * m2 : nk - 1;
-            const int k1 = 2 * m2 + 1 < nk ? 2 * m2 + 1 : nk - 1;
-            vr[2 * i]     = ld16(vg + (int64_t) (t0 + k0) * a.v1 + pp * 16);
-            vr[2 * i + 1] = ld16(vg + (int64_t) (t0 + k1) * a.v1 + pp * 16);
+        for (int i = 0; i < NC / 2; ++i) {  // part c / 32 = tid / 32 + 8 i
+            vr[2 * i]     = fa_bld16(vrs, vo0 + 128 * i, vs0);
+            vr[2 * i + 1] = fa_bld16(vrs, vo1 + 128 * i, vs0);
         }
     };
     auto store_tile = [&](int buf) {
@@ -798,10 +816,9 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
             }
         }
     };
-    // mask values of this lane's 32 keys (key 32 bk + 8 j + 4 hh + i: groups of 4),
-    // as 4 fp16 per 8-byte load when the mask rows allow it
-    uint2 mr[2][4];
-    auto load_mask = [&](int t0) {
+    // mask values of this lane's 32 keys of a tile (key 32 bk + 8 j + 4 hh + i:
+    // groups of 4), as 4 fp16 per 8-byte load when the mask rows allow it
+    auto load_mask = [&](int t0, uint2 (&mr)[2][4]) {
 #pragma unroll
         for (int bk = 0; bk < 2; ++bk) {
 #pragma unroll
@@ -831,42 +848,33 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
     float       mrun = -INFINITY, lrun = 0.0f;
     const float sl2  = a.scale * 1.4426950408889634f;  // scale * log2(e)
     const int   ntl  = (a.n_kv + BK - 1) / BK;
-    // per tile, from the mask summary of this lane's row (two tiles ahead):
-    // does the wave read the tile's mask values, does it have a live key at all
+    const bool  allr = (int) (blockIdx.x * BQ + BQ) <= a.rows;  // every row of the workgroup valid
+    // per tile, from the mask summary of this lane's row (one tile ahead): does
+    // the wave read the tile's mask values, does it have a live key at all
     const uint8_t * sp =
         a.msum ? a.msum + (((int64_t) (b % (uint32_t) a.mne3) * a.mne2 + h % a.mne2) * a.ngq + iq / 16) * ntl
                : nullptr;
     auto flag = [&](int t) -> int { return t < ntl ? (sp ? (int) sp[t] : 1) : 0; };
-    auto wave_mask = [&](int f) { return __builtin_amdgcn_ballot_w64(rvld && (f & 2)) != 0; };
-    auto wave_live = [&](int f) { return __builtin_amdgcn_ballot_w64(rvld && (f & 1)) != 0; };
-    int  fcur = flag(0), fnext = flag(1);
-    bool mcur = wave_mask(fcur);
+    int  fcur = flag(0);
     load_tile(0);
-    if (mcur) {
-        load_mask(0);
-    }
     store_tile(0);
     __syncthreads();
     for (int t = 0; t < ntl; ++t) {
-        const int cur = t & 1;
-        const int t0  = t * BK;
-        uint2     mc[2][4];
-#pragma unroll
-        for (int bk = 0; bk < 2; ++bk) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                mc[bk][j] = mcur ? mr[bk][j] : make_uint2(0, 0);
-            }
-        }
-        const int  fnn   = flag(t + 2);
-        const bool mnext = wave_mask(fnext);
+        const int cur   = t & 1;
+        const int t0    = t * BK;
+        const int fnext = flag(t + 1);
         if (t + 1 < ntl) {
             load_tile(t0 + BK);  // in flight during this tile's math
-            if (mnext) {
-                load_mask(t0 + BK);
-            }
         }
-        if (wave_live(fcur)) {
+        if (__builtin_amdgcn_ballot_w64(rvld && (fcur & 1)) != 0) {  // some row of the wave has a live key
+        const bool mload = __builtin_amdgcn_ballot_w64(rvld && (fcur & 2)) != 0;
+        // general form: mask values, -inf keys, keys past the end, invalid rows
+        // or a negative scale; else the tile is clean
+        const bool gen = mload || t0 + BK > a.n_kv || !allr || !(sl2 >= 0.0f);
+        uint2      mr[2][4];
+        if (mload) {
+            load_mask(t0, mr);  // in flight during the S MFMAs
+        }
         // S^T for keys [32 bk, 32 bk + 32) x this wave's 32 rows (two independent chains)
         fa_f32x16 sacc[2] = { fa_f32x16{}, fa_f32x16{} };
 #pragma unroll
@@ -877,20 +885,13 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
                 sacc[bk]    = fa_mma<KT>(kv, qb[ks], sacc[bk]);
             }
         }
-        // softmax update (base 2: x = (dot * scale + mask) * log2 e), in place. A
-        // full tile with no mask values and every row valid takes the short form.
-        float      tmax  = -INFINITY;
-        const bool clean = !mcur && t0 + BK <= a.n_kv && blockIdx.x * BQ + BQ <= a.rows;
-        if (clean) {
-#pragma unroll
-            for (int bk = 0; bk < 2; ++bk) {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    sacc[bk][q] *= sl2;
-                    tmax = fmaxf(tmax, sacc[bk][q]);
-                }
-            }
-        } else {
+        // softmax in base 2, x = (dot * scale + mask) * log2 e. General form: x is
+        // written over the scores and p = exp2(x - m). Clean form (every value
+        // finite, scale >= 0): the row max of the raw dots times scale * log2 e is
+        // the max of x, and p = exp2(dot * scale * log2 e - m) in one fma.
+        float tmax = -INFINITY, c1 = sl2;
+        if (gen) {
+            c1 = 1.0f;
 #pragma unroll
             for (int bk = 0; bk < 2; ++bk) {
 #pragma unroll
@@ -898,7 +899,7 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int      key = t0 + 32 * bk + 8 * j + 4 * hh + i;
-                        const uint32_t w   = i < 2 ? mc[bk][j].x : mc[bk][j].y;
+                        const uint32_t w   = mload ? (i < 2 ? mr[bk][j].x : mr[bk][j].y) : 0u;
                         const float    m = (float) __builtin_bit_cast(_Float16, (uint16_t) (w >> (16 * (i & 1))));
                         const bool     off = m == -INFINITY || key >= a.n_kv || !rvld;
                         const float    v = off ? -INFINITY : sacc[bk][4 * j + i] * sl2 + m * 1.4426950408889634f;
@@ -907,12 +908,22 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
                     }
                 }
             }
+        } else {
+#pragma unroll
+            for (int bk = 0; bk < 2; ++bk) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    tmax = fmaxf(tmax, sacc[bk][q]);
+                }
+            }
+            tmax *= sl2;
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         // Lazy rescale: p = exp2(x - mrun) against a reference max that moves only
         // when some row's max grows past it by more than 8 (p <= 2^8 stays exact
         // enough in fp32 and in the 16-bit parts); O and l are rescaled then only.
         if (__builtin_amdgcn_ballot_w64(tmax > mrun + 8.0f) != 0) {
+            __asm__ volatile("");  // a real branch: the 64 multiplies are not speculated
             const float mn  = fmaxf(mrun, tmax);
             const float alp = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mrun - mn);
             mrun            = mn;
@@ -925,7 +936,8 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
                 }
             }
         }
-        const float mn   = mrun;
+        // a row with no live key yet has mrun = -inf and only -inf values: p = 0
+        const float nmn  = mrun == -INFINITY ? 0.0f : -mrun;
         float       psum = 0.0f;
         // O^T += V^T P^T. MFMA (bk, jj) covers keys 32 bk + 16 jj + [0, 16): k-slot
         // 8 hh + 4 jh + i is key 32 bk + 16 jj + 8 jh + 4 hh + i (S^T accumulator
@@ -937,8 +949,7 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
                 x8 phi, plo;
 #pragma unroll
                 for (int slot = 0; slot < 8; ++slot) {
-                    const float    v  = sacc[bk][8 * jj + slot];
-                    const float    p  = v == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(v - mn);
+                    const float    p  = __builtin_amdgcn_exp2f(fmaf(sacc[bk][8 * jj + slot], c1, nmn));
                     const uint16_t hb = M::bits(p);
                     psum += p;
                     phi[slot] = __builtin_bit_cast(typename M::e, hb);
@@ -963,13 +974,11 @@ __global__ void __launch_bounds__(256) k_fa_mfma(const FaArgs a) {
             }
         }
         lrun += psum;
-        }  // wave_live
+        }  // live
         if (t + 1 < ntl) {
             store_tile(cur ^ 1);
         }
-        fcur  = fnext;
-        fnext = fnn;
-        mcur  = mnext;
+        fcur = fnext;
         __syncthreads();
     }
     // rows: sum over both half-waves' keys; y[b][iq][h][d], d = 32 db + 8 j + 4 hh + i
@@ -1013,7 +1022,7 @@ void flash_attn_plan(FaArgs & a, int D) {
     // divides Nh/Nkv, and one mask head when the mask does not vary by head
     a.mshared = a.mask != nullptr && a.mne2 == 1 && (a.n_q == 1 || a.rk % rb == 0);
     a.mfma    = (a.kt == MI_TYPE_F16 || a.kt == MI_TYPE_BF16) && D == 128 && a.rows >= MI_FA_MFMA_MIN_ROWS &&
-             a.n_kv > 0;
+             a.n_kv > 0 && (uint64_t) (a.n_kv + 64) * (uint64_t) (a.k1 > a.v1 ? a.k1 : a.v1) < (1ull << 32);
     if (a.mfma) {
         a.chunk  = a.n_kv;
         a.splits = 1;
