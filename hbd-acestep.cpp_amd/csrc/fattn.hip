@@ -648,27 +648,43 @@ __device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, cons
 }
 
 // Mask summary for the matrix-core path, one wave per (mask batch and head,
-// group of 16 query positions, 64-key tile): lane = key, 16 coalesced rows.
+// group of 16 query positions, 64-key tile): lane = 4 keys (4 * (lane % 16))
+// of rows lane / 16 + 4 i, as 8-byte loads when the mask rows allow it.
 // The attention kernel then loads no mask values for a tile whose values are
 // all 0 and skips the math of a tile whose keys are all -inf for its rows.
 __global__ void __launch_bounds__(64) k_fa_mask_summary(const FaArgs a) {
     const int      lane = threadIdx.x;
     const uint32_t tile = blockIdx.x, grp = blockIdx.y, mh = blockIdx.z;
     const uint32_t m3 = mh / (uint32_t) a.mne2, m2 = mh - m3 * (uint32_t) a.mne2;
-    const int      key  = (int) tile * 64 + lane;
-    const char *   mp   = a.mask + (int64_t) m3 * a.m3 + (int64_t) m2 * a.m2 + (int64_t) (key < a.n_kv ? key : 0) * 2;
-    uint16_t       hv[16];
+    const int      k4 = (int) tile * 64 + 4 * (lane & 15);
+    const char *   mp = a.mask + (int64_t) m3 * a.m3 + (int64_t) m2 * a.m2;
+    bool           live = false, nz = false;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int iq = (int) grp * 16 + r;
-        hv[r]        = *(const uint16_t *) (mp + (int64_t) (iq < a.n_q ? iq : 0) * a.m1);
-    }
-    bool live = false, nz = false;
+    for (int i = 0; i < 4; ++i) {
+        const int iq = (int) grp * 16 + (lane >> 4) + 4 * i;
+        if (iq >= a.n_q || k4 >= a.n_kv) {
+            continue;
+        }
+        const char * rp = mp + (int64_t) iq * a.m1;
+        uint16_t     hv[4];
+        if (a.mvec && k4 + 3 < a.n_kv) {
+            const uint2 w = *(const uint2 *) (rp + (int64_t) k4 * 2);
+            hv[0]         = (uint16_t) w.x;
+            hv[1]         = (uint16_t) (w.x >> 16);
+            hv[2]         = (uint16_t) w.y;
+            hv[3]         = (uint16_t) (w.y >> 16);
+        } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const bool ok = key < a.n_kv && (int) grp * 16 + r < a.n_q;
-        live          = live || (ok && hv[r] != 0xFC00u);    // not -inf
-        nz            = nz || (ok && (hv[r] & 0x7FFFu) != 0);  // not +-0
+            for (int e = 0; e < 4; ++e) {
+                hv[e] = *(const uint16_t *) (rp + (int64_t) (k4 + e < a.n_kv ? k4 + e : k4) * 2);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool ok = k4 + e < a.n_kv;
+            live          = live || (ok && hv[e] != 0xFC00u);    // not -inf
+            nz            = nz || (ok && (hv[e] & 0x7FFFu) != 0);  // not +-0
+        }
     }
     const uint64_t lv = __builtin_amdgcn_ballot_w64(live), nv = __builtin_amdgcn_ballot_w64(nz);
     if (lane == 0) {
