@@ -552,6 +552,67 @@ def attention_bench(steps: int):
         del qd, kd, qkv, qv, kv, vv, yd, zmask, wsd
         device.synchronize()
 
+# ---------------------------------------------------------------------------
+# Q8_0 matrix-vector products (reported with --gemv): ggml_mul_mat with Q8_0
+# weights at the Qwen3-4B batch-8 decode shape (qwen3-lm.h:639-651, 729, 737,
+# 755): the fused QKV, O, fused gate/up and down projections of one layer, and
+# the LM head over the 151669-row token table. Weights are repacked once (the
+# load-time layout); each call quantizes the 8 rows of x and runs the product.
+# ---------------------------------------------------------------------------
+def gemv_bench(steps: int):
+    from acestep_ops import device, ops
+    from acestep_ops.device import DTensor, Event, Graph, Stream
+
+    H, I, NH_, NKV_, Dh, V, M = 2560, 9728, 32, 8, 128, 151669, 8
+    shapes = [("QKV", H, (NH_ + 2 * NKV_) * Dh), ("O", NH_ * Dh, H), ("gate_up", H, 2 * I), ("down", I, H),
+              ("lm_head", H, V)]
+    rng = np.random.default_rng(13)
+    st = Stream()
+    sh = st.handle
+    layer_us, layer_bytes = 0.0, 0
+    for name, k, n in shapes:
+        nbk = k // 32
+        blocks = np.empty((n, nbk, 34), np.uint8)
+        blocks[:, :, 2:] = rng.integers(-127, 128, (n, nbk, 32), dtype=np.int8).view(np.uint8)
+        d = (rng.uniform(0.5, 1.0, (n, nbk)) * 2e-3).astype(np.float16).view(np.uint8).reshape(n, nbk, 2)
+        blocks[:, :, :2] = d
+        wa = ops.Q8(DTensor.from_numpy(blocks.reshape(n, nbk * 34)))
+        wr = ops.q8_0_repack(wa, stream=sh)
+        st.synchronize()
+        del wa, blocks
+        x = DTensor.from_numpy(rng.standard_normal((M, k), dtype=np.float32))
+        y = DTensor.empty((M, n), "f32")
+        ws = DTensor.empty((max(ops.mul_mat_q8_0_workspace(wr, x), 1),), "u8")
+        # `steps` calls back to back in one graph (as a decode step issues them),
+        # replayed once after a warm-up replay: the GPU time, not the host's
+        g = Graph()
+        with g.capture(st):
+            for _ in range(steps):
+                ops.mul_mat_q8_0(wr, x, out=y, workspace=ws, stream=sh)
+        g.launch()
+        st.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(sh)
+        g.launch()
+        e1.record(sh)
+        e1.synchronize()
+        us = 1000.0 * e0.elapsed_ms(e1) / steps
+        nbytes = n * nbk * 34 + M * k * 4 + M * n * 4
+        gbs = nbytes / (us * 1e-6) / 1e9
+        if name != "lm_head":
+            layer_us += us
+            layer_bytes += nbytes
+        print(json.dumps({"config": f"Q8_0 mul_mat {name}, Qwen3-4B decode batch {M}: k={k}, n={n}",
+                          "us_per_call": round(us, 2), "bytes_per_call": nbytes,
+                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}), flush=True)
+        del g, wr, x, y, ws
+        device.synchronize()
+    gbs = layer_bytes / (layer_us * 1e-6) / 1e9
+    print(json.dumps({"config": f"Q8_0 mul_mat, one Qwen3-4B layer's four projections at batch {M}",
+                      "us_per_layer": round(layer_us, 2), "bytes_per_layer": layer_bytes, "GB/s": round(gbs, 1),
+                      "frac": round(gbs / HBM_PEAK_GBS, 3)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -566,6 +627,8 @@ def main():
                     help="time the Qwen3 layer op chains at the C1/C2/C4/C5 shapes instead (one JSON line each)")
     ap.add_argument("--attention", action="store_true",
                     help="time flash attention over the KV cache at the C2 decode shape (one JSON line per cache type)")
+    ap.add_argument("--gemv", action="store_true",
+                    help="time the Q8_0 mul_mat of the Qwen3-4B decode projections and LM head at batch 8")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); every op of the path is "
@@ -584,6 +647,9 @@ def main():
         return
     if args.attention:
         attention_bench(args.steps)
+        return
+    if args.gemv:
+        gemv_bench(args.steps)
         return
     kb = block_bytes(ROWS, fused=True)
     kb_u = block_bytes(ROWS, fused=False)

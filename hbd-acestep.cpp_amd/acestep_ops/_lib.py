@@ -88,6 +88,10 @@ PROTOTYPES = {
     "mi_timestep_embedding": [_TP, _I, _I, _TP, _VP],
     "mi_flash_attn_ext_workspace": [_TP, _TP, _TP, ctypes.POINTER(ctypes.c_size_t)],
     "mi_flash_attn_ext": [_TP, _TP, _TP, _TP, _F, _F, _F, _TP, _VP, ctypes.c_size_t, _VP],
+    "mi_q8_0_repack_bytes": [ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)],
+    "mi_q8_0_repack": [_TP, _VP, ctypes.c_size_t, _VP],
+    "mi_mul_mat_q8_0_workspace": [ctypes.c_int64, ctypes.c_int64, _TP, ctypes.POINTER(ctypes.c_size_t)],
+    "mi_mul_mat_q8_0": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, _TP, _VP, ctypes.c_size_t, _VP],
     "mi_dit_block_ops": [ctypes.POINTER(MiDitBlockIO), _VP],
     "mi_qwen3_layer_ops": [ctypes.POINTER(MiQwen3LayerIO), _VP],
 }

@@ -228,3 +228,40 @@ def flash_attn_ext(q, k, v, mask, scale: float, out=None, workspace=None, max_bi
     _lib.call("mi_flash_attn_ext", _p(q), _p(k), _p(v), _p(mask), scale, max_bias, logit_softcap, _p(y), wp, wn,
               _s(stream))
     return y
+
+
+@dataclass
+class Q8R64:
+    """A Q8_0 weight [k, n] repacked by mi_q8_0_repack (``data``: u8 DTensor)."""
+    data: DTensor
+    k: int
+    n: int
+
+
+def q8_0_repack(w, stream=None) -> Q8R64:
+    """Load-time repack of a Q8_0 weight ``w`` (Q8, shape (n, k)) for mul_mat_q8_0."""
+    n, k = w.shape[-2], w.shape[-1]
+    nb = ctypes.c_size_t(0)
+    _lib.call("mi_q8_0_repack_bytes", k, n, ctypes.byref(nb))
+    dst = DTensor.empty((max(int(nb.value), 1),), "u8")
+    _lib.call("mi_q8_0_repack", _p(w), ctypes.c_void_p(dst.ptr), nb.value, _s(stream))
+    return Q8R64(dst, k, n)
+
+
+def mul_mat_q8_0_workspace(w: Q8R64, x) -> int:
+    nb = ctypes.c_size_t(0)
+    _lib.call("mi_mul_mat_q8_0_workspace", w.k, w.n, _p(x), ctypes.byref(nb))
+    return int(nb.value)
+
+
+def mul_mat_q8_0(w: Q8R64, x, out=None, workspace=None, stream=None):
+    """ggml_mul_mat(w, x): x F32 (m, k) with m <= 8 -> F32 (m, n)."""
+    y = _out(out, tuple(x.shape[:-1]) + (w.n,), "f32")
+    need = mul_mat_q8_0_workspace(w, x)
+    ws = workspace
+    if need and ws is None:
+        ws = DTensor.empty((need,), "u8")
+    wp = ctypes.c_void_p(ws.ptr) if ws is not None else None
+    wn = ws.numel() * ws.es if ws is not None else 0
+    _lib.call("mi_mul_mat_q8_0", ctypes.c_void_p(w.data.ptr), w.k, w.n, _p(x), _p(y), wp, wn, _s(stream))
+    return y

@@ -747,6 +747,116 @@ int mi_flash_attn_ext(const mi_tensor * q, const mi_tensor * k, const mi_tensor 
     return finish(launch_flash_attn(a, k->type, (int) q->ne[0], (hipStream_t) stream));
 }
 
+int mi_q8_0_repack_bytes(int64_t k, int64_t n, size_t * bytes) {
+    if (!bytes) {
+        return MI_ERR_NULL;
+    }
+    if (k <= 0 || k % 32 != 0 || n < 0) {
+        return MI_ERR_SHAPE;
+    }
+    if (k >= kMaxRows || n >= kMaxRows) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    *bytes = (size_t) ((n + 63) / 64) * (size_t) (k / 32) * 2176;
+    return MI_OK;
+}
+
+int mi_q8_0_repack(const mi_tensor * w, void * dst, size_t dst_bytes, mi_stream stream) {
+    MI_TRY(check(w));
+    if (w->type != MI_TYPE_Q8_0) {
+        return MI_ERR_TYPE;
+    }
+    if (w->ne[2] != 1 || w->ne[3] != 1) {
+        return MI_ERR_SHAPE;
+    }
+    size_t need = 0;
+    MI_TRY(mi_q8_0_repack_bytes(w->ne[0], w->ne[1], &need));
+    if (need > 0 && (!dst || dst_bytes < need)) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(dst, 16)) {
+        return MI_ERR_ALIGN;
+    }
+    return finish(launch_q8_0_repack((const char *) w->data, (int64_t) w->nb[1], (uint32_t) w->ne[0],
+                                     (uint32_t) w->ne[1], (char *) dst, (hipStream_t) stream));
+}
+
+// ggml_mul_mat(w, x) operands: w R64 [k, n], x F32 [k, m] (rows folded over ne1..ne3), y F32 [n, m]
+static int mm_desc(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y, MmvArgs & a) {
+    size_t wb = 0;
+    MI_TRY(mi_q8_0_repack_bytes(k, n, &wb));
+    MI_TRY(check(x));
+    if (x->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (x->ne[0] != k || !uniform_rows(*x)) {
+        return MI_ERR_SHAPE;
+    }
+    const int64_t m = nrows(*x);
+    if (m > 8) {
+        return MI_ERR_UNSUPPORTED;  // the matrix-vector path: up to 8 rows of x
+    }
+    (void) wb;
+    a        = MmvArgs{};
+    a.w      = (const char *) w;
+    a.k      = (uint32_t) k;
+    a.n      = (uint32_t) n;
+    a.nbk    = (uint32_t) (k / 32);
+    a.m      = (uint32_t) m;
+    a.x      = (const char *) x->data;
+    a.x1     = (int64_t) x->nb[1];
+    a.xvec   = aligned(x->data, 16) && (m <= 1 || x->nb[1] % 16 == 0);
+    if (y) {
+        MI_TRY(check(y));
+        if (y->type != MI_TYPE_F32) {
+            return MI_ERR_TYPE;
+        }
+        if (y->ne[0] != n || nrows(*y) != m || !uniform_rows(*y)) {
+            return MI_ERR_SHAPE;
+        }
+        a.y  = (char *) y->data;
+        a.y1 = (int64_t) y->nb[1];
+    }
+    mul_mat_q8_0_plan(a, num_cus());
+    return MI_OK;
+}
+
+int mi_mul_mat_q8_0_workspace(int64_t k, int64_t n, const mi_tensor * x, size_t * bytes) {
+    if (!bytes) {
+        return MI_ERR_NULL;
+    }
+    MmvArgs a;
+    MI_TRY(mm_desc(nullptr, k, n, x, nullptr, a));
+    *bytes = a.m == 0 || a.n == 0 ? 0 : mul_mat_q8_0_workspace(a);
+    return MI_OK;
+}
+
+int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
+                    void * workspace, size_t workspace_bytes, mi_stream stream) {
+    if (!y) {
+        return MI_ERR_NULL;
+    }
+    MmvArgs a;
+    MI_TRY(mm_desc(w, k, n, x, y, a));
+    if (a.m == 0 || a.n == 0) {
+        return MI_OK;
+    }
+    if (!w) {
+        return MI_ERR_NULL;
+    }
+    if (!aligned(w, 16)) {
+        return MI_ERR_ALIGN;
+    }
+    if (!workspace || workspace_bytes < mul_mat_q8_0_workspace(a)) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(workspace, 256)) {
+        return MI_ERR_ALIGN;
+    }
+    mul_mat_q8_0_bind(a, (char *) workspace);
+    return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
+}
+
 int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi_tensor * y, mi_stream stream) {
     MI_TRY(check(t));
     MI_TRY(check(y));

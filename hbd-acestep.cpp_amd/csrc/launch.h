@@ -145,6 +145,31 @@ void   flash_attn_plan(FaArgs & a, int D);
 size_t flash_attn_workspace(const FaArgs & a, int D);
 int    launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s);
 
+// ---- matmul.hip ------------------------------------------------------------
+// ggml_mul_mat(w, x), Q8_0 weights in the R64 layout, F32 x rows (m <= 8)
+struct MmvArgs {
+    const char * w;       // R64 weights: quants, then scales at w + qbytes
+    uint64_t     qbytes;  // ng * nbk * 2048
+    uint32_t     k, n, nbk, ng, npad;  // K, N (weight rows), K / 32, row groups of 64, 64 * ng
+    const char * x;       // F32 x rows: element i of row m at x + m * x1 + 4 i
+    int64_t      x1;
+    int          xvec;    // x rows 16-byte aligned
+    uint32_t     m;       // rows of x (1..8)
+    char *       y;       // F32 y: element n of row m at y + m * y1 + 4 n
+    int64_t      y1;
+    uint32_t     splits, wpg, bps;  // workgroups per row group, waves (key splits) per workgroup,
+                                    // blocks per wave (set by mul_mat_q8_0_plan)
+    char *       xq;           // workspace: quantized x [m][k]
+    float *      xd;           //            scales [m][nbk]
+    float *      part;         //            partials [splits][m][npad] (splits > 1)
+};
+
+void   mul_mat_q8_0_plan(MmvArgs & a, int cus);
+size_t mul_mat_q8_0_workspace(const MmvArgs & a);
+void   mul_mat_q8_0_bind(MmvArgs & a, char * ws);
+int    launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s);
+int    launch_q8_0_repack(const char * src, int64_t nb1, uint32_t k, uint32_t n, char * dst, hipStream_t s);
+
 // ---- tsembd.hip ------------------------------------------------------------
 int launch_timestep_embedding(const float * t, int64_t n, int64_t ts, int dim, int max_period, char * y,
                               int64_t ys, hipStream_t s);

@@ -1,0 +1,341 @@
+// ggml_mul_mat(w, x) with Q8_0 weights and F32 activations, the way ggml-cpu
+// computes it: each row of x is quantized to Q8_0 (the x86 from_float:
+// id = 127 / amax, round to nearest even, saturate), and each output is
+// sum over blocks b of (d_w[b] * d_x[b]) * sum_i q_w[i] q_x[i] -- an exact int32
+// dot per block, scaled in fp32 (ggml_vec_dot_q8_0_q8_0).
+// Reference call sites: qwen3_linear (qwen3-enc.h:86-88) for the Q/K/V, O,
+// gate/up and down projections, dit_ggml_linear (dit-graph.h:36-49), and the
+// LM head over the Q8_0 token table (qwen3-lm.h:755).
+//
+// Weights are repacked once, at load, into the "R64" layout (lossless: the same
+// 34 bytes per block): rows in groups of 64 (the last group zero-padded), and per
+// (group g, block b) the 32 quants of the 64 rows as two 1 KB halves -- half j,
+// lane l holds bytes [16 j, 16 j + 16) of row 64 g + l's block -- followed, after
+// all quants, by the scales d[g][b][l] (fp16). A wave with lane = row then reads
+// every quant byte with fully coalesced 16-byte loads.
+//
+// Matrix-vector kernel (up to 8 rows of x, the batched decode shapes): one wave
+// per (row group, key split); lanes are weight rows, the quantized x is uniform
+// across the wave and read through the scalar cache; sdot4 per 4 quants. Up to
+// 8 key splits of a row group share a workgroup and are added in LDS in wave
+// order; with more, each workgroup writes its partial sums and a small kernel
+// adds them in workgroup order, so the result does not depend on scheduling.
+#include "common.h"
+#include "launch.h"
+
+namespace mi {
+
+__global__ void __launch_bounds__(256) k_q8_0_repack(const char * src, int64_t nb1, uint32_t n, uint32_t nbk,
+                                                     uint32_t ng, char * dst) {
+    const uint64_t i     = (uint64_t) blockIdx.x * 256u + threadIdx.x;  // ((g * nbk + b) * 64 + l)
+    const uint64_t total = (uint64_t) ng * nbk * 64;
+    if (i >= total) {
+        return;
+    }
+    const uint32_t l   = (uint32_t) (i % 64);
+    const uint64_t gb  = i / 64;
+    const uint32_t b   = (uint32_t) (gb % nbk);
+    const uint32_t row = (uint32_t) (gb / nbk) * 64 + l;
+    uint32_t       q[8] = { 0, 0, 0, 0, 0, 0, 0, 0 };
+    uint16_t       d    = 0;
+    if (row < n) {
+        const uint16_t * p = (const uint16_t *) (src + (int64_t) row * nb1 + (int64_t) b * 34);
+        d                  = p[0];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            q[k] = (uint32_t) p[1 + 2 * k] | ((uint32_t) p[2 + 2 * k] << 16);
+        }
+    }
+    char * qd = dst + gb * 2048 + 16 * l;
+    *(uint4 *) qd          = make_uint4(q[0], q[1], q[2], q[3]);
+    *(uint4 *) (qd + 1024) = make_uint4(q[4], q[5], q[6], q[7]);
+    *(uint16_t *) (dst + (uint64_t) ng * nbk * 2048 + i * 2) = d;
+}
+
+// d = amax / 127, the IEEE quotient (q0 = amax * (1/127) corrected by one fma)
+__device__ __forceinline__ float mm_div127(float amax) {
+    constexpr float C  = 1.0f / 127.0f;
+    const float     q0 = amax * C;
+    const float     r  = __builtin_fmaf(-q0, 127.0f, amax);
+    return __builtin_fmaf(r, C, q0);
+}
+
+// x rows -> Q8_0 (x86 rounding), block-major: quants xq[b][m][32] and widened
+// scales xd[b][m] (all rows of a block in one 32 * m + 4 * m byte run, read with a
+// few wide scalar loads); 8 lanes per 32-element block.
+__global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
+    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t blk = gid / 8, sub = gid % 8;
+    if (blk >= a.m * a.nbk) {
+        return;  // whole groups of 8 lanes
+    }
+    const uint32_t m = blk / a.nbk, b = blk - m * a.nbk;
+    const char *   p = a.x + (int64_t) m * a.x1 + (int64_t) (b * 32 + sub * 4) * 4;
+    float          f[4];
+    if (a.xvec) {
+        const float4 v = *(const float4 *) p;
+        f[0]           = v.x;
+        f[1]           = v.y;
+        f[2]           = v.z;
+        f[3]           = v.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            f[e] = ((const float *) p)[e];
+        }
+    }
+    float amax = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
+    amax       = group_max<8>(amax);
+    const float d  = mm_div127(amax);
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    uint32_t    w  = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(f[e] * id), -128.0f, 127.0f);
+        w |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
+    }
+    *(uint32_t *) (a.xq + ((int64_t) b * a.m + m) * 32 + sub * 4) = w;
+    if (sub == 0) {
+        a.xd[b * a.m + m] = (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
+    }
+}
+
+#ifndef MI_MMV_UNROLL
+#define MI_MMV_UNROLL 4  // blocks whose weight loads are issued together
+#endif
+
+template <int M>
+__global__ void __launch_bounds__(512) k_mmv_q8_0(const MmvArgs a) {
+    extern __shared__ float red[];  // [wave][m][lane], W * M * 64 floats when W > 1
+    const uint32_t g = blockIdx.x, s1 = blockIdx.y;
+    const int      tid = threadIdx.x, l = tid & 63;
+    const int      w   = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: x loads stay scalar
+    const int      W   = (int) a.wpg;
+    const uint32_t s   = s1 * (uint32_t) W + (uint32_t) w;  // this wave's key split
+    const uint32_t b0  = s * a.bps < a.nbk ? s * a.bps : a.nbk;
+    const uint32_t b1  = b0 + a.bps < a.nbk ? b0 + a.bps : a.nbk;
+    const char *   wq  = a.w + (uint64_t) g * a.nbk * 2048 + 16 * l;
+    const char *   wd  = a.w + a.qbytes + (uint64_t) g * a.nbk * 128 + 2 * l;
+    const char * __restrict__ xq  = a.xq;
+    const float * __restrict__ xd = a.xd;
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        acc[m] = 0.0f;
+    }
+    constexpr int U = MI_MMV_UNROLL;
+    auto block = [&](const uint4 & w0, const uint4 & w1, uint16_t dh, uint32_t b) {
+        const uint32_t wv[8] = { w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w };
+        const float    dw    = (float) __builtin_bit_cast(_Float16, dh);
+        const uint32_t * xb  = (const uint32_t *) (xq + (size_t) b * (M * 32));
+        const float *    xdb = xd + (size_t) b * M;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            int isum = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                isum = __builtin_amdgcn_sdot4((int) wv[k], (int) xb[8 * m + k], isum, false);
+            }
+            acc[m] = __builtin_fmaf((float) isum, dw * xdb[m], acc[m]);
+        }
+    };
+    // two register sets of U blocks: the loads of one are in flight while the
+    // other's dot products run
+    uint4    a0[U], a1[U], c0[U], c1[U];
+    uint16_t ad[U], cd[U];
+    auto load = [&](uint4 (&w0)[U], uint4 (&w1)[U], uint16_t (&dh)[U], uint32_t bb) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            w0[u] = ld16(wq + (size_t) (bb + u) * 2048);
+            w1[u] = ld16(wq + (size_t) (bb + u) * 2048 + 1024);
+            dh[u] = *(const uint16_t *) (wd + (size_t) (bb + u) * 128);
+        }
+    };
+    auto run = [&](const uint4 (&w0)[U], const uint4 (&w1)[U], const uint16_t (&dh)[U], uint32_t bb) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            block(w0[u], w1[u], dh[u], bb + u);
+        }
+    };
+    uint32_t b = b0;
+    if (b + U <= b1) {
+        load(a0, a1, ad, b);
+    }
+    while (b + U <= b1) {
+        const bool nc = b + 2 * U <= b1;
+        if (nc) {
+            load(c0, c1, cd, b + U);
+        }
+        run(a0, a1, ad, b);
+        b += U;
+        if (!nc) {
+            break;
+        }
+        const bool na = b + 2 * U <= b1;
+        if (na) {
+            load(a0, a1, ad, b + U);
+        }
+        run(c0, c1, cd, b);
+        b += U;
+        if (!na) {
+            break;
+        }
+    }
+    for (; b < b1; ++b) {
+        block(ld16(wq + (size_t) b * 2048), ld16(wq + (size_t) b * 2048 + 1024),
+              *(const uint16_t *) (wd + (size_t) b * 128), b);
+    }
+    const uint32_t row = g * 64 + l;
+    auto store_y = [&](int m, float v) {
+        if (row < a.n) {
+            *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = v;
+        }
+    };
+    if (W == 1 && a.splits == 1) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            store_y(m, acc[m]);
+        }
+        return;
+    }
+    // the workgroup's splits, added in wave order; wave w then owns rows m = w, w + W, ...
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        red[(w * M + m) * 64 + l] = acc[m];
+    }
+    __syncthreads();
+    for (int m = w; m < M; m += W) {
+        float v = 0.0f;
+        for (int w2 = 0; w2 < W; ++w2) {
+            v += red[(w2 * M + m) * 64 + l];
+        }
+        if (a.splits == 1) {
+            store_y(m, v);
+        } else {
+            a.part[((size_t) s1 * M + m) * a.npad + row] = v;
+        }
+    }
+}
+
+// y[m][row] = sum over the workgroups' partials, in workgroup order (splits > 1)
+template <int M>
+__global__ void __launch_bounds__(256) k_mmv_reduce(const MmvArgs a) {
+    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    if (gid >= M * a.npad) {
+        return;
+    }
+    const uint32_t m = gid / a.npad, row = gid - m * a.npad;
+    if (row >= a.n) {
+        return;
+    }
+    const float * pp = a.part + (size_t) m * a.npad + row;
+    const size_t  st = (size_t) M * a.npad;
+    float         v  = 0.0f;
+    uint32_t      s2 = 0;
+    for (; s2 + 8 <= a.splits; s2 += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            t[j] = pp[(s2 + j) * st];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v += t[j];
+        }
+    }
+    for (; s2 < a.splits; ++s2) {
+        v += pp[s2 * st];
+    }
+    *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = v;
+}
+
+#ifndef MI_MMV_WAVES_PER_CU
+#define MI_MMV_WAVES_PER_CU 16  // waves to spread one product over, per CU
+#endif
+
+// key splits: enough waves to keep the loads of the whole chip in flight; up to
+// 8 splits of a row group share a workgroup (reduced in LDS), the rest go
+// through the workspace
+void mul_mat_q8_0_plan(MmvArgs & a, int cus) {
+    a.ng     = (a.n + 63) / 64;
+    a.npad   = a.ng * 64;
+    a.qbytes = (uint64_t) a.ng * a.nbk * 2048;
+    const uint32_t want = (uint32_t) (cus > 0 ? cus : 256) * MI_MMV_WAVES_PER_CU;
+    uint32_t       s    = a.ng == 0 || a.ng >= want ? 1 : (want + a.ng - 1) / a.ng;
+    if (s > a.nbk) {
+        s = a.nbk;
+    }
+    if (s < 1) {
+        s = 1;
+    }
+    a.wpg    = s < 8 ? s : 8;
+    a.splits = (s + a.wpg - 1) / a.wpg;                       // workgroups per row group
+    a.bps    = a.nbk == 0 ? 1 : (a.nbk + a.splits * a.wpg - 1) / (a.splits * a.wpg);
+}
+
+static size_t al256(size_t v) {
+    return (v + 255) & ~(size_t) 255;
+}
+
+size_t mul_mat_q8_0_workspace(const MmvArgs & a) {
+    size_t b = al256((size_t) a.m * a.k) + al256((size_t) a.m * a.nbk * 4);
+    if (a.splits > 1) {
+        b += al256((size_t) a.splits * a.m * a.npad * 4);
+    }
+    return b;
+}
+
+void mul_mat_q8_0_bind(MmvArgs & a, char * ws) {
+    a.xq  = ws;
+    a.xd  = (float *) (ws + al256((size_t) a.m * a.k));
+    char * p = (char *) a.xd + al256((size_t) a.m * a.nbk * 4);
+    a.part = a.splits > 1 ? (float *) p : nullptr;
+}
+
+int launch_q8_0_repack(const char * src, int64_t nb1, uint32_t k, uint32_t n, char * dst, hipStream_t s) {
+    const uint32_t nbk   = k / 32, ng = (n + 63) / 64;
+    const uint64_t total = (uint64_t) ng * nbk * 64;
+    if (total == 0) {
+        return MI_OK;
+    }
+    hipLaunchKernelGGL(k_q8_0_repack, dim3((uint32_t) ((total + 255) / 256)), dim3(256), 0, s, src, nb1, n, nbk, ng,
+                       dst);
+    return MI_OK;
+}
+
+int launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s) {
+    if (a.n == 0 || a.m == 0) {
+        return MI_OK;
+    }
+    const uint64_t threads = (uint64_t) a.m * a.nbk * 8;
+    hipLaunchKernelGGL(k_mmv_quant_x, dim3((uint32_t) ((threads + 255) / 256)), dim3(256), 0, s, a);
+    const dim3   grid(a.ng, a.splits), blk(64 * a.wpg);
+    const size_t lds = a.wpg > 1 ? (size_t) a.wpg * a.m * 64 * 4 : 0;
+    switch (a.m) {
+        case 1: hipLaunchKernelGGL(k_mmv_q8_0<1>, grid, blk, lds, s, a); break;
+        case 2: hipLaunchKernelGGL(k_mmv_q8_0<2>, grid, blk, lds, s, a); break;
+        case 3: hipLaunchKernelGGL(k_mmv_q8_0<3>, grid, blk, lds, s, a); break;
+        case 4: hipLaunchKernelGGL(k_mmv_q8_0<4>, grid, blk, lds, s, a); break;
+        case 5: hipLaunchKernelGGL(k_mmv_q8_0<5>, grid, blk, lds, s, a); break;
+        case 6: hipLaunchKernelGGL(k_mmv_q8_0<6>, grid, blk, lds, s, a); break;
+        case 7: hipLaunchKernelGGL(k_mmv_q8_0<7>, grid, blk, lds, s, a); break;
+        case 8: hipLaunchKernelGGL(k_mmv_q8_0<8>, grid, blk, lds, s, a); break;
+        default: return MI_ERR_UNSUPPORTED;
+    }
+    if (a.splits > 1) {
+        const dim3 rg((a.m * a.npad + 255) / 256);
+        switch (a.m) {
+            case 1: hipLaunchKernelGGL(k_mmv_reduce<1>, rg, dim3(256), 0, s, a); break;
+            case 2: hipLaunchKernelGGL(k_mmv_reduce<2>, rg, dim3(256), 0, s, a); break;
+            case 3: hipLaunchKernelGGL(k_mmv_reduce<3>, rg, dim3(256), 0, s, a); break;
+            case 4: hipLaunchKernelGGL(k_mmv_reduce<4>, rg, dim3(256), 0, s, a); break;
+            case 5: hipLaunchKernelGGL(k_mmv_reduce<5>, rg, dim3(256), 0, s, a); break;
+            case 6: hipLaunchKernelGGL(k_mmv_reduce<6>, rg, dim3(256), 0, s, a); break;
+            case 7: hipLaunchKernelGGL(k_mmv_reduce<7>, rg, dim3(256), 0, s, a); break;
+            default: hipLaunchKernelGGL(k_mmv_reduce<8>, rg, dim3(256), 0, s, a); break;
+        }
+    }
+    return MI_OK;
+}
+
+}  // namespace mi

@@ -227,6 +227,29 @@ int mi_flash_attn_ext(const mi_tensor * q, const mi_tensor * k, const mi_tensor 
 /* Layer-chain drivers: launch the fused-op sequence of one DiT block or   */
 /* one Qwen3 layer in the order of the reference's layer composers, taking */
 /* the GEMM / attention outputs (not computed by this library) as inputs.  */
+/* ggml_mul_mat(w, x) with Q8_0 weights, as ggml-cpu computes it: each row of x
+ * is quantized to Q8_0 with the x86 from_float (id = 127 / amax, round to
+ * nearest even, saturate) and each output is sum_b (d_w * d_x) * sum_i q_w q_x
+ * with an exact int32 dot per 32-block, accumulated in fp32
+ * (ggml_vec_dot_q8_0_q8_0). Replaces the Q8_0 linear layers qwen3_linear
+ * (qwen3-enc.h:86-88; called at qwen3-lm.h:639-651, 729, 737 via
+ * qwen3-enc.h:216-223) and dit_ggml_linear (dit-graph.h:36-49), and the LM head
+ * over the Q8_0 token table (qwen3-lm.h:755).
+ * Weights are repacked once, at load (as ggml-cpu's repacking buffer types
+ * do): mi_q8_0_repack copies a Q8_0 [k, n] weight (GGUF layout, rows at
+ * stride nb[1]) into dst, a lossless layout of mi_q8_0_repack_bytes(k, n)
+ * bytes (rows in groups of 64; 34 bytes per block).
+ * mi_mul_mat_q8_0: w = repacked weight [k, n]; x F32 [k, m] with m <= 8 rows
+ * (ne1 * ne2 * ne3, uniformly strided; more rows return MI_ERR_UNSUPPORTED);
+ * y F32 [n, m]. workspace: device memory of at least
+ * mi_mul_mat_q8_0_workspace() bytes, 256-byte aligned (the quantized x, and
+ * the partial sums and counters of a split k). Calls sharing a workspace race. */
+int mi_q8_0_repack_bytes(int64_t k, int64_t n, size_t * bytes);
+int mi_q8_0_repack(const mi_tensor * w, void * dst, size_t dst_bytes, mi_stream stream);
+int mi_mul_mat_q8_0_workspace(int64_t k, int64_t n, const mi_tensor * x, size_t * bytes);
+int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
+                    void * workspace, size_t workspace_bytes, mi_stream stream);
+
 /* ---------------------------------------------------------------------- */
 
 /* One ACE-Step DiT block's non-GEMM ops, in dit_ggml_build_layer order

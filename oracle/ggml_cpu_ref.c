@@ -14,6 +14,7 @@
 #include "ggml_cpu_ref.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #ifdef _OPENMP
@@ -513,4 +514,39 @@ void orc_flash_attn_ext(const float * q, const float * k, const float * v, const
             }
         }
     }
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml_mul_mat(w, x) with Q8_0 weights (qwen3-enc.h:86-88; dit-graph.h:36-49; */
+/* qwen3-lm.h:755): ggml-cpu quantizes each row of x with the vec_dot type's  */
+/* from_float (Q8_0, x86) and takes ggml_vec_dot_q8_0_q8_0 per output. Here   */
+/* the exact value of that dot, in double: sum over blocks of                 */
+/* fp16(d_w) * fp16(d_x) * (exact int32 sum of q_w * q_x).                    */
+/* ------------------------------------------------------------------------ */
+void orc_mul_mat_q8_0(const uint8_t * w, const float * x, int64_t n, int64_t k, int64_t m, float * y) {
+    const int64_t nb = k / ORC_QK8_0;
+    uint8_t *     xq = (uint8_t *) malloc((size_t) (m * nb * ORC_Q8_0_SIZE) + 1);
+    for (int64_t r = 0; r < m; r++) {
+        orc_quantize_row_q8_0_x86(x + r * k, xq + r * nb * ORC_Q8_0_SIZE, k);
+    }
+#pragma omp parallel for collapse(2) num_threads(g_threads) schedule(static)
+    for (int64_t r = 0; r < m; r++) {
+        for (int64_t j = 0; j < n; j++) {
+            double s = 0.0;
+            for (int64_t b = 0; b < nb; b++) {
+                const uint8_t * wb = w + (j * nb + b) * ORC_Q8_0_SIZE;
+                const uint8_t * xb = xq + (r * nb + b) * ORC_Q8_0_SIZE;
+                uint16_t        dw, dx;
+                memcpy(&dw, wb, 2);
+                memcpy(&dx, xb, 2);
+                int32_t isum = 0;
+                for (int i = 0; i < ORC_QK8_0; i++) {
+                    isum += (int32_t) (int8_t) wb[2 + i] * (int32_t) (int8_t) xb[2 + i];
+                }
+                s += (double) orc_fp16_to_fp32(dw) * (double) orc_fp16_to_fp32(dx) * (double) isum;
+            }
+            y[r * n + j] = (float) s;
+        }
+    }
+    free(xq);
 }

@@ -124,6 +124,13 @@ void orc_flash_attn_ext(const float * q, const float * k, const float * v, const
                         int64_t Nkv, int64_t n_q, int64_t n_kv, int64_t D, int64_t mN, int64_t mH, int64_t mQ,
                         float scale, int qconv, float * y);
 
+/* ---- ggml_mul_mat(w, x), Q8_0 weights (qwen3-enc.h:86-88; dit-graph.h:36-49;
+ *      qwen3-lm.h:755): w n rows of k / 32 Q8_0 blocks, x m rows of k F32,
+ *      y m rows of n. Each row of x is quantized with the x86 quantizer (the
+ *      vec_dot type's from_float); y is the exact value, in double, of
+ *      sum_b fp16(d_w) fp16(d_x) sum_i q_w q_x, rounded to float once. ---- */
+void orc_mul_mat_q8_0(const uint8_t * w, const float * x, int64_t n, int64_t k, int64_t m, float * y);
+
 #ifdef __cplusplus
 }
 #endif

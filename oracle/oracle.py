@@ -68,6 +68,7 @@ def lib():
         L.orc_bf16_to_fp32_n.argtypes = [_u16p, _fp, _i64]
         L.orc_flash_attn_ext.argtypes = [_fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                          ctypes.c_float, ctypes.c_int, _fp]
+        L.orc_mul_mat_q8_0.argtypes = [_u8p, _fp, _i64, _i64, _i64, _fp]
         L.orc_set_threads.argtypes = [ctypes.c_int]
         L.orc_get_threads.restype = ctypes.c_int
         _lib = L
@@ -330,3 +331,16 @@ def bf16_chain(fn, *arrays_bf16, out_bf16=True, **kw):
     xs = [bf16_to_f32(a) if isinstance(a, np.ndarray) and a.dtype == np.uint16 else a for a in arrays_bf16]
     y = fn(*xs, **kw)
     return f32_to_bf16(y) if out_bf16 else y
+
+
+def mul_mat_q8_0(w: np.ndarray, x) -> np.ndarray:
+    """ggml_mul_mat(w, x): w Q8_0 bytes (n, k/32*34), x F32 (m, k) -> F32 (m, n)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = _c32(x)
+    n = w.shape[0]
+    k = w.shape[1] // Q8_0_SIZE * QK8_0
+    assert x.shape[-1] == k
+    m = x.size // k if k else 0
+    y = np.empty((m, n), np.float32)
+    lib().orc_mul_mat_q8_0(w.ctypes.data_as(_u8p), _f(x), n, k, m, _f(y))
+    return y

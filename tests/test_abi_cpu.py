@@ -187,6 +187,33 @@ def test_flash_attn_validation():
         assert L.mi_flash_attn_ext_workspace(R(_t(qs)), R(k0), R(k0), ctypes.byref(ws)) == 0 and ws.value == 0
 
 
+def test_mul_mat_q8_0_validation():
+    k, n, m = 256, 100, 8
+    x = _t([k, m])
+    y = _t([n, m])
+    nb = ctypes.c_size_t(0)
+    mm = L.mi_mul_mat_q8_0
+    W = ctypes.c_void_p(4096)
+    assert L.mi_q8_0_repack_bytes(k, n, ctypes.byref(nb)) == 0 and nb.value == 2 * (k // 32) * 2176
+    assert L.mi_q8_0_repack_bytes(k + 16, n, ctypes.byref(nb)) == -3        # k % 32
+    assert L.mi_q8_0_repack_bytes(k, n, None) == -1
+    assert L.mi_q8_0_repack(R(_t([k, n])), W, 1 << 20, NULL_S) == -2          # F32 weight
+    assert L.mi_q8_0_repack(R(_t([k, n], Q8_0)), W, 10, NULL_S) == -6         # dst too small
+    assert mm(W, k, n, R(x), None, None, 0, NULL_S) == -1
+    assert mm(W, k, n, R(_t([k, 9])), R(_t([n, 9])), None, 0, NULL_S) == -7   # more than 8 rows of x
+    assert mm(W, k, n, R(_t([k + 32, m])), R(y), None, 0, NULL_S) == -3
+    assert mm(W, k, n, R(x), R(_t([n + 1, m])), None, 0, NULL_S) == -3
+    assert mm(W, k, n, R(_t([k, m], BF16)), R(y), None, 0, NULL_S) == -2
+    assert mm(W, k, n, R(x), R(_t([n, m], BF16)), None, 0, NULL_S) == -2
+    assert mm(ctypes.c_void_p(4098), k, n, R(x), R(y), None, 0, NULL_S) == -5  # weight alignment
+    assert L.mi_mul_mat_q8_0_workspace(k, n, R(x), ctypes.byref(nb)) == 0 and nb.value > 0
+    assert mm(W, k, n, R(x), R(y), None, 0, NULL_S) == -6                     # no workspace
+    assert mm(W, k, n, R(x), R(y), ctypes.c_void_p(1 << 20), nb.value - 1, NULL_S) == -6
+    assert mm(W, k, n, R(x), R(y), ctypes.c_void_p((1 << 20) + 16), nb.value, NULL_S) == -5
+    assert L.mi_mul_mat_q8_0_workspace(k, n, R(_t([k, 0])), ctypes.byref(nb)) == 0 and nb.value == 0
+    assert L.mi_mul_mat_q8_0_workspace(k, 0, R(x), ctypes.byref(nb)) == 0 and nb.value == 0
+
+
 def test_chain_validation():
     io = _lib.MiDitBlockIO()
     io.hidden = _t([2048, 4])

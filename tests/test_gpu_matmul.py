@@ -1,0 +1,105 @@
+"""GPU parity: ggml_mul_mat with Q8_0 weights (mi_q8_0_repack + mi_mul_mat_q8_0)
+against the oracle.
+
+The oracle is the exact value of ggml-cpu's definition (x quantized with the
+x86 Q8_0 quantizer, exact int32 block dots scaled by fp16(d_w) fp16(d_x)),
+rounded to float once. The kernel's int32 dots and the d_w * d_x products are
+exact in fp32; it rounds once per block (fma into the running sum) and once
+per added split, so the bar, written here, is
+  |y - ref| <= (K / 32 + 8) * 2^-24 * sum_k |w_k| |x'_k|  (+ 1e-30)
+with x' the dequantized quantized x. One quant of x rounded differently moves
+y by |d_w d_x q_w|, far above that bound, so the x quantization is checked
+bit for bit through y.
+"""
+import numpy as np
+import pytest
+from helpers import to_dev, to_np
+from oracle import oracle as orc
+
+from acestep_ops import ops
+from acestep_ops.device import DTensor
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(y, w, x):
+    ref = orc.mul_mat_q8_0(w, x)
+    k = x.shape[-1]
+    wf = orc.dequantize_q8_0(w).astype(np.float64)
+    xf = orc.dequantize_q8_0(orc.quantize_q8_0(x, "x86")).astype(np.float64)
+    bound = (k / 32 + 8) * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T) + 1e-30
+    err = np.abs(y.astype(np.float64) - ref)
+    assert y.shape == ref.shape
+    assert np.all(err <= bound), f"max err {err.max()} vs bound {bound[err > bound].min()}"
+
+
+def _run(n, k, m, seed, wscale=1.0, xscale=1.0, wview=None):
+    r = np.random.default_rng(seed)
+    wf = (r.standard_normal((n, k)) * wscale).astype(np.float32)
+    w = orc.quantize_q8_0(wf)
+    x = (r.standard_normal((m, k)) * xscale).astype(np.float32)
+    if wview is None:
+        dw = ops.Q8(to_dev(w))
+    else:  # rows of a wider table: row stride wview bytes
+        big = np.zeros((n, wview), np.uint8)
+        big[:, :w.shape[1]] = w
+        dw = ops.Q8(to_dev(big).view(n, wview)[:, :w.shape[1]])
+    wr = ops.q8_0_repack(dw)
+    y = to_np(ops.mul_mat_q8_0(wr, to_dev(x)))
+    _check(y, w, x)
+    return w, x, wr
+
+
+@pytest.mark.parametrize("n,k,m", [(6144, 2560, 8), (2560, 9728, 8), (2560, 4096, 1), (19456, 2560, 4),
+                                   (300, 2560, 3), (130, 64, 5), (1, 32, 8), (77, 96, 2)])
+def test_decode_shapes(dev, n, k, m):
+    """Qwen3-4B decode projections (QKV, down, O, gate/up) at batch 8 / 1 / 4, and
+    ragged row counts (a partial last group of 64 rows), one- and two-block rows."""
+    print(f"mul_mat q8_0 n={n} k={k} m={m}", flush=True)
+    _run(n, k, m, seed=n + k + m)
+
+
+def test_lm_head_single_split(dev):
+    """Many row groups (the LM head's 151669 rows, short rows here): no key split."""
+    print("mul_mat q8_0 lm-head rows", flush=True)
+    _run(151669, 64, 8, seed=11)
+
+
+def test_strided_weight_rows_and_scales(dev):
+    """Weight rows at a wider stride (a view of a larger table), and inputs with
+    large and tiny magnitudes (fp16 scales near their range ends)."""
+    print("mul_mat q8_0 strided weights", flush=True)
+    _run(200, 256, 6, seed=12, wview=256 // 32 * 34 + 68)
+    _run(200, 256, 6, seed=13, wscale=3e3, xscale=1e-3)
+    _run(200, 256, 6, seed=14, wscale=1e-4, xscale=50.0)
+
+
+def test_strided_and_unaligned_x_rows(dev):
+    print("mul_mat q8_0 strided x", flush=True)
+    r = np.random.default_rng(15)
+    n, k, m = 500, 320, 7
+    w = orc.quantize_q8_0(r.standard_normal((n, k)).astype(np.float32))
+    xbig = r.standard_normal((m, k + 3)).astype(np.float32)
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    dx = to_dev(xbig)
+    y = to_np(ops.mul_mat_q8_0(wr, dx[:, 1:k + 1]))  # rows 4-byte aligned only
+    _check(y, w, np.ascontiguousarray(xbig[:, 1:k + 1]))
+
+
+def test_zero_x_rows_and_repeat_calls_are_identical(dev):
+    """A zero row of x gives zeros; the split counters reset, so a second call with
+    the same workspace gives bit-identical results."""
+    print("mul_mat q8_0 repeat", flush=True)
+    r = np.random.default_rng(16)
+    n, k, m = 2560, 9728, 8
+    w = orc.quantize_q8_0(r.standard_normal((n, k)).astype(np.float32))
+    x = r.standard_normal((m, k)).astype(np.float32)
+    x[3] = 0.0
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    dx = to_dev(x)
+    ws = DTensor.empty((ops.mul_mat_q8_0_workspace(wr, dx),), "u8")
+    y1 = to_np(ops.mul_mat_q8_0(wr, dx, workspace=ws))
+    y2 = to_np(ops.mul_mat_q8_0(wr, dx, workspace=ws))
+    assert np.array_equal(y1, y2)
+    assert np.all(y1[3] == 0.0)
+    _check(y1, w, x)
