@@ -611,6 +611,37 @@ def gemv_bench(steps: int):
     print(json.dumps({"config": f"Q8_0 mul_mat, one Qwen3-4B layer's four projections at batch {M}",
                       "us_per_layer": round(layer_us, 2), "bytes_per_layer": layer_bytes, "GB/s": round(gbs, 1),
                       "frac": round(gbs / HBM_PEAK_GBS, 3)}), flush=True)
+    # the matrix kernel: the DiT projections at T = 6000 x 2 rows (dit-graph.h:36-49), H = 2048
+    for name, k, n, m in (("DiT QKV", 2048, 4096, 12000), ("DiT gate/up", 2048, 12288, 12000),
+                          ("DiT down", 6144, 2048, 12000), ("Qwen3-4B prefill QKV", 2560, 6144, 2048)):
+        nbk = k // 32
+        blocks = np.empty((n, nbk, 34), np.uint8)
+        blocks[:, :, 2:] = rng.integers(-127, 128, (n, nbk, 32), dtype=np.int8).view(np.uint8)
+        blocks[:, :, :2] = (rng.uniform(0.5, 1.0, (n, nbk)) * 2e-3).astype(np.float16).view(np.uint8).reshape(
+            n, nbk, 2)
+        wr = ops.q8_0_repack(ops.Q8(DTensor.from_numpy(blocks.reshape(n, nbk * 34))), stream=sh)
+        del blocks
+        x = DTensor.from_numpy(rng.standard_normal((m, k), dtype=np.float32))
+        y = DTensor.empty((m, n), "f32")
+        ws = DTensor.empty((max(ops.mul_mat_q8_0_workspace(wr, x), 1),), "u8")
+        g = Graph()
+        with g.capture(st):
+            for _ in range(steps):
+                ops.mul_mat_q8_0(wr, x, out=y, workspace=ws, stream=sh)
+        g.launch()
+        st.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(sh)
+        g.launch()
+        e1.record(sh)
+        e1.synchronize()
+        us = 1000.0 * e0.elapsed_ms(e1) / steps
+        ops_ = 2.0 * m * n * k
+        print(json.dumps({"config": f"Q8_0 mul_mat {name}: k={k}, n={n}, m={m}", "us_per_call": round(us, 2),
+                          "TOPS": round(ops_ / (us * 1e-6) / 1e12, 1),
+                          "frac_of_int8_dense": round(ops_ / (us * 1e-6) / 1e12 / 5000.0, 3)}), flush=True)
+        del g, wr, x, y, ws
+        device.synchronize()
 
 
 def main():

@@ -793,9 +793,6 @@ static int mm_desc(const void * w, int64_t k, int64_t n, const mi_tensor * x, co
         return MI_ERR_SHAPE;
     }
     const int64_t m = nrows(*x);
-    if (m > 8) {
-        return MI_ERR_UNSUPPORTED;  // the matrix-vector path: up to 8 rows of x
-    }
     (void) wb;
     a        = MmvArgs{};
     a.w      = (const char *) w;

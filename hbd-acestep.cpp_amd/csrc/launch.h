@@ -146,7 +146,7 @@ size_t flash_attn_workspace(const FaArgs & a, int D);
 int    launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s);
 
 // ---- matmul.hip ------------------------------------------------------------
-// ggml_mul_mat(w, x), Q8_0 weights in the R64 layout, F32 x rows (m <= 8)
+// ggml_mul_mat(w, x), Q8_0 weights in the R64 layout, F32 x rows
 struct MmvArgs {
     const char * w;       // R64 weights: quants, then scales at w + qbytes
     uint64_t     qbytes;  // ng * nbk * 2048
@@ -154,7 +154,8 @@ struct MmvArgs {
     const char * x;       // F32 x rows: element i of row m at x + m * x1 + 4 i
     int64_t      x1;
     int          xvec;    // x rows 16-byte aligned
-    uint32_t     m;       // rows of x (1..8)
+    uint32_t     m;       // rows of x
+    uint32_t     mp;      // row stride of the quantized x (m, or m padded to 128 for the matrix kernel)
     char *       y;       // F32 y: element n of row m at y + m * y1 + 4 n
     int64_t      y1;
     uint32_t     splits, wpg, bps;  // workgroups per row group, waves (key splits) per workgroup,

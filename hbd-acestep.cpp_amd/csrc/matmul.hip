@@ -61,8 +61,9 @@ __device__ __forceinline__ float mm_div127(float amax) {
 }
 
 // x rows -> Q8_0 (x86 rounding), block-major: quants xq[b][m][32] and widened
-// scales xd[b][m] (all rows of a block in one 32 * m + 4 * m byte run, read with a
-// few wide scalar loads); 8 lanes per 32-element block.
+// scales xd[b][m] at a row stride mp >= m (the matrix-vector kernel reads all
+// rows of a block in one 32 * m + 4 * m byte run with a few wide scalar loads;
+// the matrix kernel reads 32-row tiles); 8 lanes per 32-element block.
 __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
     const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
     const uint32_t blk = gid / 8, sub = gid % 8;
@@ -94,9 +95,9 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
         const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(f[e] * id), -128.0f, 127.0f);
         w |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
     }
-    *(uint32_t *) (a.xq + ((int64_t) b * a.m + m) * 32 + sub * 4) = w;
+    *(uint32_t *) (a.xq + ((int64_t) b * a.mp + m) * 32 + sub * 4) = w;
     if (sub == 0) {
-        a.xd[b * a.m + m] = (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
+        a.xd[(int64_t) b * a.mp + m] = (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
     }
 }
 
@@ -249,6 +250,133 @@ __global__ void __launch_bounds__(256) k_mmv_reduce(const MmvArgs a) {
     *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = v;
 }
 
+
+// Matrix kernel (more than 8 rows of x: prefill, the DiT): a workgroup of 4
+// waves owns 128 rows of x x 128 weight rows; each wave a 64 x 64 tile as 2 x 2
+// v_mfma_i32_32x32x32_i8 tiles (D rows = rows of x, columns = weight rows, so a
+// lane stores consecutive outputs). Per 32-element block: one MFMA per tile
+// gives the exact int32 block dots, and acc = fma(float(isum), d_w * d_x, acc)
+// scales them in block order -- the arithmetic of the matrix-vector kernel
+// (the d_w * d_x products come from an f32 outer-product MFMA, exactly).
+// Operands come straight from global memory in MFMA lane order: x from the
+// block-major quantized rows (lane l: row l % 32, bytes 16 (l / 32) of the
+// block), weights from the R64 layout (a 32-row half of a group is two 512-byte
+// runs), so no LDS staging is needed; one block ahead is in flight.
+typedef int mm_i32x4 __attribute__((ext_vector_type(4)));
+typedef int mm_i32x16 __attribute__((ext_vector_type(16)));
+typedef float mm_f32x16 __attribute__((ext_vector_type(16)));
+
+__global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
+    const int      tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
+    const int      hh  = l >> 5, c = l & 31;
+    const uint32_t m0  = blockIdx.y * 128 + (wv >> 1) * 64;  // rows of x (padded to 128)
+    const uint32_t n0  = blockIdx.x * 128 + (wv & 1) * 64;   // weight rows
+    const uint32_t g   = n0 / 64;                             // R64 row group
+    if (g >= a.ng) {
+        return;  // whole wave
+    }
+    const char *   wq = a.w + (uint64_t) g * a.nbk * 2048 + (size_t) hh * 1024 + 16 * c;
+    const char *   wd = a.w + a.qbytes + (uint64_t) g * a.nbk * 128 + 2 * c;
+    const char *   xq = a.xq + (size_t) (m0 + c) * 32 + hh * 16;
+    const float *  xd = a.xd + m0;
+    const uint64_t xqs = (uint64_t) a.mp * 32;  // per block
+    float          acc[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                acc[i][j][e] = 0.0f;
+            }
+        }
+    }
+    struct Blk {
+        uint4    x[2], w[2];
+        uint16_t dw[2];
+        float    dx[2];
+    };
+    auto load = [&](Blk & k, uint32_t b) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {  // x tile i: rows m0 + 32 i + c
+            k.x[i]  = *(const uint4 *) (xq + b * xqs + (size_t) i * 32 * 32);
+            k.dx[i] = xd[(size_t) b * a.mp + 32 * i + c];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {  // weight tile j: rows n0 + 32 j + c
+            k.w[j]  = *(const uint4 *) (wq + (size_t) b * 2048 + 512 * j);  // cached: every row tile of x reads it
+            k.dw[j] = *(const uint16_t *) (wd + (size_t) b * 128 + 64 * j);
+        }
+    };
+    // the block's scales d_x[m] d_w[n] as a 32 x 32 outer product on the matrix
+    // core (k = 0 carries the scales, k = 1 zeros: exact), in the D layout of the
+    // int32 dots, so each output costs one conversion and one fma
+    auto run = [&](const Blk & k) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const mm_i32x4 av = { (int) k.x[i].x, (int) k.x[i].y, (int) k.x[i].z, (int) k.x[i].w };
+            const float    sx = hh == 0 ? k.dx[i] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const mm_i32x4  bv = { (int) k.w[j].x, (int) k.w[j].y, (int) k.w[j].z, (int) k.w[j].w };
+                const mm_i32x16 d  = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, mm_i32x16{}, 0, 0, 0);
+                const float     sw = hh == 0 ? (float) __builtin_bit_cast(_Float16, k.dw[j]) : 0.0f;
+                const mm_f32x16 sc = __builtin_amdgcn_mfma_f32_32x32x2f32(sx, sw, mm_f32x16{}, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    acc[i][j][e] = __builtin_fmaf((float) d[e], sc[e], acc[i][j][e]);
+                }
+            }
+        }
+    };
+    Blk      k0, k1;
+    uint32_t b = 0;
+    if (a.nbk > 0) {
+        load(k0, 0);
+    }
+    while (b < a.nbk) {
+        const bool n1 = b + 1 < a.nbk;
+        if (n1) {
+            load(k1, b + 1);
+        }
+        run(k0);
+        ++b;
+        if (!n1) {
+            break;
+        }
+        const bool n0b = b + 1 < a.nbk;
+        if (n0b) {
+            load(k0, b + 1);
+        }
+        run(k1);
+        ++b;
+        if (!n0b) {
+            break;
+        }
+    }
+    // D lane l: column n0 + 32 j + c, rows m0 + 32 i + 8 q + 4 hh + e
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t n = n0 + 32 * j + c;
+        if (n >= a.n) {
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t m = m0 + 32 * i + 8 * q + 4 * hh + e;
+                    if (m < a.m) {
+                        *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) n * 4) = acc[i][j][4 * q + e];
+                    }
+                }
+            }
+        }
+    }
+}
+
 #ifndef MI_MMV_WAVES_PER_CU
 #define MI_MMV_WAVES_PER_CU 16  // waves to spread one product over, per CU
 #endif
@@ -260,6 +388,12 @@ void mul_mat_q8_0_plan(MmvArgs & a, int cus) {
     a.ng     = (a.n + 63) / 64;
     a.npad   = a.ng * 64;
     a.qbytes = (uint64_t) a.ng * a.nbk * 2048;
+    a.mp     = a.m <= 8 ? a.m : (a.m + 127) / 128 * 128;
+    if (a.m > 8) {  // the matrix kernel: no key split
+        a.wpg = a.splits = 1;
+        a.bps = a.nbk;
+        return;
+    }
     const uint32_t want = (uint32_t) (cus > 0 ? cus : 256) * MI_MMV_WAVES_PER_CU;
     uint32_t       s    = a.ng == 0 || a.ng >= want ? 1 : (want + a.ng - 1) / a.ng;
     if (s > a.nbk) {
@@ -278,7 +412,7 @@ static size_t al256(size_t v) {
 }
 
 size_t mul_mat_q8_0_workspace(const MmvArgs & a) {
-    size_t b = al256((size_t) a.m * a.k) + al256((size_t) a.m * a.nbk * 4);
+    size_t b = al256((size_t) a.mp * a.k) + al256((size_t) a.mp * a.nbk * 4);
     if (a.splits > 1) {
         b += al256((size_t) a.splits * a.m * a.npad * 4);
     }
@@ -287,8 +421,8 @@ size_t mul_mat_q8_0_workspace(const MmvArgs & a) {
 
 void mul_mat_q8_0_bind(MmvArgs & a, char * ws) {
     a.xq  = ws;
-    a.xd  = (float *) (ws + al256((size_t) a.m * a.k));
-    char * p = (char *) a.xd + al256((size_t) a.m * a.nbk * 4);
+    a.xd  = (float *) (ws + al256((size_t) a.mp * a.k));
+    char * p = (char *) a.xd + al256((size_t) a.mp * a.nbk * 4);
     a.part = a.splits > 1 ? (float *) p : nullptr;
 }
 
@@ -309,6 +443,10 @@ int launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s) {
     }
     const uint64_t threads = (uint64_t) a.m * a.nbk * 8;
     hipLaunchKernelGGL(k_mmv_quant_x, dim3((uint32_t) ((threads + 255) / 256)), dim3(256), 0, s, a);
+    if (a.m > 8) {
+        hipLaunchKernelGGL(k_mmq_q8_0, dim3((a.n + 127) / 128, a.mp / 128), dim3(256), 0, s, a);
+        return MI_OK;
+    }
     const dim3   grid(a.ng, a.splits), blk(64 * a.wpg);
     const size_t lds = a.wpg > 1 ? (size_t) a.wpg * a.m * 64 * 4 : 0;
     switch (a.m) {

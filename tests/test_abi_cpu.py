@@ -200,7 +200,7 @@ def test_mul_mat_q8_0_validation():
     assert L.mi_q8_0_repack(R(_t([k, n])), W, 1 << 20, NULL_S) == -2          # F32 weight
     assert L.mi_q8_0_repack(R(_t([k, n], Q8_0)), W, 10, NULL_S) == -6         # dst too small
     assert mm(W, k, n, R(x), None, None, 0, NULL_S) == -1
-    assert mm(W, k, n, R(_t([k, 9])), R(_t([n, 9])), None, 0, NULL_S) == -7   # more than 8 rows of x
+    assert mm(W, k, n, R(_t([k, 9])), R(_t([n, 9])), None, 0, NULL_S) == -6   # long x: the matrix kernel, no workspace
     assert mm(W, k, n, R(_t([k + 32, m])), R(y), None, 0, NULL_S) == -3
     assert mm(W, k, n, R(x), R(_t([n + 1, m])), None, 0, NULL_S) == -3
     assert mm(W, k, n, R(_t([k, m], BF16)), R(y), None, 0, NULL_S) == -2

@@ -1,5 +1,6 @@
 """GPU parity: ggml_mul_mat with Q8_0 weights (mi_q8_0_repack + mi_mul_mat_q8_0)
-against the oracle.
+against the oracle: the matrix-vector kernel (up to 8 rows of x) and the
+matrix kernel (more rows: prefill, the DiT).
 
 The oracle is the exact value of ggml-cpu's definition (x quantized with the
 x86 Q8_0 quantizer, exact int32 block dots scaled by fp16(d_w) fp16(d_x)),
@@ -103,3 +104,26 @@ def test_zero_x_rows_and_repeat_calls_are_identical(dev):
     assert np.array_equal(y1, y2)
     assert np.all(y1[3] == 0.0)
     _check(y1, w, x)
+
+
+@pytest.mark.parametrize("n,k,m", [(2048, 2048, 300), (640, 256, 129), (100, 96, 9), (6144, 512, 512),
+                                   (70, 32, 1000)])
+def test_matrix_kernel_shapes(dev, n, k, m):
+    """More than 8 rows of x (DiT and prefill projections): ragged row tiles of x
+    and of the weights, one-block rows, many rows."""
+    print(f"mul_mat q8_0 matrix n={n} k={k} m={m}", flush=True)
+    _run(n, k, m, seed=n * 7 + k + m)
+
+
+def test_matrix_kernel_strided_x_and_y(dev):
+    print("mul_mat q8_0 matrix strided x/y", flush=True)
+    r = np.random.default_rng(17)
+    n, k, m = 300, 320, 200
+    w = orc.quantize_q8_0(r.standard_normal((n, k)).astype(np.float32))
+    xbig = r.standard_normal((m, k + 3)).astype(np.float32)
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    ybig = DTensor.zeros((m, n + 5), "f32")
+    ops.mul_mat_q8_0(wr, to_dev(xbig)[:, 2:k + 2], out=ybig[:, 1:n + 1])
+    yb = to_np(ybig)
+    assert np.all(yb[:, 0] == 0) and np.all(yb[:, n + 1:] == 0)
+    _check(yb[:, 1:n + 1], w, np.ascontiguousarray(xbig[:, 2:k + 2]))
