@@ -27,6 +27,7 @@ STATUS = {
     -6: "MI_ERR_PARAM",
     -7: "MI_ERR_UNSUPPORTED",
     -8: "MI_ERR_HIP",
+    -9: "MI_ERR_FILE",
 }
 
 
@@ -44,6 +45,17 @@ _TP = ctypes.POINTER(MiTensor)
 _VP = ctypes.c_void_p
 _F = ctypes.c_float
 _I = ctypes.c_int
+
+
+class MiGGUFTensor(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("type", ctypes.c_int32),
+        ("n_dims", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nbytes", ctypes.c_uint64),
+        ("data", ctypes.c_void_p),
+    ]
 
 
 class MiDitBlockIO(ctypes.Structure):
@@ -92,6 +104,21 @@ PROTOTYPES = {
     "mi_q8_0_repack": [_TP, _VP, ctypes.c_size_t, _VP],
     "mi_mul_mat_q8_0_workspace": [ctypes.c_int64, ctypes.c_int64, _TP, ctypes.POINTER(ctypes.c_size_t)],
     "mi_mul_mat_q8_0": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, _TP, _VP, ctypes.c_size_t, _VP],
+    "mi_gguf_open": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)],
+    "mi_gguf_close": [_VP],
+    "mi_gguf_n_tensors": [_VP],
+    "mi_gguf_find_tensor": [_VP, ctypes.c_char_p],
+    "mi_gguf_get_tensor": [_VP, ctypes.c_int64, ctypes.POINTER(MiGGUFTensor)],
+    "mi_gguf_n_kv": [_VP],
+    "mi_gguf_find_key": [_VP, ctypes.c_char_p],
+    "mi_gguf_get_key": [_VP, ctypes.c_int64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int32)],
+    "mi_gguf_get_u32": [_VP, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)],
+    "mi_gguf_get_f32": [_VP, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)],
+    "mi_gguf_get_bool": [_VP, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)],
+    "mi_gguf_get_str": [_VP, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)],
+    "mi_gguf_upload": [_VP, ctypes.c_char_p, _I, _VP, ctypes.c_size_t, _VP],
+    "mi_gguf_upload_rows": [_VP, ctypes.POINTER(ctypes.c_char_p), _I, _VP, ctypes.c_size_t,
+                            ctypes.POINTER(ctypes.c_int64), _VP],
     "mi_dit_block_ops": [ctypes.POINTER(MiDitBlockIO), _VP],
     "mi_qwen3_layer_ops": [ctypes.POINTER(MiQwen3LayerIO), _VP],
 }
@@ -113,6 +140,9 @@ def load() -> ctypes.CDLL:
         fn.argtypes = argtypes
         fn.restype = ctypes.c_int
     lib.mi_status_str.restype = ctypes.c_char_p
+    for name in ("mi_gguf_n_tensors", "mi_gguf_find_tensor", "mi_gguf_n_kv", "mi_gguf_find_key"):
+        getattr(lib, name).restype = ctypes.c_int64
+    lib.mi_gguf_close.restype = None
     _lib = lib
     return lib
 

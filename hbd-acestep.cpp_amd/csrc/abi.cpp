@@ -198,6 +198,8 @@ const char * mi_status_str(int status) {
             return "unsupported configuration";
         case MI_ERR_HIP:
             return "HIP runtime error";
+        case MI_ERR_FILE:
+            return "file missing, unreadable, truncated or not GGUF";
         default:
             return "unknown status";
     }

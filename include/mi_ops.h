@@ -50,6 +50,7 @@ enum mi_status {
     MI_ERR_PARAM       = -6, /* invalid scalar parameter                         */
     MI_ERR_UNSUPPORTED = -7, /* valid ggml op configuration this library lacks   */
     MI_ERR_HIP         = -8, /* the HIP runtime reported an error at launch      */
+    MI_ERR_FILE        = -9, /* a file is missing, unreadable, truncated or not GGUF */
 };
 
 /* Q8_0 quantizer rounding variants (both are ggml's own):
@@ -249,6 +250,49 @@ int mi_q8_0_repack(const mi_tensor * w, void * dst, size_t dst_bytes, mi_stream 
 int mi_mul_mat_q8_0_workspace(int64_t k, int64_t n, const mi_tensor * x, size_t * bytes);
 int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
                     void * workspace, size_t workspace_bytes, mi_stream stream);
+
+/* GGUF reader and load-time weight preparation. Replaces gf_load (mmap, the
+ * header parse and the check that every tensor lies inside the file,
+ * gguf-weights.h:74-154), gf_load_tensor / gf_load_tensor_f32 (156-268),
+ * gf_load_qkv_fused / gf_load_pair_fused (270-352) and gf_get_u32 / f32 /
+ * str / bool (354-390). GGUF versions 2 and 3; tensor types with a known ggml
+ * block size (F32, F16, BF16, Q4_0..Q8_1, Q2_K..Q8_K, I8..I64, F64; other
+ * types: MI_ERR_TYPE). Malformed, truncated or misaligned files, and duplicate
+ * keys or tensor names, return MI_ERR_FILE. The handle keeps the file mapped;
+ * names, strings and tensor data pointers stay valid until mi_gguf_close. */
+typedef struct mi_gguf mi_gguf;
+typedef struct {
+    const char * name;
+    int32_t      type;    /* enum ggml_type */
+    int32_t      n_dims;  /* 1..4 */
+    int64_t      ne[4];   /* ggml order, 1 past n_dims */
+    uint64_t     nbytes;
+    const void * data;    /* host pointer into the mapped file */
+} mi_gguf_tensor;
+
+int     mi_gguf_open(const char * path, mi_gguf ** out);
+void    mi_gguf_close(mi_gguf * g);
+int64_t mi_gguf_n_tensors(const mi_gguf * g);
+int64_t mi_gguf_find_tensor(const mi_gguf * g, const char * name); /* -1 if absent */
+int     mi_gguf_get_tensor(const mi_gguf * g, int64_t idx, mi_gguf_tensor * t);
+int64_t mi_gguf_n_kv(const mi_gguf * g);
+int64_t mi_gguf_find_key(const mi_gguf * g, const char * key); /* -1 if absent */
+int     mi_gguf_get_key(const mi_gguf * g, int64_t idx, const char ** key, int32_t * gguf_type);
+/* typed values: MI_ERR_PARAM if the key is absent (the reference's getters then
+ * return 0 / 0.0 / "" / false), MI_ERR_TYPE if it holds another GGUF type */
+int mi_gguf_get_u32(const mi_gguf * g, const char * key, uint32_t * v);
+int mi_gguf_get_f32(const mi_gguf * g, const char * key, float * v);
+int mi_gguf_get_bool(const mi_gguf * g, const char * key, int * v);
+int mi_gguf_get_str(const mi_gguf * g, const char * key, const char ** v);
+/* Copy a tensor's bytes to device memory; to_f32 widens an F16 or BF16 tensor
+ * to F32 (F32 tensors copy as they are; other types: MI_ERR_TYPE). */
+int mi_gguf_upload(const mi_gguf * g, const char * name, int to_f32, void * dst, size_t dst_bytes, mi_stream stream);
+/* Concatenate the rows of n 1-D/2-D tensors that share ne0 and type into dst
+ * (q rows || k rows || v rows, or gate || up); *ne1_out = the summed ne1.
+ * Different types: MI_ERR_UNSUPPORTED (load them separately, as the reference
+ * falls back to). Calls return after the copies complete. */
+int mi_gguf_upload_rows(const mi_gguf * g, const char * const * names, int n, void * dst, size_t dst_bytes,
+                        int64_t * ne1_out, mi_stream stream);
 
 /* ---------------------------------------------------------------------- */
 

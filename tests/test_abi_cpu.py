@@ -17,7 +17,7 @@ HEADER = os.path.join(ROOT, "include", "mi_ops.h")
 
 def _declared():
     src = open(HEADER).read()
-    return sorted(set(re.findall(r"^(?:int|const char \*)\s+(mi_\w+)\s*\(", src, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t|void|const char \*)\s+(mi_\w+)\s*\(", src, flags=re.M)))
 
 
 def test_library_loads_and_exports_header_symbols():
