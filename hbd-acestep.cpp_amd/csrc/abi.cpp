@@ -856,6 +856,111 @@ int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, c
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 
+// F32 [oc, t, n] contiguous, the velocity/latent layout of the sampler
+static int lat_check(const mi_tensor * x, const mi_tensor * ref) {
+    MI_TRY(check(x));
+    if (x->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (ref && !same_shape(*x, *ref)) {
+        return MI_ERR_SHAPE;
+    }
+    if (x->ne[3] != 1) {
+        return MI_ERR_SHAPE;
+    }
+    if (x->nb[1] != (uint64_t) x->ne[0] * 4 || x->nb[2] != x->nb[1] * (uint64_t) x->ne[1]) {
+        return MI_ERR_STRIDE;
+    }
+    return MI_OK;
+}
+
+int mi_apg_buffer_bytes(const mi_tensor * cond, size_t * bytes) {
+    if (!bytes) {
+        return MI_ERR_NULL;
+    }
+    MI_TRY(lat_check(cond, nullptr));
+    *bytes = (size_t) nelements(*cond) * sizeof(double);
+    return MI_OK;
+}
+
+int mi_apg_forward(const mi_tensor * cond, const mi_tensor * uncond, float guidance_scale, float momentum,
+                   float norm_threshold, void * momentum_buf, size_t momentum_bytes, int first, const mi_tensor * out,
+                   mi_stream stream) {
+    MI_TRY(lat_check(cond, nullptr));
+    MI_TRY(lat_check(uncond, cond));
+    MI_TRY(lat_check(out, cond));
+    if (!std::isfinite(guidance_scale) || !std::isfinite(momentum) || !std::isfinite(norm_threshold)) {
+        return MI_ERR_PARAM;
+    }
+    if (cond->ne[0] > 1024) {
+        return MI_ERR_UNSUPPORTED;  // channels per workgroup
+    }
+    const size_t need = (size_t) nelements(*cond) * sizeof(double);
+    if (need > 0 && (!momentum_buf || momentum_bytes < need)) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(momentum_buf, 8)) {
+        return MI_ERR_ALIGN;
+    }
+    ApgArgs a;
+    a.cond      = (const float *) cond->data;
+    a.uncond    = (const float *) uncond->data;
+    a.out       = (float *) out->data;
+    a.ra        = (double *) momentum_buf;
+    a.oc        = (uint32_t) cond->ne[0];
+    a.t         = (uint32_t) cond->ne[1];
+    a.n         = (uint32_t) cond->ne[2];
+    a.first     = first != 0;
+    a.scale     = guidance_scale;
+    a.threshold = norm_threshold;
+    a.momentum  = (double) momentum;
+    return finish(launch_apg(a, (hipStream_t) stream));
+}
+
+int mi_flow_step(int solver, const mi_tensor * vt, const mi_tensor * xt, float t_curr, float t_next, int history,
+                 const mi_tensor * prev, const mi_tensor * prev2, mi_stream stream) {
+    MI_TRY(lat_check(vt, nullptr));
+    MI_TRY(lat_check(xt, vt));
+    if (solver != MI_SOLVER_EULER && solver != MI_SOLVER_DPM3M) {
+        return MI_ERR_PARAM;
+    }
+    if (!std::isfinite(t_curr) || !std::isfinite(t_next) || history < 0 || history > 2) {
+        return MI_ERR_PARAM;
+    }
+    FlowArgs a{};
+    if (solver == MI_SOLVER_DPM3M) {
+        MI_TRY(lat_check(prev, vt));
+        MI_TRY(lat_check(prev2, vt));
+        a.prev  = (float *) prev->data;
+        a.prev2 = (float *) prev2->data;
+    }
+    a.xt     = (float *) xt->data;
+    a.vt     = (const float *) vt->data;
+    a.n      = (uint64_t) nelements(*vt);
+    a.solver = solver == MI_SOLVER_EULER ? 0 : 1;
+    a.hist   = history;
+    a.t_curr = t_curr;
+    a.t_next = t_next;
+    return finish(launch_flow_step(a, (hipStream_t) stream));
+}
+
+int mi_flow_final(const mi_tensor * xt, const mi_tensor * vt, float t, const mi_tensor * out, mi_stream stream) {
+    MI_TRY(lat_check(vt, nullptr));
+    MI_TRY(lat_check(xt, vt));
+    MI_TRY(lat_check(out, vt));
+    if (!std::isfinite(t)) {
+        return MI_ERR_PARAM;
+    }
+    FlowArgs a{};
+    a.xt     = (float *) xt->data;
+    a.vt     = (const float *) vt->data;
+    a.out    = (float *) out->data;
+    a.n      = (uint64_t) nelements(*vt);
+    a.solver = 2;
+    a.t_curr = t;
+    return finish(launch_flow_step(a, (hipStream_t) stream));
+}
+
 int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi_tensor * y, mi_stream stream) {
     MI_TRY(check(t));
     MI_TRY(check(y));

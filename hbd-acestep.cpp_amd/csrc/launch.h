@@ -171,6 +171,31 @@ void   mul_mat_q8_0_bind(MmvArgs & a, char * ws);
 int    launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s);
 int    launch_q8_0_repack(const char * src, int64_t nb1, uint32_t k, uint32_t n, char * dst, hipStream_t s);
 
+// ---- sampler.hip -----------------------------------------------------------
+struct ApgArgs {
+    const float * cond;    // F32 [n][t][oc]
+    const float * uncond;
+    double *      ra;      // momentum running average [n][t][oc] (kept across steps)
+    float *       out;
+    uint32_t      n, t, oc;
+    int           first;   // the buffer is uninitialized: ra = diff
+    float         scale, threshold;
+    double        momentum;
+};
+struct FlowArgs {
+    float *       xt;      // updated in place (euler, dpm3m)
+    const float * vt;
+    float *       prev;    // dpm3m history (updated in place)
+    float *       prev2;
+    float *       out;     // final step
+    uint64_t      n;
+    int           solver;  // 0 euler, 1 dpm3m, 2 final
+    int           hist;    // dpm3m: stored velocities (0, 1, 2)
+    float         t_curr, t_next;
+};
+int launch_apg(const ApgArgs & a, hipStream_t s);
+int launch_flow_step(const FlowArgs & a, hipStream_t s);
+
 // ---- tsembd.hip ------------------------------------------------------------
 int launch_timestep_embedding(const float * t, int64_t n, int64_t ts, int dim, int max_period, char * y,
                               int64_t ys, hipStream_t s);

@@ -251,6 +251,31 @@ int mi_mul_mat_q8_0_workspace(int64_t k, int64_t n, const mi_tensor * x, size_t 
 int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
                     void * workspace, size_t workspace_bytes, mi_stream stream);
 
+/* The DiT sampler's per-step math on the device (dit_ggml_generate,
+ * dit-sampler.h:408-640), so the latents stay resident across steps.
+ * Latents and velocities are F32 [Oc, T, N], contiguous.
+ * mi_apg_forward: apg_forward (dit-sampler.h:66-118) for N samples at once,
+ *   in double: momentum running average (APGMomentumBuffer, 19-35; momentum
+ *   -0.75 in the reference), per-channel L2 clip over T to norm_threshold
+ *   (2.5), projection onto pred_cond (apg_project, 37-64), out = cond +
+ *   (scale - 1) * orthogonal. momentum_buf: device memory of
+ *   mi_apg_buffer_bytes() (a double per element) kept across the steps of
+ *   one generation; first = 1 on its first use (the buffer is then set).
+ *   Oc <= 1024.
+ * mi_flow_step: one solver step in place, x_next from x_t and v_t
+ *   (solvers/solver-euler.h: xt -= vt * (t_curr - t_next); solver-dpm.h:
+ *   DPM++ 3M with `history` stored velocities in prev / prev2, Euler at 0 and
+ *   AB2 at 1, then prev2 <- prev, prev <- vt; prev/prev2 ignored for Euler).
+ * mi_flow_final: the last step, out = xt - vt * t (dit-sampler.h:601-605). */
+enum { MI_SOLVER_EULER = 0, MI_SOLVER_DPM3M = 1 };
+int mi_apg_buffer_bytes(const mi_tensor * cond, size_t * bytes);
+int mi_apg_forward(const mi_tensor * cond, const mi_tensor * uncond, float guidance_scale, float momentum,
+                   float norm_threshold, void * momentum_buf, size_t momentum_bytes, int first, const mi_tensor * out,
+                   mi_stream stream);
+int mi_flow_step(int solver, const mi_tensor * vt, const mi_tensor * xt, float t_curr, float t_next, int history,
+                 const mi_tensor * prev, const mi_tensor * prev2, mi_stream stream);
+int mi_flow_final(const mi_tensor * xt, const mi_tensor * vt, float t, const mi_tensor * out, mi_stream stream);
+
 /* GGUF reader and load-time weight preparation. Replaces gf_load (mmap, the
  * header parse and the check that every tensor lies inside the file,
  * gguf-weights.h:74-154), gf_load_tensor / gf_load_tensor_f32 (156-268),

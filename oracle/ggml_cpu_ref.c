@@ -550,3 +550,94 @@ void orc_mul_mat_q8_0(const uint8_t * w, const float * x, int64_t n, int64_t k, 
     }
     free(xq);
 }
+
+/* ------------------------------------------------------------------------ */
+/* DiT sampler step math (dit-sampler.h): apg_forward (66-118) with its      */
+/* momentum buffer (19-35) and apg_project (37-64), in double, channels      */
+/* summed over T in order; Euler (solvers/solver-euler.h) and DPM++ 3M       */
+/* (solvers/solver-dpm.h) steps and the final x0 step (601-605) in fp32.     */
+/* Layout [n][t][oc].                                                        */
+/* ------------------------------------------------------------------------ */
+void orc_apg_forward(const float * cond, const float * uncond, int64_t n, int64_t t, int64_t oc, float scale,
+                     double momentum, float threshold, double * ra, int first, float * out) {
+    for (int64_t b = 0; b < n; b++) {
+        const float * pc = cond + b * t * oc;
+        const float * pu = uncond + b * t * oc;
+        double *      r  = ra + b * t * oc;
+        float *       y  = out + b * t * oc;
+        const int64_t m  = t * oc;
+        double *      d  = (double *) malloc((size_t) m * sizeof(double) + 8);
+        for (int64_t i = 0; i < m; i++) {
+            const double v = (double) pc[i] - (double) pu[i];
+            r[i]           = first ? v : v + momentum * r[i];
+            d[i]           = r[i];
+        }
+        if (threshold > 0.0f) {
+            for (int64_t c = 0; c < oc; c++) {
+                double n2 = 0.0;
+                for (int64_t k = 0; k < t; k++) {
+                    n2 += d[k * oc + c] * d[k * oc + c];
+                }
+                const double nrm = sqrt(n2 > 0.0 ? n2 : 0.0);
+                const double sc  = nrm > 1e-60 ? fmin(1.0, (double) threshold / nrm) : 1.0;
+                if (sc < 1.0) {
+                    for (int64_t k = 0; k < t; k++) {
+                        d[k * oc + c] *= sc;
+                    }
+                }
+            }
+        }
+        const double w = (double) scale - 1.0;
+        for (int64_t c = 0; c < oc; c++) {
+            double n2 = 0.0;
+            for (int64_t k = 0; k < t; k++) {
+                n2 += (double) pc[k * oc + c] * (double) pc[k * oc + c];
+            }
+            const double inv = n2 > 1e-60 ? 1.0 / sqrt(n2) : 0.0;
+            double       dot = 0.0;
+            for (int64_t k = 0; k < t; k++) {
+                dot += d[k * oc + c] * ((double) pc[k * oc + c] * inv);
+            }
+            for (int64_t k = 0; k < t; k++) {
+                const int64_t i   = k * oc + c;
+                const double  v1n = (double) pc[i] * inv;
+                const double  orth = d[i] - dot * v1n;
+                y[i]               = (float) ((double) pc[i] + w * orth);
+            }
+        }
+        free(d);
+    }
+}
+
+void orc_flow_step(int solver, float * xt, const float * vt, int64_t n, float t_curr, float t_next, int hist,
+                   float * prev, float * prev2) {
+    const float dt = t_curr - t_next;
+    for (int64_t i = 0; i < n; i++) {
+        float ve = vt[i];
+        if (solver == 1) {
+            if (hist >= 2) {
+                const float c0 = 23.0f / 12.0f, c1 = 16.0f / 12.0f, c2 = 5.0f / 12.0f;
+                ve = c0 * vt[i] - c1 * prev[i] + c2 * prev2[i];
+            } else if (hist == 1) {
+                ve = 1.5f * vt[i] - 0.5f * prev[i];
+            }
+        }
+        const float p = ve * dt;
+        xt[i]         = xt[i] - p;
+    }
+    if (solver == 1) {
+        for (int64_t i = 0; i < n; i++) {
+            if (hist >= 1) {
+                prev2[i] = prev[i];
+            }
+            prev[i] = vt[i];
+        }
+    }
+}
+
+void orc_flow_final(const float * xt, const float * vt, int64_t n, float t, float * out) {
+    for (int64_t i = 0; i < n; i++) {
+        const float p = vt[i] * t;
+        out[i]        = xt[i] - p;
+    }
+}

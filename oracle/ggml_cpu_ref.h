@@ -131,6 +131,16 @@ void orc_flash_attn_ext(const float * q, const float * k, const float * v, const
  *      sum_b fp16(d_w) fp16(d_x) sum_i q_w q_x, rounded to float once. ---- */
 void orc_mul_mat_q8_0(const uint8_t * w, const float * x, int64_t n, int64_t k, int64_t m, float * y);
 
+/* ---- DiT sampler step math (dit-sampler.h:19-118, 601-605; solvers/): APG in
+ *      double with channel sums over T in order; Euler / DPM++ 3M steps
+ *      (solver 0 / 1, hist = stored velocities) and the final x0 step in fp32,
+ *      without contraction. Layout [n][t][oc]; ra is the momentum buffer. ---- */
+void orc_apg_forward(const float * cond, const float * uncond, int64_t n, int64_t t, int64_t oc, float scale,
+                     double momentum, float threshold, double * ra, int first, float * out);
+void orc_flow_step(int solver, float * xt, const float * vt, int64_t n, float t_curr, float t_next, int hist,
+                   float * prev, float * prev2);
+void orc_flow_final(const float * xt, const float * vt, int64_t n, float t, float * out);
+
 #ifdef __cplusplus
 }
 #endif

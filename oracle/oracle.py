@@ -69,6 +69,12 @@ def lib():
         L.orc_flash_attn_ext.argtypes = [_fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                          ctypes.c_float, ctypes.c_int, _fp]
         L.orc_mul_mat_q8_0.argtypes = [_u8p, _fp, _i64, _i64, _i64, _fp]
+        _dp = ctypes.POINTER(ctypes.c_double)
+        L.orc_apg_forward.argtypes = [_fp, _fp, _i64, _i64, _i64, ctypes.c_float, ctypes.c_double, ctypes.c_float,
+                                      _dp, ctypes.c_int, _fp]
+        L.orc_flow_step.argtypes = [ctypes.c_int, _fp, _fp, _i64, ctypes.c_float, ctypes.c_float, ctypes.c_int, _fp,
+                                    _fp]
+        L.orc_flow_final.argtypes = [_fp, _fp, _i64, ctypes.c_float, _fp]
         L.orc_set_threads.argtypes = [ctypes.c_int]
         L.orc_get_threads.restype = ctypes.c_int
         _lib = L
@@ -344,3 +350,36 @@ def mul_mat_q8_0(w: np.ndarray, x) -> np.ndarray:
     y = np.empty((m, n), np.float32)
     lib().orc_mul_mat_q8_0(w.ctypes.data_as(_u8p), _f(x), n, k, m, _f(y))
     return y
+
+
+def apg_forward(cond, uncond, scale: float, ra: np.ndarray, first: bool, momentum: float = -0.75,
+                threshold: float = 2.5) -> np.ndarray:
+    """APG over samples: cond, uncond F32 (n, t, oc); ra float64 (n, t, oc), updated in place."""
+    cond, uncond = _c32(cond), _c32(uncond)
+    assert ra.dtype == np.float64 and ra.flags.c_contiguous and ra.shape == cond.shape
+    n, t, oc = cond.shape
+    out = np.empty_like(cond)
+    lib().orc_apg_forward(_f(cond), _f(uncond), n, t, oc, scale, momentum, threshold,
+                          ra.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), int(first), _f(out))
+    return out
+
+
+SOLVERS = {"euler": 0, "dpm3m": 1}
+
+
+def flow_step(solver: str, xt: np.ndarray, vt, t_curr: float, t_next: float, hist: int = 0, prev=None,
+              prev2=None) -> None:
+    """One solver step, in place on xt (and prev/prev2 for dpm3m); all F32 contiguous."""
+    vt = _c32(vt)
+    assert xt.dtype == np.float32 and xt.flags.c_contiguous
+    z = np.zeros(1, np.float32)
+    pp = prev if prev is not None else z
+    p2 = prev2 if prev2 is not None else z
+    lib().orc_flow_step(SOLVERS[solver], _f(xt), _f(vt), xt.size, t_curr, t_next, hist, _f(pp), _f(p2))
+
+
+def flow_final(xt, vt, t: float) -> np.ndarray:
+    xt, vt = _c32(xt), _c32(vt)
+    out = np.empty_like(xt)
+    lib().orc_flow_final(_f(xt), _f(vt), xt.size, t, _f(out))
+    return out

@@ -214,6 +214,32 @@ def test_mul_mat_q8_0_validation():
     assert L.mi_mul_mat_q8_0_workspace(k, 0, R(x), ctypes.byref(nb)) == 0 and nb.value == 0
 
 
+def test_sampler_validation():
+    oc, t, n = 64, 100, 2
+    c = _t([oc, t, n])
+    nb = ctypes.c_size_t(0)
+    M = ctypes.c_void_p(1 << 20)
+    assert L.mi_apg_buffer_bytes(R(c), ctypes.byref(nb)) == 0 and nb.value == oc * t * n * 8
+    apg = L.mi_apg_forward
+    assert apg(R(c), R(_t([oc, t + 1, n])), 3.0, -0.75, 2.5, M, nb.value, 1, R(c), NULL_S) == -3
+    assert apg(R(c), R(c), 3.0, -0.75, 2.5, M, nb.value, 1, R(_t([oc, t, n], BF16)), NULL_S) == -2
+    assert apg(R(c), R(c), float("inf"), -0.75, 2.5, M, nb.value, 1, R(c), NULL_S) == -6
+    assert apg(R(c), R(c), 3.0, -0.75, 2.5, None, 0, 1, R(c), NULL_S) == -6           # no momentum buffer
+    assert apg(R(c), R(c), 3.0, -0.75, 2.5, M, nb.value - 8, 1, R(c), NULL_S) == -6
+    assert apg(R(c), R(c), 3.0, -0.75, 2.5, ctypes.c_void_p((1 << 20) + 4), nb.value, 1, R(c), NULL_S) == -5
+    big = _t([1100, 2, 1])
+    assert apg(R(big), R(big), 3.0, -0.75, 2.5, M, 1 << 30, 1, R(big), NULL_S) == -7  # more than 1024 channels
+    strided = _t([oc, t, n], nb=[4, oc * 8, oc * 8 * t, oc * 8 * t * n])
+    assert apg(R(strided), R(strided), 3.0, -0.75, 2.5, M, nb.value, 1, R(strided), NULL_S) == -4
+    st = L.mi_flow_step
+    assert st(7, R(c), R(c), 1.0, 0.5, 0, None, None, NULL_S) == -6                  # unknown solver
+    assert st(0, R(c), R(c), 1.0, float("nan"), 0, None, None, NULL_S) == -6
+    assert st(1, R(c), R(c), 1.0, 0.5, 3, R(c), R(c), NULL_S) == -6                  # history 0..2
+    assert st(1, R(c), R(c), 1.0, 0.5, 0, None, R(c), NULL_S) == -1                  # dpm3m needs prev
+    assert st(0, R(c), R(_t([oc, t, n + 1])), 1.0, 0.5, 0, None, None, NULL_S) == -3
+    assert L.mi_flow_final(R(c), R(c), float("inf"), R(c), NULL_S) == -6
+
+
 def test_chain_validation():
     io = _lib.MiDitBlockIO()
     io.hidden = _t([2048, 4])
