@@ -644,6 +644,69 @@ def gemv_bench(steps: int):
         device.synchronize()
 
 
+# ---------------------------------------------------------------------------
+# One whole Qwen3-4B decoder layer on the device (reported with --decode-layer):
+# batch 8, Q8_0 weights, Q8_0 KV cache of 8192 slots per sequence, lengths
+# U[1, 8192] and the 256-bucketed read (qw3lm_forward_batch, qwen3-lm.h:626-741).
+# ---------------------------------------------------------------------------
+def decode_layer_bench(steps: int):
+    from acestep_ops import device, ops
+    from acestep_ops.device import DTensor, Event, Graph, Stream
+    from acestep_ops.qwen3 import Qwen3DecodeLayer, decode_mask
+
+    H, Nh, Nkv, D, I, N, SLOTS = 2560, 32, 8, 128, 9728, 8, 8192
+    rng = np.random.default_rng(11)
+    lens = rng.integers(1, SLOTS + 1, N)
+    pos = (lens - 1).astype(np.int32)
+    read = min(SLOTS, int((lens.max() + 255) // 256 * 256))
+    st = Stream()
+    sh = st.handle
+
+    def q8w(n, k):
+        nbk = k // 32
+        b = np.empty((n, nbk, 34), np.uint8)
+        b[:, :, 2:] = rng.integers(-127, 128, (n, nbk, 32), dtype=np.int8).view(np.uint8)
+        b[:, :, :2] = (rng.uniform(0.5, 1.0, (n, nbk)) * 2e-3).astype(np.float16).view(np.uint8).reshape(n, nbk, 2)
+        return ops.Q8(DTensor.from_numpy(b.reshape(n, nbk * 34)))
+
+    ones = lambda n: DTensor.from_numpy(np.ones(n, np.float32))  # noqa: E731
+    layer = Qwen3DecodeLayer(q8w((Nh + 2 * Nkv) * D, H), q8w(H, Nh * D), q8w(2 * I, H), q8w(H, I), ones(H), ones(H),
+                             ones(D), ones(D), H, Nh, Nkv, D, I, SLOTS, N, "q8_0", stream=sh)
+    kb = np.zeros((N, Nkv, SLOTS, D // 32 * 34), np.uint8)
+    kb[..., 2:] = rng.integers(-127, 128, kb[..., 2:].shape, dtype=np.int8).view(np.uint8)
+    kb.reshape(-1, 34)[:, :2] = np.full((kb.size // 34, 1), 1e-2, np.float16).view(np.uint8)
+    layer.k_cache = ops.Q8(DTensor.from_numpy(kb))
+    layer.v_cache = ops.Q8(DTensor.from_numpy(kb))
+    hidden = DTensor.from_numpy(rng.standard_normal((N, H), dtype=np.float32))
+    out = DTensor.empty((N, H), "f32")
+    dpos, dsets = DTensor.from_numpy(pos), DTensor.from_numpy(np.arange(N, dtype=np.int32))
+    mask = decode_mask(pos, read)
+    layer.forward(hidden, dpos, dsets, 0, read, mask, out=out)
+    st.synchronize()
+    g = Graph()
+    with g.capture(st):
+        for _ in range(steps):
+            layer.forward(hidden, dpos, dsets, 0, read, mask, out=out)
+    g.launch()
+    st.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(sh)
+    g.launch()
+    e1.record(sh)
+    e1.synchronize()
+    us = 1000.0 * e0.elapsed_ms(e1) / steps
+    wbytes = sum(w.n * (w.k // 32) * 34 for w in layer.w.values())
+    kvb = N * Nkv * read * (D // 32 * 34) * 2
+    print(json.dumps({"config": f"Qwen3-4B decode layer, batch {N}, Q8_0 weights and KV cache ({SLOTS} slots, lengths "
+                                f"U[1,{SLOTS}], read {read}), every op on the device",
+                      "us_per_layer": round(us, 2), "weight_bytes": wbytes, "kv_bytes_read": kvb,
+                      "GB/s": round((wbytes + kvb) / (us * 1e-6) / 1e9, 1),
+                      "frac": round((wbytes + kvb) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+                      "tokens_per_s_36_layers": round(N / (36 * us * 1e-6), 1)}), flush=True)
+    del layer, g
+    device.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -658,6 +721,8 @@ def main():
                     help="time the Qwen3 layer op chains at the C1/C2/C4/C5 shapes instead (one JSON line each)")
     ap.add_argument("--attention", action="store_true",
                     help="time flash attention over the KV cache at the C2 decode shape (one JSON line per cache type)")
+    ap.add_argument("--decode-layer", action="store_true",
+                    help="time one whole Qwen3-4B decoder layer at batch 8 (Q8_0 weights and KV cache), all on the device")
     ap.add_argument("--gemv", action="store_true",
                     help="time the Q8_0 mul_mat of the Qwen3-4B decode projections and LM head at batch 8")
     args = ap.parse_args()
@@ -681,6 +746,9 @@ def main():
         return
     if args.gemv:
         gemv_bench(args.steps)
+        return
+    if args.decode_layer:
+        decode_layer_bench(args.steps)
         return
     kb = block_bytes(ROWS, fused=True)
     kb_u = block_bytes(ROWS, fused=False)

@@ -1,0 +1,108 @@
+"""One Qwen3 decoder layer for batched decode, every op on the device
+(qw3lm_forward_batch, qwen3-lm.h:626-741), with Q8_0 weights and a Q8_0 or
+F16 KV cache:
+
+  norm   = rms_norm(hidden) * input_layernorm                    (630)
+  qkv    = mul_mat(W_qkv, norm); q, k, v = views of qkv           (637-642)
+  q, k   = rope(rms_norm(q|k) * q_norm|k_norm)                    (659-667)
+  cache  <- k, v at slot kv_pos of each sequence's set            (682-703)
+  attn   = flash_attn_ext(q, K[:read_len], V[:read_len], mask, 1/sqrt(D))  (706-723)
+  hidden = hidden + mul_mat(W_o, attn)                            (729-733)
+  norm2  = rms_norm(hidden) * post_attention_layernorm            (736; fused with the add)
+  hidden = hidden + mul_mat(W_down, swiglu(mul_mat(W_gate_up, norm2)))  (737-741)
+
+Shapes outermost first: hidden (N, H) F32 for N sequences of one token; the
+caches (n_sets, Nkv, max_seq, D) (ggml [D, max_seq, Nkv, n_sets]); sequence i
+uses set s0 + i, writes at pos[i] and attends to read_len slots under a mask
+(N, 1, 1, read_len) F16 that is 0 up to pos[i] and -inf after."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import ops
+from .device import DTensor
+
+
+def decode_mask(pos, read_len: int) -> DTensor:
+    """F16 (N, 1, 1, read_len): 0 for slots <= pos[i] (the token just written
+    included), -inf after -- the batched decode mask (qwen3-lm.h:582-596)."""
+    pos = np.asarray(pos)
+    m = np.where(np.arange(read_len)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float16)
+    return DTensor.from_numpy(m.reshape(len(pos), 1, 1, read_len).view(np.uint16), "f16")
+
+
+class Qwen3DecodeLayer:
+    def __init__(self, w_qkv, w_o, w_gate_up, w_down, in_norm_w, post_norm_w, q_norm_w, k_norm_w, H: int, Nh: int,
+                 Nkv: int, D: int, I: int, max_seq: int, n_sets: int, kv_type: str = "q8_0", eps: float = 1e-6,
+                 rope_theta: float = 1e6, stream=None):
+        """w_*: Q8 weights in the GGUF layout (repacked here once); norms: F32 DTensors."""
+        self.H, self.Nh, self.Nkv, self.D, self.I = H, Nh, Nkv, D, I
+        self.eps, self.theta, self.stream = eps, rope_theta, stream
+        self.w = {name: ops.q8_0_repack(w, stream=stream)
+                  for name, w in (("qkv", w_qkv), ("o", w_o), ("gu", w_gate_up), ("down", w_down))}
+        self.in_norm_w, self.post_norm_w = in_norm_w, post_norm_w
+        self.q_norm_w, self.k_norm_w = q_norm_w, k_norm_w
+        self.kv_type = kv_type
+        if kv_type == "q8_0":
+            self.k_cache = ops.Q8(DTensor.zeros((n_sets, Nkv, max_seq, D // 32 * 34), "u8"))
+            self.v_cache = ops.Q8(DTensor.zeros((n_sets, Nkv, max_seq, D // 32 * 34), "u8"))
+        elif kv_type == "f16":
+            self.k_cache = DTensor.zeros((n_sets, Nkv, max_seq, D), "f16")
+            self.v_cache = DTensor.zeros((n_sets, Nkv, max_seq, D), "f16")
+        else:
+            raise ValueError("kv_type: q8_0 or f16")
+        self._bufs = {}
+
+    def _buf(self, name, shape, dtype="f32"):
+        b = self._bufs.get(name)
+        if b is None or b.shape != tuple(shape):
+            b = DTensor.empty(tuple(shape), dtype)
+            self._bufs[name] = b
+        return b
+
+    def _cache_view(self, c, s0, n, read_len):
+        if isinstance(c, ops.Q8):
+            return ops.Q8(c.data[s0:s0 + n, :, :read_len])
+        return c[s0:s0 + n, :, :read_len]
+
+    def forward(self, hidden, pos, sets, s0: int, read_len: int, mask, out=None):
+        """hidden (N, H) F32 -> new hidden (N, H); pos, sets: (N,) I32 device tensors."""
+        N, H, Nh, Nkv, D, I = hidden.shape[0], self.H, self.Nh, self.Nkv, self.D, self.I
+        st = self.stream
+        qkv_dim = (Nh + 2 * Nkv) * D
+        norm = ops.rms_norm(hidden, self.eps, self.in_norm_w, out=self._buf("norm", (N, H)), stream=st)
+        qkv = ops.mul_mat_q8_0(self.w["qkv"], norm, out=self._buf("qkv", (N, qkv_dim)),
+                               workspace=self._ws("qkv", norm), stream=st)
+        q = qkv[:, 0:Nh * D].unflatten(1, (Nh, D))
+        k = qkv[:, Nh * D:(Nh + Nkv) * D].unflatten(1, (Nkv, D))
+        v = qkv[:, (Nh + Nkv) * D:qkv_dim].unflatten(1, (Nkv, D))
+        qo, ko = ops.qk_norm_rope(q, self.q_norm_w, pos, self.eps, D, self.theta, k=k, k_w=self.k_norm_w,
+                                  q_out=self._buf("qo", (N, Nh, D)), k_out=self._buf("ko", (N, Nkv, D)), stream=st)
+        ops.kv_store(ko.unflatten(0, (N, 1)), self.k_cache, pos, v=v.unflatten(0, (N, 1)), v_cache=self.v_cache,
+                     sets=sets, stream=st)
+        kv = self._cache_view(self.k_cache, s0, N, read_len)
+        vv = self._cache_view(self.v_cache, s0, N, read_len)
+        qf = qo.unflatten(1, (Nh, 1))
+        attn = self._buf("attn", (N, 1, Nh, D))
+        ws = self._fa_ws(qf, kv, vv)
+        ops.flash_attn_ext(qf, kv, vv, mask, 1.0 / math.sqrt(D), out=attn, workspace=ws, stream=st)
+        a2 = attn.view(N, Nh * D)
+        ao = ops.mul_mat_q8_0(self.w["o"], a2, out=self._buf("ao", (N, H)), workspace=self._ws("o", a2), stream=st)
+        h1, n2 = ops.add_rms_norm(hidden, ao, self.eps, w=self.post_norm_w, out_sum=self._buf("h1", (N, H)),
+                                  out_norm=self._buf("n2", (N, H)), stream=st)
+        gu = ops.mul_mat_q8_0(self.w["gu"], n2, out=self._buf("gu", (N, 2 * I)), workspace=self._ws("gu", n2),
+                              stream=st)
+        ff = ops.swiglu(gu, out=self._buf("ff", (N, I)), stream=st)
+        mlp = ops.mul_mat_q8_0(self.w["down"], ff, out=self._buf("mlp", (N, H)), workspace=self._ws("down", ff),
+                               stream=st)
+        return ops.add(h1, mlp, out=out if out is not None else self._buf("out", (N, H)), stream=st)
+
+    def _ws(self, name, x):
+        need = ops.mul_mat_q8_0_workspace(self.w[name], x)
+        return self._buf("ws_" + name, (max(need, 1),), "u8")
+
+    def _fa_ws(self, q, k, v):
+        need = ops.flash_attn_workspace(q, k, v)
+        return self._buf("ws_fa", (max(need, 1),), "u8")
