@@ -744,8 +744,9 @@ int mi_flash_attn_ext(const mi_tensor * q, const mi_tensor * k, const mi_tensor 
     if (!aligned(workspace, 16)) {
         return MI_ERR_ALIGN;
     }
-    a.ws   = (float *) workspace;
-    a.msum = a.mfma && a.mask ? (uint8_t *) workspace : nullptr;
+    a.ws    = (float *) workspace;
+    a.msum  = a.mfma && a.mask ? (uint8_t *) workspace : nullptr;
+    a.fpart = a.mfma && a.tsplit > 0 ? (float *) ((char *) workspace + flash_attn_part_offset(a)) : nullptr;
     return finish(launch_flash_attn(a, k->type, (int) q->ne[0], (hipStream_t) stream));
 }
 

@@ -38,6 +38,8 @@ namespace mi {
 constexpr int FA_TILE = 32;  // keys per tile
 constexpr int FA_MAXT = 16;  // tiles per split at most (the split's mask is staged in LDS)
 constexpr int FA_MAX_SPLITS = 1024;  // splits of one key range at most (the merge keeps their weights in LDS)
+// floats per row of a matrix-core split half: m, l, 2 unused, o[128] (16-byte aligned rows)
+constexpr int FA_PART = 132;
 
 template <int KT> struct FaT;
 template <> struct FaT<MI_TYPE_F32> {
@@ -728,10 +730,20 @@ k_fa_mfma(const FaArgs a) {
     const int      lane = tid & 63;
     const int      n    = lane & 31;  // this lane's query row within the wave
     const int      hh   = lane >> 5;
-    const uint32_t bg   = blockIdx.y;
+    // work item = (row block, sequence and KV head); the items after the first
+    // tfull run as two workgroups, one per half of the key tiles (the last,
+    // partial round of workgroups then ends in half the time), and leave partials
+    uint32_t item = blockIdx.x, part = 0;
+    if (item >= a.tfull) {
+        const uint32_t j = item - a.tfull;
+        item             = a.tfull + j / 2;
+        part             = 1 + (j & 1);
+    }
+    const uint32_t rbk  = item % (uint32_t) a.rblk;
+    const uint32_t bg   = item / (uint32_t) a.rblk;
     const uint32_t b    = bg / (uint32_t) a.nkv;
     const uint32_t g    = bg - b * (uint32_t) a.nkv;
-    const int      r    = blockIdx.x * BQ + wave * 32 + n;
+    const int      r    = (int) rbk * BQ + wave * 32 + n;
     const bool     rvld = r < a.rows;
     const int      rc   = rvld ? r : a.rows - 1;
     const int      iq   = rc / a.rk;
@@ -864,22 +876,24 @@ k_fa_mfma(const FaArgs a) {
     float       mrun = -INFINITY, lrun = 0.0f;
     const float sl2  = a.scale * 1.4426950408889634f;  // scale * log2(e)
     const int   ntl  = (a.n_kv + BK - 1) / BK;
-    const bool  allr = (int) (blockIdx.x * BQ + BQ) <= a.rows;  // every row of the workgroup valid
+    const bool  allr = (int) (rbk * BQ + BQ) <= a.rows;  // every row of the workgroup valid
+    const int   tb   = part == 2 ? a.tmid : 0;             // this workgroup's key tiles [tb, te)
+    const int   te   = part == 1 ? a.tmid : ntl;
     // per tile, from the mask summary of this lane's row (one tile ahead): does
     // the wave read the tile's mask values, does it have a live key at all
     const uint8_t * sp =
         a.msum ? a.msum + (((int64_t) (b % (uint32_t) a.mne3) * a.mne2 + h % a.mne2) * a.ngq + iq / 16) * ntl
                : nullptr;
-    auto flag = [&](int t) -> int { return t < ntl ? (sp ? (int) sp[t] : 1) : 0; };
-    int  fcur = flag(0);
-    load_tile(0);
+    auto flag = [&](int t) -> int { return t < te ? (sp ? (int) sp[t] : 1) : 0; };
+    int  fcur = flag(tb);
+    load_tile(tb * BK);
     store_tile(0);
     __syncthreads();
-    for (int t = 0; t < ntl; ++t) {
-        const int cur   = t & 1;
+    for (int t = tb; t < te; ++t) {
+        const int cur   = (t - tb) & 1;
         const int t0    = t * BK;
         const int fnext = flag(t + 1);
-        if (t + 1 < ntl) {
+        if (t + 1 < te) {
             load_tile(t0 + BK);  // in flight during this tile's math
         }
         if (__builtin_amdgcn_ballot_w64(rvld && (fcur & 1)) != 0) {  // some row of the wave has a live key
@@ -991,7 +1005,7 @@ k_fa_mfma(const FaArgs a) {
         }
         lrun += psum;
         }  // live
-        if (t + 1 < ntl) {
+        if (t + 1 < te) {
             store_tile(cur ^ 1);
         }
         fcur = fnext;
@@ -999,6 +1013,24 @@ k_fa_mfma(const FaArgs a) {
     }
     // rows: sum over both half-waves' keys; y[b][iq][h][d], d = 32 db + 8 j + 4 hh + i
     lrun = lrun + __shfl_xor(lrun, 32, 64);
+    if (part != 0) {  // half of the keys: (m, l, o) relative to exp2(m), merged by k_fa_mfma_combine
+        if (rvld) {
+            float * pp = a.fpart + ((size_t) (blockIdx.x - a.tfull) * BQ + wave * 32 + n) * FA_PART;
+            if (hh == 0) {
+                pp[0] = mrun;
+                pp[1] = lrun;
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    *(float4 *) (pp + 4 + 32 * db + 8 * j + 4 * hh) =
+                        make_float4(o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]);
+                }
+            }
+        }
+        return;
+    }
     if (rvld) {
         const float inv = 1.0f / lrun;  // all keys masked: 0 * inf = NaN, as ggml
         float *     yp  = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) iq * a.y2 + (int64_t) h * a.y1);
@@ -1022,6 +1054,40 @@ k_fa_mfma(const FaArgs a) {
     }
 }
 
+// Merge the two key halves of a split work item (its 128 rows): with w_i =
+// exp2(m_i - max m) (0 for a half with no live key), y = (w_0 o_0 + w_1 o_1) /
+// (w_0 l_0 + w_1 l_1); a row with no live key in either half is NaN, as ggml.
+// 8 rows per workgroup, 32 lanes per row, 4 columns per lane.
+__global__ void __launch_bounds__(256) k_fa_mfma_combine(const FaArgs a) {
+    const uint32_t row  = blockIdx.x * 8 + threadIdx.x / 32;  // split item * 128 + row of the block
+    const uint32_t j    = row / 128, rr = row % 128;
+    const uint32_t item = a.tfull + j;
+    const uint32_t rbk  = item % (uint32_t) a.rblk;
+    const uint32_t bg   = item / (uint32_t) a.rblk;
+    const int      r    = (int) (rbk * 128 + rr);
+    if (r >= a.rows) {
+        return;
+    }
+    const uint32_t b  = bg / (uint32_t) a.nkv;
+    const uint32_t g  = bg - b * (uint32_t) a.nkv;
+    const int      iq = r / a.rk;
+    const int      h  = (int) g * a.rk + (r - iq * a.rk);
+    const float *  p0 = a.fpart + ((size_t) (2 * j) * 128 + rr) * FA_PART;
+    const float *  p1 = a.fpart + ((size_t) (2 * j + 1) * 128 + rr) * FA_PART;
+    const float2   s0 = *(const float2 *) p0, s1 = *(const float2 *) p1;  // (m, l)
+    const float    mx = fmaxf(s0.x, s1.x);
+    const float    w0 = s0.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s0.x - mx);
+    const float    w1 = s1.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s1.x - mx);
+    const float    il = 1.0f / (w0 * s0.y + w1 * s1.y);
+    const int      d  = 4 * (threadIdx.x % 32);
+    const float4   o0 = *(const float4 *) (p0 + 4 + d), o1 = *(const float4 *) (p1 + 4 + d);
+    float *        yp = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) iq * a.y2 + (int64_t) h * a.y1);
+    yp[d]             = (w0 * o0.x + w1 * o1.x) * il;
+    yp[d + 1]         = (w0 * o0.y + w1 * o1.y) * il;
+    yp[d + 2]         = (w0 * o0.z + w1 * o1.z) * il;
+    yp[d + 3]         = (w0 * o0.w + w1 * o1.w) * il;
+}
+
 // query rows per wave: 4, or 8 for 16-bit and Q8_0 K/V at D = 64 (more would
 // spill registers: each row keeps its output columns and scores in registers)
 static int fa_rb(int rows, int D, int kt) {
@@ -1043,6 +1109,19 @@ void flash_attn_plan(FaArgs & a, int D) {
         a.chunk  = a.n_kv;
         a.splits = 1;
         a.ngq    = (a.n_q + 15) / 16;
+        // whole items fill full rounds of the resident workgroups (two per CU);
+        // a last round at most half full runs as key halves instead
+        a.rblk             = (a.rows + 127) / 128;
+        const int64_t items = (int64_t) a.rblk * a.nb * a.nkv;
+        const int64_t slots = (int64_t) num_cus() * 2;
+        const int64_t rest  = items % slots;
+        const int     ntl   = (a.n_kv + 63) / 64;
+        a.tmid              = (ntl + 1) / 2;
+        a.tfull             = (int) items;
+        if (items > slots && rest > 0 && 2 * rest <= slots && ntl >= 2) {
+            a.tfull = (int) (items - rest);
+        }
+        a.tsplit = (int) (items - a.tfull);
         return;
     }
     if (a.n_kv == 0 || a.rows == 0 || a.nb == 0) {  // no keys: one pass that writes NaN rows (0 * (1/0), as ggml)
@@ -1064,9 +1143,15 @@ void flash_attn_plan(FaArgs & a, int D) {
     a.splits             = (int) ((a.n_kv + a.chunk - 1) / a.chunk);
 }
 
+size_t flash_attn_part_offset(const FaArgs & a) {
+    const size_t msum = (size_t) a.nb * a.nh * a.ngq * ((a.n_kv + 63) / 64);
+    return (msum + 255) / 256 * 256;
+}
+
 size_t flash_attn_workspace(const FaArgs & a, int D) {
-    if (a.mfma) {  // the mask summary, sized for the largest mask a call may pass (one per batch and head)
-        return (size_t) a.nb * a.nh * a.ngq * ((a.n_kv + 63) / 64);
+    if (a.mfma) {  // the mask summary, sized for the largest mask a call may pass (one per batch and head),
+                   // then the partials of split items
+        return flash_attn_part_offset(a) + (size_t) a.tsplit * 2 * 128 * FA_PART * sizeof(float);
     }
     return a.splits > 1 ? (size_t) a.splits * a.nb * a.nkv * a.rows * (D + 2) * sizeof(float) : 0;
 }
@@ -1118,11 +1203,14 @@ int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
                                                        (uint32_t) (a.mne3 * a.mne2)),
                                dim3(64), 0, s, a);
         }
-        const dim3 grid((uint32_t) ((a.rows + 127) / 128), (uint32_t) (a.nb * a.nkv));
+        const dim3 grid((uint32_t) (a.tfull + 2 * a.tsplit));
         if (kt == MI_TYPE_BF16) {
             hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_BF16, 128>), grid, dim3(256), 0, s, a);
         } else {
             hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_F16, 128>), grid, dim3(256), 0, s, a);
+        }
+        if (a.tsplit > 0) {
+            hipLaunchKernelGGL(k_fa_mfma_combine, dim3((uint32_t) a.tsplit * 16), dim3(256), 0, s, a);
         }
         return MI_OK;
     }

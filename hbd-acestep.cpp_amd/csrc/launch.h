@@ -139,10 +139,16 @@ struct FaArgs {
     float        scale;
     int          rows, rblocks, chunk, splits;  // from flash_attn_plan
     float *      ws;                            // split partials (flash_attn_workspace bytes)
+    // matrix-core path: row blocks of 128 per (sequence, KV head); work items
+    // [0, tfull) whole, the next tsplit as two halves of the key tiles (tiles
+    // [0, tmid) and [tmid, end)) whose partials go to fpart
+    int          rblk, tfull, tsplit, tmid;
+    float *      fpart;
 };
 
 void   flash_attn_plan(FaArgs & a, int D);
 size_t flash_attn_workspace(const FaArgs & a, int D);
+size_t flash_attn_part_offset(const FaArgs & a);
 int    launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s);
 
 // ---- matmul.hip ------------------------------------------------------------

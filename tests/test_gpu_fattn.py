@@ -195,3 +195,34 @@ def test_mfma_prefill(dev, kt, qt, rk, masked):
         mask = np.where(np.abs(i * 1.6 - j) <= 70, 0.0, -np.inf).astype(np.float32)[None, None]
         mask[..., 5, :] = -np.inf  # one query position with every key masked: NaN rows
     _run(2, nkv * rk, nkv, n_q, n_kv, 128, kt, qt, mask=mask, seed=7)
+
+
+@pytest.mark.parametrize("kt,n_kv,masked", [("bf16", 333, True), ("f16", 269, False)])
+def test_mfma_tail_split(dev, kt, n_kv, masked):
+    """More 128-row work items than two rounds of resident workgroups fill, with a last
+    round at most half full: those last items run as two halves of the key tiles and a
+    second kernel merges the halves. 16 items over a full round (2 x 8 KV heads x one
+    extra row block, the last one ragged), an even and an odd number of key tiles; the
+    masked case has rows whose second half has no live key, and a fully masked row."""
+    # the smallest such shape on this device: the workspace holds the partials of the
+    # split items after the mask summary, so it grows past the summary exactly then
+    qall = DTensor.empty((2, 16, 64 * 400, 128), "f32")
+    kv = DTensor.empty((2, 8, n_kv, 128), kt)
+    n_q = None
+    for rblk in range(2, 400):
+        nq = 64 * rblk - 28  # rows = 2 n_q = 128 rblk - 56: a ragged last row block
+        msum = -(-(2 * 16 * ((nq + 15) // 16) * ((n_kv + 63) // 64)) // 256) * 256
+        ws = ops.flash_attn_workspace(qall[:, :, :nq], kv, kv)
+        if ws > msum:
+            assert ws == msum + (ws - msum) // (2 * 128 * 132 * 4) * (2 * 128 * 132 * 4)
+            n_q = nq
+            break
+    assert n_q is not None
+    print(f"fa mfma tail split kt={kt} n_q={n_q} n_kv={n_kv} masked={masked}", flush=True)
+    mask = None
+    if masked:
+        i = np.arange(n_q)[:, None]
+        j = np.arange(n_kv)[None, :]
+        mask = np.where(np.abs(i * (n_kv / n_q) - j) <= 40, 0.0, -np.inf).astype(np.float32)[None, None]
+        mask[..., 7, :] = -np.inf
+    _run(2, 16, 8, n_q, n_kv, 128, kt, "bf16", mask=mask, seed=11)
