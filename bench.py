@@ -4,19 +4,24 @@
 Workload (the metric's configuration): DiT block, bf16 activations, hidden
 2048, T=6000 latent frames x batch 2 (CFG pair) = 12000 rows, 16 Q / 8 KV
 heads x 128 (NEOX rope, theta 1e4, frame-index positions), SwiGLU at
-intermediate 6144. One step = the block's fused-op launches in
+intermediate 6144. One step = one block's fused-op launches in
 dit_ggml_build_layer order (reference dit-graph.h:367-448). K steps are timed
 as one replay of a HIP graph holding K consecutive blocks, as a DiT step runs
-its blocks back to back in one graph:
-  norm_sa        = rms_norm*w -> AdaLN modulate (hidden)
+its blocks back to back in one graph (dit-graph.h:498-590, the layer loop).
+A block's first op, the self-attention norm, reads the previous block's last
+output with no GEMM in between, so it runs fused into the previous block's
+last launch; the graph starts with one standalone norm for the first block:
+  [first block only] hidden_norm = rms_norm*w -> AdaLN modulate (hidden)
   q, k           = QK-norm -> rope on views of the fused QKV projection output
   h1, norm_ffn   = hidden + sa_out * gate_sa, and rms_norm*w -> AdaLN of it
                    (one pass: the gated residual fused into the FFN norm)
   ff             = swiglu(gate_up)
-  h2             = h1 + ffn_out * gate_ffn
-The same block with the residual and the norm as separate launches (six
-launches, the op-per-node structure of the reference graph) is timed too and
-reported under "unfused".
+  hidden, norm_sa = h1 + ffn_out * gate_ffn, and the next block's
+                   rms_norm*w -> AdaLN of it (one pass)
+The timed graph holds the first-block norm and K blocks of 4 launches; value
+counts its bytes. Two comparisons are timed too: the block as 5 launches with
+its own norm ("five_launch_block", no fusion across blocks), and as 6 launches,
+the op-per-node structure of the reference graph ("unfused").
 The GEMM / attention outputs between them (qkv, sa_out, gate_up, ffn_out)
 are synthetic N(0,1) bf16 tensors resident in HBM before timing starts.
 
@@ -49,15 +54,16 @@ THETA, EPS = 1e4, 1e-6
 HBM_PEAK_GBS = 8000.0
 
 
-def block_bytes(rows: int, es: int = 2, fused: bool = True) -> dict:
-    """Algorithmic bytes per launch (inputs read once + outputs written once)."""
+def block_bytes(rows: int, es: int = 2, fused: bool = True, cross: bool = False) -> dict:
+    """Algorithmic bytes per launch (inputs read once + outputs written once).
+    cross: the steady-state block of a block sequence, whose last launch also
+    makes the next block's self-attention norm (the first block's norm is
+    lead_bytes)."""
     act = rows * H * es
     vec = H * 4
     qk = rows * (NH + NKV) * D * es
-    b = {
-        "rms_norm_modulate_sa": 2 * act + 3 * vec,
-        "qk_norm_rope": 2 * qk + rows * 4 + 2 * D * 4,
-    }
+    b = {} if cross else {"rms_norm_modulate_sa": 2 * act + 3 * vec}
+    b["qk_norm_rope"] = 2 * qk + rows * 4 + 2 * D * 4
     if fused:
         # h1 = h + sa_out * gate_sa and norm_ffn = AdaLN(rms_norm(h1) * w) in one pass
         b["add_rms_norm_modulate_ffn"] = 4 * act + 4 * vec
@@ -65,8 +71,16 @@ def block_bytes(rows: int, es: int = 2, fused: bool = True) -> dict:
         b["gated_add_sa"] = 3 * act + vec
         b["rms_norm_modulate_ffn"] = 2 * act + 3 * vec
     b["swiglu"] = rows * 2 * I_FF * es + rows * I_FF * es
-    b["gated_add_ffn"] = 3 * act + vec
+    if cross:
+        b["gated_add_ffn_rms_norm_modulate_sa"] = 4 * act + 4 * vec
+    else:
+        b["gated_add_ffn"] = 3 * act + vec
     return b
+
+
+def lead_bytes(rows: int, es: int = 2) -> int:
+    """The first block's standalone self-attention norm."""
+    return 2 * rows * H * es + 3 * H * 4
 
 
 def bf16_bits(a: np.ndarray) -> np.ndarray:
@@ -124,50 +138,64 @@ def _setup():
         lambda: ops.rms_norm_modulate(h1, ff_w, scale_ff, shift_ff, EPS, out=norm_ff, stream=sh),
         fused[3], fused[4],
     ]
+    # the steady-state block of a sequence: the FFN gated residual writes the
+    # next block's input (hidden, in place) and that block's self-attention
+    # norm (its weights and AdaLN vectors stand in for the next block's)
+    cross = [
+        fused[1], fused[2], fused[3],
+        lambda: ops.add_rms_norm(h1, ffn_out, EPS, gate=gate_ff, w=sa_w, scale=scale_sa, shift=shift_sa,
+                                 out_sum=hidden, out_norm=norm_sa, stream=sh),
+    ]
+    lead = fused[0]
     # plain bf16 copy of a known size (the SwiGLU output, 147.456 MB each way):
     # the reference point for scaling the FETCH_SIZE / WRITE_SIZE counters
     ff_copy = DTensor.empty((BATCH, T_FRAMES, I_FF), "bf16")
     calib = lambda: ops.cpy(ff, ff_copy, stream=sh)  # noqa: E731
     keep = (hidden, qkv, sa_out, gate_up, ffn_out, adaln, sa_w, ff_w, q_w, k_w, pos, norm_sa, norm_ff, h1, h2, q_out,
             k_out, ff, ff_copy)
-    return fused, unfused, calib, stream, keep
+    return fused, unfused, cross, lead, calib, stream, keep
 
 
 def pmc_pass():
-    """Each fused launch once, then the calibration copy, eagerly (for rocprofv3 --pmc)."""
+    """Each fused launch once (the 5-launch block, then the cross-block
+    residual + norm), then the calibration copy, eagerly (for rocprofv3 --pmc)."""
     from acestep_ops import device
 
-    fused, _, calib, stream, _keep = _setup()
+    fused, _, cross, _lead, calib, stream, _keep = _setup()
     for f in fused:
         f()
+    cross[-1]()
     calib()
     stream.synchronize()
     device.synchronize()
-    print("pmc pass: 5 block launches + 1 calibration copy (bf16, 147456000 B read, 147456000 B written)",
-          flush=True)
+    print("pmc pass: 5 block launches + the cross-block residual and norm + 1 calibration copy (bf16, 147456000 B "
+          "read, 147456000 B written)", flush=True)
 
 
 def gpu_bench(steps: int, warmup: int):
     from acestep_ops import device
     from acestep_ops.device import Event, Graph
 
-    fused, unfused, _calib, stream, _keep = _setup()
+    fused, unfused, cross, lead, _calib, stream, _keep = _setup()
     sh = stream.handle
 
-    def graph_of(launches, copies=1):
+    def graph_of(launches, copies=1, first=None):
         """One HIP graph holding `copies` consecutive blocks (a DiT step runs its
         blocks back to back in one graph, so the ~11 us cost of launching a
-        graph is paid once per graph, not once per block)."""
+        graph is paid once per graph, not once per block), after `first`."""
         g = Graph()
         with g.capture(stream):
+            if first is not None:
+                first()
             for _ in range(copies):
                 for f in launches:
                     f()
         return g
 
-    def time_steps(launches, n):
-        """Device time of exactly n blocks: one replay of an n-block graph."""
-        g = graph_of(launches, n)
+    def time_steps(launches, n, first=None):
+        """Device time of exactly n blocks (and `first`): one replay of an
+        n-block graph, divided by n."""
+        g = graph_of(launches, n, first)
         g.launch()  # first replay pays one-time costs
         stream.synchronize()
         a, b = Event(), Event()
@@ -195,25 +223,29 @@ def gpu_bench(steps: int, warmup: int):
         return [1000.0 * float(np.mean([ev[i][j].elapsed_ms(ev[i][j + 1]) for i in range(n)]))
                 for j in range(len(launches))]
 
-    g_fused, g_unfused = graph_of(fused), graph_of(unfused)
+    g_cross, g_fused, g_unfused = graph_of(cross), graph_of(fused), graph_of(unfused)
     if warmup:
+        graph_of(cross, warmup, lead).launch()
         graph_of(fused, warmup).launch()
         graph_of(unfused, warmup).launch()
     stream.synchronize()
 
-    # timed region: K blocks, one replay of a K-block graph
+    # timed region: the first block's norm and K blocks, one replay of that graph
     device.synchronize()
     t0 = time.perf_counter()
-    ms_step = time_steps(fused, steps)
+    ms_step = time_steps(cross, steps, lead)
     device.synchronize()
     wall = time.perf_counter() - t0
+    ms_five = time_steps(fused, steps)
     ms_unfused = time_steps(unfused, steps)
 
+    names_c = list(block_bytes(ROWS, cross=True).keys())
     names_f = list(block_bytes(ROWS, fused=True).keys())
     names_u = list(block_bytes(ROWS, fused=False).keys())
+    pk_c = dict(zip(names_c, per_kernel(cross, steps, g_cross)))
     pk_f = dict(zip(names_f, per_kernel(fused, steps, g_fused)))
     pk_u = dict(zip(names_u, per_kernel(unfused, steps, g_unfused)))
-    return ms_step, ms_unfused, wall, pk_f, pk_u
+    return ms_step, ms_five, ms_unfused, wall, pk_c, pk_f, pk_u
 
 
 def cpu_bench(rows: int, reps: int, threads: int):
@@ -750,11 +782,13 @@ def main():
     if args.decode_layer:
         decode_layer_bench(args.steps)
         return
-    kb = block_bytes(ROWS, fused=True)
+    kb = block_bytes(ROWS, cross=True)
+    kb_f = block_bytes(ROWS, fused=True)
     kb_u = block_bytes(ROWS, fused=False)
     total_bytes = sum(kb.values())
-    ms_step, ms_unfused, wall, per_k, per_k_u = gpu_bench(args.steps, args.warmup)
-    value = total_bytes / (ms_step * 1e-3) / 1e9
+    graph_bytes = args.steps * total_bytes + lead_bytes(ROWS)  # what the timed graph moves
+    ms_step, ms_five, ms_unfused, wall, per_k, per_k_f, per_k_u = gpu_bench(args.steps, args.warmup)
+    value = graph_bytes / (args.steps * ms_step * 1e-3) / 1e9
     dom = "swiglu"
     dom_gbs = kb[dom] / (per_k[dom] * 1e-6) / 1e9
 
@@ -802,11 +836,16 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "ACE-Step DiT block fused ops, bf16, H=2048, T=6000 x N=2 (12000 rows), 16/8 heads "
-                               "x 128, SwiGLU I=6144; 5 launches/step (gated residual fused into the FFN norm); "
-                               "K steps timed as one replay of a HIP graph of K consecutive blocks",
-                   "rows": ROWS, "hidden": H, "intermediate": I_FF, "bytes_per_step": total_bytes},
+                               "x 128, SwiGLU I=6144; 4 launches/step (each gated residual fused with the norm "
+                               "after it: the FFN norm, and the next block's self-attention norm); K steps timed as "
+                               "one replay of a HIP graph of the first block's norm + K consecutive blocks",
+                   "rows": ROWS, "hidden": H, "intermediate": I_FF, "bytes_per_step": total_bytes,
+                   "bytes_first_block_norm": lead_bytes(ROWS)},
         "per_kernel_us": {k: round(v, 2) for k, v in per_k.items()},
         "per_kernel_gbs": {k: round(kb[k] / (per_k[k] * 1e-6) / 1e9, 1) for k in kb},
+        "five_launch_block": {"us_per_block": round(ms_five * 1e3, 2), "bytes_per_step": sum(kb_f.values()),
+                              "gbs": round(sum(kb_f.values()) / (ms_five * 1e-3) / 1e9, 1),
+                              "per_kernel_us": {k: round(v, 2) for k, v in per_k_f.items()}},
         "unfused": {"us_per_block": round(ms_unfused * 1e3, 2), "bytes_per_step": sum(kb_u.values()),
                     "gbs": round(sum(kb_u.values()) / (ms_unfused * 1e-3) / 1e9, 1),
                     "per_kernel_us": {k: round(v, 2) for k, v in per_k_u.items()}},
