@@ -708,7 +708,9 @@ __device__ __forceinline__ uint4 fa_bld16(fa_rsrc r, uint32_t voff, uint32_t sof
 #ifndef MI_FA_MFMA_WPE
 #define MI_FA_MFMA_WPE 2  // waves per SIMD: 2 caps registers at 256 (two workgroups per CU, 144 KB of LDS)
 #endif
-template <int KT, int D>
+// MSK: a mask (and its summary) is given; without one the kernel is compiled
+// with no per-tile summary reads at all.
+template <int KT, int D, bool MSK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MI_FA_MFMA_WPE, MI_FA_MFMA_WPE)))
 k_fa_mfma(const FaArgs a) {
     using M          = FaM<KT>;
@@ -882,9 +884,22 @@ k_fa_mfma(const FaArgs a) {
     // per tile, from the mask summary of this lane's row (one tile ahead): does
     // the wave read the tile's mask values, does it have a live key at all
     const uint8_t * sp =
-        a.msum ? a.msum + (((int64_t) (b % (uint32_t) a.mne3) * a.mne2 + h % a.mne2) * a.ngq + iq / 16) * ntl
-               : nullptr;
-    auto flag = [&](int t) -> int { return t < te ? (sp ? (int) sp[t] : 1) : 0; };
+        MSK ? a.msum + (((int64_t) (b % (uint32_t) a.mne3) * a.mne2 + h % a.mne2) * a.ngq + iq / 16) * ntl
+            : nullptr;
+    // The tile loop, compiled twice in the masked kernel: with the per-tile
+    // summary reads (MK), and without them for a workgroup whose mask rows are
+    // all zero over its key range (every summary byte 1: live, no nonzero
+    // value) -- the padding mask of unpadded DiT sequences. The second version
+    // runs as fast as the unmasked kernel; the first is ~15 % slower.
+    auto tiles = [&](auto mtag) {
+    constexpr bool MK = decltype(mtag)::value;
+    auto flag = [&](int t) -> int {
+        if constexpr (MK) {
+            return t < te ? (int) sp[t] : 0;
+        } else {
+            return t < te ? 1 : 0;
+        }
+    };
     int  fcur = flag(tb);
     load_tile(tb * BK);
     store_tile(0);
@@ -1010,6 +1025,22 @@ k_fa_mfma(const FaArgs a) {
         }
         fcur = fnext;
         __syncthreads();
+    }
+    };
+    bool clean = !MSK;
+    if constexpr (MSK) {
+        bool c = true;
+        if (rvld) {
+            for (int t = tb; t < te; ++t) {
+                c = c && sp[t] == 1;
+            }
+        }
+        clean = __syncthreads_and(c) != 0;  // workgroup-uniform: the waves share the K/V tiles
+    }
+    if (clean) {
+        tiles(std::false_type{});
+    } else {
+        tiles(std::true_type{});
     }
     // rows: sum over both half-waves' keys; y[b][iq][h][d], d = 32 db + 8 j + 4 hh + i
     lrun = lrun + __shfl_xor(lrun, 32, 64);
@@ -1205,9 +1236,17 @@ int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
         }
         const dim3 grid((uint32_t) (a.tfull + 2 * a.tsplit));
         if (kt == MI_TYPE_BF16) {
-            hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_BF16, 128>), grid, dim3(256), 0, s, a);
+            if (a.msum) {
+                hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_BF16, 128, true>), grid, dim3(256), 0, s, a);
+            } else {
+                hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_BF16, 128, false>), grid, dim3(256), 0, s, a);
+            }
         } else {
-            hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_F16, 128>), grid, dim3(256), 0, s, a);
+            if (a.msum) {
+                hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_F16, 128, true>), grid, dim3(256), 0, s, a);
+            } else {
+                hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_F16, 128, false>), grid, dim3(256), 0, s, a);
+            }
         }
         if (a.tsplit > 0) {
             hipLaunchKernelGGL(k_fa_mfma_combine, dim3((uint32_t) a.tsplit * 16), dim3(256), 0, s, a);

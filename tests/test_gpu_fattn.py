@@ -180,20 +180,28 @@ def test_empty_key_range_is_nan(dev):
     assert np.isnan(y).all()
 
 
-@pytest.mark.parametrize("kt,qt,rk,masked", [("bf16", "bf16", 2, False), ("bf16", "f32", 2, True),
-                                              ("f16", "f32", 4, True), ("f16", "bf16", 2, False)])
+@pytest.mark.parametrize("kt,qt,rk,masked", [("bf16", "bf16", 2, False), ("bf16", "f32", 2, "window"),
+                                              ("f16", "f32", 4, "window"), ("f16", "bf16", 2, False),
+                                              ("bf16", "bf16", 2, "zero"), ("f16", "f32", 4, "one_key")])
 def test_mfma_prefill(dev, kt, qt, rk, masked):
     """The matrix-core path (128 query rows per workgroup, 64-key tiles): 203 query
     positions x rk heads per KV head (a ragged last row block), 333 keys (a ragged last
-    tile), 2 batch elements, with or without a window mask."""
+    tile), 2 batch elements, with no mask, a window mask, an all-zero mask (every
+    workgroup takes the loop without mask reads), or a zero mask with one -inf key in
+    one query position (its workgroup reads the mask, the others do not)."""
     print(f"fa mfma prefill kt={kt} qt={qt} rk={rk} masked={masked}", flush=True)
     n_q, n_kv, nkv = 203, 333, 2
     mask = None
-    if masked:
+    if masked == "window":
         i = np.arange(n_q)[:, None]
         j = np.arange(n_kv)[None, :]
         mask = np.where(np.abs(i * 1.6 - j) <= 70, 0.0, -np.inf).astype(np.float32)[None, None]
         mask[..., 5, :] = -np.inf  # one query position with every key masked: NaN rows
+    elif masked == "zero":
+        mask = np.zeros((1, 1, n_q, n_kv), np.float32)
+    elif masked == "one_key":
+        mask = np.zeros((1, 1, n_q, n_kv), np.float32)
+        mask[..., 150, 77] = -np.inf
     _run(2, nkv * rk, nkv, n_q, n_kv, 128, kt, qt, mask=mask, seed=7)
 
 
