@@ -254,6 +254,27 @@ def mul_mat_q8_0_workspace(w: Q8R64, x) -> int:
     return int(nb.value)
 
 
+def mul_mat_q8_0_swiglu_workspace(w: Q8R64, gu) -> int:
+    n = ctypes.c_size_t(0)
+    _lib.call("mi_mul_mat_q8_0_swiglu_workspace", w.k, w.n, _p(gu), ctypes.byref(n))
+    return int(n.value)
+
+
+def mul_mat_q8_0_swiglu(w: Q8R64, gu, swapped: bool = False, out=None, workspace=None, stream=None):
+    """ggml_mul_mat(w, ggml_swiglu(gu)) in one call: gu F32 (m, 2k) -> F32 (m, n),
+    bit-identical to swiglu followed by mul_mat_q8_0."""
+    y = _out(out, tuple(gu.shape[:-1]) + (w.n,), "f32")
+    need = mul_mat_q8_0_swiglu_workspace(w, gu)
+    ws = workspace
+    if need and ws is None:
+        ws = DTensor.empty((need,), "u8")
+    wp = ctypes.c_void_p(ws.ptr) if ws is not None else None
+    wn = ws.numel() * ws.es if ws is not None else 0
+    _lib.call("mi_mul_mat_q8_0_swiglu", ctypes.c_void_p(w.data.ptr), w.k, w.n, _p(gu), int(bool(swapped)), _p(y), wp,
+              wn, _s(stream))
+    return y
+
+
 def mul_mat_q8_0(w: Q8R64, x, out=None, workspace=None, stream=None):
     """ggml_mul_mat(w, x): x F32 (m, k) with m <= 8 -> F32 (m, n)."""
     y = _out(out, tuple(x.shape[:-1]) + (w.n,), "f32")

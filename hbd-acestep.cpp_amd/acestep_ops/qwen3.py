@@ -9,7 +9,8 @@ F16 KV cache:
   attn   = flash_attn_ext(q, K[:read_len], V[:read_len], mask, 1/sqrt(D))  (706-723)
   hidden = hidden + mul_mat(W_o, attn)                            (729-733)
   norm2  = rms_norm(hidden) * post_attention_layernorm            (736; fused with the add)
-  hidden = hidden + mul_mat(W_down, swiglu(mul_mat(W_gate_up, norm2)))  (737-741)
+  hidden = hidden + mul_mat(W_down, swiglu(mul_mat(W_gate_up, norm2)))  (737-741;
+           swiglu and the down product as one call, mul_mat_q8_0_swiglu)
 
 Shapes outermost first: hidden (N, H) F32 for N sequences of one token; the
 caches (n_sets, Nkv, max_seq, D) (ggml [D, max_seq, Nkv, n_sets]); sequence i
@@ -94,13 +95,18 @@ class Qwen3DecodeLayer:
                                   out_norm=self._buf("n2", (N, H)), stream=st)
         gu = ops.mul_mat_q8_0(self.w["gu"], n2, out=self._buf("gu", (N, 2 * I)), workspace=self._ws("gu", n2),
                               stream=st)
-        ff = ops.swiglu(gu, out=self._buf("ff", (N, I)), stream=st)
-        mlp = ops.mul_mat_q8_0(self.w["down"], ff, out=self._buf("mlp", (N, H)), workspace=self._ws("down", ff),
-                               stream=st)
+        # swiglu and the down projection in one call: the SwiGLU values are made
+        # inside the quantization of the product's x (bit-identical to the two ops)
+        mlp = ops.mul_mat_q8_0_swiglu(self.w["down"], gu, out=self._buf("mlp", (N, H)),
+                                      workspace=self._ws_glu("down", gu), stream=st)
         return ops.add(h1, mlp, out=out if out is not None else self._buf("out", (N, H)), stream=st)
 
     def _ws(self, name, x):
         need = ops.mul_mat_q8_0_workspace(self.w[name], x)
+        return self._buf("ws_" + name, (max(need, 1),), "u8")
+
+    def _ws_glu(self, name, gu):
+        need = ops.mul_mat_q8_0_swiglu_workspace(self.w[name], gu)
         return self._buf("ws_" + name, (max(need, 1),), "u8")
 
     def _fa_ws(self, q, k, v):

@@ -857,6 +857,69 @@ int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, c
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 
+// gu F32 [2k, m] -> the descriptor of the SwiGLU input x [k, m] (the gate half's
+// view) with g / u pointed at the two halves
+static int mm_glu_desc(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped, const mi_tensor * y,
+                       MmvArgs & a) {
+    if (!gu) {
+        return MI_ERR_NULL;
+    }
+    MI_TRY(check(gu));
+    if (gu->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (k <= 0 || gu->ne[0] != 2 * k) {
+        return MI_ERR_SHAPE;
+    }
+    mi_tensor x = *gu;
+    x.ne[0]     = k;
+    MI_TRY(mm_desc(w, k, n, &x, y, a));
+    const char * lo = (const char *) gu->data;
+    const char * hi = lo + k * 4;
+    a.glu           = 1;
+    a.g             = swapped ? hi : lo;
+    a.u             = swapped ? lo : hi;
+    a.gu1           = (int64_t) gu->nb[1];
+    a.xvec          = aligned(lo, 16) && aligned(hi, 16) && (a.m <= 1 || gu->nb[1] % 16 == 0);
+    return MI_OK;
+}
+
+int mi_mul_mat_q8_0_swiglu_workspace(int64_t k, int64_t n, const mi_tensor * gu, size_t * bytes) {
+    if (!bytes) {
+        return MI_ERR_NULL;
+    }
+    MmvArgs a;
+    MI_TRY(mm_glu_desc(nullptr, k, n, gu, 0, nullptr, a));
+    *bytes = a.m == 0 || a.n == 0 ? 0 : mul_mat_q8_0_workspace(a);
+    return MI_OK;
+}
+
+int mi_mul_mat_q8_0_swiglu(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
+                           const mi_tensor * y, void * workspace, size_t workspace_bytes, mi_stream stream) {
+    if (!y) {
+        return MI_ERR_NULL;
+    }
+    MmvArgs a;
+    MI_TRY(mm_glu_desc(w, k, n, gu, swapped, y, a));
+    if (a.m == 0 || a.n == 0) {
+        return MI_OK;
+    }
+    if (!w) {
+        return MI_ERR_NULL;
+    }
+    if (!aligned(w, 16)) {
+        return MI_ERR_ALIGN;
+    }
+    if (!workspace || workspace_bytes < mul_mat_q8_0_workspace(a)) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(workspace, 256)) {
+        return MI_ERR_ALIGN;
+    }
+    mul_mat_q8_0_bind(a, (char *) workspace);
+    return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
+}
+
 // F32 [oc, t, n] contiguous, the velocity/latent layout of the sampler
 static int lat_check(const mi_tensor * x, const mi_tensor * ref) {
     MI_TRY(check(x));

@@ -287,6 +287,33 @@ template <int L> __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// silu(x) = x / (1 + e^-x) for SwiGLU (glu.hip) and the SwiGLU prologue of the
+// Q8_0 product (matmul.hip): e^-x as v_exp_f32 (2^t) on t = -x*log2(e), with the
+// rounding error of that product recovered by an fma and folded back in first
+// order, so e^-x is good to ~1 ulp over the finite range; the quotient is
+// x * v_rcp_f32(1 + e^-x).
+#ifndef MI_SILU_CORR
+#define MI_SILU_CORR 1  // recover the rounding error of -x*log2(e) (first order)
+#endif
+
+__device__ __forceinline__ float silu_f(float x) {
+    constexpr float LOG2E = 1.44269504088896340736f;  // rounded log2(e)
+    const float     t     = -x * LOG2E;
+#if MI_SILU_CORR
+    constexpr float LOG2E_LO = 1.925963033500011e-08f;  // log2(e) - LOG2E
+    constexpr float LN2      = 0.693147180559945309417f;
+    const float     terr     = __builtin_fmaf(-x, LOG2E_LO, __builtin_fmaf(-x, LOG2E, -t));
+    const float     e0       = __builtin_amdgcn_exp2f(t);
+    // first-order correction only where 2^t is finite and t finite (for t = -inf
+    // the residual is +inf and 0*inf would give NaN)
+    const float     e        = __builtin_fabsf(t) < 128.0f ? __builtin_fmaf(e0, terr * LN2, e0) : e0;
+#else
+    const float e = __builtin_amdgcn_exp2f(t);
+#endif
+    const float d = 1.0f + e;
+    return x * __builtin_amdgcn_rcpf(d);
+}
+
 template <int L> __device__ __forceinline__ float group_max(float v) {
     if constexpr (L >= 2) {
         v = fmaxf(v, dpp_f<0xB1>(v));

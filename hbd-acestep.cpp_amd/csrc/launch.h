@@ -166,6 +166,10 @@ struct MmvArgs {
     int64_t      y1;
     uint32_t     splits, wpg, bps;  // workgroups per row group, waves (key splits) per workgroup,
                                     // blocks per wave (set by mul_mat_q8_0_plan)
+    int          glu;          // 1: x = silu(g) * u (the SwiGLU prologue), rows at stride gu1
+    const char * g;
+    const char * u;
+    int64_t      gu1;
     char *       xq;           // workspace: quantized x [m][k]
     float *      xd;           //            scales [m][nbk]
     float *      part;         //            partials [splits][m][npad] (splits > 1)

@@ -71,19 +71,32 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
         return;  // whole groups of 8 lanes
     }
     const uint32_t m = blk / a.nbk, b = blk - m * a.nbk;
-    const char *   p = a.x + (int64_t) m * a.x1 + (int64_t) (b * 32 + sub * 4) * 4;
     float          f[4];
-    if (a.xvec) {
-        const float4 v = *(const float4 *) p;
-        f[0]           = v.x;
-        f[1]           = v.y;
-        f[2]           = v.z;
-        f[3]           = v.w;
-    } else {
+    auto           ld4 = [&](const char * p, float (&v)[4]) {
+        if (a.xvec) {
+            const float4 q = *(const float4 *) p;
+            v[0]           = q.x;
+            v[1]           = q.y;
+            v[2]           = q.z;
+            v[3]           = q.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = ((const float *) p)[e];
+            }
+        }
+    };
+    if (a.glu) {  // x = silu(g) * u, as mi_swiglu computes it
+        const int64_t off = (int64_t) m * a.gu1 + (int64_t) (b * 32 + sub * 4) * 4;
+        float         g[4], u[4];
+        ld4(a.g + off, g);
+        ld4(a.u + off, u);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            f[e] = ((const float *) p)[e];
+            f[e] = silu_f(g[e]) * u[e];
         }
+    } else {
+        ld4(a.x + (int64_t) m * a.x1 + (int64_t) (b * 32 + sub * 4) * 4, f);
     }
     float amax = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
     amax       = group_max<8>(amax);

@@ -224,10 +224,6 @@ int mi_flash_attn_ext(const mi_tensor * q, const mi_tensor * k, const mi_tensor 
                       float scale, float max_bias, float logit_softcap, const mi_tensor * y, void * workspace,
                       size_t workspace_bytes, mi_stream stream);
 
-/* ---------------------------------------------------------------------- */
-/* Layer-chain drivers: launch the fused-op sequence of one DiT block or   */
-/* one Qwen3 layer in the order of the reference's layer composers, taking */
-/* the GEMM / attention outputs (not computed by this library) as inputs.  */
 /* ggml_mul_mat(w, x) with Q8_0 weights, as ggml-cpu computes it: each row of x
  * is quantized to Q8_0 with the x86 from_float (id = 127 / amax, round to
  * nearest even, saturate) and each output is sum_b (d_w * d_x) * sum_i q_w q_x
@@ -240,16 +236,28 @@ int mi_flash_attn_ext(const mi_tensor * q, const mi_tensor * k, const mi_tensor 
  * do): mi_q8_0_repack copies a Q8_0 [k, n] weight (GGUF layout, rows at
  * stride nb[1]) into dst, a lossless layout of mi_q8_0_repack_bytes(k, n)
  * bytes (rows in groups of 64; 34 bytes per block).
- * mi_mul_mat_q8_0: w = repacked weight [k, n]; x F32 [k, m] with m <= 8 rows
- * (ne1 * ne2 * ne3, uniformly strided; more rows return MI_ERR_UNSUPPORTED);
- * y F32 [n, m]. workspace: device memory of at least
- * mi_mul_mat_q8_0_workspace() bytes, 256-byte aligned (the quantized x, and
- * the partial sums and counters of a split k). Calls sharing a workspace race. */
+ * mi_mul_mat_q8_0: w = repacked weight [k, n]; x F32 [k, m] (m = ne1 * ne2 *
+ * ne3 rows, uniformly strided; up to 8 rows take the matrix-vector kernel,
+ * more the matrix-core kernel); y F32 [n, m]. workspace: device memory of at
+ * least mi_mul_mat_q8_0_workspace() bytes, 256-byte aligned (the quantized x,
+ * and the partial sums of a split k). Calls sharing a workspace race. */
 int mi_q8_0_repack_bytes(int64_t k, int64_t n, size_t * bytes);
 int mi_q8_0_repack(const mi_tensor * w, void * dst, size_t dst_bytes, mi_stream stream);
 int mi_mul_mat_q8_0_workspace(int64_t k, int64_t n, const mi_tensor * x, size_t * bytes);
 int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
                     void * workspace, size_t workspace_bytes, mi_stream stream);
+
+/* The SwiGLU -> down projection pair as one call: y = ggml_mul_mat(w,
+ * ggml_swiglu(gu)) (qwen3-enc.h:221-223, the Qwen3 MLP; dit-graph.h:265-268,
+ * the DiT MLP). gu F32 [2k, m] (gate = first half of each row, or the second
+ * when swapped), w repacked [k, n], y F32 [n, m]. The SwiGLU values are
+ * computed inside the quantization of x, with the arithmetic of mi_swiglu, so
+ * y is bit-identical to mi_swiglu followed by mi_mul_mat_q8_0; the [k, m]
+ * SwiGLU output never goes to memory. Workspace as mi_mul_mat_q8_0 for an x
+ * of m rows of k. */
+int mi_mul_mat_q8_0_swiglu_workspace(int64_t k, int64_t n, const mi_tensor * gu, size_t * bytes);
+int mi_mul_mat_q8_0_swiglu(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
+                           const mi_tensor * y, void * workspace, size_t workspace_bytes, mi_stream stream);
 
 /* The DiT sampler's per-step math on the device (dit_ggml_generate,
  * dit-sampler.h:408-640), so the latents stay resident across steps.
@@ -320,6 +328,9 @@ int mi_gguf_upload_rows(const mi_gguf * g, const char * const * names, int n, vo
                         int64_t * ne1_out, mi_stream stream);
 
 /* ---------------------------------------------------------------------- */
+/* Layer-chain drivers: launch the fused-op sequence of one DiT block or   */
+/* one Qwen3 layer in the order of the reference's layer composers, taking */
+/* the GEMM / attention outputs (not computed by this library) as inputs.  */
 
 /* One ACE-Step DiT block's non-GEMM ops, in dit_ggml_build_layer order
  * (dit-graph.h:367-448). hidden is updated in place. Each residual add is

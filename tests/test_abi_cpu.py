@@ -212,6 +212,20 @@ def test_mul_mat_q8_0_validation():
     assert mm(W, k, n, R(x), R(y), ctypes.c_void_p((1 << 20) + 16), nb.value, NULL_S) == -5
     assert L.mi_mul_mat_q8_0_workspace(k, n, R(_t([k, 0])), ctypes.byref(nb)) == 0 and nb.value == 0
     assert L.mi_mul_mat_q8_0_workspace(k, 0, R(x), ctypes.byref(nb)) == 0 and nb.value == 0
+    # the SwiGLU prologue: gu [2k, m]
+    gu = _t([2 * k, m])
+    mg = L.mi_mul_mat_q8_0_swiglu
+    assert L.mi_mul_mat_q8_0_swiglu_workspace(k, n, R(gu), ctypes.byref(nb)) == 0 and nb.value > 0
+    wsn = nb.value
+    assert L.mi_mul_mat_q8_0_workspace(k, n, R(x), ctypes.byref(nb)) == 0 and nb.value == wsn  # as for x [k, m]
+    assert L.mi_mul_mat_q8_0_swiglu_workspace(k, n, R(gu), None) == -1
+    assert L.mi_mul_mat_q8_0_swiglu_workspace(k, n, None, ctypes.byref(nb)) == -1
+    assert mg(W, k, n, R(_t([2 * k + 2, m])), 0, R(y), None, 0, NULL_S) == -3     # not 2k wide
+    assert mg(W, k, n, R(_t([2 * k, m], BF16)), 0, R(y), None, 0, NULL_S) == -2
+    assert mg(W, k, n, R(gu), 0, R(_t([n, m + 1])), None, 0, NULL_S) == -3         # y rows
+    assert mg(W, k, n, R(gu), 0, None, None, 0, NULL_S) == -1
+    assert mg(W, k, n, R(gu), 1, R(y), ctypes.c_void_p(1 << 20), wsn - 1, NULL_S) == -6
+    assert mg(W, k, n, R(gu), 1, R(y), ctypes.c_void_p((1 << 20) + 16), wsn, NULL_S) == -5
 
 
 def test_sampler_validation():

@@ -127,3 +127,39 @@ def test_matrix_kernel_strided_x_and_y(dev):
     yb = to_np(ybig)
     assert np.all(yb[:, 0] == 0) and np.all(yb[:, n + 1:] == 0)
     _check(yb[:, 1:n + 1], w, np.ascontiguousarray(xbig[:, 2:k + 2]))
+
+
+@pytest.mark.parametrize("n,k,m,swapped", [(2560, 9728, 8, False), (300, 256, 3, True), (640, 256, 129, False),
+                                           (100, 96, 1000, True)])
+def test_swiglu_prologue_matches_swiglu_then_mul_mat(dev, n, k, m, swapped):
+    """mi_mul_mat_q8_0_swiglu (the SwiGLU computed inside the quantization of x)
+    against mi_swiglu followed by mi_mul_mat_q8_0: bit-identical, for the decode
+    kernel (m <= 8) and the matrix kernel, gate first or second; and the product
+    against the oracle on the SwiGLU values the device produced. Gate values down
+    to -100 take silu's overflow branch (e^-x = inf, silu = -0)."""
+    print(f"mul_mat q8_0 swiglu n={n} k={k} m={m} swapped={swapped}", flush=True)
+    r = np.random.default_rng(n + k + m)
+    w = orc.quantize_q8_0((r.standard_normal((n, k)) * 0.05).astype(np.float32))
+    gu = (r.standard_normal((m, 2 * k)) * 2.0).astype(np.float32)
+    gu[:, :: 97] = -100.0
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    dgu = to_dev(gu)
+    y_f = to_np(ops.mul_mat_q8_0_swiglu(wr, dgu, swapped=swapped))
+    ff = ops.swiglu(dgu, swapped=swapped)
+    y_u = to_np(ops.mul_mat_q8_0(wr, ff))
+    assert np.array_equal(y_f, y_u)
+    _check(y_f, w, to_np(ff))
+
+
+def test_swiglu_prologue_strided_rows(dev):
+    """gu rows at a stride that is not a multiple of 16 bytes (element loads)."""
+    print("mul_mat q8_0 swiglu strided", flush=True)
+    r = np.random.default_rng(21)
+    n, k, m = 200, 128, 5
+    w = orc.quantize_q8_0(r.standard_normal((n, k)).astype(np.float32))
+    big = r.standard_normal((m, 2 * k + 1)).astype(np.float32)
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    dgu = to_dev(big)[:, :2 * k]
+    y_f = to_np(ops.mul_mat_q8_0_swiglu(wr, dgu))
+    y_u = to_np(ops.mul_mat_q8_0(wr, ops.swiglu(dgu)))
+    assert np.array_equal(y_f, y_u)
