@@ -275,6 +275,21 @@ def mul_mat_q8_0_swiglu(w: Q8R64, gu, swapped: bool = False, out=None, workspace
     return y
 
 
+def mul_mat_q8_0_rms_norm(w: Q8R64, x, norm_w, eps: float, out=None, workspace=None, stream=None):
+    """ggml_mul_mat(w, rms_norm(x) * norm_w) in one call: x F32 (m, k) -> F32 (m, n),
+    equal to rms_norm followed by mul_mat_q8_0."""
+    y = _out(out, tuple(x.shape[:-1]) + (w.n,), "f32")
+    need = mul_mat_q8_0_workspace(w, x)
+    ws = workspace
+    if need and ws is None:
+        ws = DTensor.empty((need,), "u8")
+    wp = ctypes.c_void_p(ws.ptr) if ws is not None else None
+    wn = ws.numel() * ws.es if ws is not None else 0
+    _lib.call("mi_mul_mat_q8_0_rms_norm", ctypes.c_void_p(w.data.ptr), w.k, w.n, _p(x), _p(norm_w),
+              ctypes.c_float(eps), _p(y), wp, wn, _s(stream))
+    return y
+
+
 def mul_mat_q8_0(w: Q8R64, x, out=None, workspace=None, stream=None):
     """ggml_mul_mat(w, x): x F32 (m, k) with m <= 8 -> F32 (m, n)."""
     y = _out(out, tuple(x.shape[:-1]) + (w.n,), "f32")

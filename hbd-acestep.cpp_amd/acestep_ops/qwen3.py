@@ -3,7 +3,8 @@
 F16 KV cache:
 
   norm   = rms_norm(hidden) * input_layernorm                    (630)
-  qkv    = mul_mat(W_qkv, norm); q, k, v = views of qkv           (637-642)
+  qkv    = mul_mat(W_qkv, norm); q, k, v = views of qkv           (637-642;
+           the norm and the product as one call, mul_mat_q8_0_rms_norm)
   q, k   = rope(rms_norm(q|k) * q_norm|k_norm)                    (659-667)
   cache  <- k, v at slot kv_pos of each sequence's set            (682-703)
   attn   = flash_attn_ext(q, K[:read_len], V[:read_len], mask, 1/sqrt(D))  (706-723)
@@ -73,9 +74,11 @@ class Qwen3DecodeLayer:
         N, H, Nh, Nkv, D, I = hidden.shape[0], self.H, self.Nh, self.Nkv, self.D, self.I
         st = self.stream
         qkv_dim = (Nh + 2 * Nkv) * D
-        norm = ops.rms_norm(hidden, self.eps, self.in_norm_w, out=self._buf("norm", (N, H)), stream=st)
-        qkv = ops.mul_mat_q8_0(self.w["qkv"], norm, out=self._buf("qkv", (N, qkv_dim)),
-                               workspace=self._ws("qkv", norm), stream=st)
+        # the input norm and the QKV product in one call: the normalized rows are
+        # made inside the quantization of the product's x
+        qkv = ops.mul_mat_q8_0_rms_norm(self.w["qkv"], hidden, self.in_norm_w, self.eps,
+                                        out=self._buf("qkv", (N, qkv_dim)), workspace=self._ws("qkv", hidden),
+                                        stream=st)
         q = qkv[:, 0:Nh * D].unflatten(1, (Nh, D))
         k = qkv[:, Nh * D:(Nh + Nkv) * D].unflatten(1, (Nkv, D))
         v = qkv[:, (Nh + Nkv) * D:qkv_dim].unflatten(1, (Nkv, D))

@@ -920,6 +920,45 @@ int mi_mul_mat_q8_0_swiglu(const void * w, int64_t k, int64_t n, const mi_tensor
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 
+int mi_mul_mat_q8_0_rms_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * norm_w,
+                             float eps, const mi_tensor * y, void * workspace, size_t workspace_bytes,
+                             mi_stream stream) {
+    if (!y || !norm_w) {
+        return MI_ERR_NULL;
+    }
+    MmvArgs a;
+    MI_TRY(mm_desc(w, k, n, x, y, a));
+    MI_TRY(check(norm_w));
+    if (norm_w->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (norm_w->ne[0] != k || nrows(*norm_w) != 1 || norm_w->nb[0] != 4) {
+        return MI_ERR_SHAPE;
+    }
+    if (!(eps >= 0.0f)) {
+        return MI_ERR_PARAM;
+    }
+    if (a.m == 0 || a.n == 0) {
+        return MI_OK;
+    }
+    if (!w) {
+        return MI_ERR_NULL;
+    }
+    if (!aligned(w, 16)) {
+        return MI_ERR_ALIGN;
+    }
+    if (!workspace || workspace_bytes < mul_mat_q8_0_workspace(a)) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(workspace, 256)) {
+        return MI_ERR_ALIGN;
+    }
+    a.nw  = (const float *) norm_w->data;
+    a.eps = eps;
+    mul_mat_q8_0_bind(a, (char *) workspace);
+    return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
+}
+
 // F32 [oc, t, n] contiguous, the velocity/latent layout of the sampler
 static int lat_check(const mi_tensor * x, const mi_tensor * ref) {
     MI_TRY(check(x));

@@ -166,6 +166,8 @@ struct MmvArgs {
     int64_t      y1;
     uint32_t     splits, wpg, bps;  // workgroups per row group, waves (key splits) per workgroup,
                                     // blocks per wave (set by mul_mat_q8_0_plan)
+    const float * nw;          // non-null: x = rms_norm(x) * nw (the norm prologue), with eps
+    float        eps;
     int          glu;          // 1: x = silu(g) * u (the SwiGLU prologue), rows at stride gu1
     const char * g;
     const char * u;

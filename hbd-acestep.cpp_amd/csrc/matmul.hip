@@ -114,6 +114,78 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
     }
 }
 
+// RMSNorm*w and the quantization of x in one kernel (the norm -> product
+// prologue), one workgroup per row: the scale from the double sum of the float
+// squares and x' = (x * scale) * w, the arithmetic of mi_rms_norm on F32 rows
+// (only the order of the double additions differs, which leaves the float mean
+// unchanged short of a double rounding tie); then x' is quantized as
+// k_mmv_quant_x does, 8 lanes per 32-element block.
+__global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
+    __shared__ double red[4];
+    __shared__ float  scl;
+    const uint32_t m   = blockIdx.x;
+    const int      tid = threadIdx.x;
+    const char *   xr  = a.x + (int64_t) m * a.x1;
+    auto           ld4 = [&](const char * p, float (&v)[4]) {
+        if (a.xvec) {
+            const float4 q = *(const float4 *) p;
+            v[0]           = q.x;
+            v[1]           = q.y;
+            v[2]           = q.z;
+            v[3]           = q.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = ((const float *) p)[e];
+            }
+        }
+    };
+    double ss = 0.0;
+    for (uint32_t i = 4u * (uint32_t) tid; i < a.k; i += 1024u) {
+        float v[4];
+        ld4(xr + (size_t) i * 4, v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            ss += (double) (v[e] * v[e]);
+        }
+    }
+    ss = group_sum<64>(ss);
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = ss;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        scl = rms_scale(red[0] + red[1] + red[2] + red[3], (int) a.k, a.eps);
+    }
+    __syncthreads();
+    const float    scale = scl;
+    const uint32_t sub   = (uint32_t) tid & 7u;
+    for (uint32_t b = (uint32_t) tid >> 3; b < a.nbk; b += 32u) {  // the 8 lanes of a block share b
+        const uint32_t i0 = b * 32u + sub * 4u;
+        float          f[4];
+        ld4(xr + (size_t) i0 * 4, f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float v = f[e] * scale;
+            f[e]          = v * a.nw[i0 + e];
+        }
+        float amax = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
+        amax       = group_max<8>(amax);
+        const float d  = mm_div127(amax);
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        uint32_t    w  = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(f[e] * id), -128.0f, 127.0f);
+            w |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
+        }
+        *(uint32_t *) (a.xq + ((int64_t) b * a.mp + m) * 32 + sub * 4) = w;
+        if (sub == 0) {
+            a.xd[(int64_t) b * a.mp + m] = (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
+        }
+    }
+}
+
 #ifndef MI_MMV_UNROLL
 #define MI_MMV_UNROLL 4  // blocks whose weight loads are issued together
 #endif
@@ -454,8 +526,12 @@ int launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s) {
     if (a.n == 0 || a.m == 0) {
         return MI_OK;
     }
-    const uint64_t threads = (uint64_t) a.m * a.nbk * 8;
-    hipLaunchKernelGGL(k_mmv_quant_x, dim3((uint32_t) ((threads + 255) / 256)), dim3(256), 0, s, a);
+    if (a.nw) {
+        hipLaunchKernelGGL(k_mmv_quant_x_norm, dim3(a.m), dim3(256), 0, s, a);
+    } else {
+        const uint64_t threads = (uint64_t) a.m * a.nbk * 8;
+        hipLaunchKernelGGL(k_mmv_quant_x, dim3((uint32_t) ((threads + 255) / 256)), dim3(256), 0, s, a);
+    }
     if (a.m > 8) {
         hipLaunchKernelGGL(k_mmq_q8_0, dim3((a.n + 127) / 128, a.mp / 128), dim3(256), 0, s, a);
         return MI_OK;

@@ -259,6 +259,18 @@ int mi_mul_mat_q8_0_swiglu_workspace(int64_t k, int64_t n, const mi_tensor * gu,
 int mi_mul_mat_q8_0_swiglu(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
                            const mi_tensor * y, void * workspace, size_t workspace_bytes, mi_stream stream);
 
+/* The RMSNorm -> product pair as one call: y = ggml_mul_mat(w,
+ * ggml_mul(ggml_rms_norm(x, eps), norm_w)) (qwen3-lm.h:632-639, the input norm
+ * feeding the fused QKV projection; qwen3_rms_norm, qwen3-enc.h:114-120). x F32
+ * [k, m], norm_w F32 [k], y F32 [n, m]. The normalized rows are computed inside
+ * the quantization of x with the arithmetic of mi_rms_norm (only the order of
+ * the double additions of the sum of squares differs), so y equals
+ * mi_rms_norm followed by mi_mul_mat_q8_0 and the normalized rows never go to
+ * memory. Workspace: mi_mul_mat_q8_0_workspace() for the same x. */
+int mi_mul_mat_q8_0_rms_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * norm_w,
+                             float eps, const mi_tensor * y, void * workspace, size_t workspace_bytes,
+                             mi_stream stream);
+
 /* The DiT sampler's per-step math on the device (dit_ggml_generate,
  * dit-sampler.h:408-640), so the latents stay resident across steps.
  * Latents and velocities are F32 [Oc, T, N], contiguous.

@@ -212,6 +212,16 @@ def test_mul_mat_q8_0_validation():
     assert mm(W, k, n, R(x), R(y), ctypes.c_void_p((1 << 20) + 16), nb.value, NULL_S) == -5
     assert L.mi_mul_mat_q8_0_workspace(k, n, R(_t([k, 0])), ctypes.byref(nb)) == 0 and nb.value == 0
     assert L.mi_mul_mat_q8_0_workspace(k, 0, R(x), ctypes.byref(nb)) == 0 and nb.value == 0
+    # the norm prologue: norm_w F32 [k]
+    mn = L.mi_mul_mat_q8_0_rms_norm
+    nw = _t([k])
+    assert L.mi_mul_mat_q8_0_workspace(k, n, R(x), ctypes.byref(nb)) == 0
+    assert mn(W, k, n, R(x), None, ctypes.c_float(1e-6), R(y), None, 0, NULL_S) == -1
+    assert mn(W, k, n, R(x), R(_t([k], BF16)), ctypes.c_float(1e-6), R(y), None, 0, NULL_S) == -2
+    assert mn(W, k, n, R(x), R(_t([k + 32])), ctypes.c_float(1e-6), R(y), None, 0, NULL_S) == -3
+    assert mn(W, k, n, R(x), R(nw), ctypes.c_float(-1.0), R(y), None, 0, NULL_S) == -6
+    assert mn(W, k, n, R(x), R(nw), ctypes.c_float(1e-6), R(y), None, 0, NULL_S) == -6   # no workspace
+    assert mn(W, k, n, R(x), R(nw), ctypes.c_float(1e-6), None, None, 0, NULL_S) == -1
     # the SwiGLU prologue: gu [2k, m]
     gu = _t([2 * k, m])
     mg = L.mi_mul_mat_q8_0_swiglu

@@ -163,3 +163,27 @@ def test_swiglu_prologue_strided_rows(dev):
     y_f = to_np(ops.mul_mat_q8_0_swiglu(wr, dgu))
     y_u = to_np(ops.mul_mat_q8_0(wr, ops.swiglu(dgu)))
     assert np.array_equal(y_f, y_u)
+
+
+@pytest.mark.parametrize("n,k,m,view", [(6144, 2560, 8, False), (300, 256, 3, True), (640, 256, 129, False),
+                                        (100, 96, 1000, True)])
+def test_rms_norm_prologue_matches_norm_then_mul_mat(dev, n, k, m, view):
+    """mi_mul_mat_q8_0_rms_norm (RMSNorm*w computed inside the quantization of x)
+    against mi_rms_norm followed by mi_mul_mat_q8_0: bit-identical, for the decode and
+    matrix kernels, with 16-byte aligned rows or rows 4 bytes off (element loads);
+    rows of very different scales. Then the product against the oracle on the
+    normalized rows the device produced."""
+    print(f"mul_mat q8_0 rms_norm n={n} k={k} m={m} view={view}", flush=True)
+    r = np.random.default_rng(n + k + m + 1)
+    w = orc.quantize_q8_0((r.standard_normal((n, k)) * 0.05).astype(np.float32))
+    x = r.standard_normal((m, k + (1 if view else 0))).astype(np.float32)
+    x *= np.float32(10.0) ** r.integers(-3, 4, (m, 1)).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    dx = to_dev(x)[:, 1:] if view else to_dev(x)
+    dnw = to_dev(nw)
+    y_f = to_np(ops.mul_mat_q8_0_rms_norm(wr, dx, dnw, 1e-6))
+    norm = ops.rms_norm(dx, 1e-6, dnw)
+    y_u = to_np(ops.mul_mat_q8_0(wr, norm))
+    assert np.array_equal(y_f, y_u)
+    _check(y_f, w, to_np(norm))
