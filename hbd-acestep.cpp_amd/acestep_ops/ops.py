@@ -290,6 +290,23 @@ def mul_mat_q8_0_rms_norm(w: Q8R64, x, norm_w, eps: float, out=None, workspace=N
     return y
 
 
+def mul_mat_q8_0_add_rms_norm(w: Q8R64, a, b, norm_w, eps: float, out_sum=None, out=None, workspace=None,
+                              stream=None):
+    """sum = a + b; y = ggml_mul_mat(w, rms_norm(sum) * norm_w) in one call: a, b F32 (m, k)
+    -> (sum (m, k), y (m, n)), equal to add_rms_norm followed by mul_mat_q8_0."""
+    sm = _out(out_sum, a.shape, "f32")
+    y = _out(out, tuple(a.shape[:-1]) + (w.n,), "f32")
+    need = mul_mat_q8_0_workspace(w, a)
+    ws = workspace
+    if need and ws is None:
+        ws = DTensor.empty((need,), "u8")
+    wp = ctypes.c_void_p(ws.ptr) if ws is not None else None
+    wn = ws.numel() * ws.es if ws is not None else 0
+    _lib.call("mi_mul_mat_q8_0_add_rms_norm", ctypes.c_void_p(w.data.ptr), w.k, w.n, _p(a), _p(b), _p(norm_w),
+              ctypes.c_float(eps), _p(sm), _p(y), wp, wn, _s(stream))
+    return sm, y
+
+
 def mul_mat_q8_0(w: Q8R64, x, out=None, workspace=None, stream=None):
     """ggml_mul_mat(w, x): x F32 (m, k) with m <= 8 -> F32 (m, n)."""
     y = _out(out, tuple(x.shape[:-1]) + (w.n,), "f32")

@@ -9,7 +9,8 @@ F16 KV cache:
   cache  <- k, v at slot kv_pos of each sequence's set            (682-703)
   attn   = flash_attn_ext(q, K[:read_len], V[:read_len], mask, 1/sqrt(D))  (706-723)
   hidden = hidden + mul_mat(W_o, attn)                            (729-733)
-  norm2  = rms_norm(hidden) * post_attention_layernorm            (736; fused with the add)
+  norm2  = rms_norm(hidden) * post_attention_layernorm            (736; the add, the norm and the
+           gate/up product as one call, mul_mat_q8_0_add_rms_norm)
   hidden = hidden + mul_mat(W_down, swiglu(mul_mat(W_gate_up, norm2)))  (737-741;
            swiglu and the down product as one call, mul_mat_q8_0_swiglu)
 
@@ -94,10 +95,10 @@ class Qwen3DecodeLayer:
         ops.flash_attn_ext(qf, kv, vv, mask, 1.0 / math.sqrt(D), out=attn, workspace=ws, stream=st)
         a2 = attn.view(N, Nh * D)
         ao = ops.mul_mat_q8_0(self.w["o"], a2, out=self._buf("ao", (N, H)), workspace=self._ws("o", a2), stream=st)
-        h1, n2 = ops.add_rms_norm(hidden, ao, self.eps, w=self.post_norm_w, out_sum=self._buf("h1", (N, H)),
-                                  out_norm=self._buf("n2", (N, H)), stream=st)
-        gu = ops.mul_mat_q8_0(self.w["gu"], n2, out=self._buf("gu", (N, 2 * I)), workspace=self._ws("gu", n2),
-                              stream=st)
+        # the residual add, the post-attention norm and the gate/up product in one call
+        h1, gu = ops.mul_mat_q8_0_add_rms_norm(self.w["gu"], hidden, ao, self.post_norm_w, self.eps,
+                                               out_sum=self._buf("h1", (N, H)), out=self._buf("gu", (N, 2 * I)),
+                                               workspace=self._ws("gu", hidden), stream=st)
         # swiglu and the down projection in one call: the SwiGLU values are made
         # inside the quantization of the product's x (bit-identical to the two ops)
         mlp = ops.mul_mat_q8_0_swiglu(self.w["down"], gu, out=self._buf("mlp", (N, H)),

@@ -920,14 +920,44 @@ int mi_mul_mat_q8_0_swiglu(const void * w, int64_t k, int64_t n, const mi_tensor
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 
-int mi_mul_mat_q8_0_rms_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * norm_w,
-                             float eps, const mi_tensor * y, void * workspace, size_t workspace_bytes,
-                             mi_stream stream) {
+static int mm_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * b,
+                   const mi_tensor * norm_w, float eps, const mi_tensor * sum, const mi_tensor * y, void * workspace,
+                   size_t workspace_bytes, mi_stream stream) {
     if (!y || !norm_w) {
         return MI_ERR_NULL;
     }
     MmvArgs a;
     MI_TRY(mm_desc(w, k, n, x, y, a));
+    if (b) {  // the residual addend and the sum: F32 rows of x's shape, uniformly strided
+        if (!sum) {
+            return MI_ERR_NULL;
+        }
+        MI_TRY(check(b));
+        MI_TRY(check(sum));
+        if (b->type != MI_TYPE_F32 || sum->type != MI_TYPE_F32) {
+            return MI_ERR_TYPE;
+        }
+        if (!same_shape(*b, *x) || !same_shape(*sum, *x) || !uniform_rows(*b) || !uniform_rows(*sum) ||
+            b->nb[0] != 4 || sum->nb[0] != 4) {
+            return MI_ERR_SHAPE;
+        }
+        // the second pass forms a + b again from the inputs: sum must not overlap them
+        auto span_overlap = [&](const mi_tensor & p, const mi_tensor & q) {
+            const char * p0 = (const char *) p.data;
+            const char * q0 = (const char *) q.data;
+            const char * p1 = p0 + (size_t) (a.m - 1) * p.nb[1] + (size_t) k * 4;
+            const char * q1 = q0 + (size_t) (a.m - 1) * q.nb[1] + (size_t) k * 4;
+            return p0 < q1 && q0 < p1;
+        };
+        if (a.m > 0 && (span_overlap(*sum, *x) || span_overlap(*sum, *b))) {
+            return MI_ERR_PARAM;
+        }
+        a.ab   = (const char *) b->data;
+        a.ab1  = (int64_t) b->nb[1];
+        a.sum  = (char *) sum->data;
+        a.sum1 = (int64_t) sum->nb[1];
+        a.xvec = a.xvec && aligned(b->data, 16) && (a.m <= 1 || b->nb[1] % 16 == 0);
+    }
     MI_TRY(check(norm_w));
     if (norm_w->type != MI_TYPE_F32) {
         return MI_ERR_TYPE;
@@ -957,6 +987,21 @@ int mi_mul_mat_q8_0_rms_norm(const void * w, int64_t k, int64_t n, const mi_tens
     a.eps = eps;
     mul_mat_q8_0_bind(a, (char *) workspace);
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
+}
+
+int mi_mul_mat_q8_0_rms_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * norm_w,
+                             float eps, const mi_tensor * y, void * workspace, size_t workspace_bytes,
+                             mi_stream stream) {
+    return mm_norm(w, k, n, x, nullptr, norm_w, eps, nullptr, y, workspace, workspace_bytes, stream);
+}
+
+int mi_mul_mat_q8_0_add_rms_norm(const void * w, int64_t k, int64_t n, const mi_tensor * a, const mi_tensor * b,
+                                 const mi_tensor * norm_w, float eps, const mi_tensor * sum, const mi_tensor * y,
+                                 void * workspace, size_t workspace_bytes, mi_stream stream) {
+    if (!b) {
+        return MI_ERR_NULL;
+    }
+    return mm_norm(w, k, n, a, b, norm_w, eps, sum, y, workspace, workspace_bytes, stream);
 }
 
 // F32 [oc, t, n] contiguous, the velocity/latent layout of the sampler

@@ -168,6 +168,10 @@ struct MmvArgs {
                                     // blocks per wave (set by mul_mat_q8_0_plan)
     const float * nw;          // non-null: x = rms_norm(x) * nw (the norm prologue), with eps
     float        eps;
+    const char * ab;           // non-null (with nw): x = x + ab first, rows at stride ab1,
+    int64_t      ab1;          // the sum written to sum (rows at stride sum1)
+    char *       sum;
+    int64_t      sum1;
     int          glu;          // 1: x = silu(g) * u (the SwiGLU prologue), rows at stride gu1
     const char * g;
     const char * u;

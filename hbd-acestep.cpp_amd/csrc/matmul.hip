@@ -119,7 +119,10 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
 // squares and x' = (x * scale) * w, the arithmetic of mi_rms_norm on F32 rows
 // (only the order of the double additions differs, which leaves the float mean
 // unchanged short of a double rounding tie); then x' is quantized as
-// k_mmv_quant_x does, 8 lanes per 32-element block.
+// k_mmv_quant_x does, 8 lanes per 32-element block. With an addend (a.ab), x is
+// the residual sum a.x + a.ab, written to a.sum in the first pass (the
+// arithmetic of mi_add_rms_norm) and formed again from the two inputs in the
+// second.
 __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
     __shared__ double red[4];
     __shared__ float  scl;
@@ -140,10 +143,30 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
             }
         }
     };
+    const char * br = a.ab ? a.ab + (int64_t) m * a.ab1 : nullptr;
+    // x (or the residual sum) at element i: 4 floats
+    auto xv = [&](uint32_t i, float (&v)[4]) {
+        ld4(xr + (size_t) i * 4, v);
+        if (br) {
+            float b4[4];
+            ld4(br + (size_t) i * 4, b4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = v[e] + b4[e];
+            }
+        }
+    };
     double ss = 0.0;
     for (uint32_t i = 4u * (uint32_t) tid; i < a.k; i += 1024u) {
         float v[4];
-        ld4(xr + (size_t) i * 4, v);
+        xv(i, v);
+        if (a.sum) {
+            float * sp = (float *) (a.sum + (int64_t) m * a.sum1) + i;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sp[e] = v[e];
+            }
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             ss += (double) (v[e] * v[e]);
@@ -163,7 +186,7 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
     for (uint32_t b = (uint32_t) tid >> 3; b < a.nbk; b += 32u) {  // the 8 lanes of a block share b
         const uint32_t i0 = b * 32u + sub * 4u;
         float          f[4];
-        ld4(xr + (size_t) i0 * 4, f);
+        xv(i0, f);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const float v = f[e] * scale;

@@ -271,6 +271,16 @@ int mi_mul_mat_q8_0_rms_norm(const void * w, int64_t k, int64_t n, const mi_tens
                              float eps, const mi_tensor * y, void * workspace, size_t workspace_bytes,
                              mi_stream stream);
 
+/* The same with the residual add before the norm: sum = a + b (written, F32 [k,
+ * m], for the next residual), y = ggml_mul_mat(w, rms_norm(sum) * norm_w)
+ * (qwen3-lm.h:729-737: the attention residual, the post-attention norm and the
+ * gate/up projection), equal to mi_add_rms_norm followed by mi_mul_mat_q8_0.
+ * a, b, sum: F32 [k, m], uniformly strided rows; sum must not overlap a or b
+ * (MI_ERR_PARAM). Workspace as mi_mul_mat_q8_0 for x = a. */
+int mi_mul_mat_q8_0_add_rms_norm(const void * w, int64_t k, int64_t n, const mi_tensor * a, const mi_tensor * b,
+                                 const mi_tensor * norm_w, float eps, const mi_tensor * sum, const mi_tensor * y,
+                                 void * workspace, size_t workspace_bytes, mi_stream stream);
+
 /* The DiT sampler's per-step math on the device (dit_ggml_generate,
  * dit-sampler.h:408-640), so the latents stay resident across steps.
  * Latents and velocities are F32 [Oc, T, N], contiguous.

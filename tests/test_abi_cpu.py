@@ -222,6 +222,14 @@ def test_mul_mat_q8_0_validation():
     assert mn(W, k, n, R(x), R(nw), ctypes.c_float(-1.0), R(y), None, 0, NULL_S) == -6
     assert mn(W, k, n, R(x), R(nw), ctypes.c_float(1e-6), R(y), None, 0, NULL_S) == -6   # no workspace
     assert mn(W, k, n, R(x), R(nw), ctypes.c_float(1e-6), None, None, 0, NULL_S) == -1
+    # with the residual add: sum = a + b must not overlap a or b
+    ma = L.mi_mul_mat_q8_0_add_rms_norm
+    eps = ctypes.c_float(1e-6)
+    assert ma(W, k, n, R(x), None, R(nw), eps, R(x), R(y), None, 0, NULL_S) == -1
+    assert ma(W, k, n, R(x), R(_t([k, m])), R(nw), eps, None, R(y), None, 0, NULL_S) == -1
+    assert ma(W, k, n, R(x), R(_t([k, m + 1])), R(nw), eps, R(_t([k, m])), R(y), None, 0, NULL_S) == -3
+    assert ma(W, k, n, R(x), R(_t([k, m], BF16)), R(nw), eps, R(_t([k, m])), R(y), None, 0, NULL_S) == -2
+    assert ma(W, k, n, R(x), R(_t([k, m])), R(nw), eps, R(x), R(y), None, 0, NULL_S) == -6   # sum aliases a
     # the SwiGLU prologue: gu [2k, m]
     gu = _t([2 * k, m])
     mg = L.mi_mul_mat_q8_0_swiglu

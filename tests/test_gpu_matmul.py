@@ -187,3 +187,25 @@ def test_rms_norm_prologue_matches_norm_then_mul_mat(dev, n, k, m, view):
     y_u = to_np(ops.mul_mat_q8_0(wr, norm))
     assert np.array_equal(y_f, y_u)
     _check(y_f, w, to_np(norm))
+
+
+@pytest.mark.parametrize("n,k,m", [(19456, 2560, 8), (300, 256, 3), (640, 256, 129)])
+def test_add_rms_norm_prologue_matches_add_norm_then_mul_mat(dev, n, k, m):
+    """mi_mul_mat_q8_0_add_rms_norm (sum = a + b written, RMSNorm*w of it made inside
+    the quantization of x) against mi_add_rms_norm followed by mi_mul_mat_q8_0: the
+    sum bit-identical, the product bit-identical; then the product against the oracle
+    on the normalized rows the device produced."""
+    print(f"mul_mat q8_0 add_rms_norm n={n} k={k} m={m}", flush=True)
+    r = np.random.default_rng(n + k + m + 2)
+    w = orc.quantize_q8_0((r.standard_normal((n, k)) * 0.05).astype(np.float32))
+    a = r.standard_normal((m, k)).astype(np.float32)
+    b = (r.standard_normal((m, k)) * 0.3).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    da, db, dnw = to_dev(a), to_dev(b), to_dev(nw)
+    s_f, y_f = ops.mul_mat_q8_0_add_rms_norm(wr, da, db, dnw, 1e-6)
+    s_u, n_u = ops.add_rms_norm(da, db, 1e-6, w=dnw)
+    y_u = to_np(ops.mul_mat_q8_0(wr, n_u))
+    assert np.array_equal(to_np(s_f), to_np(s_u))
+    assert np.array_equal(to_np(y_f), y_u)
+    _check(to_np(y_f), w, to_np(n_u))
