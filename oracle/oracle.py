@@ -10,7 +10,7 @@ call them in the order the reference's graph builders emit them, citing the
 builder lines, so a fused GPU kernel is compared against the unfused ggml
 node sequence it replaces.
 
-bf16 activations (a BASELINE extension; the reference computes in F32) are
+bf16 activations (measured beside the reference's F32; the reference computes in F32) are
 checked as: bf16 -> f32 (exact), the fp32 node chain, f32 -> bf16 (RNE).
 """
 from __future__ import annotations

@@ -13,14 +13,14 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels through the C ABI)")
 
 
-def _gpu_box() -> bool:
+def _have_gpu() -> bool:
     return os.path.exists("/dev/kfd")
 
 
 def pytest_collection_modifyitems(config, items):
     # Without a GPU device node (this build container) GPU tests are skipped;
-    # on a GPU box they always run, so a broken device fails instead of skipping.
-    if _gpu_box():
+    # on a machine with a GPU they always run, so a broken device fails instead of skipping.
+    if _have_gpu():
         return
     skip = pytest.mark.skip(reason="no GPU device in this container")
     for item in items:
