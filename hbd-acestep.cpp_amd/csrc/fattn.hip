@@ -889,8 +889,7 @@ k_fa_mfma(const FaArgs a) {
     // The tile loop, compiled twice in the masked kernel: with the per-tile
     // summary reads (MK), and without them for a workgroup whose mask rows are
     // all zero over its key range (every summary byte 1: live, no nonzero
-    // value) -- the padding mask of unpadded DiT sequences. The second version
-    // runs as fast as the unmasked kernel; the first is ~15 % slower.
+    // value) -- the padding mask of unpadded DiT sequences.
     auto tiles = [&](auto mtag) {
     constexpr bool MK = decltype(mtag)::value;
     auto flag = [&](int t) -> int {
