@@ -40,6 +40,7 @@ constexpr int FA_MAXT = 16;  // tiles per split at most (the split's mask is sta
 constexpr int FA_MAX_SPLITS = 1024;  // splits of one key range at most (the merge keeps their weights in LDS)
 // floats per row of a matrix-core split half: m, l, 2 unused, o[128] (16-byte aligned rows)
 constexpr int FA_PART = 132;
+constexpr int FA_SUM_T = 4;  // 64-key tiles per wave of the mask summary
 
 template <int KT> struct FaT;
 template <> struct FaT<MI_TYPE_F32> {
@@ -650,48 +651,73 @@ __device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, cons
 }
 
 // Mask summary for the matrix-core path, one wave per (mask batch and head,
-// group of 16 query positions, 64-key tile): lane = 4 keys (4 * (lane % 16))
-// of rows lane / 16 + 4 i, as 8-byte loads when the mask rows allow it.
+// group of 16 query positions, FA_SUM_T consecutive 64-key tiles): lane = 4
+// keys (4 * (lane % 16)) of rows lane / 16 + 4 i of each tile, as 8-byte loads
+// when the mask rows allow it.
 // The attention kernel then loads no mask values for a tile whose values are
 // all 0 and skips the math of a tile whose keys are all -inf for its rows.
 __global__ void __launch_bounds__(64) k_fa_mask_summary(const FaArgs a) {
+    // FA_SUM_T consecutive tiles per wave: all of their loads are issued before
+    // any flag is formed
     const int      lane = threadIdx.x;
-    const uint32_t tile = blockIdx.x, grp = blockIdx.y, mh = blockIdx.z;
+    const uint32_t grp = blockIdx.y, mh = blockIdx.z;
     const uint32_t m3 = mh / (uint32_t) a.mne2, m2 = mh - m3 * (uint32_t) a.mne2;
-    const int      k4 = (int) tile * 64 + 4 * (lane & 15);
-    const char *   mp = a.mask + (int64_t) m3 * a.m3 + (int64_t) m2 * a.m2;
-    bool           live = false, nz = false;
+    const char *   mp  = a.mask + (int64_t) m3 * a.m3 + (int64_t) m2 * a.m2;
+    const int      ntl = (a.n_kv + 63) / 64;
+    const int      kl  = 4 * (lane & 15);  // this lane's 4 keys within a tile
+    uint16_t       hv[FA_SUM_T][4][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int iq = (int) grp * 16 + (lane >> 4) + 4 * i;
-        if (iq >= a.n_q || k4 >= a.n_kv) {
-            continue;
-        }
-        const char * rp = mp + (int64_t) iq * a.m1;
-        uint16_t     hv[4];
-        if (a.mvec && k4 + 3 < a.n_kv) {
-            const uint2 w = *(const uint2 *) (rp + (int64_t) k4 * 2);
-            hv[0]         = (uint16_t) w.x;
-            hv[1]         = (uint16_t) (w.x >> 16);
-            hv[2]         = (uint16_t) w.y;
-            hv[3]         = (uint16_t) (w.y >> 16);
-        } else {
+    for (int tt = 0; tt < FA_SUM_T; ++tt) {
+        const int tile = (int) blockIdx.x * FA_SUM_T + tt;
+        const int k4   = tile * 64 + kl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int iq = (int) grp * 16 + (lane >> 4) + 4 * i;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                hv[e] = *(const uint16_t *) (rp + (int64_t) (k4 + e < a.n_kv ? k4 + e : k4) * 2);
+                hv[tt][i][e] = 0;
+            }
+            if (tile >= ntl || iq >= a.n_q || k4 >= a.n_kv) {
+                continue;
+            }
+            const char * rp = mp + (int64_t) iq * a.m1;
+            if (a.mvec && k4 + 3 < a.n_kv) {
+                const uint2 w = *(const uint2 *) (rp + (int64_t) k4 * 2);
+                hv[tt][i][0]  = (uint16_t) w.x;
+                hv[tt][i][1]  = (uint16_t) (w.x >> 16);
+                hv[tt][i][2]  = (uint16_t) w.y;
+                hv[tt][i][3]  = (uint16_t) (w.y >> 16);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (k4 + e < a.n_kv) {
+                        hv[tt][i][e] = *(const uint16_t *) (rp + (int64_t) (k4 + e) * 2);
+                    }
+                }
             }
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const bool ok = k4 + e < a.n_kv;
-            live          = live || (ok && hv[e] != 0xFC00u);    // not -inf
-            nz            = nz || (ok && (hv[e] & 0x7FFFu) != 0);  // not +-0
-        }
     }
-    const uint64_t lv = __builtin_amdgcn_ballot_w64(live), nv = __builtin_amdgcn_ballot_w64(nz);
-    if (lane == 0) {
-        const int ntl = (a.n_kv + 63) / 64;
-        a.msum[((int64_t) mh * a.ngq + grp) * ntl + tile] = (uint8_t) ((lv ? 1 : 0) | (nv ? 2 : 0));
+#pragma unroll
+    for (int tt = 0; tt < FA_SUM_T; ++tt) {
+        const int tile = (int) blockIdx.x * FA_SUM_T + tt;
+        const int k4   = tile * 64 + kl;
+        bool      live = false, nz = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int  iq    = (int) grp * 16 + (lane >> 4) + 4 * i;
+            const bool rowok = tile < ntl && iq < a.n_q;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool     ok = rowok && k4 + e < a.n_kv;
+                const uint16_t h  = hv[tt][i][e];
+                live              = live || (ok && h != 0xFC00u);          // not -inf
+                nz                = nz || (ok && (h & 0x7FFFu) != 0);      // not +-0
+            }
+        }
+        const uint64_t lv = __builtin_amdgcn_ballot_w64(live), nv = __builtin_amdgcn_ballot_w64(nz);
+        if (lane == 0 && tile < ntl) {
+            a.msum[((int64_t) mh * a.ngq + grp) * ntl + tile] = (uint8_t) ((lv ? 1 : 0) | (nv ? 2 : 0));
+        }
     }
 }
 
@@ -1229,7 +1255,8 @@ int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
     }
     if (a.mfma) {
         if (a.msum != nullptr) {
-            hipLaunchKernelGGL(k_fa_mask_summary, dim3((uint32_t) ((a.n_kv + 63) / 64), (uint32_t) a.ngq,
+            hipLaunchKernelGGL(k_fa_mask_summary, dim3((uint32_t) (((a.n_kv + 63) / 64 + FA_SUM_T - 1) / FA_SUM_T),
+                                                       (uint32_t) a.ngq,
                                                        (uint32_t) (a.mne3 * a.mne2)),
                                dim3(64), 0, s, a);
         }
