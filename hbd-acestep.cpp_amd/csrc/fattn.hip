@@ -1054,13 +1054,15 @@ k_fa_mfma(const FaArgs a) {
     };
     bool clean = !MSK;
     if constexpr (MSK) {
-        bool c = true;
+        // independent loads (no short-circuit): a chain of dependent byte loads
+        // would cost a memory latency per tile
+        uint32_t c = 1;
         if (rvld) {
             for (int t = tb; t < te; ++t) {
-                c = c && sp[t] == 1;
+                c &= (uint32_t) (sp[t] == 1);
             }
         }
-        clean = __syncthreads_and(c) != 0;  // workgroup-uniform: the waves share the K/V tiles
+        clean = __syncthreads_and((int) c) != 0;  // workgroup-uniform: the waves share the K/V tiles
     }
     if (clean) {
         tiles(std::false_type{});
