@@ -1,7 +1,8 @@
 """acestep_ops -- MI355X (gfx950) per-layer fused ops of acestep.cpp's Qwen3 LM
 and ACE-Step DiT graph builders, behind the C ABI of include/mi_ops.h.
 
-``acestep_ops.ops`` holds the torch-facing wrappers (ggml op names);
+``acestep_ops.ops`` holds one wrapper per entry point (ggml op names) over
+``device.DTensor`` views;
 ``acestep_ops._lib`` the ctypes binding. The HIP library is the only compute
 path; importing the ops without the built library raises ImportError.
 """

@@ -62,7 +62,7 @@ class MiDitBlockIO(ctypes.Structure):
     _fields_ = [(n, MiTensor) for n in (
         "hidden", "adaln", "sa_norm_w", "ffn_norm_w", "norm_sa",
         "q", "k", "q_w", "k_w", "q_out", "k_out", "pos",
-        "sa_out", "ca_norm_w", "norm_ca", "ca_q", "ca_q_w", "ca_q_out", "ca_out",
+        "sa_out", "ca_norm_w", "norm_ca", "ca_q", "ca_q_w", "ca_q_out", "ca_out", "ca_k", "ca_k_w", "ca_k_out",
         "norm_ffn", "gate_up", "ff", "ffn_out")] + [
         ("eps", ctypes.c_float), ("rope_freq_base", ctypes.c_float),
         ("n_dims", ctypes.c_int), ("use_cross_attn", ctypes.c_int)]

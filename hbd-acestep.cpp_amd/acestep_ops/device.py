@@ -207,6 +207,18 @@ class DTensor:
     def numel(self) -> int:
         return math.prod(self.shape)
 
+    def extent(self):
+        """Byte range [lo, hi) of the buffer this view can address (lo == hi when empty)."""
+        if self.numel() == 0:
+            return self.offset, self.offset
+        lo = hi = self.offset
+        for n, s in zip(self.shape, self.strides):
+            if s >= 0:
+                hi += (n - 1) * s * self.es
+            else:
+                lo += (n - 1) * s * self.es
+        return lo, hi + self.es
+
     def is_contiguous(self) -> bool:
         return self.strides == _contig_strides(self.shape)
 

@@ -55,6 +55,9 @@ def desc(t) -> MiTensor:
         blck = 1
     if len(shape) > 4:
         raise ValueError("at most 4 dimensions")
+    lo, hi = x.extent()
+    if lo < 0 or hi > x.buf.nbytes:
+        raise ValueError(f"view bytes [{lo}, {hi}) fall outside its {x.buf.nbytes}-byte allocation")
     ne = shape[::-1]
     nb = nbytes[::-1]
     while len(ne) < 4:  # outer dims of size 1 continue contiguously

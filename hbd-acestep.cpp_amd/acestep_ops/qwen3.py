@@ -14,6 +14,12 @@ F16 KV cache:
   hidden = hidden + mul_mat(W_down, swiglu(mul_mat(W_gate_up, norm2)))  (737-741;
            swiglu and the down product as one call, mul_mat_q8_0_swiglu)
 
+With clamp_fp16 (qwen3-lm.h:53, set from the CLI at pipeline-lm.cpp:616) V is
+clamped to the fp16 range before the cache store (674-677) and both residual
+sums are clamped (730-733, 738-741); the post-attention sum is then its own
+add + norm call ahead of the gate/up product, since the fused add + norm +
+product call has no clamp.
+
 Shapes outermost first: hidden (N, H) F32 for N sequences of one token; the
 caches (n_sets, Nkv, max_seq, D) (ggml [D, max_seq, Nkv, n_sets]); sequence i
 uses set s0 + i, writes at pos[i] and attends to read_len slots under a mask
@@ -27,6 +33,8 @@ import numpy as np
 from . import ops
 from .device import DTensor
 
+FP16_MAX = 65504.0
+
 
 def decode_mask(pos, read_len: int) -> DTensor:
     """F16 (N, 1, 1, read_len): 0 for slots <= pos[i] (the token just written
@@ -39,10 +47,11 @@ def decode_mask(pos, read_len: int) -> DTensor:
 class Qwen3DecodeLayer:
     def __init__(self, w_qkv, w_o, w_gate_up, w_down, in_norm_w, post_norm_w, q_norm_w, k_norm_w, H: int, Nh: int,
                  Nkv: int, D: int, I: int, max_seq: int, n_sets: int, kv_type: str = "q8_0", eps: float = 1e-6,
-                 rope_theta: float = 1e6, stream=None):
+                 rope_theta: float = 1e6, clamp_fp16: bool = False, stream=None):
         """w_*: Q8 weights in the GGUF layout (repacked here once); norms: F32 DTensors."""
         self.H, self.Nh, self.Nkv, self.D, self.I = H, Nh, Nkv, D, I
         self.eps, self.theta, self.stream = eps, rope_theta, stream
+        self.clamp_fp16 = bool(clamp_fp16)
         self.w = {name: ops.q8_0_repack(w, stream=stream)
                   for name, w in (("qkv", w_qkv), ("o", w_o), ("gu", w_gate_up), ("down", w_down))}
         self.in_norm_w, self.post_norm_w = in_norm_w, post_norm_w
@@ -85,6 +94,8 @@ class Qwen3DecodeLayer:
         v = qkv[:, (Nh + Nkv) * D:qkv_dim].unflatten(1, (Nkv, D))
         qo, ko = ops.qk_norm_rope(q, self.q_norm_w, pos, self.eps, D, self.theta, k=k, k_w=self.k_norm_w,
                                   q_out=self._buf("qo", (N, Nh, D)), k_out=self._buf("ko", (N, Nkv, D)), stream=st)
+        if self.clamp_fp16:
+            ops.clamp(v, -FP16_MAX, FP16_MAX, out=v, stream=st)
         ops.kv_store(ko.unflatten(0, (N, 1)), self.k_cache, pos, v=v.unflatten(0, (N, 1)), v_cache=self.v_cache,
                      sets=sets, stream=st)
         kv = self._cache_view(self.k_cache, s0, N, read_len)
@@ -95,15 +106,24 @@ class Qwen3DecodeLayer:
         ops.flash_attn_ext(qf, kv, vv, mask, 1.0 / math.sqrt(D), out=attn, workspace=ws, stream=st)
         a2 = attn.view(N, Nh * D)
         ao = ops.mul_mat_q8_0(self.w["o"], a2, out=self._buf("ao", (N, H)), workspace=self._ws("o", a2), stream=st)
-        # the residual add, the post-attention norm and the gate/up product in one call
-        h1, gu = ops.mul_mat_q8_0_add_rms_norm(self.w["gu"], hidden, ao, self.post_norm_w, self.eps,
-                                               out_sum=self._buf("h1", (N, H)), out=self._buf("gu", (N, 2 * I)),
-                                               workspace=self._ws("gu", hidden), stream=st)
+        if self.clamp_fp16:
+            h1, n2 = ops.add_rms_norm(hidden, ao, self.eps, w=self.post_norm_w, clamp=(-FP16_MAX, FP16_MAX),
+                                      out_sum=self._buf("h1", (N, H)), out_norm=self._buf("n2", (N, H)), stream=st)
+            gu = ops.mul_mat_q8_0(self.w["gu"], n2, out=self._buf("gu", (N, 2 * I)), workspace=self._ws("gu", n2),
+                                  stream=st)
+        else:
+            # the residual add, the post-attention norm and the gate/up product in one call
+            h1, gu = ops.mul_mat_q8_0_add_rms_norm(self.w["gu"], hidden, ao, self.post_norm_w, self.eps,
+                                                   out_sum=self._buf("h1", (N, H)), out=self._buf("gu", (N, 2 * I)),
+                                                   workspace=self._ws("gu", hidden), stream=st)
         # swiglu and the down projection in one call: the SwiGLU values are made
         # inside the quantization of the product's x (bit-identical to the two ops)
         mlp = ops.mul_mat_q8_0_swiglu(self.w["down"], gu, out=self._buf("mlp", (N, H)),
                                       workspace=self._ws_glu("down", gu), stream=st)
-        return ops.add(h1, mlp, out=out if out is not None else self._buf("out", (N, H)), stream=st)
+        y = out if out is not None else self._buf("out", (N, H))
+        if self.clamp_fp16:
+            return ops.add_clamp(h1, mlp, -FP16_MAX, FP16_MAX, out=y, stream=st)
+        return ops.add(h1, mlp, out=y, stream=st)
 
     def _ws(self, name, x):
         need = ops.mul_mat_q8_0_workspace(self.w[name], x)

@@ -63,9 +63,12 @@ extern "C" int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream s) {
     if (io->use_cross_attn) {
         MI_TRY(mi_add_rms_norm(&io->hidden, &io->sa_out, &gate_sa, 0, 0.0f, 0.0f, &io->ca_norm_w, nullptr, nullptr,
                                io->eps, &io->hidden, &io->norm_ca, s));
-        // cross-attention Q-norm (328-329)
+        // cross-attention Q-norm and K-norm, per head, no rope (328-331)
         if (io->ca_q.data) {
             MI_TRY(mi_rms_norm(&io->ca_q, &io->ca_q_w, io->eps, &io->ca_q_out, s));
+        }
+        if (io->ca_k.data) {
+            MI_TRY(mi_rms_norm(&io->ca_k, &io->ca_k_w, io->eps, &io->ca_k_out, s));
         }
         // [CA, O-proj] -> residual add (432) fused with the FFN norm (442-443)
         MI_TRY(mi_add_rms_norm(&io->hidden, &io->ca_out, nullptr, 0, 0.0f, 0.0f, &io->ffn_norm_w, &scale_ff,

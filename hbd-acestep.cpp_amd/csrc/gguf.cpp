@@ -266,11 +266,15 @@ int gguf_parse(mi_gguf * g) {
         if (t.ne[0] % blk != 0) {
             return MI_ERR_FILE;
         }
-        __int128 nb = (__int128) (t.ne[0] / blk) * bytes;
+        // element count and byte count with every product checked: a
+        // wrapped product would describe a huge tensor over a small region
+        int64_t nel = t.ne[0], nb = 0;
         for (int d = 1; d < 4; ++d) {
-            nb *= t.ne[d];
+            if (__builtin_mul_overflow(nel, t.ne[d], &nel)) {
+                return MI_ERR_FILE;
+            }
         }
-        if (nb > (__int128) g->size) {
+        if (__builtin_mul_overflow(nel / blk, bytes, &nb) || (uint64_t) nb > g->size) {
             return MI_ERR_FILE;
         }
         t.nbytes = (uint64_t) nb;

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MI_OPS_ABI_VERSION 1
+#define MI_OPS_ABI_VERSION 2
 
 enum mi_type {
     MI_TYPE_F32  = 0,
@@ -357,13 +357,14 @@ int mi_gguf_upload_rows(const mi_gguf * g, const char * const * names, int n, vo
 /* One ACE-Step DiT block's non-GEMM ops, in dit_ggml_build_layer order
  * (dit-graph.h:367-448). hidden is updated in place. Each residual add is
  * fused with the RMSNorm that reads it (mi_add_rms_norm), so the block runs
- * as 5 launches without cross attention (8 with):
+ * as 5 launches without cross attention (8 with, both CA norms given):
  *   pre-SA:   norm_sa   = rms_norm_modulate(hidden, sa_norm_w, scale_sa, shift_sa)
  *   SA:       q_out/k_out = qk_norm_rope(q, k)   [q, k: views of the QKV GEMM output]
  *   post-SA:  hidden    = hidden + sa_out * gate_sa, fused with
  *               norm_ca  = rms_norm(hidden) * ca_norm_w            (cross attention), or
  *               norm_ffn = rms_norm_modulate(hidden, ffn_norm_w, scale_ffn, shift_ffn)
  *   CA:       ca_q_out  = rms_norm(ca_q) * ca_q_w   (when ca_q.data != NULL)
+ *             ca_k_out  = rms_norm(ca_k) * ca_k_w   (when ca_k.data != NULL)
  *             hidden    = hidden + ca_out, fused with norm_ffn as above
  *   FFN:      ff        = swiglu(gate_up)
  *   post-FFN: hidden    = hidden + ffn_out * gate_ffn
@@ -377,8 +378,9 @@ typedef struct mi_dit_block_io {
     mi_tensor q, k, q_w, k_w, q_out, k_out, pos; /* self-attn QK-norm + rope */
     mi_tensor sa_out;                    /* [H, S, N] O-projection output */
     mi_tensor ca_norm_w, norm_ca;        /* cross-attn norm (optional) */
-    mi_tensor ca_q, ca_q_w, ca_q_out;    /* cross-attn Q-norm (optional) */
+    mi_tensor ca_q, ca_q_w, ca_q_out;    /* cross-attn Q-norm (optional), dit-graph.h:328-329 */
     mi_tensor ca_out;                    /* cross-attn output (optional) */
+    mi_tensor ca_k, ca_k_w, ca_k_out;    /* cross-attn K-norm (optional), dit-graph.h:330-331 */
     mi_tensor norm_ffn;                  /* [H, S, N] out */
     mi_tensor gate_up, ff;               /* [2I, S, N] -> [I, S, N] */
     mi_tensor ffn_out;                   /* [H, S, N] down-projection output */

@@ -27,7 +27,7 @@ def test_library_loads_and_exports_header_symbols():
     for name in names:
         assert hasattr(lib, name), f"{name} not exported"
     assert set(names) == set(_lib.PROTOTYPES), "ctypes prototypes out of sync with mi_ops.h"
-    assert lib.mi_abi_version() == 1
+    assert lib.mi_abi_version() == 2
     assert lib.mi_status_str(-3) == b"inconsistent shapes"
 
 

@@ -134,6 +134,11 @@ def test_malformed_files(tmp_path):
     assert _rc(put("kvtype.gguf", bad_kv)) == -9
     nested = b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + gw._str("n") + struct.pack("<IIQ", gw.ARR, gw.ARR, 1)
     assert _rc(put("nested.gguf", nested + struct.pack("<IQ", gw.U8, 0))) == -9
+    # element or byte counts that overflow 64 bits (a wrapped product would describe
+    # a huge tensor over a 0-byte region)
+    assert _rc(put("nel_ovf.gguf", gw.build(KV, [("x", 0, [2 ** 61, 2 ** 61, 16], b"")])[0])) == -9
+    assert _rc(put("nb_ovf.gguf", gw.build(KV, [("x", 0, [2 ** 60, 2], b"")])[0])) == -9
+    assert _rc(put("q8_ovf.gguf", gw.build(KV, [("x", 8, [2 ** 61, 2 ** 2], b"")])[0])) == -9
     huge = b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + struct.pack("<Q", 1 << 60)
     assert _rc(put("hugestr.gguf", huge)) == -9
 

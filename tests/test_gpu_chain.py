@@ -6,6 +6,7 @@ import ctypes
 import numpy as np
 import pytest
 
+import dit_block_case
 from helpers import assert_bf16_ulp, assert_f32_close, randn, rng, to_dev, to_np, tsembd_bar
 from oracle import oracle as orc
 
@@ -26,85 +27,47 @@ def test_timestep_embedding(dev):
     assert not y[:, 6].any()
 
 
-def _ref_dit_block(h, ad, saw, ffw, q, k, qw, kw, pos, sa_out, gu, ffn_out, H, D, theta):
-    shift_sa, scale_sa, gate_sa, shift_ff, scale_ff, gate_ff = (ad[i * H:(i + 1) * H] for i in range(6))
-    norm_sa = orc.rms_norm_modulate(h, saw, scale_sa, shift_sa, EPS)
-    qo = orc.qk_norm_rope(q, qw, pos, EPS, D, theta)
-    ko = orc.qk_norm_rope(k, kw, pos, EPS, D, theta)
-    h1 = orc.gated_add(h, sa_out, gate_sa)
-    norm_ff = orc.rms_norm_modulate(h1, ffw, scale_ff, shift_ff, EPS)
-    ff = orc.swiglu(gu)
-    h2 = orc.gated_add(h1, ffn_out, gate_ff)
-    return norm_sa, qo, ko, norm_ff, ff, h2
+class _DevStorage:
+    """Device storage for the shared DiT block case."""
+
+    @staticmethod
+    def empty(shape, dtype):
+        return DTensor.empty(shape, dtype)
+
+    @staticmethod
+    def up(a, dtype):
+        return DTensor.from_numpy(a, dtype)
 
 
-# This test's process segfaulted twice on the GPU host inside torch's
-# host->device copy (its first statement after the previous test), when the
-# suite ran under torch's bundled ROCm 7.0 HIP runtime. The suite no longer
-# loads torch, but no fault in this library's code has been shown to explain
-# the aborts, so the test stays off the GPU. Its five launches are the per-op
-# entry points that the other GPU tests and the bench run.
-@pytest.mark.skip(reason="kept off the GPU after two aborts of this test under torch's ROCm 7.0 runtime; no cause in this library's code has been shown")
+@pytest.mark.parametrize("cross", [False, True], ids=["self_only", "cross_attn"])
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
-def test_dit_block_chain(dev, dt):
-    """ACE-Step DiT block (H=2048, 16/8 heads x 128, I=6144) on S=96 x N=2 rows."""
-    bf16 = dt == "bf16"
-    H, nh, nkv, D, I, S, N, theta = 2048, 16, 8, 128, 6144, 96, 2, 1e4
-    R = S * N
-    h = randn((N, S, H), seed=1)
-    ad = randn((6 * H,), seed=2, scale=0.1)
-    saw = randn((H,), seed=3, scale=0.1, mean=1.0)
-    ffw = randn((H,), seed=4, scale=0.1, mean=1.0)
-    qkv = randn((N, S, (nh + 2 * nkv) * D), seed=5)
-    sa_out = randn((N, S, H), seed=6)
-    gu = randn((N, S, 2 * I), seed=7)
-    ffn_out = randn((N, S, H), seed=8)
-    qw = randn((D,), seed=9, scale=0.1, mean=1.0)
-    kw = randn((D,), seed=10, scale=0.1, mean=1.0)
-    pos = np.tile(np.arange(S, dtype=np.int32), N)
-
-    cv = orc.f32_to_bf16 if bf16 else (lambda a: a)
-    hh, qkvh, sah, guh, ffh = (cv(a) for a in (h, qkv, sa_out, gu, ffn_out))
-    d = lambda a: to_dev(a, dev, bf16=bf16)  # noqa: E731
-    hd, qkvd, sad, gud, ffd = d(hh), d(qkvh), d(sah), d(guh), d(ffh)
-    qd = qkvd.view(R, -1)[:, :nh * D].unflatten(1, (nh, D))
-    kd = qkvd.view(R, -1)[:, nh * D:(nh + nkv) * D].unflatten(1, (nkv, D))
-    act = "bf16" if bf16 else "f32"
-    norm_sa = DTensor.empty((N, S, H), act)
-    norm_ff = DTensor.empty((N, S, H), act)
-    q_out = DTensor.empty((R, nh, D), act)
-    k_out = DTensor.empty((R, nkv, D), act)
-    ff = DTensor.empty((N, S, I), act)
-    io = _lib.MiDitBlockIO()
-    io.hidden, io.adaln = ops.desc(hd), ops.desc(to_dev(ad, dev))
-    keep = [to_dev(a, dev) for a in (saw, ffw, qw, kw, pos)]
-    io.sa_norm_w, io.ffn_norm_w = ops.desc(keep[0]), ops.desc(keep[1])
-    io.norm_sa, io.norm_ffn = ops.desc(norm_sa), ops.desc(norm_ff)
-    io.q, io.k, io.q_w, io.k_w = ops.desc(qd), ops.desc(kd), ops.desc(keep[2]), ops.desc(keep[3])
-    io.q_out, io.k_out, io.pos = ops.desc(q_out), ops.desc(k_out), ops.desc(keep[4])
-    io.sa_out, io.gate_up, io.ff, io.ffn_out = ops.desc(sad), ops.desc(gud), ops.desc(ff), ops.desc(ffd)
-    io.eps, io.rope_freq_base, io.n_dims, io.use_cross_attn = EPS, theta, D, 0
+def test_dit_block_chain(dev, dt, cross):
+    """ACE-Step DiT block (H=2048, 16/8 heads x 128, I=6144) on S=96 x N=2 rows,
+    with and without the cross-attention branch (dit-graph.h:426-433), against
+    the unfused node sequence. Every descriptor is checked against its
+    allocation on the host first (ops.desc and test_chain_descriptors_cpu)."""
+    print(f"dit block chain {dt} cross={cross}", flush=True)
+    io, host, outs, _keep = dit_block_case.build(dt, cross, _DevStorage)
     _lib.call("mi_dit_block_ops", ctypes.byref(io), None)
     device.synchronize()
-
-    f = orc.bf16_to_f32 if bf16 else (lambda a: a)
-    qh = f(qkvh).reshape(R, -1)[:, :nh * D].reshape(R, nh, D)
-    kh = f(qkvh).reshape(R, -1)[:, nh * D:(nh + nkv) * D].reshape(R, nkv, D)
-    refs = _ref_dit_block(f(hh).reshape(R, H), ad, saw, ffw, qh, kh, qw, kw, pos, f(sah).reshape(R, H),
-                          f(guh).reshape(R, 2 * I), f(ffh).reshape(R, H), H, D, theta)
-    outs = [norm_sa, q_out, k_out, norm_ff, ff, hd]
-    floors = [True, True, True, True, False, True]
-    for name, o, r, fl in zip(["norm_sa", "q", "k", "norm_ffn", "ff", "hidden"], outs, refs, floors):
+    refs = dit_block_case.reference(dt, cross, host)
+    for name, r in refs.items():
         print("check", name, flush=True)
-        got = to_np(o).reshape(r.shape)
-        if bf16:
-            assert_bf16_ulp(got, orc.f32_to_bf16(r))
+        got = to_np(outs[name]).reshape(r.shape)
+        if name in dit_block_case.BIT_EXACT:
+            assert np.array_equal(got, r), name
+        elif dt == "bf16":
+            assert_bf16_ulp(got, r, row_floor=dit_block_case.ROW_FLOOR[name])
         else:
-            assert_f32_close(got, r, row_floor=fl)
+            assert_f32_close(got, r, row_floor=dit_block_case.ROW_FLOOR[name])
 
 
-def test_qwen3_layer_chain_decode(dev):
-    """Qwen3-4B-shaped decode step, batch 8, F32, clamp_fp16 on, Q8_0 KV cache."""
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_qwen3_layer_chain_decode(dev, dt):
+    """Qwen3-4B-shaped decode step, batch 8, clamp_fp16 on, Q8_0 KV cache; F32
+    and the bf16 activations of the batch-8 decode configuration."""
+    print(f"qwen3 layer chain decode {dt}", flush=True)
+    bf16 = dt == "bf16"
     H, nh, nkv, D, I, N, max_seq, theta = 2560, 32, 8, 128, 9728, 8, 8192, 1e6
     r = rng(3)
     h = randn((N, H), seed=1)
@@ -120,21 +83,25 @@ def test_qwen3_layer_chain_decode(dev):
     kw = randn((D,), seed=9, scale=0.1, mean=1.0)
     pos = r.integers(0, max_seq, N).astype(np.int32)
     sets = np.arange(N, dtype=np.int32)
+    act = "bf16" if bf16 else "f32"
+    if bf16:
+        h, qkv, attn_out, gu, mlp_out = (orc.f32_to_bf16(a) for a in (h, qkv, attn_out, gu, mlp_out))
+    up = lambda a: DTensor.from_numpy(a, act)  # noqa: E731
 
-    hd, qkvd = to_dev(h, dev), to_dev(qkv, dev)
+    hd, qkvd = up(h), up(qkv)
     qd = qkvd[:, :nh * D].unflatten(1, (nh, D))
     kd = qkvd[:, nh * D:(nh + nkv) * D].unflatten(1, (nkv, D))
     vd = qkvd[:, (nh + nkv) * D:].unflatten(1, (nkv, D))
     rb = D // 32 * 34
     kc = DTensor.zeros((N, nkv, max_seq, rb), "u8")
     vc = DTensor.zeros((N, nkv, max_seq, rb), "u8")
-    norm = DTensor.empty((N, H))
-    norm2 = DTensor.empty((N, H))
-    q_out = DTensor.empty((N, nh, D))
-    k_out = DTensor.empty((N, nkv, D))
-    ff = DTensor.empty((N, I))
+    norm = DTensor.empty((N, H), act)
+    norm2 = DTensor.empty((N, H), act)
+    q_out = DTensor.empty((N, nh, D), act)
+    k_out = DTensor.empty((N, nkv, D), act)
+    ff = DTensor.empty((N, I), act)
     err = DTensor.zeros((1,), "i32")
-    keep = [to_dev(a, dev) for a in (w_in, w_post, qw, kw, pos, pos, sets, attn_out, gu, mlp_out)]
+    keep = [to_dev(a, dev) for a in (w_in, w_post, qw, kw, pos, pos, sets)] + [up(a) for a in (attn_out, gu, mlp_out)]
     io = _lib.MiQwen3LayerIO()
     io.hidden, io.in_norm_w, io.post_norm_w = ops.desc(hd), ops.desc(keep[0]), ops.desc(keep[1])
     io.norm, io.norm2 = ops.desc(norm), ops.desc(norm2)
@@ -148,27 +115,31 @@ def test_qwen3_layer_chain_decode(dev):
     _lib.call("mi_qwen3_layer_ops", ctypes.byref(io), None)
     device.synchronize()
 
-    # oracle: qw3lm_forward_batch node order (qwen3-lm.h:632-741)
-    n1 = orc.rms_norm_mul(h, w_in, EPS)
+    # oracle: qw3lm_forward_batch node order (qwen3-lm.h:632-741); in bf16 each
+    # stored node output is rounded to bf16 before the next node reads it
+    ch = orc.bf16_chain if bf16 else (lambda fn, *a, **kw: fn(*a, **kw))
+    f32 = orc.bf16_to_f32 if bf16 else (lambda a: a)
+    n1 = ch(orc.rms_norm_mul, h, w_in, EPS)
     qh = qkv[:, :nh * D].reshape(N, nh, D)
     kh = qkv[:, nh * D:(nh + nkv) * D].reshape(N, nkv, D)
-    vh = orc.clamp(qkv[:, (nh + nkv) * D:].reshape(N, nkv, D), -65504.0, 65504.0)
-    qo = orc.qk_norm_rope(qh, qw, pos, EPS, D, theta)
-    ko = orc.qk_norm_rope(kh, kw, pos, EPS, D, theta)
-    h1 = orc.add_clamp(h, attn_out)
-    n2 = orc.rms_norm_mul(h1, w_post, EPS)
-    ffr = orc.swiglu(gu)
-    h2 = orc.add_clamp(h1, mlp_out)
-    assert_f32_close(to_np(norm), n1)
-    assert_f32_close(to_np(q_out), qo, row_floor=True)
-    assert_f32_close(to_np(k_out), ko, row_floor=True)
+    vh = ch(orc.clamp, qkv[:, (nh + nkv) * D:].reshape(N, nkv, D), -65504.0, 65504.0)
+    qo = ch(orc.qk_norm_rope, qh, qw, pos, EPS, D, theta)
+    ko = ch(orc.qk_norm_rope, kh, kw, pos, EPS, D, theta)
+    h1 = ch(orc.add_clamp, h, attn_out)
+    n2 = ch(orc.rms_norm_mul, h1, w_post, EPS)
+    ffr = ch(orc.swiglu, gu)
+    h2 = ch(orc.add_clamp, h1, mlp_out)
+    close = (lambda a, b, **kw: assert_bf16_ulp(a, b, **kw)) if bf16 else assert_f32_close
+    close(to_np(norm), n1)
+    close(to_np(q_out), qo, row_floor=True)
+    close(to_np(k_out), ko, row_floor=True)
     assert np.array_equal(to_np(hd), h2)  # add + clamp is bit-exact
-    assert_f32_close(to_np(norm2), n2)
-    assert_f32_close(to_np(ff), ffr)
+    close(to_np(norm2), n2)
+    close(to_np(ff), ffr)
     assert int(err.item()) == 0
     kch, vch = to_np(kc), to_np(vc)
-    kq = orc.quantize_q8_0(to_np(k_out), "x86")  # the store quantizes the kernel's own k_out
-    vq = orc.quantize_q8_0(vh, "x86")
+    kq = orc.quantize_q8_0(f32(to_np(k_out)), "x86")  # the store quantizes the kernel's own k_out
+    vq = orc.quantize_q8_0(f32(vh), "x86")
     for b in range(N):
         assert np.array_equal(kch[b, :, pos[b]], kq[b])
         assert np.array_equal(vch[b, :, pos[b]], vq[b])
