@@ -32,7 +32,10 @@ once at its storage type (bf16 activations, f32 vectors).
 cpu_baseline: the CPU oracle (a restatement of the ggml-cpu arithmetic)
 running the reference's unfused F32 node graph for the same block on a row
 sample, OpenMP over rows, threads = logical CPUs / 2 (the reference's
-backend policy) capped by the job's CPU share.
+backend policy) capped by the job's CPU share, built for the host's x86-64
+level (AVX-512 when present); a second run uses every CPU of the job's
+share. The host's CPU model, sockets, physical cores and logical CPUs are
+recorded from lscpu.
 """
 from __future__ import annotations
 
@@ -248,10 +251,45 @@ def gpu_bench(steps: int, warmup: int):
     return ms_step, ms_five, ms_unfused, wall, pk_c, pk_f, pk_u
 
 
-def cpu_bench(rows: int, reps: int, threads: int):
+def host_cpu() -> dict:
+    """The host's CPU as lscpu reports it, the CPUs this job may run on, and the
+    x86-64 level of the oracle build the CPU baseline loads (v4 with AVX-512)."""
+    info = {}
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
+    except Exception:  # noqa: BLE001 -- lscpu is optional; /proc/cpuinfo covers the flags
+        pass
+    flags = set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("flags"):
+                flags = set(line.split(":", 1)[1].split())
+                break
+    except OSError:
+        pass
+    as_int = lambda k: int(info[k]) if info.get(k, "").isdigit() else None  # noqa: E731
+    sockets, cps, tpc = as_int("Socket(s)"), as_int("Core(s) per socket"), as_int("Thread(s) per core")
+    logical = os.cpu_count() or 1
+    share = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else logical
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    job = min(share, omp) if omp > 0 else share
+    v4 = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags
+    return {"cpu_model": info.get("Model name", "unknown"), "sockets": sockets,
+            "physical_cores": sockets * cps if sockets and cps else None, "threads_per_core": tpc,
+            "logical_cpus": logical, "job_cpus": job, "isa": "x86-64-v4" if v4 else "x86-64-v3"}
+
+
+def cpu_bench(rows: int, reps: int, threads: int, isa: str = "x86-64-v3"):
     """The reference's unfused F32 node graph for one DiT block on `rows` rows."""
     from oracle import oracle as orc
 
+    if orc._lib is None:
+        orc.use_isa("v4" if isa == "x86-64-v4" else "v3")
     orc.set_threads(threads)
     rng = np.random.default_rng(7)
     x = rng.standard_normal((rows, H), dtype=np.float32)
@@ -807,19 +845,35 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = max(1, min((os.cpu_count() or 2) // 2, int(os.environ.get("OMP_NUM_THREADS", "16"))))
-        med, spent = cpu_bench(args.cpu_rows, args.cpu_reps, threads)
+        hc = host_cpu()
+        # the reference's backend policy: hardware_concurrency() / 2 threads
+        # (backend.h:28-35), within the CPUs this job may use
+        threads = max(1, min(hc["logical_cpus"] // 2, hc["job_cpus"]))
+        med, spent = cpu_bench(args.cpu_rows, args.cpu_reps, threads, hc["isa"])
         scale = ROWS / args.cpu_rows
         cpu_block_s = med * scale
+        all_t = hc["job_cpus"]
+        if all_t != threads:
+            med_a, spent_a = cpu_bench(args.cpu_rows, max(8, args.cpu_reps // 2), all_t, hc["isa"])
+            all_run = {"threads": all_t, "us_per_block": round(med_a * scale * 1e6, 1),
+                       "value": round(total_bytes / (med_a * scale) / 1e9, 3), "cpu_s": round(spent_a, 1)}
+        else:
+            all_run = {"threads": all_t, "same_as_policy_run": True,
+                       "note": "every logical CPU this job may use is already in the policy run"}
         cpu = {
             "value": round(total_bytes / cpu_block_s / 1e9, 3),
             "unit": "GB/s",
             "cores": threads,
+            "threads": threads,
             "kind": "port",
             "us_per_block": round(cpu_block_s * 1e6, 1),
+            "host": hc,
+            "all_logical_threads": all_run,
             "sample": (f"reference's unfused F32 ggml node graph of one DiT block (rms_norm, mul, add, rope, swiglu "
-                       f"nodes, ggml-cpu arithmetic restated in C, OpenMP over rows) on {args.cpu_rows} of {ROWS} "
-                       f"rows, median of {args.cpu_reps} reps after 3 warm-ups ({spent:.1f} s of CPU work)"
+                       f"nodes, ggml-cpu arithmetic restated in C, built -O3 -march={hc['isa']}, OpenMP over rows) "
+                       f"on {args.cpu_rows} of {ROWS} rows, {threads} threads (logical CPUs / 2, the reference's "
+                       f"backend policy, within the job's {hc['job_cpus']} CPUs), median of {args.cpu_reps} reps "
+                       f"after 3 warm-ups ({spent:.1f} s of CPU work)"
                        + (f", scaled x{scale:.2f} to the full block" if args.cpu_rows != ROWS else "")
                        + "; GB/s uses the same bf16 byte accounting as value"),
         }

@@ -201,6 +201,13 @@ def kv_store(k, k_cache, pos0, v=None, v_cache=None, sets=None, rounding: int = 
     _lib.call("mi_kv_store", _p(k), _p(k_cache), _p(v), _p(v_cache), _p(pos0), _p(sets), rounding, ep, _s(stream))
 
 
+def scale(x, s: float, out=None, stream=None):
+    """ggml_scale: x * s (the timestep scaling in front of the embedding, dit-graph.h:87)."""
+    y = _out(out, x.shape, x.dtype)
+    _lib.call("mi_scale", _p(x), ctypes.c_float(s), _p(y), _s(stream))
+    return y
+
+
 def timestep_embedding(t, dim: int, max_period: int = 10000, out=None, stream=None):
     y = _out(out, (t.shape[0], dim), "f32")
     _lib.call("mi_timestep_embedding", _p(t), dim, max_period, _p(y), _s(stream))

@@ -1109,6 +1109,15 @@ int mi_flow_final(const mi_tensor * xt, const mi_tensor * vt, float t, const mi_
     return finish(launch_flow_step(a, (hipStream_t) stream));
 }
 
+int mi_scale(const mi_tensor * x, float s, const mi_tensor * y, mi_stream stream) {
+    MI_TRY(check_act(x));
+    MI_TRY(check_act(y));
+    if (!same_shape(*x, *y)) {
+        return MI_ERR_SHAPE;
+    }
+    return finish(launch_scale(*x, s, *y, (hipStream_t) stream));
+}
+
 int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi_tensor * y, mi_stream stream) {
     MI_TRY(check(t));
     MI_TRY(check(y));

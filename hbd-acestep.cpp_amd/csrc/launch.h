@@ -213,6 +213,7 @@ int launch_apg(const ApgArgs & a, hipStream_t s);
 int launch_flow_step(const FlowArgs & a, hipStream_t s);
 
 // ---- tsembd.hip ------------------------------------------------------------
+int launch_scale(const mi_tensor & x, float sc, const mi_tensor & y, hipStream_t s);
 int launch_timestep_embedding(const float * t, int64_t n, int64_t ts, int dim, int max_period, char * y,
                               int64_t ys, hipStream_t s);
 

@@ -195,6 +195,12 @@ int mi_cpy_q8_0(const mi_tensor * src, const mi_tensor * dst, int rounding, mi_s
 int mi_kv_store(const mi_tensor * k, const mi_tensor * k_cache, const mi_tensor * v, const mi_tensor * v_cache,
                 const mi_tensor * pos0, const mi_tensor * sets, int rounding, int32_t * d_err, mi_stream stream);
 
+/* ggml_scale(x, s): y = x * s, one fp32 multiply per element (the result
+ * rounded to y's type). Replaces the timestep scaling ggml_scale(t, 1000) in
+ * front of the embedding (dit-graph.h:87). x, y: activations of one shape
+ * (F32/BF16/F16, contiguous rows, any row strides); y == x allowed. */
+int mi_scale(const mi_tensor * x, float s, const mi_tensor * y, mi_stream stream);
+
 /* ggml_timestep_embedding(t, dim, max_period): t F32 [n] -> y F32 [dim, n].
  * Replaces dit-graph.h:90 (dim 256, max_period 10000). */
 int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi_tensor * y, mi_stream stream);

@@ -517,6 +517,84 @@ void orc_flash_attn_ext(const float * q, const float * k, const float * v, const
 }
 
 /* ------------------------------------------------------------------------ */
+/* The same op as ggml-cpu computes it for an F16 V (ggml upstream, not in    */
+/* this checkout: ops.cpp ggml_compute_forward_flash_attn_ext_f16_one_chunk,  */
+/* dbrain/ggml 292516d5): one key at a time, the score in float              */
+/* (s = dot * scale + mask), M and S in float; the output accumulated in      */
+/* FP16: on a new maximum VKQ16 *= ms = expf(Mold - M) (vs = 1), else          */
+/* vs = expf(s - M); then VKQ16 += v * vs, each element rounded to fp16;     */
+/* S = S * ms + vs; finally y = f32(VKQ16) * (1 / S). The dot is taken in     */
+/* double and rounded to float (ggml's SIMD f32 lane order is not restated). */
+/* bud receives, per output element, the fp16 rounding errors of VKQ16 as    */
+/* they propagate to y (each rounding's exact size, carried through later    */
+/* rescales, divided by S).                                                  */
+/* ------------------------------------------------------------------------ */
+void orc_flash_attn_ext_f16acc(const float * q, const float * k, const uint16_t * v16, const float * mask,
+                               int64_t N, int64_t Nh, int64_t Nkv, int64_t n_q, int64_t n_kv, int64_t D, int64_t mN,
+                               int64_t mH, int64_t mQ, float scale, int qconv, float * y, float * bud) {
+    const int64_t rk = Nh / Nkv;
+#pragma omp parallel for collapse(3) num_threads(g_threads) schedule(static)
+    for (int64_t b = 0; b < N; b++) {
+        for (int64_t h = 0; h < Nh; h++) {
+            for (int64_t iq = 0; iq < n_q; iq++) {
+                double          qc[1024];
+                uint16_t        acc[1024];
+                double          err[1024];
+                const int64_t   g  = h / rk;
+                const float *   kk = k + (b * Nkv + g) * n_kv * D;
+                const uint16_t * vv = v16 + (b * Nkv + g) * n_kv * D;
+                const float *   mm = mask ? mask + (((b % mN) * mH + (h % mH)) * mQ + iq) * n_kv : NULL;
+                fa_convert_q(q + ((b * Nh + h) * n_q + iq) * D, D, qconv, qc);
+                for (int64_t d = 0; d < D; d++) {
+                    acc[d] = orc_fp32_to_fp16(0.0f);
+                    err[d] = 0.0;
+                }
+                float S = 0.0f, M = -INFINITY;
+                for (int64_t j = 0; j < n_kv; j++) {
+                    const float mv = mm ? mm[j] : 0.0f;
+                    if (mv == -INFINITY) {
+                        continue;
+                    }
+                    double dot = 0.0;
+                    for (int64_t d = 0; d < D; d++) {
+                        dot += qc[d] * (double) kk[j * D + d];
+                    }
+                    float       sc   = (float) dot;
+                    sc               = sc * scale;
+                    sc               = sc + mv;
+                    const float Mold = M;
+                    float       ms = 1.0f, vs = 1.0f;
+                    if (sc > M) {
+                        M  = sc;
+                        ms = expf(Mold - M);
+                        for (int64_t d = 0; d < D; d++) {
+                            const float x = orc_fp16_to_fp32(acc[d]) * ms;
+                            acc[d]        = orc_fp32_to_fp16(x);
+                            err[d]        = err[d] * ms + fabs((double) orc_fp16_to_fp32(acc[d]) - (double) x);
+                        }
+                    } else {
+                        vs = expf(sc - M);
+                    }
+                    for (int64_t d = 0; d < D; d++) {
+                        const float x = fmaf(orc_fp16_to_fp32(vv[j * D + d]), vs, orc_fp16_to_fp32(acc[d]));
+                        acc[d]        = orc_fp32_to_fp16(x);
+                        err[d] += fabs((double) orc_fp16_to_fp32(acc[d]) - (double) x);
+                    }
+                    S = S * ms + vs;
+                }
+                const float S_inv = 1.0f / S; /* all masked: 0 * inf = NaN, as the exact oracle */
+                float *     yo    = y + ((b * n_q + iq) * Nh + h) * D;
+                float *     bo    = bud + ((b * n_q + iq) * Nh + h) * D;
+                for (int64_t d = 0; d < D; d++) {
+                    yo[d] = orc_fp16_to_fp32(acc[d]) * S_inv;
+                    bo[d] = (float) (err[d] / (double) S);
+                }
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* ggml_mul_mat(w, x) with Q8_0 weights (qwen3-enc.h:86-88; dit-graph.h:36-49; */
 /* qwen3-lm.h:755): ggml-cpu quantizes each row of x with the vec_dot type's  */
 /* from_float (Q8_0, x86) and takes ggml_vec_dot_q8_0_q8_0 per output. Here   */

@@ -123,6 +123,9 @@ void orc_timestep_embedding_f32(const float * t, int64_t n, int dim, int max_per
 void orc_flash_attn_ext(const float * q, const float * k, const float * v, const float * mask, int64_t N, int64_t Nh,
                         int64_t Nkv, int64_t n_q, int64_t n_kv, int64_t D, int64_t mN, int64_t mH, int64_t mQ,
                         float scale, int qconv, float * y);
+void orc_flash_attn_ext_f16acc(const float * q, const float * k, const uint16_t * v16, const float * mask,
+                               int64_t N, int64_t Nh, int64_t Nkv, int64_t n_q, int64_t n_kv, int64_t D, int64_t mN,
+                               int64_t mH, int64_t mQ, float scale, int qconv, float * y, float * bud);
 
 /* ---- ggml_mul_mat(w, x), Q8_0 weights (qwen3-enc.h:86-88; dit-graph.h:36-49;
  *      qwen3-lm.h:755): w n rows of k / 32 Q8_0 blocks, x m rows of k F32,

@@ -41,6 +41,17 @@ def build() -> str:
     return _LIB_PATH
 
 
+def use_isa(isa: str) -> str:
+    """Load the x86-64-v3 build ("v3", the checker's) or the x86-64-v4 build
+    ("v4", AVX-512) of the same source; only before the first call into it."""
+    global _LIB_PATH
+    path = os.path.join(_HERE, "_build", "liborc.so" if isa == "v3" else f"liborc_{isa}.so")
+    if _lib is not None and path != _LIB_PATH:
+        raise RuntimeError("the oracle library is already loaded")
+    _LIB_PATH = path
+    return path
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -68,6 +79,8 @@ def lib():
         L.orc_bf16_to_fp32_n.argtypes = [_u16p, _fp, _i64]
         L.orc_flash_attn_ext.argtypes = [_fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                          ctypes.c_float, ctypes.c_int, _fp]
+        L.orc_flash_attn_ext_f16acc.argtypes = [_fp, _fp, _u16p, _fp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                                _i64, ctypes.c_float, ctypes.c_int, _fp, _fp]
         L.orc_mul_mat_q8_0.argtypes = [_u8p, _fp, _i64, _i64, _i64, _fp]
         _dp = ctypes.POINTER(ctypes.c_double)
         L.orc_apg_forward.argtypes = [_fp, _fp, _i64, _i64, _i64, ctypes.c_float, ctypes.c_double, ctypes.c_float,
@@ -291,6 +304,32 @@ def flash_attn_ext(q, k, v, mask, scale: float, k_type: str = "f16") -> np.ndarr
     lib().orc_flash_attn_ext(_f(q), _f(k), _f(v), mp, N, Nh, Nkv, n_q, n_kv, D, mN, mH, mQ, scale, QCONV[k_type],
                              _f(y))
     return y
+
+
+def flash_attn_ext_f16acc(q, k, v16, mask, scale: float, k_type: str = "f16"):
+    """ggml-cpu's flash attention for an F16 V: the output accumulated in fp16
+    one key at a time (see orc_flash_attn_ext_f16acc). v16: uint16 fp16 bits
+    (N, Nkv, n_kv, D); other arguments as flash_attn_ext. Returns (y, bud):
+    y (N, n_q, Nh, D) and, per element, the fp16 accumulation's rounding
+    errors carried to y."""
+    q, k = _c32(q), _c32(k)
+    v16 = np.ascontiguousarray(v16, dtype=np.uint16)
+    N, Nh, n_q, D = q.shape
+    _, Nkv, n_kv, _ = k.shape
+    assert k.shape == v16.shape == (N, Nkv, n_kv, D) and Nh % Nkv == 0 and D <= 1024
+    if mask is not None:
+        mask = _c32(mask)
+        mN, mH, mQ, mk = mask.shape
+        assert mk == n_kv and mQ >= n_q
+        mp = _f(mask)
+    else:
+        mN = mH = mQ = 1
+        mp = None
+    y = np.empty((N, n_q, Nh, D), np.float32)
+    bud = np.empty((N, n_q, Nh, D), np.float32)
+    lib().orc_flash_attn_ext_f16acc(_f(q), _f(k), v16.ctypes.data_as(_u16p), mp, N, Nh, Nkv, n_q, n_kv, D, mN, mH,
+                                    mQ, scale, QCONV[k_type], _f(y), _f(bud))
+    return y, bud
 
 
 # ---------------------------------------------------------------------------

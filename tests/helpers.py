@@ -72,6 +72,24 @@ def assert_bf16_ulp(a_bits, ref_bits, max_ulp=1, row_floor=False, tol=1e-5):
     return int(d.max()) if d.size else 0
 
 
+def assert_mul_mat_q8_0(y, w, x):
+    """ggml_mul_mat with Q8_0 weights w (n, k/32*34 bytes) and F32 x (m, k): the
+    exact value of ggml-cpu's definition (x quantized with the x86 Q8_0
+    quantizer, exact int32 block dots scaled by fp16(d_w) fp16(d_x)), and the
+    kernels' rounding bound: one rounding per block (fma into the running sum)
+    and per added split, |y - ref| <= (K/32 + 8) 2^-24 sum_k |w_k| |x'_k|."""
+    from oracle import oracle as orc
+
+    ref = orc.mul_mat_q8_0(w, x)
+    k = x.shape[-1]
+    wf = orc.dequantize_q8_0(w).astype(np.float64)
+    xf = orc.dequantize_q8_0(orc.quantize_q8_0(x, "x86")).astype(np.float64)
+    bound = (k / 32 + 8) * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T) + 1e-30
+    err = np.abs(np.asarray(y, np.float64) - ref)
+    assert y.shape == ref.shape
+    assert np.all(err <= bound), f"max err {err.max()} vs bound {bound[err > bound].min()}"
+
+
 def frac_bitexact(a: np.ndarray, ref: np.ndarray) -> float:
     a = np.ascontiguousarray(a)
     ref = np.ascontiguousarray(ref)

@@ -27,6 +27,37 @@ def test_timestep_embedding(dev):
     assert not y[:, 6].any()
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_scale(dev, dt):
+    """ggml_scale: y = x * s, one rounding (bit-exact); in place and on a strided view."""
+    bf16 = dt == "bf16"
+    x = randn((37, 300), seed=21) * 10
+    x[0, :4] = [np.inf, -0.0, np.nan, 3e38]
+    xh = orc.f32_to_bf16(x) if bf16 else x
+    f = orc.bf16_to_f32 if bf16 else (lambda a: a)
+    cv = orc.f32_to_bf16 if bf16 else (lambda a: a)
+    d = to_dev(xh, dev, bf16=bf16)
+    for s in (1000.0, -0.37, 2.0 ** -20):
+        y = to_np(ops.scale(d, s))
+        assert np.array_equal(y.view(np.uint8), cv(orc.scale(f(xh), s)).view(np.uint8)), s
+    v = d[3:30:2, 7:263]  # rows at a stride, columns offset
+    y = to_np(ops.scale(v, 1000.0))
+    assert np.array_equal(y.view(np.uint8), cv(orc.scale(f(xh)[3:30:2, 7:263], 1000.0)).view(np.uint8))
+    ops.scale(d, 0.5, out=d)
+    assert np.array_equal(to_np(d).view(np.uint8), cv(orc.scale(f(xh), 0.5)).view(np.uint8))
+
+
+def test_timestep_scale_then_embedding(dev):
+    """The DiT's timestep path: t ~ U[0, 1] for the CFG pair's one graph, scaled by
+    1000 (ggml_scale, dit-graph.h:87), then the 256-wide sinusoidal embedding (90)."""
+    t = rng(5).uniform(0, 1, 1).astype(np.float32)
+    ts = ops.scale(to_dev(t, dev), 1000.0)
+    tsh = orc.scale(t, 1000.0)
+    assert np.array_equal(to_np(ts).view(np.uint32), tsh.view(np.uint32))
+    y = to_np(ops.timestep_embedding(ts, 256, 10000))
+    tsembd_bar(y, orc.timestep_embedding(tsh, 256, 10000), tsh, 256, 10000)
+
+
 class _DevStorage:
     """Device storage for the shared DiT block case."""
 

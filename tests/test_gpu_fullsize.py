@@ -11,13 +11,18 @@ compare every element, at the same bars as the small-shape tests:
   C5  Qwen3-4B prefill into a Q8_0 KV cache: K, V [8, 2048, 8, 128] quantized
       at slot offsets U[0, 6144) of an 8192-slot cache (int8 quants and fp16
       scales bit-exact), then dequantized back through get_rows (bit-exact)
+  C4, C5 F32 QK-norm -> rope over all 16384 tokens (16/8 and 32/8 heads): the
+      persistent kernel's multi-item walk, <= 1e-5 with the row floor; C5 as
+      the chain the configuration describes: QK-norm + rope from the fused QKV
+      output, the kernel's own K and the V view stored as Q8_0 (bit-exact
+      against the oracle quantizing those very values), then gathered back
 """
 import os
 
 import numpy as np
 import pytest
 
-from helpers import assert_bf16_ulp, to_dev, to_np
+from helpers import assert_bf16_ulp, assert_f32_close, to_dev, to_np
 from oracle import oracle as orc
 
 from acestep_ops import Q8_0_CPU_X86, ops
@@ -123,3 +128,63 @@ def test_c5_kv_store_q8_0_full_size(dev):
     for cache_d, cache_h in ((kc, kch), (vc, vch)):
         y = to_np(ops.get_rows(ops.Q8(cache_d.view(-1, rb)), to_dev(ids)))
         assert np.array_equal(y.view(np.uint32), orc.dequantize_q8_0(cache_h.reshape(-1, rb)[ids]).view(np.uint32))
+
+
+def _qkv_rope(rng, B, T, NH, NKV, D, theta, pos):
+    R = B * T
+    qkv = _normal(rng, (R, (NH + 2 * NKV) * D))
+    q_w, k_w = _normal(rng, (D,), 0.1, 1.0), _normal(rng, (D,), 0.1, 1.0)
+    d_qkv = to_dev(qkv)
+    q = d_qkv[:, :NH * D].unflatten(1, (NH, D))
+    k = d_qkv[:, NH * D:(NH + NKV) * D].unflatten(1, (NKV, D))
+    q_out, k_out = ops.qk_norm_rope(q, to_dev(q_w), to_dev(pos), EPS, D, theta, k=k, k_w=to_dev(k_w))
+    return qkv, q_w, k_w, d_qkv, q_out, k_out
+
+
+def _check_rope(qkv, q_w, k_w, q_out, k_out, NH, NKV, D, theta, pos):
+    R = qkv.shape[0]
+    qh = qkv[:, :NH * D].reshape(R, NH, D)
+    kh = qkv[:, NH * D:(NH + NKV) * D].reshape(R, NKV, D)
+    ko = to_np(k_out)
+    assert_f32_close(to_np(q_out), orc.qk_norm_rope(qh, q_w, pos, EPS, D, theta), row_floor=True)
+    assert_f32_close(ko, orc.qk_norm_rope(kh, k_w, pos, EPS, D, theta), row_floor=True)
+    return ko
+
+
+def test_c4_qk_norm_rope_f32_full_size(dev):
+    print("full size C4: F32 QK-norm -> rope, 4 x 4096 tokens, 16/8 heads x 128", flush=True)
+    B, T, NH, NKV, D = 4, 4096, 16, 8, 128
+    rng = np.random.default_rng(44)
+    pos = np.tile(np.arange(T, dtype=np.int32), B)
+    qkv, q_w, k_w, _, q_out, k_out = _qkv_rope(rng, B, T, NH, NKV, D, 1e6, pos)
+    _check_rope(qkv, q_w, k_w, q_out, k_out, NH, NKV, D, 1e6, pos)
+
+
+def test_c5_rope_store_gather_chain_full_size(dev):
+    print("full size C5 chain: F32 QK-norm -> rope (8 x 2048, 32/8 heads), K/V -> Q8_0 cache, get_rows back",
+          flush=True)
+    B, T, NH, NKV, D, max_seq = 8, 2048, 32, 8, 128, 8192
+    rng = np.random.default_rng(55)
+    s0 = rng.integers(0, 6144, B).astype(np.int32)
+    pos = (s0[:, None] + np.arange(T, dtype=np.int32)[None, :]).reshape(-1)  # kv_pos + i (qwen3-lm.h:516-522)
+    qkv, q_w, k_w, d_qkv, q_out, k_out = _qkv_rope(rng, B, T, NH, NKV, D, 1e6, pos)
+    ko = _check_rope(qkv, q_w, k_w, q_out, k_out, NH, NKV, D, 1e6, pos)
+    v_dev = d_qkv[:, (NH + NKV) * D:].unflatten(1, (NKV, D)).unflatten(0, (B, T))
+    rb = D // 32 * 34
+    kc = DTensor.full_byte((B, NKV, max_seq, rb), 0xA5)
+    vc = DTensor.full_byte((B, NKV, max_seq, rb), 0x5A)
+    ops.kv_store(k_out.unflatten(0, (B, T)), ops.Q8(kc), to_dev(s0), v=v_dev, v_cache=ops.Q8(vc),
+                 rounding=Q8_0_CPU_X86)
+    kch, vch = to_np(kc), to_np(vc)
+    k_src = ko.reshape(B, T, NKV, D)
+    v_src = qkv[:, (NH + NKV) * D:].reshape(B, T, NKV, D)
+    for b in range(B):
+        for src, cache in ((k_src, kch), (v_src, vch)):
+            want = orc.quantize_q8_0(np.ascontiguousarray(src[b].transpose(1, 0, 2)), "x86")
+            assert np.array_equal(cache[b, :, s0[b]:s0[b] + T], want), f"sequence {b}"
+    ids = np.concatenate([((b * NKV + h) * max_seq + s0[b] + np.arange(T)) for b in range(B) for h in range(NKV)])
+    ids = ids.astype(np.int32)
+    for cache_d, src in ((kc, k_src), (vc, v_src)):
+        y = to_np(ops.get_rows(ops.Q8(cache_d.view(-1, rb)), to_dev(ids)))
+        want = orc.dequantize_q8_0(orc.quantize_q8_0(np.ascontiguousarray(src.transpose(0, 2, 1, 3)), "x86"))
+        assert np.array_equal(y.view(np.uint32), want.reshape(-1, D).view(np.uint32))

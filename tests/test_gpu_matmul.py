@@ -14,7 +14,7 @@ bit for bit through y.
 """
 import numpy as np
 import pytest
-from helpers import to_dev, to_np
+from helpers import assert_mul_mat_q8_0, to_dev, to_np
 from oracle import oracle as orc
 
 from acestep_ops import ops
@@ -24,14 +24,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _check(y, w, x):
-    ref = orc.mul_mat_q8_0(w, x)
-    k = x.shape[-1]
-    wf = orc.dequantize_q8_0(w).astype(np.float64)
-    xf = orc.dequantize_q8_0(orc.quantize_q8_0(x, "x86")).astype(np.float64)
-    bound = (k / 32 + 8) * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T) + 1e-30
-    err = np.abs(y.astype(np.float64) - ref)
-    assert y.shape == ref.shape
-    assert np.all(err <= bound), f"max err {err.max()} vs bound {bound[err > bound].min()}"
+    assert_mul_mat_q8_0(y, w, x)
 
 
 def _run(n, k, m, seed, wscale=1.0, xscale=1.0, wview=None):

@@ -1,33 +1,41 @@
 """A whole Qwen3 decode layer on the device (acestep_ops.qwen3.Qwen3DecodeLayer:
 norm, Q8_0 QKV product, QK-norm + rope, KV-cache write, flash attention over
 the cache, O product, fused residual add + norm, gate/up product, SwiGLU, down
-product, residual add) against the same chain of oracle ops
+product, residual add) against the oracle, stage by stage
 (qw3lm_forward_batch, qwen3-lm.h:626-741).
 
-Each op is held to its own bar in its own tests; here the chain is compared
-end to end: the final hidden state within 2e-4 of its largest magnitude (the
-products' fp32 roundings and the attention's 1e-4 * max|V| bar, passed through
-two residual branches), and the cache slots written bit for bit except where a
-rounding difference upstream moved a value across a Q8_0 rounding boundary
-(at most one quantization step, in at most 1 % of the written elements)."""
+Every stage is checked against the oracle applied to the device's own inputs
+of that stage (read back from the layer's buffers), at that op's own bar:
+  norm -> QKV product            Q8_0 product bound (the x quantization exact)
+  QK-norm -> rope                1e-5, row floor
+  cache slots (K and V)          bit-exact: Q8_0 of the device's k_out and V,
+                                 or their fp16 values
+  attention                      the kernels' derived bound (tests/fa_bound.py)
+  O product, gate/up, down       Q8_0 product bound
+  residual sums                  bit-exact (clamped to +-65504 with clamp_fp16)
+With clamp_fp16 (qwen3-lm.h:53) the layer clamps V before the cache store
+(674-677) and both residual sums (730-733, 738-741): the case drives V and the
+hidden state past the fp16 range."""
 import numpy as np
 import pytest
-from helpers import to_dev, to_np
+from fa_bound import fa_bound
+from helpers import assert_f32_close, assert_mul_mat_q8_0, to_dev, to_np
 from oracle import oracle as orc
 
 from acestep_ops import ops
 from acestep_ops.qwen3 import Qwen3DecodeLayer, decode_mask
 
 pytestmark = pytest.mark.gpu
+LIM = 65504.0
 
 
 def _w(r, n, k, s=0.05):
     return orc.quantize_q8_0((r.standard_normal((n, k)) * s).astype(np.float32))
 
 
-@pytest.mark.parametrize("kv_type", ["q8_0", "f16"])
-def test_decode_layer_matches_oracle_chain(dev, kv_type):
-    print(f"qwen3 decode layer kv={kv_type}", flush=True)
+@pytest.mark.parametrize("kv_type,clamp", [("q8_0", False), ("f16", False), ("q8_0", True)])
+def test_decode_layer_stage_by_stage(dev, kv_type, clamp):
+    print(f"qwen3 decode layer kv={kv_type} clamp_fp16={clamp}", flush=True)
     r = np.random.default_rng(31)
     H, Nh, Nkv, D, I, N, max_seq, n_sets, s0 = 256, 4, 2, 128, 512, 4, 512, 6, 1
     eps, theta = 1e-6, 1e6
@@ -35,9 +43,15 @@ def test_decode_layer_matches_oracle_chain(dev, kv_type):
     nw_in, nw_post = (1 + 0.1 * r.standard_normal(H)).astype(np.float32), (1 + 0.1 * r.standard_normal(H)).astype(
         np.float32)
     qn, kn = (1 + 0.1 * r.standard_normal(D)).astype(np.float32), (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    hidden = (r.standard_normal((N, H)) * 0.8).astype(np.float32)
+    if clamp:
+        # V of most tokens past the fp16 range; the normalized x stays below 127 * 65504,
+        # where its Q8_0 block scale would overflow fp16 (in ggml as here)
+        nw_in[3] = 4e6
+        hidden[0, :3] = [7e4, -9e4, 6e4]    # residual sums past the fp16 range
     layer = Qwen3DecodeLayer(ops.Q8(to_dev(Wqkv)), ops.Q8(to_dev(Wo)), ops.Q8(to_dev(Wgu)), ops.Q8(to_dev(Wd)),
                              to_dev(nw_in), to_dev(nw_post), to_dev(qn), to_dev(kn), H, Nh, Nkv, D, I, max_seq,
-                             n_sets, kv_type, eps, theta)
+                             n_sets, kv_type, eps, theta, clamp_fp16=clamp)
     # earlier tokens already in the caches (random but finite), then this step's
     pos = np.array([0, 37, 200, 255], np.int32)
     read_len = 256
@@ -45,55 +59,73 @@ def test_decode_layer_matches_oracle_chain(dev, kv_type):
     vc0 = (r.standard_normal((n_sets, Nkv, max_seq, D)) * 0.5).astype(np.float32)
     if kv_type == "q8_0":
         kq, vq = orc.quantize_q8_0(kc0, "x86"), orc.quantize_q8_0(vc0, "x86")
-        layer.k_cache = ops.Q8(to_dev(kq))
-        layer.v_cache = ops.Q8(to_dev(vq))
-        kcache, vcache = orc.dequantize_q8_0(kq), orc.dequantize_q8_0(vq)
+        layer.k_cache, layer.v_cache = ops.Q8(to_dev(kq)), ops.Q8(to_dev(vq))
+        kcache0 = orc.dequantize_q8_0(kq)
     else:
         kh, vh = orc.f32_to_f16(kc0), orc.f32_to_f16(vc0)
         layer.k_cache, layer.v_cache = to_dev(kh, f16=True), to_dev(vh, f16=True)
-        kcache, vcache = orc.f16_to_f32(kh), orc.f16_to_f32(vh)
-    hidden = (r.standard_normal((N, H)) * 0.8).astype(np.float32)
+        kcache0 = orc.f16_to_f32(kh)
     sets = np.arange(s0, s0 + N, dtype=np.int32)
     y = to_np(layer.forward(to_dev(hidden), to_dev(pos), to_dev(sets), s0, read_len, decode_mask(pos, read_len)))
+    b = {k: to_np(v) for k, v in layer._bufs.items() if not k.startswith("ws")}
 
-    # the oracle chain
+    # 1. input norm -> QKV product (one call); V then clamped in place when clamp_fp16
+    qkv = b["qkv"]
+    qkv_pre = qkv.copy()
+    v_cols = slice((Nh + Nkv) * D, (Nh + 2 * Nkv) * D)
     norm = orc.rms_norm_mul(hidden, nw_in, eps)
-    qkv = orc.mul_mat_q8_0(Wqkv, norm)
+    if clamp:
+        # V values at +-65504 are exactly those whose product lies past the range;
+        # the others are the product itself (checked with the rest below)
+        vd = qkv[:, v_cols]
+        vref = orc.mul_mat_q8_0(Wqkv, norm)[:, v_cols]
+        at_lim = np.abs(vd) == LIM
+        assert at_lim.sum() > vd.size // 4 and np.all(np.abs(vd) <= LIM)
+        assert np.all(np.sign(vd[at_lim]) == np.sign(vref[at_lim]))
+        assert np.all(np.abs(vref[at_lim]) >= LIM * (1 - 1e-5)) and np.all(np.abs(vref[~at_lim]) <= LIM * (1 + 1e-5))
+        qkv_pre[:, v_cols] = np.where(at_lim, vref, vd)
+    assert_mul_mat_q8_0(qkv_pre, Wqkv, norm)
+    # 2. QK-norm -> rope on the device's q, k
     q = qkv[:, :Nh * D].reshape(N, Nh, D)
     k = qkv[:, Nh * D:(Nh + Nkv) * D].reshape(N, Nkv, D)
-    v = qkv[:, (Nh + Nkv) * D:].reshape(N, Nkv, D)
-    qo = orc.qk_norm_rope(q, qn, pos, eps, D, theta)
-    ko = orc.qk_norm_rope(k, kn, pos, eps, D, theta)
+    v = qkv[:, v_cols].reshape(N, Nkv, D)
+    assert_f32_close(b["qo"], orc.qk_norm_rope(q, qn, pos, eps, D, theta), row_floor=True)
+    assert_f32_close(b["ko"], orc.qk_norm_rope(k, kn, pos, eps, D, theta), row_floor=True)
+    # 3. the written cache slots: the device's own k_out and (clamped) V, bit-exact
     if kv_type == "q8_0":
-        kw, vw = orc.dequantize_q8_0(orc.quantize_q8_0(ko, "x86")), orc.dequantize_q8_0(orc.quantize_q8_0(v, "x86"))
+        kdev = to_np(layer.k_cache.data)
+        vdev = to_np(layer.v_cache.data)
+        kw, vw = orc.quantize_q8_0(b["ko"], "x86"), orc.quantize_q8_0(v, "x86")
+        kcache, vcache = orc.dequantize_q8_0(kdev), orc.dequantize_q8_0(vdev)
     else:
-        kw, vw = orc.f16_to_f32(orc.f32_to_f16(ko)), orc.f16_to_f32(orc.f32_to_f16(v))
+        kdev, vdev = to_np(layer.k_cache), to_np(layer.v_cache)
+        kw, vw = orc.f32_to_f16(b["ko"]), orc.f32_to_f16(v)
+        kcache, vcache = orc.f16_to_f32(kdev), orc.f16_to_f32(vdev)
     for i in range(N):
-        kcache[s0 + i, :, pos[i]] = kw[i]
-        vcache[s0 + i, :, pos[i]] = vw[i]
+        assert np.array_equal(kdev[s0 + i, :, pos[i]], kw[i])
+        assert np.array_equal(vdev[s0 + i, :, pos[i]], vw[i])
+    assert np.array_equal(kcache[0], kcache0[0])  # an untouched set keeps its contents
+    # 4. attention over the device's cache, with the device's q
     mask = np.where(np.arange(read_len)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float32)
-    attn = orc.flash_attn_ext(qo.reshape(N, Nh, 1, D), kcache[s0:s0 + N, :, :read_len],
-                              vcache[s0:s0 + N, :, :read_len], mask.reshape(N, 1, 1, read_len), 1.0 / np.sqrt(D),
-                              kv_type)
-    o = orc.mul_mat_q8_0(Wo, attn.reshape(N, Nh * D))
-    h1 = orc.add(hidden, o)
-    n2 = orc.rms_norm_mul(h1, nw_post, eps)
-    ref = orc.add(h1, orc.mul_mat_q8_0(Wd, orc.swiglu(orc.mul_mat_q8_0(Wgu, n2))))
-
-    assert np.all(np.isfinite(y))
-    assert np.max(np.abs(y - ref)) <= 2e-4 * np.max(np.abs(ref)), np.max(np.abs(y - ref))
-    # the written cache slots
-    if kv_type == "q8_0":
-        kdev = orc.dequantize_q8_0(to_np(layer.k_cache.data))
-        vdev = orc.dequantize_q8_0(to_np(layer.v_cache.data))
+    mask = mask.reshape(N, 1, 1, read_len)
+    qf = b["qo"].reshape(N, Nh, 1, D)
+    kr, vr = kcache[s0:s0 + N, :, :read_len], vcache[s0:s0 + N, :, :read_len]
+    attn = b["attn"]
+    ref = orc.flash_attn_ext(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type)
+    bound = fa_bound(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type)
+    assert np.all(np.abs(attn - ref) <= bound)
+    # 5. O product; the residual sum (clamped with clamp_fp16) bit-exact
+    assert_mul_mat_q8_0(b["ao"], Wo, attn.reshape(N, Nh * D))
+    h1 = orc.add_clamp(hidden, b["ao"]) if clamp else orc.add(hidden, b["ao"])
+    assert np.array_equal(b["h1"], h1)
+    # 6. post-attention norm -> gate/up product
+    if clamp:
+        assert_f32_close(b["n2"], orc.rms_norm_mul(h1, nw_post, eps))
+        assert_mul_mat_q8_0(b["gu"], Wgu, b["n2"])
     else:
-        kdev, vdev = orc.f16_to_f32(to_np(layer.k_cache)), orc.f16_to_f32(to_np(layer.v_cache))
-    for i in range(N):
-        for got, want in ((kdev[s0 + i, :, pos[i]], kw[i]), (vdev[s0 + i, :, pos[i]], vw[i])):
-            diff = got != want
-            assert diff.mean() <= 0.01
-            if diff.any():
-                step = np.max(np.abs(want)) / 127 * 1.01 if kv_type == "q8_0" else np.max(np.abs(want)) * 2 ** -10
-                assert np.max(np.abs(got - want)) <= step
-    # untouched slots keep their contents
-    assert np.array_equal(kdev[0], kcache[0]) and np.array_equal(vdev[0], vcache[0])
+        assert_mul_mat_q8_0(b["gu"], Wgu, orc.rms_norm_mul(h1, nw_post, eps))
+    # 7. SwiGLU -> down product; the last residual sum bit-exact
+    assert_mul_mat_q8_0(b["mlp"], Wd, orc.swiglu(b["gu"]))
+    out = orc.add_clamp(h1, b["mlp"]) if clamp else orc.add(h1, b["mlp"])
+    assert np.array_equal(y, out)
+    assert np.all(np.isfinite(y))

@@ -157,3 +157,58 @@ def test_q8_0_conversion_is_the_x86_quantizer():
     y = _fa(q, k, v, k_type="q8_0", scale=0.01)
     assert np.array_equal(y, _fa(x86, k, v, k_type="f32", scale=0.01))
     assert not np.array_equal(y, _fa(ref, k, v, k_type="f32", scale=0.01))
+
+
+# ---------------------------------------------------------------------------
+# ggml-cpu's F16-V variant (orc_flash_attn_ext_f16acc): the output accumulated
+# in fp16 one key at a time
+# ---------------------------------------------------------------------------
+def _f16(x):
+    return orc.f32_to_f16(np.asarray(x, np.float32))
+
+
+def test_f16acc_exact_when_every_partial_sum_is_an_fp16_integer():
+    """q = 0: every score is 0, vs = 1, S = n; small integer V keeps every
+    partial sum an integer below 2048, so nothing rounds: y = sum(v) * (1/n)
+    and the budget is 0."""
+    r = np.random.default_rng(3)
+    n, D = 300, 64
+    v = r.integers(-3, 4, (1, 1, n, D)).astype(np.float32)
+    k = _rand((1, 1, n, D), 4)
+    q = np.zeros((1, 2, 1, D), np.float32)
+    y, bud = orc.flash_attn_ext_f16acc(q, k, _f16(v), None, 0.125)
+    want = v[0, 0].sum(axis=0).astype(np.float32) * np.float32(1.0 / np.float32(n))
+    for h in range(2):
+        assert np.array_equal(y[0, 0, h], want)
+    assert not bud.any()
+
+
+def test_f16acc_stalls_at_2048_like_fp16():
+    """V = 1 for 3000 keys of equal score: the fp16 count reaches 2048, where
+    2048 + 1 rounds back to 2048 (ties to even), so y = 2048 * (1/3000) while
+    the exact value is 1. An fp32 accumulation would give 1."""
+    n, D = 3000, 32
+    q = np.zeros((1, 1, 1, D), np.float32)
+    k = _rand((1, 1, n, D), 5)
+    v = np.ones((1, 1, n, D), np.float32)
+    y, bud = orc.flash_attn_ext_f16acc(q, k, _f16(v), None, 0.125)
+    assert np.all(y == np.float32(2048.0) * np.float32(np.float32(1.0) / np.float32(n)))
+    assert np.allclose(bud, (n - 2048) / n, rtol=1e-6)
+    assert np.all(orc.flash_attn_ext(q, k, v, None, 0.125) == 1.0)
+
+
+@pytest.mark.parametrize("n_kv", [40, 700, 4096])
+def test_f16acc_within_its_budget_of_the_exact_value(n_kv):
+    """Random scores, masks and V: the fp16 result differs from the exact
+    value by at most its own carried rounding errors plus the fp32 softmax's
+    (1e-5 of the output scale); and masked keys drop out as in the exact oracle."""
+    N, Nh, Nkv, n_q, D = 2, 4, 2, 3, 128
+    q, k = _rand((N, Nh, n_q, D), 6), _rand((N, Nkv, n_kv, D), 7)
+    v16 = _f16(_rand((N, Nkv, n_kv, D), 8))
+    vf = orc.f16_to_f32(v16)
+    m = np.where(np.random.default_rng(9).random((N, 1, n_q, n_kv)) < 0.3, -np.inf, 0.0).astype(np.float32)
+    m[..., 0] = 0.0
+    y, bud = orc.flash_attn_ext_f16acc(q, k, v16, m, 1.0 / np.sqrt(D))
+    ref = orc.flash_attn_ext(q, k, vf, m, 1.0 / np.sqrt(D), "f16")
+    assert np.all(np.abs(y - ref) <= bud + 1e-5 * np.abs(vf).max())
+    assert bud.max() > 0

@@ -132,6 +132,21 @@ def test_elementwise_ieee_and_ggml_clamp_semantics():
     assert y[5] == 1.0 and np.signbit(y[6])
 
 
+def test_scale_is_the_correctly_rounded_product():
+    """ggml_scale: y = x * s rounded once. The product of two floats is exact in
+    double (24 + 24 significand bits), so rounding the double product to float
+    once is the correctly rounded fp32 product. Catches: a reciprocal-based or
+    double-rounded scale, a dropped sign, x + s."""
+    r = np.random.default_rng(9)
+    x = (r.standard_normal(4096) * np.exp2(r.integers(-140, 120, 4096))).astype(np.float32)
+    x[:6] = [0.0, -0.0, np.inf, -np.inf, 1.17549435e-38, 3.4e38]
+    for s in (1000.0, -0.37, 3.0, 2.0 ** -30, 1e30):
+        want = (x.astype(np.float64) * np.float64(np.float32(s))).astype(np.float32)
+        assert np.array_equal(_u32(orc.scale(x, s)), _u32(want)), s
+    y = orc.scale(np.float32([np.nan, 1.0]), 2.0)
+    assert np.isnan(y[0]) and y[1] == 2.0
+
+
 # ---------------------------------------------------------------------------
 # NEOX rope
 # ---------------------------------------------------------------------------
