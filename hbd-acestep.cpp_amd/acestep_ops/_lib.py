@@ -68,6 +68,12 @@ class MiDitBlockIO(ctypes.Structure):
         ("n_dims", ctypes.c_int), ("use_cross_attn", ctypes.c_int)]
 
 
+class MiRock4Tables(ctypes.Structure):
+    _fields_ = [("ms", ctypes.POINTER(ctypes.c_int32)), ("fpa", ctypes.POINTER(ctypes.c_double)),
+                ("fpb", ctypes.POINTER(ctypes.c_double)), ("recf", ctypes.POINTER(ctypes.c_double)),
+                ("ms_len", ctypes.c_int32), ("recf_len", ctypes.c_int32)]
+
+
 class MiQwen3LayerIO(ctypes.Structure):
     _fields_ = [(n, MiTensor) for n in (
         "hidden", "in_norm_w", "post_norm_w", "norm", "norm2",
@@ -116,6 +122,11 @@ PROTOTYPES = {
     "mi_apg_forward": [_TP, _TP, _F, _F, _F, _VP, ctypes.c_size_t, _I, _TP, _VP],
     "mi_flow_step": [_I, _TP, _TP, _F, _F, _I, _TP, _TP, _VP],
     "mi_flow_final": [_TP, _TP, _F, _TP, _VP],
+    "mi_flow_step_sde": [_TP, _TP, _TP, _F, _F, _VP],
+    "mi_stork4_workspace": [_TP, ctypes.POINTER(ctypes.c_size_t)],
+    "mi_stork4_step": [_TP, _TP, _F, _F, _I, _F, _F, _TP, _TP, _I, ctypes.POINTER(MiRock4Tables), _VP,
+                       ctypes.c_size_t, _VP],
+    "mi_dcw": [_I, _TP, _TP, _F, _F, _F, _F, _VP],
     "mi_gguf_open": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)],
     "mi_gguf_close": [_VP],
     "mi_gguf_n_tensors": [_VP],

@@ -8,6 +8,7 @@
 
 #include <atomic>
 #include <cmath>
+#include <vector>
 
 #include "launch.h"
 
@@ -1107,6 +1108,220 @@ int mi_flow_final(const mi_tensor * xt, const mi_tensor * vt, float t, const mi_
     a.solver = 2;
     a.t_curr = t;
     return finish(launch_flow_step(a, (hipStream_t) stream));
+}
+
+int mi_flow_step_sde(const mi_tensor * vt, const mi_tensor * xt, const mi_tensor * noise, float t_curr, float t_next,
+                     mi_stream stream) {
+    MI_TRY(lat_check(vt, nullptr));
+    MI_TRY(lat_check(xt, vt));
+    MI_TRY(lat_check(noise, vt));
+    if (!std::isfinite(t_curr) || !std::isfinite(t_next)) {
+        return MI_ERR_PARAM;
+    }
+    FlowArgs a{};
+    a.xt     = (float *) xt->data;
+    a.vt     = (const float *) vt->data;
+    a.noise  = (const float *) noise->data;
+    a.n      = (uint64_t) nelements(*vt);
+    a.solver = 3;
+    a.t_curr = t_curr;
+    a.t_next = t_next;
+    return finish(launch_flow_step(a, (hipStream_t) stream));
+}
+
+int mi_stork4_workspace(const mi_tensor * xt, size_t * bytes) {
+    if (!bytes) {
+        return MI_ERR_NULL;
+    }
+    MI_TRY(lat_check(xt, nullptr));
+    *bytes = STORK_WS_XNEXT + (size_t) nelements(*xt) * sizeof(float);
+    return MI_OK;
+}
+
+// _rock4_mdegr (solver-stork.h:140-159): the tabulated degree for s, its row
+// in the finishing tables, and its offset in the recurrence table
+static void rock4_degree(const mi_rock4_tables & t, int s, int & mdeg, int & mz, int & mr) {
+    int mp1 = 1;
+    for (int i = 0; i < t.ms_len; i++) {
+        if (t.ms[i] >= s) {
+            mdeg = t.ms[i];
+            mz   = i;
+            mr   = mp1 - 1;
+            return;
+        }
+        mp1 += t.ms[i] * 2 - 1;
+    }
+    mz   = t.ms_len - 1;
+    mdeg = t.ms[mz];
+    mr   = mp1 - 1;
+}
+
+// The fp32 scalar chain of one sub-stepping attempt (solver-stork.h:179-264),
+// in the reference's order; false when the tables are too short for it.
+static bool rock4_plan(const mi_rock4_tables & t, int s, float t_curr, float t_next, StorkPlan & p) {
+    const int smax = t.ms[t.ms_len - 1];
+    if (s > smax) {
+        s = smax;
+    }
+    int mdeg = 0, mz = 0, mr = 0;
+    rock4_degree(t, s, mdeg, mz, mr);
+    if (mdeg < 1 || mdeg > STORK_MAX_DEG || mr < 0 || (int64_t) mr + 2 * (int64_t) (mdeg - 2) + 2 >= t.recf_len ||
+        mr >= t.recf_len) {
+        return false;
+    }
+    const float dt = t_curr - t_next;
+    p.mdeg         = mdeg;
+    float ci1 = t_curr, ci2 = t_curr, ci3 = t_curr;
+    for (int j = 1; j <= mdeg; j++) {
+        if (j == 1) {
+            p.t1_first = -dt * (float) t.recf[mr];
+            ci1        = t_curr + p.t1_first;
+            ci2        = ci1;
+        } else {
+            float * c   = p.sub[j - 2];
+            c[3]        = ci1 - t_curr;
+            c[0]        = -dt * (float) t.recf[mr + 2 * (j - 2) + 1];
+            c[2]        = -(float) t.recf[mr + 2 * (j - 2) + 2];
+            c[1]        = 1.0f - c[2];
+            const float nw = c[0] + c[1] * ci2 + c[2] * ci3;
+            ci3            = ci2;
+            ci2            = nw;
+            ci1            = nw;
+        }
+    }
+    const double * fa = t.fpa + 6 * mz;
+    const double * fb = t.fpb + 4 * mz;
+    const float    a0 = -dt * (float) fa[0];
+    p.fin_diff[0]     = ci1 - t_curr;
+    float c2f         = ci1 + a0;
+    const float a1 = -dt * (float) fa[1], a2 = -dt * (float) fa[2];
+    p.fin_diff[1]  = c2f - t_curr;
+    c2f            = ci1 + a1 + a2;
+    const float a3 = -dt * (float) fa[3], a4 = -dt * (float) fa[4], a5 = -dt * (float) fa[5];
+    p.fin_diff[2]  = c2f - t_curr;
+    c2f            = ci1 + a3 + a4 + a5;
+    p.fin_diff[3]  = c2f - t_curr;
+    for (int k = 0; k < 4; ++k) {
+        p.fpb[k] = -dt * (float) fb[k];
+    }
+    return true;
+}
+
+int mi_stork4_step(const mi_tensor * vt, const mi_tensor * xt, float t_curr, float t_next, int history, float h_prev,
+                   float h_prev2, const mi_tensor * prev, const mi_tensor * prev2, int substeps,
+                   const mi_rock4_tables * tables, void * workspace, size_t workspace_bytes, mi_stream stream) {
+    MI_TRY(lat_check(vt, nullptr));
+    MI_TRY(lat_check(xt, vt));
+    MI_TRY(lat_check(prev, vt));
+    MI_TRY(lat_check(prev2, vt));
+    if (!tables || !tables->ms || !tables->fpa || !tables->fpb || !tables->recf) {
+        return MI_ERR_NULL;
+    }
+    if (!std::isfinite(t_curr) || !std::isfinite(t_next) || !std::isfinite(h_prev) || !std::isfinite(h_prev2) ||
+        history < 0) {
+        return MI_ERR_PARAM;
+    }
+    const mi_rock4_tables & tb = *tables;
+    if (tb.ms_len < 1 || tb.recf_len < 1) {
+        return MI_ERR_PARAM;
+    }
+    for (int i = 0; i < tb.ms_len; ++i) {
+        if (tb.ms[i] < 1 || (i > 0 && tb.ms[i] <= tb.ms[i - 1])) {
+            return MI_ERR_PARAM;
+        }
+    }
+    if (tb.ms[tb.ms_len - 1] > STORK_MAX_DEG) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    const size_t n = (size_t) nelements(*vt);
+    if (!workspace || workspace_bytes < STORK_WS_XNEXT + n * sizeof(float)) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(workspace, 256)) {
+        return MI_ERR_ALIGN;
+    }
+    StorkArgs a{};
+    a.xt     = (float *) xt->data;
+    a.vt     = (const float *) vt->data;
+    a.prev   = (float *) prev->data;
+    a.prev2  = (float *) prev2->data;
+    a.status = (uint32_t *) workspace;
+    a.part   = (double *) ((char *) workspace + STORK_WS_STATUS);
+    a.xnext  = (float *) ((char *) workspace + STORK_WS_XNEXT);
+    a.n      = (uint64_t) n;
+    a.hist   = history > 2 ? 2 : history;
+    a.h1     = h_prev;
+    a.h2     = h_prev2;
+    a.dt     = t_curr - t_next;
+    // The derivative order the step sizes allow (solver-stork.h:75-111); the
+    // guards on the velocities' sums of squares run on the device.
+    a.max_order = 0;
+    if (a.hist >= 1 && h_prev != 0.0f) {
+        a.max_order = 1;
+        if (a.hist >= 2 && h_prev2 != 0.0f) {
+            const double h1 = (double) h_prev, h2 = (double) h_prev2, den = h1 * h2 * (h1 + h2);
+            if (!(std::fabs(den) < 1e-30)) {
+                a.max_order = 2;
+                a.c2        = 2.0 / den;
+            }
+        }
+    }
+    // The halving sequence of sub-step counts (solver-stork.h:302-309); counts
+    // that map to the degree of the attempt before give its result again and
+    // are skipped.
+    std::vector<StorkPlan> plans;
+    if (a.hist > 0) {
+        int s = substeps >= 2 ? substeps : 2;
+        while (s >= 2) {
+            StorkPlan p;
+            if (!rock4_plan(tb, s, t_curr, t_next, p)) {
+                return MI_ERR_PARAM;
+            }
+            if (plans.empty() || plans.back().mdeg != p.mdeg) {
+                if ((int) plans.size() == STORK_MAX_ATTEMPTS) {
+                    return MI_ERR_UNSUPPORTED;
+                }
+                p.attempt                = (int32_t) plans.size();
+                a.att_deg[plans.size()] = p.mdeg;
+                plans.push_back(p);
+            }
+            s /= 2;
+        }
+    }
+    a.n_attempts = (int) plans.size();
+    return finish(launch_stork4(a, plans.data(), (hipStream_t) stream));
+}
+
+int mi_dcw(int mode, const mi_tensor * xt, const mi_tensor * vt, float t_curr, float t_next, float scaler,
+           float high_scaler, mi_stream stream) {
+    MI_TRY(lat_check(vt, nullptr));
+    MI_TRY(lat_check(xt, vt));
+    if (mode < MI_DCW_LOW || mode > MI_DCW_PIX) {
+        return MI_ERR_PARAM;
+    }
+    if (!std::isfinite(t_curr) || !std::isfinite(t_next) || !std::isfinite(scaler) || !std::isfinite(high_scaler)) {
+        return MI_ERR_PARAM;
+    }
+    if (xt->ne[0] > UINT32_MAX || xt->ne[1] > UINT32_MAX || xt->ne[2] > UINT32_MAX) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    // the per-mode effective scalers (dit-sampler.h:641-644)
+    const float s_low = t_curr * scaler, s_high = (1.0f - t_curr) * scaler;
+    const float s_dh = (1.0f - t_curr) * high_scaler;
+    DcwArgs     a{};
+    a.xt     = (float *) xt->data;
+    a.vt     = (const float *) vt->data;
+    a.oc     = (uint32_t) xt->ne[0];
+    a.t      = (uint32_t) xt->ne[1];
+    a.n      = (uint32_t) xt->ne[2];
+    a.t_next = t_next;
+    a.pix    = mode == MI_DCW_PIX;
+    a.lo_s   = mode == MI_DCW_LOW || mode == MI_DCW_DOUBLE ? s_low : mode == MI_DCW_PIX ? scaler : 0.0f;
+    a.hi_s   = mode == MI_DCW_HIGH ? s_high : mode == MI_DCW_DOUBLE ? s_dh : 0.0f;
+    if (a.lo_s == 0.0f && a.hi_s == 0.0f) {
+        return MI_OK;  // the reference returns before the transform
+    }
+    return finish(launch_dcw(a, (hipStream_t) stream));
 }
 
 int mi_scale(const mi_tensor * x, float s, const mi_tensor * y, mi_stream stream) {

@@ -204,13 +204,61 @@ struct FlowArgs {
     float *       prev;    // dpm3m history (updated in place)
     float *       prev2;
     float *       out;     // final step
+    const float * noise;   // sde: the step's N(0,1) draws
     uint64_t      n;
-    int           solver;  // 0 euler, 1 dpm3m, 2 final
+    int           solver;  // 0 euler, 1 dpm3m, 2 final, 3 sde
     int           hist;    // dpm3m: stored velocities (0, 1, 2)
     float         t_curr, t_next;
 };
 int launch_apg(const ApgArgs & a, hipStream_t s);
 int launch_flow_step(const FlowArgs & a, hipStream_t s);
+
+// STORK4: one step is a statistics pass (the derivative guards' sums of
+// squares), one launch per sub-stepping attempt (halving degrees), and a commit
+// pass. The fp32 scalar chains of each attempt are computed on the host in the
+// reference's order and travel in the attempt's kernel arguments.
+constexpr int STORK_MAX_DEG      = 160;  // largest ROCK4 degree accepted
+constexpr int STORK_MAX_ATTEMPTS = 16;
+constexpr int STORK_STAT_BLOCKS  = 256;
+struct StorkPlan {
+    float   t1_first;                  // j = 1: -dt * recf[mr]
+    float   fin_diff[4];               // time offsets of the four finishing velocities
+    float   fpb[4];                    // -dt * fpb[mz][k]
+    int32_t mdeg;
+    int32_t attempt;                   // index in the step's attempt list
+    float   sub[STORK_MAX_DEG - 1][4]; // j = 2..mdeg: temp1, temp2, temp3, diff
+};
+struct StorkArgs {
+    float *       xt;          // updated in place by the commit pass
+    const float * vt;
+    float *       prev;        // latest stored velocity (step size h1), rotated by the commit
+    float *       prev2;       // the one before (h2)
+    uint32_t *    status;      // workspace: [0] Euler fallbacks this generation, [1] derivative
+                               // order, [2] accepted degree, [4..4+STORK_MAX_ATTEMPTS) non-finite flags
+    double *      part;        // workspace: [STORK_STAT_BLOCKS][3] sums of squares (vt, dv, d2v)
+    float *       xnext;       // workspace: [n] the latest attempt's result
+    uint64_t      n;
+    int           hist;        // stored velocities (0: Euler bootstrap)
+    int           max_order;   // derivative order the step sizes allow (0, 1, 2)
+    float         h1, h2, dt;
+    double        c2;          // 2 / (h1 h2 (h1 + h2)) for d2v
+    int           n_attempts;
+    int32_t       att_deg[STORK_MAX_ATTEMPTS];
+};
+constexpr size_t STORK_WS_STATUS = 256;
+constexpr size_t STORK_WS_XNEXT  = STORK_WS_STATUS + ((STORK_STAT_BLOCKS * 3 * sizeof(double) + 255) / 256) * 256;
+int launch_stork4(const StorkArgs & a, const StorkPlan * plans, hipStream_t s);
+
+// DCW: Haar band correction after a solver step, per frame pair and channel.
+struct DcwArgs {
+    float *       xt;      // [n][t][oc], in place
+    const float * vt;
+    uint32_t      n, t, oc;
+    float         t_next;
+    float         lo_s, hi_s;  // band scalers (0: band untouched)
+    int           pix;         // pixel-space mode: xt += lo_s (xt - denoised)
+};
+int launch_dcw(const DcwArgs & a, hipStream_t s);
 
 // ---- tsembd.hip ------------------------------------------------------------
 int launch_scale(const mi_tensor & x, float sc, const mi_tensor & y, hipStream_t s);

@@ -312,6 +312,55 @@ int mi_flow_step(int solver, const mi_tensor * vt, const mi_tensor * xt, float t
                  const mi_tensor * prev, const mi_tensor * prev2, mi_stream stream);
 int mi_flow_final(const mi_tensor * xt, const mi_tensor * vt, float t, const mi_tensor * out, mi_stream stream);
 
+/* The other solvers of solvers/solver-registry.h:30-33 and the DCW correction.
+ *
+ * mi_flow_step_sde: the SDE ancestral step (solvers/solver-sde.h:17-38),
+ *   x0 = xt - vt * t_curr; xt = t_next * noise + (1 - t_next) * x0, fp32 in
+ *   that order. noise: F32 [Oc, T, N], the step's standard normal draws (the
+ *   reference draws them on the host with Philox from seed_b + step + 1,
+ *   philox.h; the caller brings them).
+ *
+ * mi_stork4_step: one STORK4 step (solvers/solver-stork.h:269-323) in place.
+ *   history = velocities stored so far (0: the Euler bootstrap step, 289-296);
+ *   prev / prev2 hold the latest two with their step sizes h_prev / h_prev2
+ *   (the dt of the steps that stored them); on return prev2 <- prev and
+ *   prev <- vt (the caller shifts h_prev2 <- h_prev, h_prev <- t_curr - t_next).
+ *   Velocity derivatives by forward difference and the three-point formula
+ *   with the reference's guards (69-126); ROCK4 sub-stepping of `substeps`
+ *   (reference default 10; at least 2, clamped to the largest degree) halved
+ *   while any result is not finite, then Euler (298-318). tables: the ROCK4
+ *   coefficient tables, host memory (solver-stork4-constants.h:
+ *   STORK4_MS / FPA / FPB / RECF), degrees ascending and <= 160.
+ *   workspace: mi_stork4_workspace() bytes of device memory, 256-aligned, kept
+ *   for the whole generation; its first four 32-bit words report the number
+ *   of Euler fallbacks since the bootstrap step, the last step's derivative
+ *   order, and the degree it accepted (0: Euler). Calls sharing a workspace race.
+ *
+ * mi_dcw: the Differential Correction in Wavelet domain after a solver step
+ *   (dit-sampler.h:613-667, dwt-haar.h), per sample, in place:
+ *   denoised = xt - vt * t_next; low: the Haar low band of xt moves by
+ *   t_curr * scaler * (xL - yL); high: the high band by (1 - t_curr) * scaler;
+ *   double: low by t_curr * scaler and high by (1 - t_curr) * high_scaler;
+ *   pix: xt += scaler * (xt - denoised). A zero effective scaler leaves xt
+ *   untouched. The reference applies it only to solvers that inject no noise. */
+typedef struct mi_rock4_tables {
+    const int32_t * ms;        /* [ms_len] degrees, ascending */
+    const double *  fpa;       /* [ms_len][6] finishing coefficients A */
+    const double *  fpb;       /* [ms_len][4] finishing coefficients B */
+    const double *  recf;      /* [recf_len] recurrence coefficients */
+    int32_t         ms_len;
+    int32_t         recf_len;
+} mi_rock4_tables;
+enum { MI_DCW_LOW = 0, MI_DCW_HIGH = 1, MI_DCW_DOUBLE = 2, MI_DCW_PIX = 3 };
+int mi_flow_step_sde(const mi_tensor * vt, const mi_tensor * xt, const mi_tensor * noise, float t_curr, float t_next,
+                     mi_stream stream);
+int mi_stork4_workspace(const mi_tensor * xt, size_t * bytes);
+int mi_stork4_step(const mi_tensor * vt, const mi_tensor * xt, float t_curr, float t_next, int history, float h_prev,
+                   float h_prev2, const mi_tensor * prev, const mi_tensor * prev2, int substeps,
+                   const mi_rock4_tables * tables, void * workspace, size_t workspace_bytes, mi_stream stream);
+int mi_dcw(int mode, const mi_tensor * xt, const mi_tensor * vt, float t_curr, float t_next, float scaler,
+           float high_scaler, mi_stream stream);
+
 /* GGUF reader and load-time weight preparation. Replaces gf_load (mmap, the
  * header parse and the check that every tensor lies inside the file,
  * gguf-weights.h:74-154), gf_load_tensor / gf_load_tensor_f32 (156-268),

@@ -719,3 +719,296 @@ void orc_flow_final(const float * xt, const float * vt, int64_t n, float t, floa
         out[i]        = xt[i] - p;
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* The other sampler steps: SDE ancestral (solvers/solver-sde.h:17-38) with  */
+/* the step's standard normal draws given, STORK4 (solvers/solver-stork.h),  */
+/* and DCW (dit-sampler.h:613-667 over dwt-haar.h). fp32 in the reference's  */
+/* operation order, the derivative sums in double. Layout [n][t][oc].        */
+/* ------------------------------------------------------------------------ */
+void orc_sde_step(float * xt, const float * vt, const float * noise, int64_t n, float t_curr, float t_next) {
+    /* solver-sde.h:33-36 */
+    for (int64_t i = 0; i < n; i++) {
+        const float x0 = xt[i] - vt[i] * t_curr;
+        xt[i]          = t_next * noise[i] + (1.0f - t_next) * x0;
+    }
+}
+
+/* _stork_rms (solver-stork.h:34-41): double sum in index order */
+static double stork_rms(const float * d, int64_t n) {
+    double s = 0.0;
+    for (int64_t i = 0; i < n; i++) {
+        s += (double) d[i] * (double) d[i];
+    }
+    return sqrt(s / (double) n);
+}
+
+/* _stork_taylor_approx (solver-stork.h:45-64) */
+static void stork_taylor(float * out, int order, float diff, const float * v, const float * dv, const float * d2v,
+                         int64_t n) {
+    if (order >= 2) {
+        const float h = 0.5f * diff * diff;
+        for (int64_t i = 0; i < n; i++) {
+            out[i] = v[i] + diff * dv[i] + h * d2v[i];
+        }
+    } else if (order == 1) {
+        for (int64_t i = 0; i < n; i++) {
+            out[i] = v[i] + diff * dv[i];
+        }
+    } else {
+        memcpy(out, v, (size_t) n * sizeof(float));
+    }
+}
+
+/* _stork_compute_derivatives (solver-stork.h:69-126) with the two most recent
+ * records as (prev, h1) and (prev2, h2); hist = records stored (0, 1, 2+) */
+static int stork_derivatives(const float * vt, int64_t n, int hist, const float * prev, float h1, const float * prev2,
+                             float h2, float * dv, float * d2v) {
+    if (hist < 1 || h1 == 0.0f) {
+        return 0;
+    }
+    for (int64_t i = 0; i < n; i++) {
+        dv[i] = (prev[i] - vt[i]) / h1;
+    }
+    const double vt_rms = stork_rms(vt, n);
+    const double dv_rms = stork_rms(dv, n);
+    if (vt_rms > 0.0 && dv_rms * fabs((double) h1) > 5.0 * vt_rms) {
+        return 0;
+    }
+    if (hist < 2 || h2 == 0.0f) {
+        return 1;
+    }
+    const double h1d = (double) h1, h2d = (double) h2;
+    const double den = h1d * h2d * (h1d + h2d);
+    if (fabs(den) < 1e-30) {
+        return 1;
+    }
+    const double c = 2.0 / den;
+    for (int64_t i = 0; i < n; i++) {
+        d2v[i] = (float) (c * ((double) prev2[i] * h1d - (double) prev[i] * (h1d + h2d) + (double) vt[i] * h2d));
+    }
+    const double d2v_rms = stork_rms(d2v, n);
+    if (vt_rms > 0.0 && d2v_rms * (double) h1 * (double) h1 > 5.0 * vt_rms) {
+        return 1;
+    }
+    return 2;
+}
+
+/* _rock4_mdegr (solver-stork.h:140-159) */
+static void rock4_mdegr(int s, const int32_t * ms, int ms_len, int * mdeg, int * mz, int * mr) {
+    int mp1 = 1;
+    for (int i = 0; i < ms_len; i++) {
+        if (ms[i] >= s) {
+            *mdeg = ms[i];
+            *mz   = i;
+            *mr   = mp1 - 1;
+            return;
+        }
+        mp1 += ms[i] * 2 - 1;
+    }
+    *mz   = ms_len - 1;
+    *mdeg = ms[*mz];
+    *mr   = mp1 - 1;
+}
+
+static int all_finite(const float * x, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        if (!isfinite(x[i])) {
+            return 0;
+        }
+    }
+    return 1;
+}
+
+/* _rock4_substep (solver-stork.h:163-267): the Chebyshev recurrence over the
+ * degree, then the 4-stage finishing blend; returns 1 when out is finite */
+static int rock4_substep(float * out, const float * xt, const float * vt, int s, float t_curr, float t_prev, int order,
+                         const float * dv, const float * d2v, int64_t n, const orc_rock4 * tab, int * mdeg_out) {
+    const int smax = tab->ms[tab->ms_len - 1];
+    if (s > smax) {
+        s = smax;
+    }
+    int mdeg, mz, mr;
+    rock4_mdegr(s, tab->ms, tab->ms_len, &mdeg, &mz, &mr);
+    *mdeg_out      = mdeg;
+    const float dt = t_curr - t_prev;
+    const size_t b = (size_t) n * sizeof(float) + 4;
+    float *      y2 = (float *) malloc(b), *y1 = (float *) malloc(b), *yj = (float *) malloc(b);
+    float *      va = (float *) malloc(b), *f1 = (float *) malloc(b), *f2 = (float *) malloc(b);
+    float *      f3 = (float *) malloc(b), *f4 = (float *) malloc(b);
+    memcpy(y2, xt, (size_t) n * sizeof(float));
+    memcpy(y1, xt, (size_t) n * sizeof(float));
+    float ci1 = t_curr, ci2 = t_curr, ci3 = t_curr;
+    for (int j = 1; j <= mdeg; j++) {
+        if (j == 1) {
+            const float t1 = -dt * (float) tab->recf[mr];
+            ci1            = t_curr + t1;
+            ci2            = ci1;
+            for (int64_t i = 0; i < n; i++) {
+                y1[i] = xt[i] + t1 * vt[i];
+            }
+        } else {
+            const float diff = ci1 - t_curr;
+            stork_taylor(va, order, diff, vt, dv, d2v, n);
+            const float t1     = -dt * (float) tab->recf[mr + 2 * (j - 2) + 1];
+            const float t3     = -(float) tab->recf[mr + 2 * (j - 2) + 2];
+            const float t2     = 1.0f - t3;
+            const float ci1_nw = t1 + t2 * ci2 + t3 * ci3;
+            for (int64_t i = 0; i < n; i++) {
+                yj[i] = t1 * va[i] + t2 * y1[i] + t3 * y2[i];
+            }
+            float * r = y2;
+            y2        = y1;
+            y1        = yj;
+            yj        = r;
+            ci3       = ci2;
+            ci2       = ci1_nw;
+            ci1       = ci1_nw;
+        }
+    }
+    const double * fa = tab->fpa + 6 * mz;
+    const double * fb = tab->fpb + 4 * mz;
+    const float    a0 = -dt * (float) fa[0];
+    stork_taylor(f1, order, ci1 - t_curr, vt, dv, d2v, n);
+    float       c2f = ci1 + a0;
+    const float a1 = -dt * (float) fa[1], a2 = -dt * (float) fa[2];
+    stork_taylor(f2, order, c2f - t_curr, vt, dv, d2v, n);
+    c2f            = ci1 + a1 + a2;
+    const float a3 = -dt * (float) fa[3], a4 = -dt * (float) fa[4], a5 = -dt * (float) fa[5];
+    stork_taylor(f3, order, c2f - t_curr, vt, dv, d2v, n);
+    c2f            = ci1 + a3 + a4 + a5;
+    const float b0 = -dt * (float) fb[0], b1 = -dt * (float) fb[1], b2 = -dt * (float) fb[2], b3 = -dt * (float) fb[3];
+    stork_taylor(f4, order, c2f - t_curr, vt, dv, d2v, n);
+    for (int64_t i = 0; i < n; i++) {
+        out[i] = y1[i] + b0 * f1[i] + b1 * f2[i] + b2 * f3[i] + b3 * f4[i];
+    }
+    free(y2), free(y1), free(yj), free(va), free(f1), free(f2), free(f3), free(f4);
+    return all_finite(out, n);
+}
+
+/* solver_stork4_step (solver-stork.h:269-323). prev/prev2 hold the two most
+ * recent velocity records with step sizes h1/h2 (hist = records stored); they
+ * are rotated (prev2 <- prev, prev <- vt) as _stork_update_history appends.
+ * info[0] = derivative order, info[1] = degree of the accepted sub-stepping
+ * (0: Euler), info[2] = 1 when every attempt was non-finite (Euler fallback). */
+void orc_stork4_step(float * xt, const float * vt, int64_t n, float t_curr, float t_next, int hist, float h1,
+                     float h2, float * prev, float * prev2, int substeps, const orc_rock4 * tab, int * info) {
+    const float dt = t_curr - t_next;
+    info[0] = info[1] = info[2] = 0;
+    if (hist == 0) {
+        for (int64_t i = 0; i < n; i++) {
+            xt[i] -= vt[i] * dt;
+        }
+    } else {
+        const size_t b   = (size_t) n * sizeof(float) + 4;
+        float *      dv  = (float *) calloc(1, b);
+        float *      d2v = (float *) calloc(1, b);
+        float *      nxt = (float *) malloc(b);
+        const int    ord = stork_derivatives(vt, n, hist, prev, h1, prev2, h2, dv, d2v);
+        int          s   = substeps >= 2 ? substeps : 2, ok = 0, mdeg = 0;
+        while (s >= 2) {
+            if (rock4_substep(nxt, xt, vt, s, t_curr, t_next, ord, dv, d2v, n, tab, &mdeg)) {
+                ok = 1;
+                break;
+            }
+            s /= 2;
+        }
+        info[0] = ord;
+        if (ok) {
+            memcpy(xt, nxt, (size_t) n * sizeof(float));
+            info[1] = mdeg;
+        } else {
+            for (int64_t i = 0; i < n; i++) {
+                xt[i] -= vt[i] * dt;
+            }
+            info[2] = 1;
+        }
+        free(dv), free(d2v), free(nxt);
+    }
+    if (hist >= 1) {
+        memcpy(prev2, prev, (size_t) n * sizeof(float));
+    }
+    memcpy(prev, vt, (size_t) n * sizeof(float));
+}
+
+/* DCW (dit-sampler.h:626-664): per sample, denoised = xt - vt * t_next, then
+ * the Haar band correction of dwt-haar.h (forward 27-52, inverse 56-77, low
+ * 84-101, high 105-122, double 127-152, pix 157-166). mode 0 low, 1 high,
+ * 2 double, 3 pix; the effective scalers follow dit-sampler.h:641-644. */
+static void haar_fwd(const float * src, int64_t t, int64_t c, float * lo, float * hi) {
+    const float k = 0.70710678118654752440f;
+    for (int64_t l = 0; l < (t + 1) / 2; l++) {
+        const float * a = src + 2 * l * c;
+        if (2 * l + 1 < t) {
+            const float * b = a + c;
+            for (int64_t j = 0; j < c; j++) {
+                lo[l * c + j] = (a[j] + b[j]) * k;
+                hi[l * c + j] = (a[j] - b[j]) * k;
+            }
+        } else {
+            for (int64_t j = 0; j < c; j++) {
+                lo[l * c + j] = a[j] * k;
+                hi[l * c + j] = a[j] * k;
+            }
+        }
+    }
+}
+
+static void haar_inv(const float * lo, const float * hi, int64_t t, int64_t c, float * out) {
+    const float k = 0.70710678118654752440f;
+    for (int64_t l = 0; l < (t + 1) / 2; l++) {
+        for (int64_t j = 0; j < c; j++) {
+            out[2 * l * c + j] = (lo[l * c + j] + hi[l * c + j]) * k;
+        }
+        if (2 * l + 1 < t) {
+            for (int64_t j = 0; j < c; j++) {
+                out[(2 * l + 1) * c + j] = (lo[l * c + j] - hi[l * c + j]) * k;
+            }
+        }
+    }
+}
+
+void orc_dcw(int mode, float * xt, const float * vt, int64_t n, int64_t t, int64_t oc, float t_curr, float t_next,
+             float scaler, float high_scaler) {
+    const float s_low = t_curr * scaler, s_high = (1.0f - t_curr) * scaler;
+    const float s_dh = (1.0f - t_curr) * high_scaler, s_pix = scaler;
+    const int64_t m  = t * oc, tl = (t + 1) / 2;
+    const size_t  b  = (size_t) (tl * oc) * sizeof(float) + 4;
+    float *       den = (float *) malloc((size_t) m * sizeof(float) + 4);
+    float *       xl = (float *) malloc(b), *xh = (float *) malloc(b), *yl = (float *) malloc(b),
+            *yh = (float *) malloc(b);
+    for (int64_t s = 0; s < n; s++) {
+        float *       x = xt + s * m;
+        const float * v = vt + s * m;
+        for (int64_t i = 0; i < m; i++) {
+            den[i] = x[i] - v[i] * t_next;
+        }
+        if (mode == 3) {
+            if (s_pix != 0.0f) {
+                for (int64_t i = 0; i < m; i++) {
+                    x[i] = x[i] + s_pix * (x[i] - den[i]);
+                }
+            }
+            continue;
+        }
+        const float lo_s = mode == 0 || mode == 2 ? s_low : 0.0f;
+        const float hi_s = mode == 1 ? s_high : mode == 2 ? s_dh : 0.0f;
+        if (lo_s == 0.0f && hi_s == 0.0f) {
+            continue;
+        }
+        haar_fwd(x, t, oc, xl, xh);
+        haar_fwd(den, t, oc, yl, yh);
+        if (lo_s != 0.0f) {
+            for (int64_t i = 0; i < tl * oc; i++) {
+                xl[i] = xl[i] + lo_s * (xl[i] - yl[i]);
+            }
+        }
+        if (hi_s != 0.0f) {
+            for (int64_t i = 0; i < tl * oc; i++) {
+                xh[i] = xh[i] + hi_s * (xh[i] - yh[i]);
+            }
+        }
+        haar_inv(xl, xh, t, oc, x);
+    }
+    free(den), free(xl), free(xh), free(yl), free(yh);
+}

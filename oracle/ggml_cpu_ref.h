@@ -144,6 +144,27 @@ void orc_flow_step(int solver, float * xt, const float * vt, int64_t n, float t_
                    float * prev, float * prev2);
 void orc_flow_final(const float * xt, const float * vt, int64_t n, float t, float * out);
 
+/* ---- The other sampler steps: SDE ancestral (solvers/solver-sde.h:17-38)
+ *      with the step's N(0,1) draws given as noise; STORK4
+ *      (solvers/solver-stork.h:269-323) over ROCK4 tables (degrees ms,
+ *      finishing coefficients fpa [ms_len][6] / fpb [ms_len][4], recurrence
+ *      coefficients recf), prev/prev2 = the two latest velocities with step
+ *      sizes h1/h2, rotated on return; info[3] = derivative order, accepted
+ *      degree (0 = Euler), Euler fallback flag. DCW (dit-sampler.h:613-667,
+ *      dwt-haar.h) on [n][t][oc], mode 0 low, 1 high, 2 double, 3 pix. ---- */
+typedef struct orc_rock4 {
+    const int32_t * ms;
+    const double *  fpa;
+    const double *  fpb;
+    const double *  recf;
+    int             ms_len, recf_len;
+} orc_rock4;
+void orc_sde_step(float * xt, const float * vt, const float * noise, int64_t n, float t_curr, float t_next);
+void orc_stork4_step(float * xt, const float * vt, int64_t n, float t_curr, float t_next, int hist, float h1,
+                     float h2, float * prev, float * prev2, int substeps, const orc_rock4 * tab, int * info);
+void orc_dcw(int mode, float * xt, const float * vt, int64_t n, int64_t t, int64_t oc, float t_curr, float t_next,
+             float scaler, float high_scaler);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,12 @@ def use_isa(isa: str) -> str:
     return path
 
 
+class Rock4(ctypes.Structure):
+    """orc_rock4: ROCK4 tables (degrees, finishing and recurrence coefficients)."""
+    _fields_ = [("ms", _i32p), ("fpa", ctypes.POINTER(ctypes.c_double)), ("fpb", ctypes.POINTER(ctypes.c_double)),
+                ("recf", ctypes.POINTER(ctypes.c_double)), ("ms_len", ctypes.c_int), ("recf_len", ctypes.c_int)]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -88,6 +94,11 @@ def lib():
         L.orc_flow_step.argtypes = [ctypes.c_int, _fp, _fp, _i64, ctypes.c_float, ctypes.c_float, ctypes.c_int, _fp,
                                     _fp]
         L.orc_flow_final.argtypes = [_fp, _fp, _i64, ctypes.c_float, _fp]
+        L.orc_sde_step.argtypes = [_fp, _fp, _fp, _i64, ctypes.c_float, ctypes.c_float]
+        L.orc_stork4_step.argtypes = [_fp, _fp, _i64, ctypes.c_float, ctypes.c_float, ctypes.c_int, ctypes.c_float,
+                                      ctypes.c_float, _fp, _fp, ctypes.c_int, ctypes.POINTER(Rock4), _i32p]
+        L.orc_dcw.argtypes = [ctypes.c_int, _fp, _fp, _i64, _i64, _i64, ctypes.c_float, ctypes.c_float,
+                              ctypes.c_float, ctypes.c_float]
         L.orc_set_threads.argtypes = [ctypes.c_int]
         L.orc_get_threads.restype = ctypes.c_int
         _lib = L
@@ -422,3 +433,48 @@ def flow_final(xt, vt, t: float) -> np.ndarray:
     out = np.empty_like(xt)
     lib().orc_flow_final(_f(xt), _f(vt), xt.size, t, _f(out))
     return out
+
+
+def sde_step(xt: np.ndarray, vt, noise, t_curr: float, t_next: float) -> None:
+    """SDE ancestral step in place on xt (solver-sde.h:33-36) with the given N(0,1) draws."""
+    vt, noise = _c32(vt), _c32(noise)
+    assert xt.dtype == np.float32 and xt.flags.c_contiguous and vt.size == xt.size == noise.size
+    lib().orc_sde_step(_f(xt), _f(vt), _f(noise), xt.size, t_curr, t_next)
+
+
+def rock4_struct(ms, fpa, fpb, recf):
+    """Keep-alive tuple (Rock4, arrays) for ROCK4 tables given as numpy arrays."""
+    ms = np.ascontiguousarray(ms, np.int32)
+    fpa = np.ascontiguousarray(fpa, np.float64).reshape(len(ms), 6)
+    fpb = np.ascontiguousarray(fpb, np.float64).reshape(len(ms), 4)
+    recf = np.ascontiguousarray(recf, np.float64)
+    dp = ctypes.POINTER(ctypes.c_double)
+    r = Rock4(ms.ctypes.data_as(_i32p), fpa.ctypes.data_as(dp), fpb.ctypes.data_as(dp), recf.ctypes.data_as(dp),
+              len(ms), len(recf))
+    return r, (ms, fpa, fpb, recf)
+
+
+def stork4_step(xt: np.ndarray, vt, t_curr: float, t_next: float, hist: int, h1: float, h2: float,
+                prev: np.ndarray, prev2: np.ndarray, substeps: int, tables) -> tuple:
+    """STORK4 step in place on xt, prev, prev2 (solver-stork.h:269-323); tables = (ms, fpa, fpb, recf).
+    Returns (derivative order, accepted degree or 0, Euler fallback)."""
+    vt = _c32(vt)
+    for a in (xt, prev, prev2):
+        assert a.dtype == np.float32 and a.flags.c_contiguous and a.size == vt.size
+    r, keep = rock4_struct(*tables)
+    info = np.zeros(3, np.int32)
+    lib().orc_stork4_step(_f(xt), _f(vt), xt.size, t_curr, t_next, hist, h1, h2, _f(prev), _f(prev2), substeps,
+                          ctypes.byref(r), info.ctypes.data_as(_i32p))
+    del keep
+    return int(info[0]), int(info[1]), bool(info[2])
+
+
+DCW_MODES = {"low": 0, "high": 1, "double": 2, "pix": 3}
+
+
+def dcw(mode: str, xt: np.ndarray, vt, t_curr: float, t_next: float, scaler: float, high_scaler: float = 0.0) -> None:
+    """DCW correction in place on xt (n, t, oc) after a solver step (dit-sampler.h:626-664)."""
+    vt = _c32(vt)
+    assert xt.dtype == np.float32 and xt.flags.c_contiguous and xt.ndim == 3 and vt.shape == xt.shape
+    n, t, oc = xt.shape
+    lib().orc_dcw(DCW_MODES.get(mode, 0), _f(xt), _f(vt), n, t, oc, t_curr, t_next, scaler, high_scaler)

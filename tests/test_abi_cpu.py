@@ -272,6 +272,54 @@ def test_sampler_validation():
     assert L.mi_flow_final(R(c), R(c), float("inf"), R(c), NULL_S) == -6
 
 
+def _rock4(ms, fpa_rows=None, recf_len=None):
+    ms = (ctypes.c_int32 * len(ms))(*ms)
+    nrec = recf_len if recf_len is not None else sum(2 * m - 1 for m in ms)
+    fpa = (ctypes.c_double * (6 * len(ms)))()
+    fpb = (ctypes.c_double * (4 * len(ms)))()
+    recf = (ctypes.c_double * max(nrec, 1))()
+    tab = _lib.MiRock4Tables(ctypes.cast(ms, ctypes.POINTER(ctypes.c_int32)),
+                             ctypes.cast(fpa, ctypes.POINTER(ctypes.c_double)),
+                             ctypes.cast(fpb, ctypes.POINTER(ctypes.c_double)),
+                             ctypes.cast(recf, ctypes.POINTER(ctypes.c_double)), len(ms), nrec)
+    tab._keep = (ms, fpa, fpb, recf)
+    return tab
+
+
+def test_other_solvers_validation():
+    oc, t, n = 64, 100, 2
+    c = _t([oc, t, n])
+    sde = L.mi_flow_step_sde
+    assert sde(R(c), R(c), R(_t([oc, t, n + 1])), 1.0, 0.5, NULL_S) == -3          # noise shape
+    assert sde(R(c), R(c), R(_t([oc, t, n], BF16)), 1.0, 0.5, NULL_S) == -2
+    assert sde(R(c), R(c), R(c), float("nan"), 0.5, NULL_S) == -6
+    nb = ctypes.c_size_t(0)
+    assert L.mi_stork4_workspace(R(c), ctypes.byref(nb)) == 0 and nb.value >= oc * t * n * 4
+    W = ctypes.c_void_p(1 << 20)
+    st = L.mi_stork4_step
+    tab = _rock4([1, 2, 4, 10, 20])
+    assert st(R(c), R(c), 1.0, 0.9, 1, 0.1, 0.0, R(c), R(c), 10, None, W, nb.value, NULL_S) == -1
+    assert st(R(c), R(c), 1.0, 0.9, 1, 0.1, 0.0, R(c), R(c), 10, R(tab), None, 0, NULL_S) == -6
+    assert st(R(c), R(c), 1.0, 0.9, 1, 0.1, 0.0, R(c), R(c), 10, R(tab), W, nb.value - 4, NULL_S) == -6
+    assert st(R(c), R(c), 1.0, 0.9, 1, 0.1, 0.0, R(c), R(c), 10, R(tab), ctypes.c_void_p((1 << 20) + 64),
+              nb.value, NULL_S) == -5
+    assert st(R(c), R(c), 1.0, 0.9, -1, 0.1, 0.0, R(c), R(c), 10, R(tab), W, nb.value, NULL_S) == -6
+    assert st(R(c), R(c), 1.0, float("inf"), 1, 0.1, 0.0, R(c), R(c), 10, R(tab), W, nb.value, NULL_S) == -6
+    assert st(R(c), R(c), 1.0, 0.9, 1, 0.1, 0.0, R(_t([oc, t + 1, n])), R(c), 10, R(tab), W, nb.value,
+              NULL_S) == -3
+    bad = _rock4([1, 4, 2])                                                        # degrees not ascending
+    assert st(R(c), R(c), 1.0, 0.9, 1, 0.1, 0.0, R(c), R(c), 10, R(bad), W, nb.value, NULL_S) == -6
+    big = _rock4([2, 200])                                                         # degree above 160
+    assert st(R(c), R(c), 1.0, 0.9, 1, 0.1, 0.0, R(c), R(c), 10, R(big), W, nb.value, NULL_S) == -7
+    short = _rock4([1, 2, 4, 10, 20], recf_len=30)                                 # recf too short for 20
+    assert st(R(c), R(c), 1.0, 0.9, 1, 0.1, 0.0, R(c), R(c), 20, R(short), W, nb.value, NULL_S) == -6
+    dcw = L.mi_dcw
+    assert dcw(4, R(c), R(c), 0.5, 0.4, 0.3, 0.0, NULL_S) == -6                     # unknown mode
+    assert dcw(0, R(c), R(_t([oc, t, n + 1])), 0.5, 0.4, 0.3, 0.0, NULL_S) == -3
+    assert dcw(0, R(c), R(c), 0.5, 0.4, float("nan"), 0.0, NULL_S) == -6
+    assert dcw(0, R(c), R(c), 0.5, 0.4, 0.0, 0.7, NULL_S) == 0                      # low band scaler 0: no launch
+
+
 def test_chain_validation():
     io = _lib.MiDitBlockIO()
     io.hidden = _t([2048, 4])
