@@ -17,6 +17,8 @@ F32, F16, Q8_0, I32, BF16 = 0, 1, 8, 26, 30
 # enum mi_q8_0_rounding
 Q8_0_CPU_X86, Q8_0_REF = 0, 1
 
+NOALLOC_SCRATCH_BYTES = 32 << 20  # MI_MUL_MAT_NOALLOC_SCRATCH_BYTES
+
 STATUS = {
     0: "MI_OK",
     -1: "MI_ERR_NULL",
@@ -28,6 +30,7 @@ STATUS = {
     -7: "MI_ERR_UNSUPPORTED",
     -8: "MI_ERR_HIP",
     -9: "MI_ERR_FILE",
+    -10: "MI_ERR_SCRATCH",
 }
 
 
@@ -111,6 +114,7 @@ PROTOTYPES = {
     "mi_q8_0_repack": [_TP, _VP, ctypes.c_size_t, _VP],
     "mi_mul_mat_q8_0_workspace": [ctypes.c_int64, ctypes.c_int64, _TP, ctypes.POINTER(ctypes.c_size_t)],
     "mi_mul_mat_q8_0": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, _TP, _VP, ctypes.c_size_t, _VP],
+    "mi_mul_mat_q8_0_noalloc": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, _TP, _VP],
     "mi_mul_mat_q8_0_rms_norm": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, _TP, ctypes.c_float, _TP, _VP,
                                  ctypes.c_size_t, _VP],
     "mi_mul_mat_q8_0_add_rms_norm": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, _TP, _TP, ctypes.c_float, _TP, _TP,

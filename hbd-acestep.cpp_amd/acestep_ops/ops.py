@@ -264,6 +264,14 @@ def mul_mat_q8_0_workspace(w: Q8R64, x) -> int:
     return int(nb.value)
 
 
+def mul_mat_q8_0_noalloc(w: Q8R64, x, out=None, stream=None):
+    """mul_mat_q8_0 on the library's static per-GPU scratch: no workspace, no allocation
+    in the call (out must then be given by a caller that cannot allocate)."""
+    y = _out(out, tuple(x.shape[:-1]) + (w.n,), "f32")
+    _lib.call("mi_mul_mat_q8_0_noalloc", ctypes.c_void_p(w.data.ptr), w.k, w.n, _p(x), _p(y), _s(stream))
+    return y
+
+
 def mul_mat_q8_0_swiglu_workspace(w: Q8R64, gu) -> int:
     n = ctypes.c_size_t(0)
     _lib.call("mi_mul_mat_q8_0_swiglu_workspace", w.k, w.n, _p(gu), ctypes.byref(n))

@@ -8,6 +8,7 @@
 
 #include <atomic>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "launch.h"
@@ -201,6 +202,8 @@ const char * mi_status_str(int status) {
             return "HIP runtime error";
         case MI_ERR_FILE:
             return "file missing, unreadable, truncated or not GGUF";
+        case MI_ERR_SCRATCH:
+            return "needs more scratch than the library's static buffer holds";
         default:
             return "unknown status";
     }
@@ -855,6 +858,61 @@ int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, c
         return MI_ERR_ALIGN;
     }
     mul_mat_q8_0_bind(a, (char *) workspace);
+    return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
+}
+
+// Scratch of mi_mul_mat_q8_0_noalloc: one static array per GPU, loaded with the
+// library's code object. Host code never uses this name as an address (on the
+// host it is only a stand-in for the symbol): each device's address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) char scratch[MI_MUL_MAT_NOALLOC_SCRATCH_BYTES];
+
+static int noalloc_scratch(void ** out) {
+    constexpr int            MAX_DEV = 64;
+    static std::atomic<void *> addr[MAX_DEV];
+    static std::mutex          mu;
+    int                        dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
+        return MI_ERR_HIP;
+    }
+    void * p = addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(mu);
+        p = addr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+                (void) hipGetLastError();
+                return MI_ERR_HIP;
+            }
+            addr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return MI_OK;
+}
+
+int mi_mul_mat_q8_0_noalloc(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
+                            mi_stream stream) {
+    if (!y) {
+        return MI_ERR_NULL;
+    }
+    MmvArgs a;
+    MI_TRY(mm_desc(w, k, n, x, y, a));
+    if (a.m == 0 || a.n == 0) {
+        return MI_OK;
+    }
+    if (!w) {
+        return MI_ERR_NULL;
+    }
+    if (!aligned(w, 16)) {
+        return MI_ERR_ALIGN;
+    }
+    if (mul_mat_q8_0_workspace(a) > MI_MUL_MAT_NOALLOC_SCRATCH_BYTES) {
+        return MI_ERR_SCRATCH;
+    }
+    void * ws = nullptr;
+    MI_TRY(noalloc_scratch(&ws));
+    mul_mat_q8_0_bind(a, (char *) ws);
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 

@@ -51,6 +51,7 @@ enum mi_status {
     MI_ERR_UNSUPPORTED = -7, /* valid ggml op configuration this library lacks   */
     MI_ERR_HIP         = -8, /* the HIP runtime reported an error at launch      */
     MI_ERR_FILE        = -9, /* a file is missing, unreadable, truncated or not GGUF */
+    MI_ERR_SCRATCH     = -10, /* the call needs more than the library's static scratch */
 };
 
 /* Q8_0 quantizer rounding variants (both are ggml's own):
@@ -252,6 +253,22 @@ int mi_q8_0_repack(const mi_tensor * w, void * dst, size_t dst_bytes, mi_stream 
 int mi_mul_mat_q8_0_workspace(int64_t k, int64_t n, const mi_tensor * x, size_t * bytes);
 int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
                     void * workspace, size_t workspace_bytes, mi_stream stream);
+
+/* mi_mul_mat_q8_0 without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Its scratch (the quantized x and the partial sums of
+ * a split k) is one static device array of MI_MUL_MAT_NOALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends; a call that needs more
+ * (mi_mul_mat_q8_0_workspace() above the limit: Qwen3 decode at any batch up
+ * to 8 and prefill chunks up to about m * k = 28M fit) returns MI_ERR_SCRATCH
+ * before any launch. Every call on one GPU uses the same array, so calls that
+ * overlap on one GPU (other streams, other host threads) race; stream-ordered
+ * calls do not. Nothing in it has to start at zero: a call writes every
+ * scratch value it reads. y is bit-identical to mi_mul_mat_q8_0's. */
+#define MI_MUL_MAT_NOALLOC_SCRATCH_BYTES ((size_t) 32 << 20)
+int mi_mul_mat_q8_0_noalloc(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
+                            mi_stream stream);
 
 /* The SwiGLU -> down projection pair as one call: y = ggml_mul_mat(w,
  * ggml_swiglu(gu)) (qwen3-enc.h:221-223, the Qwen3 MLP; dit-graph.h:265-268,

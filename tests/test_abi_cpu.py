@@ -212,6 +212,16 @@ def test_mul_mat_q8_0_validation():
     assert mm(W, k, n, R(x), R(y), ctypes.c_void_p((1 << 20) + 16), nb.value, NULL_S) == -5
     assert L.mi_mul_mat_q8_0_workspace(k, n, R(_t([k, 0])), ctypes.byref(nb)) == 0 and nb.value == 0
     assert L.mi_mul_mat_q8_0_workspace(k, 0, R(x), ctypes.byref(nb)) == 0 and nb.value == 0
+    # the allocation-free variant: same checks, and a scratch need above the static array
+    na = L.mi_mul_mat_q8_0_noalloc
+    assert na(W, k, n, R(x), None, NULL_S) == -1
+    assert na(W, k, n, R(_t([k + 32, m])), R(y), NULL_S) == -3
+    assert na(ctypes.c_void_p(4098), k, n, R(x), R(y), NULL_S) == -5
+    big_k, big_m = 8192, 8192                                                 # 64 MiB of quantized x
+    assert L.mi_mul_mat_q8_0_workspace(big_k, 64, R(_t([big_k, big_m])), ctypes.byref(nb)) == 0
+    assert nb.value > _lib.NOALLOC_SCRATCH_BYTES
+    assert na(W, big_k, 64, R(_t([big_k, big_m])), R(_t([64, big_m])), NULL_S) == -10
+    assert L.mi_status_str(-10) == b"needs more scratch than the library's static buffer holds"
     # the norm prologue: norm_w F32 [k]
     mn = L.mi_mul_mat_q8_0_rms_norm
     nw = _t([k])
