@@ -225,6 +225,12 @@ __device__ __forceinline__ void st8(char * p, const uint2 & v) {
 #endif
 }
 
+// An optimization barrier on a register quad: its value is treated as changed,
+// so values derived from it before are recomputed after, not kept live.
+__device__ __forceinline__ void opaque(uint4 & v) {
+    asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+
 // ---------------------------------------------------------------------------
 // cross-lane reductions
 // ---------------------------------------------------------------------------

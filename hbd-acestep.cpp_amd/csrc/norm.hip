@@ -204,17 +204,25 @@ __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {
             }
         }
         __syncthreads();
+        // the R row scales in one pass (each costs ~40 instructions, the same
+        // for one lane as for all 64): lane r sums row r's wave partials, in
+        // wave order, and computes its scale; row r then reads lane r
+        float scl;
+        {
+            const int rr  = lane < R ? lane : 0;
+            acc_t     tot = 0;
+            for (int q = 0; q < nw; ++q) {
+                tot += part[it & 1][rr][q];
+            }
+            scl = rms_scale(tot, a.n, a.eps);
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t row = rbase + r;
             if (row >= a.rows) {
                 continue;
             }
-            acc_t tot = 0;
-            for (int q = 0; q < nw; ++q) {
-                tot += part[it & 1][r][q];
-            }
-            const float scale = rms_scale(tot, a.n, a.eps);
+            const float scale = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scl), r));
             char *      yp    = a.y + (int64_t) row * a.yr.s1;
 #pragma unroll
             for (int j = 0; j < C; ++j) {

@@ -79,6 +79,7 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
     constexpr int R    = 64 / L;     // head rows per batch
     constexpr int PF   = MI_ROPE_PF;
     constexpr int PL   = (HALF + 63) / 64;  // cos/sin pairs per lane
+    static_assert(PF <= L, "a round's batch scales are computed by the first PF lanes of each row group");
 
     __shared__ float tab[4][2][HALF];  // per wave: cos | sin (theta staged in the cos half)
     __shared__ float wt[2][D];         // Q and K norm weights
@@ -198,6 +199,38 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
                     ahead();
                 }
             }
+            // the round's row scales in one pass: after the row sums, lane j < PF
+            // of each L-lane group takes batch j's sum and computes its scale;
+            // batch k's rows then read lane k of their group
+            float scl = 1.0f;
+            if constexpr (NORM) {
+                sq_t<TI> mine = 0;
+#pragma unroll
+                for (int k = 0; k < PF; ++k) {
+                    float x0[VI], x1[VI];
+                    unpack16<TI>(c0[k], x0);
+                    unpack16<TI>(c1[k], x1);
+                    sq_t<TI> ss = 0;
+#pragma unroll
+                    for (int e = 0; e < VI; ++e) {
+                        ss = sq_acc<TI>(ss, x0[e]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < VI; ++e) {
+                        ss = sq_acc<TI>(ss, x1[e]);
+                    }
+                    ss   = group_sum<L>(ss);
+                    mine = j == k ? ss : mine;
+                }
+                scl = rms_scale(mine, D, a.eps);
+                // unpack again below rather than keeping the round's floats live
+                // (that costs a wave slot per SIMD)
+#pragma unroll
+                for (int k = 0; k < PF; ++k) {
+                    opaque(c0[k]);
+                    opaque(c1[k]);
+                }
+            }
 #pragma unroll
             for (int k = 0; k < PF; ++k) {
                 if (b0 + k >= it.bend) {
@@ -210,18 +243,8 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
                 unpack16<TI>(c0[k], x0);
                 unpack16<TI>(c1[k], x1);
                 if constexpr (NORM) {
-                    sq_t<TI> ss = 0;
-#pragma unroll
-                    for (int e = 0; e < VI; ++e) {
-                        ss = sq_acc<TI>(ss, x0[e]);
-                    }
-#pragma unroll
-                    for (int e = 0; e < VI; ++e) {
-                        ss = sq_acc<TI>(ss, x1[e]);
-                    }
-                    ss                = group_sum<L>(ss);
-                    const float scale = rms_scale(ss, D, a.eps);
-                    const float * w   = wt[sg];
+                    const float   scale = __shfl(scl, g * L + k, 64);
+                    const float * w     = wt[sg];
 #pragma unroll
                     for (int e = 0; e < VI; ++e) {
                         x0[e] = x0[e] * scale * w[j * VI + e];
