@@ -362,7 +362,7 @@ def _qwen3_configs():
         return tab
 
     def layer(name, dt, T, H, NH_, NKV_, I, *, clamp=False, emb_rows=0, kv=None, split_glu=False, theta=1e6,
-              pos=None):
+              pos=None, fuse_kv=False):
         """Launch list + algorithmic bytes for one Qwen3 layer at one shape."""
         from acestep_ops.device import Stream
 
@@ -409,9 +409,10 @@ def _qwen3_configs():
             add("get_rows_q8_0", lambda: ops.get_rows(ops.Q8(tab), ids, out=emb, stream=sh),
                 T * Q8_ROW(H) + T * 4 + T * H * 4)
         add("rms_norm", lambda: ops.rms_norm(h, EPS, w_in, out=norm, stream=sh), 2 * act + H * 4)
-        add("qk_norm_rope", lambda: ops.qk_norm_rope(q, qw, p, EPS, D, theta, k=k, k_w=kw, q_out=q_out, k_out=k_out,
-                                                     stream=sh),
-            2 * T * (NH_ + NKV_) * D * es + T * 4 + 2 * D * 4)
+        if not fuse_kv:
+            add("qk_norm_rope", lambda: ops.qk_norm_rope(q, qw, p, EPS, D, theta, k=k, k_w=kw, q_out=q_out,
+                                                         k_out=k_out, stream=sh),
+                2 * T * (NH_ + NKV_) * D * es + T * 4 + 2 * D * 4)
         if kv is not None:
             n_seq, T_seq, max_seq, s0 = kv
             kc = DTensor.zeros((n_seq, NKV_, max_seq, Q8_ROW(D)), "u8")
@@ -421,8 +422,16 @@ def _qwen3_configs():
             p0 = DTensor.from_numpy(np.asarray(s0, np.int32))
             keep += [kc, vc, p0]
             n_kv = n_seq * T_seq * NKV_ * D
-            add("kv_store_q8_0", lambda: ops.kv_store(kk, ops.Q8(kc), p0, v=vv, v_cache=ops.Q8(vc), stream=sh),
-                2 * (n_kv * es + n_kv // 32 * 34) + n_seq * 4)
+            if fuse_kv:
+                # QK-norm -> rope, and K/V straight into the Q8_0 caches: one launch
+                vf = qkv[:, (NH_ + NKV_) * D:].unflatten(1, (NKV_, D))
+                add("qk_norm_rope_kv_store_q8_0",
+                    lambda: ops.qk_norm_rope_kv_store(q, qw, k, kw, vf, p, EPS, D, theta, ops.Q8(kc), ops.Q8(vc), p0,
+                                                      q_out=q_out, stream=sh),
+                    2 * T * NH_ * D * es + 2 * (n_kv * es + n_kv // 32 * 34) + T * 4 + n_seq * 4 + 2 * D * 4)
+            else:
+                add("kv_store_q8_0", lambda: ops.kv_store(kk, ops.Q8(kc), p0, v=vv, v_cache=ops.Q8(vc), stream=sh),
+                    2 * (n_kv * es + n_kv // 32 * 34) + n_seq * 4)
             if T_seq > 1:
                 # dequantize the written K and V rows back (get_rows on the caches viewed as row tables)
                 rows = (np.arange(n_seq)[:, None, None] * NKV_ + np.arange(NKV_)[None, None, :]) * max_seq + \
@@ -453,8 +462,8 @@ def _qwen3_configs():
     yield lambda: layer("C1 Qwen3-0.6B layer, fp32, T=512 (split SwiGLU, Q8_0 embedding 151669x1024)", "f32", 512,
                         1024, 16, 8, 3072, emb_rows=151669, split_glu=True)
     dpos = r.integers(0, 8192, 8)
-    yield lambda: layer("C2 Qwen3-4B decode layer, bf16, batch 8 (Q8_0 KV store, 8192 slots)", "bf16", 8, 2560, 32,
-                        8, 9728, kv=(8, 1, 8192, dpos), pos=dpos)
+    yield lambda: layer("C2 Qwen3-4B decode layer, bf16, batch 8 (QK-norm/rope fused with the Q8_0 KV store, "
+                        "8192 slots)", "bf16", 8, 2560, 32, 8, 9728, kv=(8, 1, 8192, dpos), pos=dpos, fuse_kv=True)
     yield lambda: layer("C4 Qwen3-1.7B prefill layer, fp32, 4x4096 (clamp, Q8_0 embedding 151669x2048)", "f32",
                         16384, 2048, 16, 8, 6144, clamp=True, emb_rows=151669)
     s0 = r.integers(0, 6144, 8)

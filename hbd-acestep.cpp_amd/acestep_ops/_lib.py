@@ -106,6 +106,8 @@ PROTOTYPES = {
     "mi_cpy": [_TP, _TP, _VP],
     "mi_cpy_q8_0": [_TP, _TP, _I, _VP],
     "mi_kv_store": [_TP, _TP, _TP, _TP, _TP, _TP, _I, _VP, _VP],
+    "mi_qk_norm_rope_kv_store": [_TP, _TP, _TP, _TP, _TP, _TP, _TP, _F, _I, _F, _F, _F, _I, _TP, _TP, _TP, _TP, _I,
+                                 _VP, _VP],
     "mi_scale": [_TP, _F, _TP, _VP],
     "mi_timestep_embedding": [_TP, _I, _I, _TP, _VP],
     "mi_flash_attn_ext_workspace": [_TP, _TP, _TP, ctypes.POINTER(ctypes.c_size_t)],

@@ -201,6 +201,19 @@ def kv_store(k, k_cache, pos0, v=None, v_cache=None, sets=None, rounding: int = 
     _lib.call("mi_kv_store", _p(k), _p(k_cache), _p(v), _p(v_cache), _p(pos0), _p(sets), rounding, ep, _s(stream))
 
 
+def qk_norm_rope_kv_store(q, q_w, k, k_w, v, pos, eps: float, n_dims: int, freq_base: float, k_cache, v_cache,
+                          pos0, sets=None, clamp_v: bool = False, rounding: int = _lib.Q8_0_CPU_X86, freq_scale=1.0,
+                          attn_factor=1.0, q_out=None, err=None, stream=None):
+    """qk_norm_rope then kv_store in one launch: q (tokens, Nh, D) -> q_out; k, v (tokens, Nkv, D)
+    -> the caches at slots pos0[b] + t (tokens = B sequences x T)."""
+    qo = _out(q_out, q.shape, q.dtype)
+    ep = ctypes.c_void_p(err.ptr) if err is not None else None
+    _lib.call("mi_qk_norm_rope_kv_store", _p(q), _p(q_w), _p(qo), _p(k), _p(k_w), _p(v), _p(pos), eps, n_dims,
+              freq_base, freq_scale, attn_factor, int(bool(clamp_v)), _p(k_cache), _p(v_cache), _p(pos0), _p(sets),
+              rounding, ep, _s(stream))
+    return qo
+
+
 def scale(x, s: float, out=None, stream=None):
     """ggml_scale: x * s (the timestep scaling in front of the embedding, dit-graph.h:87)."""
     y = _out(out, x.shape, x.dtype)

@@ -92,12 +92,11 @@ class Qwen3DecodeLayer:
         q = qkv[:, 0:Nh * D].unflatten(1, (Nh, D))
         k = qkv[:, Nh * D:(Nh + Nkv) * D].unflatten(1, (Nkv, D))
         v = qkv[:, (Nh + Nkv) * D:qkv_dim].unflatten(1, (Nkv, D))
-        qo, ko = ops.qk_norm_rope(q, self.q_norm_w, pos, self.eps, D, self.theta, k=k, k_w=self.k_norm_w,
-                                  q_out=self._buf("qo", (N, Nh, D)), k_out=self._buf("ko", (N, Nkv, D)), stream=st)
-        if self.clamp_fp16:
-            ops.clamp(v, -FP16_MAX, FP16_MAX, out=v, stream=st)
-        ops.kv_store(ko.unflatten(0, (N, 1)), self.k_cache, pos, v=v.unflatten(0, (N, 1)), v_cache=self.v_cache,
-                     sets=sets, stream=st)
+        # QK-norm -> rope, the V clamp and the K/V cache store in one launch (the
+        # new tokens' slots are their positions)
+        qo = ops.qk_norm_rope_kv_store(q, self.q_norm_w, k, self.k_norm_w, v, pos, self.eps, D, self.theta,
+                                       self.k_cache, self.v_cache, pos, sets=sets, clamp_v=self.clamp_fp16,
+                                       q_out=self._buf("qo", (N, Nh, D)), stream=st)
         kv = self._cache_view(self.k_cache, s0, N, read_len)
         vv = self._cache_view(self.v_cache, s0, N, read_len)
         qf = qo.unflatten(1, (Nh, 1))

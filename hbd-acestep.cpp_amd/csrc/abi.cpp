@@ -615,6 +615,127 @@ int mi_kv_store(const mi_tensor * k, const mi_tensor * k_cache, const mi_tensor 
     return finish(launch_row_copy(rk, v ? &rv : nullptr, k->type, k_cache->type, rounding, (hipStream_t) stream));
 }
 
+int mi_qk_norm_rope_kv_store(const mi_tensor * q, const mi_tensor * q_w, const mi_tensor * q_out, const mi_tensor * k,
+                             const mi_tensor * k_w, const mi_tensor * v, const mi_tensor * pos, float eps, int n_dims,
+                             float freq_base, float freq_scale, float attn_factor, int clamp_v,
+                             const mi_tensor * k_cache, const mi_tensor * v_cache, const mi_tensor * pos0,
+                             const mi_tensor * sets, int rounding, int32_t * d_err, mi_stream stream) {
+    if (!q || !q_out || !k || !v || !pos || !k_cache || !v_cache || !pos0) {
+        return MI_ERR_NULL;
+    }
+    const bool norm = q_w != nullptr;
+    if ((k_w != nullptr) != norm) {
+        return MI_ERR_PARAM;
+    }
+    // Q, K as mi_qk_norm_rope (K's output shape is K's own)
+    MI_TRY(check_act(q));
+    MI_TRY(check_act(q_out));
+    MI_TRY(check_act(k));
+    MI_TRY(check_act(v));
+    if (!same_shape(*q, *q_out) || k->ne[0] != q->ne[0] || k->ne[2] != q->ne[2] || k->ne[3] != q->ne[3] ||
+        !same_shape(*k, *v)) {
+        return MI_ERR_SHAPE;
+    }
+    if (k->type != q->type || v->type != q->type || q_out->type != q->type) {
+        return MI_ERR_TYPE;
+    }
+    const int64_t D = q->ne[0];
+    if (norm) {
+        MI_TRY(check_vec(q_w, D));
+        MI_TRY(check_vec(k_w, D));
+        if (!(eps >= 0.0f) || std::isinf(eps)) {
+            return MI_ERR_PARAM;
+        }
+    }
+    MI_TRY(check(pos));
+    if (pos->type != MI_TYPE_I32) {
+        return MI_ERR_TYPE;
+    }
+    if (pos->ne[0] != q->ne[2] || pos->ne[1] != 1 || pos->ne[2] != 1 || pos->ne[3] != 1) {
+        return MI_ERR_SHAPE;
+    }
+    if (n_dims <= 0 || n_dims % 2 != 0 || n_dims > D) {
+        return MI_ERR_PARAM;
+    }
+    if (!(freq_base > 0.0f) || !std::isfinite(freq_scale) || !std::isfinite(attn_factor)) {
+        return MI_ERR_PARAM;
+    }
+    if (q->ne[2] * q->ne[3] >= kMaxRows || q->ne[1] * 256 >= kMaxRows || k->ne[1] * 256 >= kMaxRows) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    // the caches and the sequences as mi_kv_store: token t of the flat
+    // [ne2 * ne3] order belongs to sequence t / T, T = tokens / B
+    MI_TRY(check(k_cache));
+    MI_TRY(check(v_cache));
+    if (k_cache->type != MI_TYPE_Q8_0 && !is_act(k_cache->type)) {
+        return MI_ERR_TYPE;
+    }
+    if (!same_shape(*k_cache, *v_cache) || k_cache->type != v_cache->type || k_cache->nb[1] != v_cache->nb[1] ||
+        k_cache->nb[2] != v_cache->nb[2] || k_cache->nb[3] != v_cache->nb[3]) {
+        return MI_ERR_SHAPE;
+    }
+    if (k_cache->ne[0] != D || k_cache->ne[2] != k->ne[1]) {
+        return MI_ERR_SHAPE;
+    }
+    MI_TRY(check(pos0));
+    if (pos0->type != MI_TYPE_I32) {
+        return MI_ERR_TYPE;
+    }
+    const int64_t n_tok = q->ne[2] * q->ne[3];
+    const int64_t B     = pos0->ne[0];
+    if (pos0->ne[1] != 1 || pos0->ne[2] != 1 || pos0->ne[3] != 1 || B <= 0 || n_tok % B != 0) {
+        return MI_ERR_SHAPE;
+    }
+    if (sets) {
+        MI_TRY(check(sets));
+        if (sets->type != MI_TYPE_I32) {
+            return MI_ERR_TYPE;
+        }
+        if (sets->ne[0] != B || sets->ne[1] != 1 || sets->ne[2] != 1 || sets->ne[3] != 1) {
+            return MI_ERR_SHAPE;
+        }
+    }
+    if (rounding != MI_Q8_0_CPU_X86 && rounding != MI_Q8_0_REF) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(d_err, 4)) {
+        return MI_ERR_ALIGN;
+    }
+    HeadArgs a;
+    a.seg[0]      = make_seg(*q, *q_out, norm ? q_w : nullptr);
+    a.seg[1]      = make_seg(*k, *k, norm ? k_w : nullptr);  // K's destination is the cache
+    a.nseg        = 2;
+    a.ntok        = (uint32_t) n_tok;
+    a.ne2         = (uint32_t) q->ne[2];
+    a.pos         = (const int32_t *) pos->data;
+    a.theta_scale = powf(freq_base, -2.0f / (float) n_dims);  // the host libm powf, as ggml-cpu
+    a.freq_scale  = freq_scale;
+    a.mscale      = attn_factor;
+    a.eps         = eps;
+    a.ne0         = (int) D;
+    a.n_dims      = n_dims;
+    a.norm        = norm ? 1 : 0;
+    HeadKV kv;
+    kv.v       = (const char *) v->data;
+    kv.vs1     = (int64_t) v->nb[1];
+    kv.vs2     = (int64_t) v->nb[2];
+    kv.vs3     = (int64_t) v->nb[3];
+    kv.kc      = (char *) k_cache->data;
+    kv.vc      = (char *) v_cache->data;
+    kv.cnb1    = (int64_t) k_cache->nb[1];
+    kv.cnb2    = (int64_t) k_cache->nb[2];
+    kv.cnb3    = (int64_t) k_cache->nb[3];
+    kv.max_seq = k_cache->ne[1];
+    kv.n_sets  = k_cache->ne[3];
+    kv.pos0    = (const int32_t *) pos0->data;
+    kv.sets    = sets ? (const int32_t *) sets->data : nullptr;
+    kv.T       = (uint32_t) (n_tok / B);
+    kv.dT      = FastDiv(kv.T);
+    kv.clamp_v = clamp_v != 0;
+    kv.d_err   = d_err;
+    return finish(launch_heads_kv(a, kv, q->type, k_cache->type, rounding, (hipStream_t) stream));
+}
+
 // ggml_flash_attn_ext shape rules; fills the launcher's descriptor (without data pointers' workspace)
 static int fa_desc(const mi_tensor * q, const mi_tensor * k, const mi_tensor * v, const mi_tensor * mask,
                    const mi_tensor * y, FaArgs & a) {

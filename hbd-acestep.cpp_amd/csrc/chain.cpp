@@ -84,17 +84,13 @@ extern "C" int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream s) {
     return MI_OK;
 }
 
-extern "C" int mi_qwen3_layer_ops(const mi_qwen3_layer_io * io, mi_stream s) {
-    if (!io) {
-        return MI_ERR_NULL;
-    }
+// QK-norm -> rope (qwen3-lm.h:660-667) to q_out / k_out, the V clamp before
+// the cache cast (674-677, in place), then the KV store of every sequence, K
+// and V, in one launch (682-703)
+static int qwen3_rope_and_store(const mi_qwen3_layer_io * io, mi_stream s) {
     const float lim = 65504.0f;
-    // pre-attention RMSNorm (qwen3-lm.h:632)
-    MI_TRY(mi_rms_norm(&io->hidden, &io->in_norm_w, io->eps, &io->norm, s));
-    // [QKV GEMM] -> QK-norm -> rope (660-667)
     MI_TRY(mi_qk_norm_rope(&io->q, &io->q_w, &io->q_out, &io->k, &io->k_w, &io->k_out, &io->pos, io->eps,
                            io->n_dims, io->rope_freq_base, 1.0f, 1.0f, s));
-    // V clamp before the cache cast (674-677), in place
     if (io->clamp_fp16 && io->v.data) {
         MI_TRY(mi_add_clamp(&io->v, nullptr, -lim, lim, &io->v, s));
     }
@@ -109,6 +105,29 @@ extern "C" int mi_qwen3_layer_ops(const mi_qwen3_layer_io * io, mi_stream s) {
         const mi_tensor vv = io->v.data ? seq_view(io->v, B) : mi_tensor{};
         MI_TRY(mi_kv_store(&kk, &io->k_cache, io->v.data ? &vv : nullptr, io->v.data ? &io->v_cache : nullptr,
                            &io->pos0, io->sets.data ? &io->sets : nullptr, io->kv_rounding, io->d_err, s));
+    }
+    return MI_OK;
+}
+
+extern "C" int mi_qwen3_layer_ops(const mi_qwen3_layer_io * io, mi_stream s) {
+    if (!io) {
+        return MI_ERR_NULL;
+    }
+    const float lim = 65504.0f;
+    // pre-attention RMSNorm (qwen3-lm.h:632)
+    MI_TRY(mi_rms_norm(&io->hidden, &io->in_norm_w, io->eps, &io->norm, s));
+    // [QKV GEMM] -> QK-norm -> rope (660-667), V clamp (674-677) and the KV store
+    // (682-703) in one launch when the caller takes K from the cache only
+    if (io->k_cache.data && !io->k_out.data) {
+        if (!io->v.data) {
+            return MI_ERR_NULL;
+        }
+        MI_TRY(mi_qk_norm_rope_kv_store(&io->q, &io->q_w, &io->q_out, &io->k, &io->k_w, &io->v, &io->pos, io->eps,
+                                        io->n_dims,
+                                        io->rope_freq_base, 1.0f, 1.0f, io->clamp_fp16, &io->k_cache, &io->v_cache,
+                                        &io->pos0, io->sets.data ? &io->sets : nullptr, io->kv_rounding, io->d_err, s));
+    } else {
+        MI_TRY(qwen3_rope_and_store(io, s));
     }
     // [FA, O-proj] -> residual add (+ clamp) (730-733) fused with the
     // post-attention RMSNorm (736)

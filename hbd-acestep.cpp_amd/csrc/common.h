@@ -225,6 +225,34 @@ __device__ __forceinline__ void st8(char * p, const uint2 & v) {
 #endif
 }
 
+// round an fp32 value to the storage type and back (identity for F32)
+template <int T> __device__ __forceinline__ float round_to(float v) {
+    if constexpr (T == MI_TYPE_BF16) {
+        return __uint_as_float((uint32_t) f32_to_bf16_bits(v) << 16);
+    } else if constexpr (T == MI_TYPE_F16) {
+        return (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(v));
+    } else {
+        return v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 block quantizer pieces (ggml's two variants, see quant.hip)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float round_half_away(float v) {
+    const float t = __builtin_truncf(v);
+    return fabsf(v - t) >= 0.5f ? t + __builtin_copysignf(1.0f, v) : t;
+}
+
+// d = amax / 127: amax * RN(1/127) corrected by one fma, equal to the IEEE
+// quotient for every non-negative float (checked exhaustively on the host)
+__device__ __forceinline__ float div127(float amax) {
+    constexpr float C  = 1.0f / 127.0f;
+    const float     q0 = amax * C;
+    const float     r  = __builtin_fmaf(-q0, 127.0f, amax);
+    return __builtin_fmaf(r, C, q0);
+}
+
 // An optimization barrier on a register quad: its value is treated as changed,
 // so values derived from it before are recomputed after, not kept live.
 __device__ __forceinline__ void opaque(uint4 & v) {

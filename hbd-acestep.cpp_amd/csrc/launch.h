@@ -66,6 +66,27 @@ struct HeadArgs {
 // q and (optionally) k share positions and head size. Returns mi_status.
 int launch_heads(HeadArgs & a, int tin, int tout, hipStream_t s);
 
+// QK-norm -> rope of seg[0] (Q, to its y) and seg[1] (K), and V, with K and V
+// written into KV caches: flat token t (i2 + i3 * ne2) belongs to sequence
+// b = t / T at slot pos0[b] + t % T of cache set sets[b] (b when sets is null).
+struct HeadKV {
+    const char *    v;             // V rows [D, Nkv, ne2, ne3] (activation type)
+    int64_t         vs1, vs2, vs3;
+    char *          kc;            // caches [D, max_seq, Nkv, n_sets], one type
+    char *          vc;
+    int64_t         cnb1, cnb2, cnb3;
+    int64_t         max_seq, n_sets;
+    const int32_t * pos0;
+    const int32_t * sets;
+    uint32_t        T;             // tokens per sequence
+    FastDiv         dT;
+    int             clamp_v;       // V clamped to [-65504, 65504] before the cache cast
+    int32_t *       d_err;         // invalid slots or sets, counted per K and V row
+};
+// MI_ERR_UNSUPPORTED when the shapes or alignments are not the fused kernel's
+// (D in {64, 128, 256} rotated whole, 16-byte aligned rows, same in/out type).
+int launch_heads_kv(HeadArgs & a, const HeadKV & kv, int tin, int tcache, int rounding, hipStream_t s);
+
 // ---- glu.hip ---------------------------------------------------------------
 int launch_swiglu(const char * g, const char * u, int64_t gs, int64_t us, int tin, char * y, int64_t ys, int tout,
                   int64_t rows, int64_t n, bool vec_ok, hipStream_t s);

@@ -48,16 +48,6 @@ struct NormArgs {
 #define MI_NORM_R 4  // rows per workgroup iteration when each thread owns one vector
 #endif
 
-// round an fp32 value to the storage type and back (identity for F32)
-template <int T> __device__ __forceinline__ float round_to(float v) {
-    if constexpr (T == MI_TYPE_BF16) {
-        return __uint_as_float((uint32_t) f32_to_bf16_bits(v) << 16);
-    } else if constexpr (T == MI_TYPE_F16) {
-        return (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(v));
-    } else {
-        return v;
-    }
-}
 
 template <int TI, int TO, int MODE, int ADD, int C, int R>
 __global__ void __launch_bounds__(512) k_rms_rows(const NormArgs a) {

@@ -27,10 +27,6 @@
 
 namespace mi {
 
-__device__ __forceinline__ float round_half_away(float v) {
-    const float t = __builtin_truncf(v);
-    return fabsf(v - t) >= 0.5f ? t + __builtin_copysignf(1.0f, v) : t;
-}
 
 // 8 consecutive source elements (32 bytes of F32, 16 of BF16/F16), 16-byte aligned
 template <int TI> __device__ __forceinline__ void load8(const char * p, float * f) {
@@ -97,13 +93,6 @@ __device__ __forceinline__ void row_ptrs(const RowCopy & R, uint32_t w, const ch
     dst                = R.dst + slot * R.cnb1 + (int64_t) i1 * R.cnb2 + set * R.cnb3;
 }
 
-// d = amax / 127 (see the header: equal to the IEEE quotient)
-__device__ __forceinline__ float div127(float amax) {
-    constexpr float C  = 1.0f / 127.0f;
-    const float     q0 = amax * C;
-    const float     r  = __builtin_fmaf(-q0, 127.0f, amax);
-    return __builtin_fmaf(r, C, q0);
-}
 
 template <int TI, int ROUND>
 __global__ void __launch_bounds__(256) k_row_q8(const RowCopy K, const RowCopy V, uint32_t nbk, uint32_t total,

@@ -498,3 +498,313 @@ int launch_heads(HeadArgs & a, int tin, int tout, hipStream_t s) {
 }
 
 }  // namespace mi
+
+// ---------------------------------------------------------------------------
+// QK-norm -> rope fused with the KV-cache store (decode: qwen3-lm.h:660-703).
+// One wave per (token, batch of R head rows) over the Q, K and V batches of
+// every token, with k_heads' lane layout and arithmetic (the same VI-element
+// chunks per lane, the same row sums and group reduction, the same theta chain
+// and sincos_rot), so Q equals mi_qk_norm_rope's output bit for bit and the
+// cache holds what mi_kv_store writes from it. K is rounded to the activation
+// type before the cache cast, as the separate ops store and reload it; V is
+// clamped first when asked (qwen3-lm.h:674-677). Q8_0 caches: a 32-element
+// block spans 32 / VI lanes of a row; they share the block's amax (DPP max),
+// each writes its VI quants (2-byte aligned) and the first the fp16 scale.
+namespace mi {
+
+template <int TI, int TC, int D, int ROUND>
+__global__ void __launch_bounds__(256) k_heads_kv(const HeadArgs a, const HeadKV kv, uint32_t nbq, uint32_t nbk,
+                                                  FastDiv dnbt) {
+    constexpr int VI   = TT<TI>::VEC;
+    constexpr int EI   = TT<TI>::ES;
+    constexpr int HALF = D / 2;
+    constexpr int L    = HALF / VI;  // lanes per head row
+    constexpr int R    = 64 / L;     // head rows per batch
+    constexpr int PL   = (HALF + 63) / 64;
+    constexpr int LPB  = 32 / VI;    // lanes per Q8_0 block
+
+    __shared__ float tab[4][2][HALF];
+
+    const int      lane = threadIdx.x & 63;
+    const uint32_t wv   = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int      j    = lane % L;
+    const int      g    = lane / L;
+    const uint32_t item = blockIdx.x * 4 + wv;
+    if (item >= a.ntok * dnbt.d) {
+        return;  // whole wave
+    }
+    const uint32_t tok = dnbt.div(item);
+    const uint32_t bt  = item - tok * dnbt.d;
+    const int      sg  = bt < nbq ? 0 : (bt < nbq + nbk ? 1 : 2);  // Q, K, V: wave-uniform
+    const uint32_t h   = (bt - (sg == 0 ? 0u : sg == 1 ? nbq : nbq + nbk)) * R + g;
+    const uint32_t i3  = a.dne2.div(tok);
+    const uint32_t i2  = tok - i3 * a.ne2;
+    const HeadSeg & S  = a.seg[sg == 0 ? 0 : 1];
+    const bool     ok  = h < S.heads;  // V has K's heads
+
+    const char * xp = sg == 2 ? kv.v + (int64_t) i3 * kv.vs3 + (int64_t) i2 * kv.vs2 + (int64_t) h * kv.vs1
+                              : S.x + (int64_t) i3 * S.xs3 + (int64_t) i2 * S.xs2 + (int64_t) h * S.xs1;
+    uint4 c0 = make_uint4(0, 0, 0, 0), c1 = make_uint4(0, 0, 0, 0);
+    if (ok) {
+        c0 = ld16(xp + (size_t) (j * VI) * EI);
+        c1 = ld16(xp + (size_t) (HALF + j * VI) * EI);
+    }
+    float x0[VI], x1[VI];
+    unpack16<TI>(c0, x0);
+    unpack16<TI>(c1, x1);
+
+    if (sg < 2) {
+        float cv[VI], sv[VI];
+        if (a.pos) {
+            float *     ct = tab[wv][0];
+            float *     st = tab[wv][1];
+            const float p  = (float) a.pos[i2];
+            if (lane == 0) {
+                float th = p;
+                ct[0]    = th;
+                for (int i = 1; i < HALF; ++i) {
+                    th    = th * a.theta_scale;
+                    ct[i] = th;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            float th[PL];
+#pragma unroll
+            for (int q = 0; q < PL; ++q) {
+                th[q] = lane + 64 * q < HALF ? ct[lane + 64 * q] : 0.0f;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int q = 0; q < PL; ++q) {
+                if (lane + 64 * q < HALF) {
+                    float sn, cs;
+                    sincos_rot(a.freq_scale * th[q], &sn, &cs);
+                    ct[lane + 64 * q] = cs * a.mscale;
+                    st[lane + 64 * q] = sn * a.mscale;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int e = 0; e < VI; ++e) {
+                cv[e] = ct[j * VI + e];
+                sv[e] = st[j * VI + e];
+            }
+        }
+        if (a.norm) {
+            sq_t<TI> ss = 0;
+#pragma unroll
+            for (int e = 0; e < VI; ++e) {
+                ss = sq_acc<TI>(ss, x0[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < VI; ++e) {
+                ss = sq_acc<TI>(ss, x1[e]);
+            }
+            ss                = group_sum<L>(ss);
+            const float scale = rms_scale(ss, D, a.eps);
+            if (S.w) {
+#pragma unroll
+                for (int e = 0; e < VI; ++e) {
+                    x0[e] = x0[e] * scale * S.w[j * VI + e];
+                    x1[e] = x1[e] * scale * S.w[HALF + j * VI + e];
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < VI; ++e) {
+                    x0[e] = x0[e] * scale;
+                    x1[e] = x1[e] * scale;
+                }
+            }
+        }
+        if (a.pos) {
+#pragma unroll
+            for (int e = 0; e < VI; ++e) {
+                const float a0  = x0[e] * cv[e];
+                const float b0_ = x1[e] * sv[e];
+                const float a1  = x0[e] * sv[e];
+                const float b1  = x1[e] * cv[e];
+                x0[e]           = a0 - b0_;
+                x1[e]           = a1 + b1;
+            }
+        }
+        if (sg == 0) {
+            if (ok) {
+                char * yp = S.y + (int64_t) i3 * S.ys3 + (int64_t) i2 * S.ys2 + (int64_t) h * S.ys1;
+                store_vec<TI, VI>(yp + (size_t) (j * VI) * EI, x0);
+                store_vec<TI, VI>(yp + (size_t) (HALF + j * VI) * EI, x1);
+            }
+            return;
+        }
+    } else if (kv.clamp_v) {
+#pragma unroll
+        for (int e = 0; e < VI; ++e) {
+            const float c0_ = x0[e] < 65504.0f ? x0[e] : 65504.0f;
+            const float c1_ = x1[e] < 65504.0f ? x1[e] : 65504.0f;
+            x0[e]           = c0_ > -65504.0f ? c0_ : -65504.0f;
+            x1[e]           = c1_ > -65504.0f ? c1_ : -65504.0f;
+        }
+    }
+    // K or V to the cache, from the value the activation type holds
+#pragma unroll
+    for (int e = 0; e < VI; ++e) {
+        x0[e] = round_to<TI>(x0[e]);
+        x1[e] = round_to<TI>(x1[e]);
+    }
+    const uint32_t b    = kv.dT.div(tok);
+    const int64_t  slot = (int64_t) kv.pos0[b] + (tok - b * kv.T);
+    const int64_t  set  = kv.sets ? (int64_t) kv.sets[b] : (int64_t) b;
+    if (slot < 0 || slot >= kv.max_seq || set < 0 || set >= kv.n_sets) {
+        if (ok && j == 0 && kv.d_err) {
+            atomicAdd(kv.d_err, 1);
+        }
+        return;
+    }
+    char * crow = (sg == 1 ? kv.kc : kv.vc) + slot * kv.cnb1 + (int64_t) h * kv.cnb2 + set * kv.cnb3;
+    if constexpr (TC == MI_TYPE_Q8_0) {
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+            const float * f    = part ? x1 : x0;
+            const int     el   = (part ? HALF : 0) + j * VI;  // first element of this lane's chunk
+            float         amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < VI; ++e) {
+                amax = fmaxf(amax, fabsf(f[e]));
+            }
+            amax          = group_max<LPB>(amax);
+            const float d = div127(amax);
+            float       id;
+            if constexpr (ROUND == MI_Q8_0_REF) {
+                id = d != 0.0f ? 1.0f / d : 0.0f;
+            } else {
+                id = amax != 0.0f ? 127.0f / amax : 0.0f;
+            }
+            uint32_t wq[VI / 4];
+#pragma unroll
+            for (int q = 0; q < VI / 4; ++q) {
+                uint32_t acc = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v = f[4 * q + e] * id;
+                    float       r;
+                    if constexpr (ROUND == MI_Q8_0_REF) {
+                        r = round_half_away(v);
+                    } else {
+                        r = __builtin_amdgcn_fmed3f(__builtin_rintf(v), -128.0f, 127.0f);
+                    }
+                    acc |= ((uint32_t) (int32_t) r & 0xffu) << (8 * e);
+                }
+                wq[q] = acc;
+            }
+            if (ok) {
+                char *     bp = crow + (size_t) (el / 32) * 34;
+                uint16_t * qp = (uint16_t *) (bp + 2 + el % 32);
+#pragma unroll
+                for (int q = 0; q < VI / 4; ++q) {
+                    qp[2 * q]     = (uint16_t) (wq[q] & 0xffffu);
+                    qp[2 * q + 1] = (uint16_t) (wq[q] >> 16);
+                }
+                if (el % 32 == 0) {
+                    *(uint16_t *) bp = f32_to_f16_bits(d);
+                }
+            }
+        }
+    } else {
+        constexpr int EC = TT<TC>::ES;
+        if (ok) {
+            store_vec<TC, VI>(crow + (size_t) (j * VI) * EC, x0);
+            store_vec<TC, VI>(crow + (size_t) (HALF + j * VI) * EC, x1);
+        }
+    }
+}
+
+template <int TI, int TC, int D>
+static void launch_kv_d(const HeadArgs & a, const HeadKV & kv, int rounding, uint32_t nbq, uint32_t nbk,
+                        uint32_t nbt, hipStream_t s) {
+    const uint64_t waves = (uint64_t) a.ntok * nbt;
+    const dim3     grid((uint32_t) ((waves + 3) / 4));
+    if constexpr (TC == MI_TYPE_Q8_0) {
+        if (rounding == MI_Q8_0_REF) {
+            hipLaunchKernelGGL((k_heads_kv<TI, TC, D, MI_Q8_0_REF>), grid, dim3(256), 0, s, a, kv, nbq, nbk,
+                               FastDiv(nbt));
+            return;
+        }
+    }
+    hipLaunchKernelGGL((k_heads_kv<TI, TC, D, MI_Q8_0_CPU_X86>), grid, dim3(256), 0, s, a, kv, nbq, nbk, FastDiv(nbt));
+}
+
+template <int TI, int TC>
+static int launch_kv_t(const HeadArgs & a, const HeadKV & kv, int rounding, hipStream_t s) {
+    const int      VI  = TT<TI>::VEC;
+    const int      L   = a.ne0 / 2 / VI;
+    const uint32_t R   = (uint32_t) (64 / L);
+    const uint32_t nbq = (a.seg[0].heads + R - 1) / R;
+    const uint32_t nbk = (a.seg[1].heads + R - 1) / R;
+    const uint32_t nbt = nbq + 2 * nbk;
+    switch (a.ne0) {
+        case 64:
+            launch_kv_d<TI, TC, 64>(a, kv, rounding, nbq, nbk, nbt, s);
+            return MI_OK;
+        case 128:
+            launch_kv_d<TI, TC, 128>(a, kv, rounding, nbq, nbk, nbt, s);
+            return MI_OK;
+        case 256:
+            launch_kv_d<TI, TC, 256>(a, kv, rounding, nbq, nbk, nbt, s);
+            return MI_OK;
+        default:
+            return MI_ERR_UNSUPPORTED;
+    }
+}
+
+template <int TI>
+static int launch_kv_c(const HeadArgs & a, const HeadKV & kv, int tcache, int rounding, hipStream_t s) {
+    switch (tcache) {
+        case MI_TYPE_Q8_0:
+            return launch_kv_t<TI, MI_TYPE_Q8_0>(a, kv, rounding, s);
+        case MI_TYPE_F16:
+            return launch_kv_t<TI, MI_TYPE_F16>(a, kv, rounding, s);
+        case MI_TYPE_BF16:
+            return launch_kv_t<TI, MI_TYPE_BF16>(a, kv, rounding, s);
+        case MI_TYPE_F32:
+            return launch_kv_t<TI, MI_TYPE_F32>(a, kv, rounding, s);
+        default:
+            return MI_ERR_TYPE;
+    }
+}
+
+int launch_heads_kv(HeadArgs & a, const HeadKV & kv, int tin, int tcache, int rounding, hipStream_t s) {
+    if (a.ntok == 0) {
+        return MI_OK;
+    }
+    a.dne2 = FastDiv(a.ne2);
+    // the k_heads fast-path layout: whole rotation (or none), 16-byte rows
+    bool fast = (a.pos == nullptr || a.n_dims == a.ne0) && (a.ne0 == 64 || a.ne0 == 128 || a.ne0 == 256) &&
+                (uint64_t) a.ntok * (a.seg[0].heads + 2ull * a.seg[1].heads) < (1ull << 31);
+    for (int i = 0; i < 2 && fast; ++i) {
+        const HeadSeg & S = a.seg[i];
+        fast = aligned(S.x, 16) && S.xs1 % 16 == 0 && S.xs2 % 16 == 0 && S.xs3 % 16 == 0 && (!S.w || aligned(S.w, 16));
+    }
+    const HeadSeg & Q = a.seg[0];
+    fast = fast && aligned(Q.y, 16) && Q.ys1 % 16 == 0 && Q.ys2 % 16 == 0 && Q.ys3 % 16 == 0;
+    fast = fast && aligned(kv.v, 16) && kv.vs1 % 16 == 0 && kv.vs2 % 16 == 0 && kv.vs3 % 16 == 0;
+    // cache rows: 16-byte vectors for F16/BF16/F32 (half a row for F32 of D = 64 is 128 bytes);
+    // Q8_0 rows are 2-byte aligned blocks
+    const size_t ca = tcache == MI_TYPE_Q8_0 ? 2 : 16;
+    fast = fast && aligned(kv.kc, ca) && aligned(kv.vc, ca) && kv.cnb1 % ca == 0 && kv.cnb2 % ca == 0 &&
+           kv.cnb3 % ca == 0;
+    if (!fast) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    switch (tin) {
+        case MI_TYPE_F32:
+            return launch_kv_c<MI_TYPE_F32>(a, kv, tcache, rounding, s);
+        case MI_TYPE_BF16:
+            return launch_kv_c<MI_TYPE_BF16>(a, kv, tcache, rounding, s);
+        default:
+            return launch_kv_c<MI_TYPE_F16>(a, kv, tcache, rounding, s);
+    }
+}
+
+}  // namespace mi

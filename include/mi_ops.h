@@ -196,6 +196,27 @@ int mi_cpy_q8_0(const mi_tensor * src, const mi_tensor * dst, int rounding, mi_s
 int mi_kv_store(const mi_tensor * k, const mi_tensor * k_cache, const mi_tensor * v, const mi_tensor * v_cache,
                 const mi_tensor * pos0, const mi_tensor * sets, int rounding, int32_t * d_err, mi_stream stream);
 
+/* QK-norm -> NEOX rope and the KV-cache store as one launch, replacing a
+ * decode step's q/k norms, ropes, V clamp and per-sequence ggml_cpy nodes
+ * (qwen3-lm.h:660-703). Equal, bit for bit, to mi_qk_norm_rope(q, q_w, q_out,
+ * k, k_w, k_out, pos, ...), then (clamp_v) mi_add_clamp(v, NULL, -65504,
+ * 65504, v), then mi_kv_store of k_out and v viewed as B = pos0.ne[0]
+ * sequences of tokens / B tokens each (token t of the flat ne2 * ne3 order is
+ * token t % T of sequence t / T): the roped K never goes to memory and V is
+ * not modified.
+ *   q, q_out: [D, Nh, ne2, ne3]; k, v: [D, Nkv, ne2, ne3]; one activation type
+ *   q_w, k_w: F32 [D] or both NULL (rope only); pos: I32 [ne2]
+ *   k_cache, v_cache: [D, max_seq, Nkv, n_sets], one type (Q8_0/F16/BF16/F32)
+ *   pos0, sets, rounding, d_err: as mi_kv_store
+ * Needs D in {64, 128, 256} rotated whole (n_dims == D) and 16-byte aligned
+ * q/k/v/q_out rows (2-byte for Q8_0 caches, 16-byte otherwise); other
+ * layouts return MI_ERR_UNSUPPORTED (use the three calls). */
+int mi_qk_norm_rope_kv_store(const mi_tensor * q, const mi_tensor * q_w, const mi_tensor * q_out, const mi_tensor * k,
+                             const mi_tensor * k_w, const mi_tensor * v, const mi_tensor * pos, float eps, int n_dims,
+                             float freq_base, float freq_scale, float attn_factor, int clamp_v,
+                             const mi_tensor * k_cache, const mi_tensor * v_cache, const mi_tensor * pos0,
+                             const mi_tensor * sets, int rounding, int32_t * d_err, mi_stream stream);
+
 /* ggml_scale(x, s): y = x * s, one fp32 multiply per element (the result
  * rounded to y's type). Replaces the timestep scaling ggml_scale(t, 1000) in
  * front of the embedding (dit-graph.h:87). x, y: activations of one shape
@@ -468,6 +489,9 @@ int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream stream);
  *   norm   = rms_norm(hidden) * in_norm_w
  *   q/k    = qk_norm_rope(q, k)                [views of the QKV GEMM output]
  *   (clamp v in place when clamp_fp16), kv_store(k_out, v -> caches at pos0/sets)
+ *     (with a cache and k_out.data NULL these are one mi_qk_norm_rope_kv_store
+ *     launch instead: K goes only to the cache, and v is left unclamped in
+ *     place; the cache gets the clamped values either way)
  *   hidden = hidden + attn_out   (clamped to +-65504 when clamp_fp16), fused with
  *   norm2  = rms_norm(hidden) * post_norm_w
  *   ff     = swiglu(gate_up)

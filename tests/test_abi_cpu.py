@@ -150,6 +150,38 @@ def test_q8_get_rows_kv_validation():
     assert L.mi_timestep_embedding(R(_t([4])), 256, 10000, R(_t([256, 5])), NULL_S) == -3
 
 
+def test_qk_norm_rope_kv_store_validation():
+    D, Nh, Nkv, n_tok = 128, 32, 8, 8
+    q, qo = _t([D, Nh, n_tok], BF16), _t([D, Nh, n_tok], BF16)
+    k, v = _t([D, Nkv, n_tok], BF16), _t([D, Nkv, n_tok], BF16)
+    w, pos, pos0 = _t([D]), _t([n_tok], I32), _t([8], I32)
+    kc, vc = _t([D, 512, Nkv, 8], Q8_0), _t([D, 512, Nkv, 8], Q8_0)
+    f = L.mi_qk_norm_rope_kv_store
+
+    def call(q=q, qw=w, qo=qo, k=k, kw=w, v=v, pos=pos, n_dims=D, kc=kc, vc=vc, pos0=pos0, sets=None, rounding=0,
+             err=None):
+        return f(R(q) if q else None, R(qw) if qw else None, R(qo) if qo else None, R(k) if k else None,
+                 R(kw) if kw else None, R(v) if v else None, R(pos) if pos else None, 1e-6, n_dims, 1e6, 1.0, 1.0, 0,
+                 R(kc) if kc else None, R(vc) if vc else None, R(pos0) if pos0 else None, R(sets) if sets else None,
+                 rounding, err, NULL_S)
+
+    assert call(v=None) == -1
+    assert call(kc=None) == -1
+    assert call(kw=None) == -6                                   # one norm weight without the other
+    assert call(v=_t([D, Nkv, n_tok + 1], BF16)) == -3
+    assert call(v=_t([D, Nkv, n_tok])) == -2                      # V of another type
+    assert call(qo=_t([D, Nh, n_tok])) == -2                      # q_out of another type
+    assert call(pos=_t([n_tok + 1], I32)) == -3
+    assert call(n_dims=3) == -6
+    assert call(vc=_t([D, 512, Nkv, 8], 1)) == -3                 # caches of different types
+    assert call(kc=_t([D, 512, Nkv + 1, 8], Q8_0), vc=_t([D, 512, Nkv + 1, 8], Q8_0)) == -3
+    assert call(pos0=_t([3], I32)) == -3                          # 8 tokens are not 3 sequences
+    assert call(sets=_t([8])) == -2
+    assert call(rounding=5) == -6
+    assert call(err=ctypes.c_void_p(4098)) == -5
+    assert call(n_dims=64) == -7                                  # partial rotation: the three calls
+
+
 def test_flash_attn_validation():
     D, n_q, Nh, N, n_kv, Nkv = 128, 1, 32, 8, 256, 8
     q = _t([D, n_q, Nh, N])

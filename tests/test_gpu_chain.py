@@ -174,3 +174,55 @@ def test_qwen3_layer_chain_decode(dev, dt):
     for b in range(N):
         assert np.array_equal(kch[b, :, pos[b]], kq[b])
         assert np.array_equal(vch[b, :, pos[b]], vq[b])
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_qwen3_layer_fused_kv_path(dev, dt):
+    """The driver with k_out empty (QK-norm, rope, V clamp and KV store as one
+    mi_qk_norm_rope_kv_store launch) against the driver with k_out (the three
+    calls), same inputs: every output and both caches bit-identical; V is left
+    as it was on the fused path."""
+    print(f"qwen3 layer fused kv path {dt}", flush=True)
+    H, nh, nkv, D, I, N, max_seq = 2560, 32, 8, 128, 9728, 8, 8192
+    r = rng(5)
+    act = dt
+    mk = lambda a: DTensor.from_numpy(orc.f32_to_bf16(a), "bf16") if dt == "bf16" else DTensor.from_numpy(a)  # noqa
+    qkv0 = randn((N, (nh + 2 * nkv) * D), seed=12)
+    qkv0[2, (nh + nkv) * D + 5] = -9e4
+    consts = [to_dev(a, dev) for a in (randn((H,), seed=16, scale=0.1, mean=1.0), randn((H,), seed=17, scale=0.1,
+              mean=1.0), randn((D,), seed=18, scale=0.1, mean=1.0), randn((D,), seed=19, scale=0.1, mean=1.0),
+              r.integers(0, max_seq, N).astype(np.int32), np.arange(N, dtype=np.int32))]
+    ins = [mk(randn((N, H), seed=13)), mk(randn((N, 2 * I), seed=14)), mk(randn((N, H), seed=15))]
+    res = []
+    for fused in (False, True):
+        hd, qkvd = mk(randn((N, H), seed=11)), mk(qkv0)
+        qd = qkvd[:, :nh * D].unflatten(1, (nh, D))
+        kd = qkvd[:, nh * D:(nh + nkv) * D].unflatten(1, (nkv, D))
+        vd = qkvd[:, (nh + nkv) * D:].unflatten(1, (nkv, D))
+        rb = D // 32 * 34
+        kc, vc = DTensor.zeros((N, nkv, max_seq, rb), "u8"), DTensor.zeros((N, nkv, max_seq, rb), "u8")
+        outs = dict(norm=DTensor.empty((N, H), act), norm2=DTensor.empty((N, H), act),
+                    q_out=DTensor.empty((N, nh, D), act), ff=DTensor.empty((N, I), act))
+        k_out = DTensor.empty((N, nkv, D), act)
+        io = _lib.MiQwen3LayerIO()
+        io.hidden, io.in_norm_w, io.post_norm_w = ops.desc(hd), ops.desc(consts[0]), ops.desc(consts[1])
+        io.norm, io.norm2 = ops.desc(outs["norm"]), ops.desc(outs["norm2"])
+        io.q, io.k, io.v = ops.desc(qd), ops.desc(kd), ops.desc(vd)
+        io.q_w, io.k_w, io.q_out, io.pos = (ops.desc(consts[2]), ops.desc(consts[3]), ops.desc(outs["q_out"]),
+                                            ops.desc(consts[4]))
+        if not fused:
+            io.k_out = ops.desc(k_out)
+        io.k_cache, io.v_cache = ops.desc(ops.Q8(kc)), ops.desc(ops.Q8(vc))
+        io.pos0, io.sets = ops.desc(consts[4]), ops.desc(consts[5])
+        io.attn_out, io.gate_up, io.ff, io.mlp_out = (ops.desc(ins[0]), ops.desc(ins[1]), ops.desc(outs["ff"]),
+                                                      ops.desc(ins[2]))
+        io.eps, io.rope_freq_base, io.n_dims, io.clamp_fp16, io.kv_rounding = EPS, 1e6, D, 1, _lib.Q8_0_CPU_X86
+        _lib.call("mi_qwen3_layer_ops", ctypes.byref(io), None)
+        device.synchronize()
+        res.append({**{k: to_np(v) for k, v in outs.items()}, "hidden": to_np(hd), "kc": to_np(kc),
+                    "vc": to_np(vc), "v": to_np(vd)})
+    a, b = res
+    for name in ("norm", "norm2", "q_out", "ff", "hidden", "kc", "vc"):
+        assert np.array_equal(a[name], b[name]), name
+    v0 = to_np(mk(qkv0)[:, (nh + nkv) * D:].unflatten(1, (nkv, D)))
+    assert np.array_equal(b["v"], v0) and not np.array_equal(a["v"], v0)  # only the three calls clamp V in place

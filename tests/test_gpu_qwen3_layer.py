@@ -7,15 +7,18 @@ product, residual add) against the oracle, stage by stage
 Every stage is checked against the oracle applied to the device's own inputs
 of that stage (read back from the layer's buffers), at that op's own bar:
   norm -> QKV product            Q8_0 product bound (the x quantization exact)
-  QK-norm -> rope                1e-5, row floor
-  cache slots (K and V)          bit-exact: Q8_0 of the device's k_out and V,
+  QK-norm -> rope                1e-5, row floor (the layer writes K only to the
+                                 cache, in the same launch; the device's roped K
+                                 is recomputed from its QKV buffer by
+                                 mi_qk_norm_rope, which that launch equals)
+  cache slots (K and V)          bit-exact: Q8_0 of the device's roped K and V,
                                  or their fp16 values
   attention                      the kernels' derived bound (tests/fa_bound.py)
   O product, gate/up, down       Q8_0 product bound
   residual sums                  bit-exact (clamped to +-65504 with clamp_fp16)
 With clamp_fp16 (qwen3-lm.h:53) the layer clamps V before the cache store
-(674-677) and both residual sums (730-733, 738-741): the case drives V and the
-hidden state past the fp16 range."""
+(674-677; the QKV buffer keeps the product) and both residual sums (730-733,
+738-741): the case drives V and the hidden state past the fp16 range."""
 import numpy as np
 import pytest
 from fa_bound import fa_bound
@@ -69,37 +72,36 @@ def test_decode_layer_stage_by_stage(dev, kv_type, clamp):
     y = to_np(layer.forward(to_dev(hidden), to_dev(pos), to_dev(sets), s0, read_len, decode_mask(pos, read_len)))
     b = {k: to_np(v) for k, v in layer._bufs.items() if not k.startswith("ws")}
 
-    # 1. input norm -> QKV product (one call); V then clamped in place when clamp_fp16
+    # 1. input norm -> QKV product (one call)
     qkv = b["qkv"]
-    qkv_pre = qkv.copy()
     v_cols = slice((Nh + Nkv) * D, (Nh + 2 * Nkv) * D)
     norm = orc.rms_norm_mul(hidden, nw_in, eps)
-    if clamp:
-        # V values at +-65504 are exactly those whose product lies past the range;
-        # the others are the product itself (checked with the rest below)
-        vd = qkv[:, v_cols]
-        vref = orc.mul_mat_q8_0(Wqkv, norm)[:, v_cols]
-        at_lim = np.abs(vd) == LIM
-        assert at_lim.sum() > vd.size // 4 and np.all(np.abs(vd) <= LIM)
-        assert np.all(np.sign(vd[at_lim]) == np.sign(vref[at_lim]))
-        assert np.all(np.abs(vref[at_lim]) >= LIM * (1 - 1e-5)) and np.all(np.abs(vref[~at_lim]) <= LIM * (1 + 1e-5))
-        qkv_pre[:, v_cols] = np.where(at_lim, vref, vd)
-    assert_mul_mat_q8_0(qkv_pre, Wqkv, norm)
-    # 2. QK-norm -> rope on the device's q, k
+    assert_mul_mat_q8_0(qkv, Wqkv, norm)
+    # 2. QK-norm -> rope on the device's q, k. The layer writes K only to the
+    # cache (one launch with the store, bit-identical to mi_qk_norm_rope then
+    # mi_kv_store); the device's roped K is mi_qk_norm_rope on the same buffer.
     q = qkv[:, :Nh * D].reshape(N, Nh, D)
     k = qkv[:, Nh * D:(Nh + Nkv) * D].reshape(N, Nkv, D)
     v = qkv[:, v_cols].reshape(N, Nkv, D)
+    dq = layer._bufs["qkv"]
+    _, ko = ops.qk_norm_rope(dq[:, :Nh * D].unflatten(1, (Nh, D)), to_dev(qn), to_dev(pos), eps, D, theta,
+                             k=dq[:, Nh * D:(Nh + Nkv) * D].unflatten(1, (Nkv, D)), k_w=to_dev(kn))
+    ko = to_np(ko)
     assert_f32_close(b["qo"], orc.qk_norm_rope(q, qn, pos, eps, D, theta), row_floor=True)
-    assert_f32_close(b["ko"], orc.qk_norm_rope(k, kn, pos, eps, D, theta), row_floor=True)
-    # 3. the written cache slots: the device's own k_out and (clamped) V, bit-exact
+    assert_f32_close(ko, orc.qk_norm_rope(k, kn, pos, eps, D, theta), row_floor=True)
+    if clamp:
+        # V past the fp16 range for most tokens; the cache gets it clamped (674-677)
+        assert (np.abs(v) > LIM).sum() > v.size // 4
+        v = orc.clamp(v, -LIM, LIM)
+    # 3. the written cache slots: the device's roped K and (clamped) V, bit-exact
     if kv_type == "q8_0":
         kdev = to_np(layer.k_cache.data)
         vdev = to_np(layer.v_cache.data)
-        kw, vw = orc.quantize_q8_0(b["ko"], "x86"), orc.quantize_q8_0(v, "x86")
+        kw, vw = orc.quantize_q8_0(ko, "x86"), orc.quantize_q8_0(v, "x86")
         kcache, vcache = orc.dequantize_q8_0(kdev), orc.dequantize_q8_0(vdev)
     else:
         kdev, vdev = to_np(layer.k_cache), to_np(layer.v_cache)
-        kw, vw = orc.f32_to_f16(b["ko"]), orc.f32_to_f16(v)
+        kw, vw = orc.f32_to_f16(ko), orc.f32_to_f16(v)
         kcache, vcache = orc.f16_to_f32(kdev), orc.f16_to_f32(vdev)
     for i in range(N):
         assert np.array_equal(kdev[s0 + i, :, pos[i]], kw[i])
