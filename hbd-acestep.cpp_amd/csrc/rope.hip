@@ -389,8 +389,28 @@ static void launch_persistent(uint64_t items, hipStream_t s, Args... args) {
     hipLaunchKernelGGL(kernel, dim3((uint32_t) grid), dim3(256), 0, s, args...);
 }
 
+template <int TI, int TC, int D, int ROUND, bool TOCACHE>
+__global__ void k_heads_kv(const HeadArgs a, const HeadKV kv, uint32_t nbq, uint32_t nbk, FastDiv dnbt);
+
 template <int TI, int TO, int D>
 static void launch_fast(const HeadArgs & a, hipStream_t s) {
+    {
+        // Tokens with more head batches than one load round (F32 rows: Qwen3's
+        // 16 + 8 or 32 + 8 heads of 128 are 6 or 10 batches of 4 rows) take the
+        // one-shot kernel, a wave per (token, batch) with its own cos/sin: the
+        // persistent kernel would walk those batches in several dependent rounds.
+        constexpr int  L   = D / 2 / TT<TI>::VEC;
+        constexpr int  R   = 64 / L;
+        const uint32_t nbq = (a.seg[0].heads + R - 1) / R;
+        const uint32_t nbk = a.nseg > 1 ? (a.seg[1].heads + R - 1) / R : 0u;
+        if (nbq + nbk > (uint32_t) MI_ROPE_PF) {
+            const uint64_t waves = (uint64_t) a.ntok * (nbq + nbk);
+            HeadKV         kv{};
+            hipLaunchKernelGGL((k_heads_kv<TI, TI, D, 0, false>), dim3((uint32_t) ((waves + 3) / 4)), dim3(256), 0,
+                               s, a, kv, nbq, nbk, FastDiv(nbq + nbk));
+            return;
+        }
+    }
     constexpr int  L   = D / 2 / TT<TI>::VEC;
     constexpr int  R   = 64 / L;
     const uint32_t h0  = a.seg[0].heads;
@@ -500,7 +520,9 @@ int launch_heads(HeadArgs & a, int tin, int tout, hipStream_t s) {
 }  // namespace mi
 
 // ---------------------------------------------------------------------------
-// QK-norm -> rope fused with the KV-cache store (decode: qwen3-lm.h:660-703).
+// QK-norm -> rope fused with the KV-cache store (decode: qwen3-lm.h:660-703);
+// with TOCACHE false, the one-shot form of the plain QK-norm -> rope (K to its
+// output like Q, no V batches).
 // One wave per (token, batch of R head rows) over the Q, K and V batches of
 // every token, with k_heads' lane layout and arithmetic (the same VI-element
 // chunks per lane, the same row sums and group reduction, the same theta chain
@@ -512,7 +534,7 @@ int launch_heads(HeadArgs & a, int tin, int tout, hipStream_t s) {
 // each writes its VI quants (2-byte aligned) and the first the fp16 scale.
 namespace mi {
 
-template <int TI, int TC, int D, int ROUND>
+template <int TI, int TC, int D, int ROUND, bool TOCACHE = true>
 __global__ void __launch_bounds__(256) k_heads_kv(const HeadArgs a, const HeadKV kv, uint32_t nbq, uint32_t nbk,
                                                   FastDiv dnbt) {
     constexpr int VI   = TT<TI>::VEC;
@@ -630,7 +652,7 @@ __global__ void __launch_bounds__(256) k_heads_kv(const HeadArgs a, const HeadKV
                 x1[e]           = a1 + b1;
             }
         }
-        if (sg == 0) {
+        if (sg == 0 || !TOCACHE) {
             if (ok) {
                 char * yp = S.y + (int64_t) i3 * S.ys3 + (int64_t) i2 * S.ys2 + (int64_t) h * S.ys1;
                 store_vec<TI, VI>(yp + (size_t) (j * VI) * EI, x0);
