@@ -721,6 +721,18 @@ __global__ void __launch_bounds__(64) k_fa_mask_summary(const FaArgs a) {
     }
 }
 
+// Lanes l and l ^ 32 combined: v_permlane32_swap of a value with itself leaves
+// each lane its own value and its partner's, in one order or the other, so the
+// max and the (commutative) sum do not depend on which.
+__device__ __forceinline__ float fa_xhalf_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float fa_xhalf_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // raw buffer loads (32-bit offsets, range-checked: reads past the end return 0)
 typedef __amdgpu_buffer_rsrc_t fa_rsrc;
 __device__ __forceinline__ fa_rsrc fa_make_rsrc(const char * base, uint32_t bytes) {
@@ -743,7 +755,7 @@ k_fa_mfma(const FaArgs a) {
     using x8         = typename M::x8;
     constexpr int BQ = 128, BK = 64;
     constexpr int KS = D * 2 + 16;   // K row stride in LDS (bytes): 16-byte bank spread
-    constexpr int VS = BK * 2 + 16;  // V^T row stride (bytes)
+    constexpr int VS = BK * 2 + 8;   // V^T row stride (bytes): 34 words, conflict-free reads
     constexpr int KC = D * 2 / 16;   // 16-byte chunks per K/V row
     constexpr int NC = BK * KC / 256;  // chunks per thread per tile (K and V each; even)
     constexpr int NKS = D / 16;      // k-steps of the S MFMA
@@ -988,7 +1000,7 @@ k_fa_mfma(const FaArgs a) {
             }
             tmax *= sl2;
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = fa_xhalf_max(tmax);  // the row's other 32 keys sit in lane ^ 32
         // Lazy rescale: p = exp2(x - mrun) against a reference max that moves only
         // when some row's max grows past it by more than 8 (p <= 2^8 stays exact
         // enough in fp32 and in the 16-bit parts); O and l are rescaled then only.
@@ -1070,7 +1082,7 @@ k_fa_mfma(const FaArgs a) {
         tiles(std::true_type{});
     }
     // rows: sum over both half-waves' keys; y[b][iq][h][d], d = 32 db + 8 j + 4 hh + i
-    lrun = lrun + __shfl_xor(lrun, 32, 64);
+    lrun = fa_xhalf_sum(lrun);
     if (part != 0) {  // half of the keys: (m, l, o) relative to exp2(m), merged by k_fa_mfma_combine
         if (rvld) {
             float * pp = a.fpart + ((size_t) (blockIdx.x - a.tfull) * BQ + wave * 32 + n) * FA_PART;
