@@ -266,13 +266,13 @@ __global__ void __launch_bounds__(256) k_rms_rows_generic(const NormArgs a) {
             }
             return v;
         };
-        double s = 0.0;
+        sq_t<TI> s = 0;  // the fast kernels' accumulator: double for F32 rows, fp32 fma for BF16/F16
         for (int i = lane; i < a.n; i += 64) {
             const float f = xval(i);
             if (sp) {
                 store_elem<TO>(sp + (size_t) i * EO, f);
             }
-            s += (double) (f * f);
+            s = sq_acc<TI>(s, f);
         }
         s                 = group_sum<64>(s);
         const float scale = rms_scale(s, a.n, a.eps);

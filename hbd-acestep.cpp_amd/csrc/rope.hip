@@ -317,10 +317,10 @@ __global__ void __launch_bounds__(256) k_heads_generic(const HeadArgs a) {
             char *         yp = S.y + (int64_t) i3 * S.ys3 + (int64_t) i2 * S.ys2 + (int64_t) h * S.ys1;
             float          scale = 1.0f;
             if (a.norm) {
-                double s = 0.0;
+                sq_t<TI> s = 0;  // the fast kernels' accumulator: double for F32 rows, fp32 fma for BF16/F16
                 for (int i = lane; i < a.ne0; i += 64) {
                     const float f = load_elem<TI>(xp + (size_t) i * EI);
-                    s += (double) (f * f);
+                    s             = sq_acc<TI>(s, f);
                 }
                 s     = group_sum<64>(s);
                 scale = rms_scale(s, a.ne0, a.eps);

@@ -75,6 +75,27 @@ def test_rms_norm_unaligned_generic_path(dev):
     assert_f32_close(to_np(y), ref)
 
 
+def test_rms_norm_bf16_generic_path_matches_fast_path(dev):
+    """A BF16 view 2 bytes off 16-byte alignment takes the generic kernel, its
+    aligned copy the fast one. Both sum the squares in fp32 (the fast kernels'
+    accumulator for 16-bit rows); the orders differ, so the final rounding may
+    too: each result within 1 ulp of the oracle and of the other, and almost all
+    outputs bit-identical."""
+    n, rows = 2048, 37
+    xb = orc.f32_to_bf16(randn((rows * n + 1,), seed=21))
+    w = randn((n,), seed=22, scale=0.1, mean=1.0)
+    wd = to_dev(w, dev)
+    un = to_dev(xb, dev, bf16=True)[1:].view(rows, n)
+    al = to_dev(np.ascontiguousarray(xb[1:]).reshape(rows, n), dev, bf16=True)
+    yg = to_np(ops.rms_norm(un, EPS, w=wd))
+    yf = to_np(ops.rms_norm(al, EPS, w=wd))
+    ref = _ref(xb[1:].reshape(rows, n), w, EPS, True)
+    assert_bf16_ulp(yg, ref)
+    assert_bf16_ulp(yf, ref)
+    assert_bf16_ulp(yg, yf)
+    assert frac_bitexact(yg, yf) >= 0.99
+
+
 @pytest.mark.parametrize("rows,n", [(600, 2048), (37, 1024), (5, 3000)])
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_rms_norm_modulate(dev, rows, n, dt):

@@ -7,7 +7,7 @@ bf16: within 1 ulp of the oracle's RNE-rounded result.
 """
 import numpy as np
 import pytest
-from helpers import assert_bf16_ulp, assert_f32_close, randn, rng, to_dev, to_np
+from helpers import assert_bf16_ulp, assert_f32_close, frac_bitexact, randn, rng, to_dev, to_np
 from oracle import oracle as orc
 
 from acestep_ops import ops
@@ -67,6 +67,27 @@ def test_rope_only_and_4d_batch(dev, dt):
     pos = np.arange(S, dtype=np.int32) * 3
     y = ops.rope_ext(to_dev(host, dev, bf16=bf16), to_dev(pos, dev), D, 2, 1e4)
     _check(y, lambda a: orc.rope_neox(a, pos, D, 1e4), host, bf16)
+
+
+def test_qk_norm_bf16_generic_path_matches_fast_path(dev):
+    """QK-norm -> rope on a BF16 view 2 bytes off 16-byte alignment (the generic
+    kernel) and on its aligned copy (the fast one): both sum each head row's
+    squares in fp32, in different orders, so each is within 1 ulp of the oracle
+    and of the other, and almost all outputs are bit-identical."""
+    T, nh, D = 40, 16, 128
+    xb = orc.f32_to_bf16(randn((T * nh * D + 1,), seed=31))
+    w = randn((D,), seed=32, scale=0.1, mean=1.0)
+    pos = rng(33).integers(0, 4096, T).astype(np.int32)
+    wd, pd = to_dev(w, dev), to_dev(pos, dev)
+    un = to_dev(xb, dev, bf16=True)[1:].view(T, nh, D)
+    al = to_dev(np.ascontiguousarray(xb[1:]).reshape(T, nh, D), dev, bf16=True)
+    yg = to_np(ops.qk_norm_rope(un, wd, pd, EPS, D, 1e6)[0])
+    yf = to_np(ops.qk_norm_rope(al, wd, pd, EPS, D, 1e6)[0])
+    ref = orc.bf16_chain(lambda a: orc.qk_norm_rope(a, w, pos, EPS, D, 1e6), xb[1:].reshape(T, nh, D))
+    assert_bf16_ulp(yg, ref, row_floor=True)
+    assert_bf16_ulp(yf, ref, row_floor=True)
+    assert_bf16_ulp(yg, yf, row_floor=True)
+    assert frac_bitexact(yg, yf) >= 0.99
 
 
 def test_rope_partial_dims_generic(dev):
