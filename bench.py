@@ -81,6 +81,32 @@ def block_bytes(rows: int, es: int = 2, fused: bool = True, cross: bool = False)
     return b
 
 
+def block_bytes_ca(rows: int, es: int = 2) -> dict:
+    """Algorithmic bytes per launch of the steady-state block with the
+    reference's cross-attention extras (dit-graph.h:428-433): the self-attention
+    gated residual fused with the cross-attention RMSNorm*w, the per-head
+    cross-attention Q-norm (328-331), and the cross-attention residual add fused
+    with the FFN norm -> AdaLN."""
+    act = rows * H * es
+    vec = H * 4
+    qk = rows * (NH + NKV) * D * es
+    return {
+        "qk_norm_rope": 2 * qk + rows * 4 + 2 * D * 4,
+        "gated_add_sa_rms_norm_ca": 4 * act + 2 * vec,
+        "rms_norm_ca_q": 2 * rows * NH * D * es + D * 4,
+        "add_ca_rms_norm_modulate_ffn": 4 * act + 3 * vec,
+        "swiglu": rows * 2 * I_FF * es + rows * I_FF * es,
+        "gated_add_ffn_rms_norm_modulate_sa": 4 * act + 4 * vec,
+    }
+
+
+# the block with the reference's cross-attention extras as separate nodes
+# (norm, Q-norm and residual add on top of the 6-launch block): its bytes and
+# the time they take at 70 % of the HBM peak
+CA_REF_BYTES = 1425.53e6
+CA_REF_US_AT_70 = 254.6
+
+
 def lead_bytes(rows: int, es: int = 2) -> int:
     """The first block's standalone self-attention norm."""
     return 2 * rows * H * es + 3 * H * 4
@@ -123,6 +149,13 @@ def _setup():
     q_out = DTensor.empty((ROWS, NH, D), "bf16")
     k_out = DTensor.empty((ROWS, NKV, D), "bf16")
     ff = DTensor.empty((BATCH, T_FRAMES, I_FF), "bf16")
+    # cross attention: its query projection and output (synthetic, resident),
+    # the norm weights, and the normalized outputs
+    ca_q = dev_bf16((ROWS, NH, D))
+    ca_out = dev_bf16((BATCH, T_FRAMES, H))
+    ca_w, ca_q_w = dev_f32((H,), 0.1, 1.0), dev_f32((D,), 0.1, 1.0)
+    norm_ca = DTensor.empty((BATCH, T_FRAMES, H), "bf16")
+    ca_q_out = DTensor.empty((ROWS, NH, D), "bf16")
     stream = Stream()
     sh = stream.handle
     device.synchronize()
@@ -149,14 +182,26 @@ def _setup():
         lambda: ops.add_rms_norm(h1, ffn_out, EPS, gate=gate_ff, w=sa_w, scale=scale_sa, shift=shift_sa,
                                  out_sum=hidden, out_norm=norm_sa, stream=sh),
     ]
+    # the steady-state block with cross attention (chain.cpp's use_cross_attn
+    # branch, in the same launch order)
+    cross_ca = [
+        fused[1],
+        lambda: ops.add_rms_norm(hidden, sa_out, EPS, gate=gate_sa, w=ca_w, out_sum=h1, out_norm=norm_ca, stream=sh),
+        lambda: ops.rms_norm(ca_q, EPS, w=ca_q_w, out=ca_q_out, stream=sh),
+        lambda: ops.add_rms_norm(h1, ca_out, EPS, w=ff_w, scale=scale_ff, shift=shift_ff, out_sum=h2,
+                                 out_norm=norm_ff, stream=sh),
+        fused[3],
+        lambda: ops.add_rms_norm(h2, ffn_out, EPS, gate=gate_ff, w=sa_w, scale=scale_sa, shift=shift_sa,
+                                 out_sum=hidden, out_norm=norm_sa, stream=sh),
+    ]
     lead = fused[0]
     # plain bf16 copy of a known size (the SwiGLU output, 147.456 MB each way):
     # the reference point for scaling the FETCH_SIZE / WRITE_SIZE counters
     ff_copy = DTensor.empty((BATCH, T_FRAMES, I_FF), "bf16")
     calib = lambda: ops.cpy(ff, ff_copy, stream=sh)  # noqa: E731
     keep = (hidden, qkv, sa_out, gate_up, ffn_out, adaln, sa_w, ff_w, q_w, k_w, pos, norm_sa, norm_ff, h1, h2, q_out,
-            k_out, ff, ff_copy)
-    return fused, unfused, cross, lead, calib, stream, keep
+            k_out, ff, ff_copy, ca_q, ca_out, ca_w, ca_q_w, norm_ca, ca_q_out)
+    return fused, unfused, cross, cross_ca, lead, calib, stream, keep
 
 
 def pmc_pass():
@@ -164,7 +209,7 @@ def pmc_pass():
     residual + norm), then the calibration copy, eagerly (for rocprofv3 --pmc)."""
     from acestep_ops import device
 
-    fused, _, cross, _lead, calib, stream, _keep = _setup()
+    fused, _, cross, _cross_ca, _lead, calib, stream, _keep = _setup()
     for f in fused:
         f()
     cross[-1]()
@@ -179,7 +224,7 @@ def gpu_bench(steps: int, warmup: int):
     from acestep_ops import device
     from acestep_ops.device import Event, Graph
 
-    fused, unfused, cross, lead, _calib, stream, _keep = _setup()
+    fused, unfused, cross, cross_ca, lead, _calib, stream, _keep = _setup()
     sh = stream.handle
 
     def graph_of(launches, copies=1, first=None):
@@ -226,11 +271,12 @@ def gpu_bench(steps: int, warmup: int):
         return [1000.0 * float(np.mean([ev[i][j].elapsed_ms(ev[i][j + 1]) for i in range(n)]))
                 for j in range(len(launches))]
 
-    g_cross, g_fused, g_unfused = graph_of(cross), graph_of(fused), graph_of(unfused)
+    g_cross, g_fused, g_unfused, g_ca = graph_of(cross), graph_of(fused), graph_of(unfused), graph_of(cross_ca)
     if warmup:
         graph_of(cross, warmup, lead).launch()
         graph_of(fused, warmup).launch()
         graph_of(unfused, warmup).launch()
+        graph_of(cross_ca, warmup).launch()
     stream.synchronize()
 
     # timed region: the first block's norm and K blocks, one replay of that graph
@@ -241,6 +287,7 @@ def gpu_bench(steps: int, warmup: int):
     wall = time.perf_counter() - t0
     ms_five = time_steps(fused, steps)
     ms_unfused = time_steps(unfused, steps)
+    ms_ca = time_steps(cross_ca, steps)
 
     names_c = list(block_bytes(ROWS, cross=True).keys())
     names_f = list(block_bytes(ROWS, fused=True).keys())
@@ -248,7 +295,8 @@ def gpu_bench(steps: int, warmup: int):
     pk_c = dict(zip(names_c, per_kernel(cross, steps, g_cross)))
     pk_f = dict(zip(names_f, per_kernel(fused, steps, g_fused)))
     pk_u = dict(zip(names_u, per_kernel(unfused, steps, g_unfused)))
-    return ms_step, ms_five, ms_unfused, wall, pk_c, pk_f, pk_u
+    pk_ca = dict(zip(list(block_bytes_ca(ROWS).keys()), per_kernel(cross_ca, steps, g_ca)))
+    return ms_step, ms_five, ms_unfused, wall, pk_c, pk_f, pk_u, (ms_ca, pk_ca)
 
 
 def host_cpu() -> dict:
@@ -838,7 +886,9 @@ def main():
     kb_u = block_bytes(ROWS, fused=False)
     total_bytes = sum(kb.values())
     graph_bytes = args.steps * total_bytes + lead_bytes(ROWS)  # what the timed graph moves
-    ms_step, ms_five, ms_unfused, wall, per_k, per_k_f, per_k_u = gpu_bench(args.steps, args.warmup)
+    ms_step, ms_five, ms_unfused, wall, per_k, per_k_f, per_k_u, (ms_ca, per_k_ca) = gpu_bench(args.steps,
+                                                                                                args.warmup)
+    kb_ca = block_bytes_ca(ROWS)
     value = graph_bytes / (args.steps * ms_step * 1e-3) / 1e9
     dom = "swiglu"
     dom_gbs = kb[dom] / (per_k[dom] * 1e-6) / 1e9
@@ -916,6 +966,12 @@ def main():
         "unfused": {"us_per_block": round(ms_unfused * 1e3, 2), "bytes_per_step": sum(kb_u.values()),
                     "gbs": round(sum(kb_u.values()) / (ms_unfused * 1e-3) / 1e9, 1),
                     "per_kernel_us": {k: round(v, 2) for k, v in per_k_u.items()}},
+        "block_with_cross_attn": {
+            "launches": len(kb_ca), "us_per_block": round(ms_ca * 1e3, 2), "bytes_per_step": sum(kb_ca.values()),
+            "gbs": round(sum(kb_ca.values()) / (ms_ca * 1e-3) / 1e9, 1),
+            "reference_structure_bytes": CA_REF_BYTES, "reference_structure_us_at_70pct": CA_REF_US_AT_70,
+            "per_kernel_us": {k: round(v, 2) for k, v in per_k_ca.items()},
+            "per_kernel_gbs": {k: round(kb_ca[k] / (per_k_ca[k] * 1e-6) / 1e9, 1) for k in kb_ca}},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_swiglu (bf16)",
                      "bytes_per_launch": kb[dom]},
