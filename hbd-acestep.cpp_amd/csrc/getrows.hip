@@ -78,23 +78,60 @@ __global__ void __launch_bounds__(256) k_get_rows_q8_0(const GetRowsArgs a) {
 
 // Q8_0 rows whose byte length is a multiple of 16 (ne0 % 256 == 0) in a
 // 16-byte aligned table: the wave copies its row into LDS with coalesced
-// 16-byte loads, all issued at once (one memory round trip per id), then each
-// lane decodes groups of 8 outputs from LDS and writes them with 16-byte
-// stores. LDS per wave: the row's nc 16-byte chunks (nc <= 9*64, ne0 <= 8192).
-template <int TO>
+// 16-byte loads, all issued at once, then each lane decodes groups of 8 outputs
+// from LDS and writes them with 16-byte stores. A wave walks ids a grid stride
+// apart, and the next id's row loads are issued (into the registers just copied
+// to LDS) before this id's outputs are written, so their memory latency runs
+// under the stores. LDS per wave: the row's nc 16-byte chunks (nc <= 9*64,
+// ne0 <= 8192).
+#ifndef MI_GR_LDS_WG_PER_CU
+#define MI_GR_LDS_WG_PER_CU 16  // grid cap of the LDS kernel, in workgroups per CU
+#endif
+// MAXC: 64-lane load rounds per row, ceil(nc / 64) (the registers that carry the
+// next row stay live through the stores, so only the rounds the row needs)
+template <int TO, int MAXC>
 __global__ void __launch_bounds__(256) k_get_rows_q8_0_lds(const GetRowsArgs a, int nc) {
     extern __shared__ uint4 stage_all[];
     constexpr int    EO   = TT<TO>::ES;
     constexpr int    OPS  = 16 / EO;  // outputs per 16-byte store: 4 (F32) or 8 (BF16)
-    constexpr int    MAXC = 9;
     const int        lane = threadIdx.x & 63;
     const uint32_t   wv   = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint4 *          stage = stage_all + wv * nc;
     const uint16_t * s16   = (const uint16_t *) stage;
-    for (uint32_t i = blockIdx.x * 4 + wv; i < a.n_ids; i += gridDim.x * 4) {
-        const int64_t r   = a.ids[(int64_t) i * a.ids_stride];
-        char *        yp  = a.y + (int64_t) i * a.ynb1;
-        if (r < 0 || r >= a.n_rows) {
+    const uint32_t   step  = gridDim.x * 4;
+    uint4            v[MAXC];
+    // the row of id `id`; its loads are issued into v when it is valid
+    auto fetch = [&](uint32_t id) -> int64_t {
+        const int64_t r = a.ids[(int64_t) id * a.ids_stride];
+        if (r >= 0 && r < a.n_rows) {
+            const char * row = a.table + r * a.tnb1;
+#pragma unroll
+            for (int k = 0; k < MAXC; ++k) {
+                const int c = lane + 64 * k;
+                if (c < nc) {
+                    v[k] = ld16(row + (size_t) c * 16);
+                }
+            }
+        }
+        return r;
+    };
+    uint32_t i = blockIdx.x * 4 + wv;
+    int64_t  r = i < a.n_ids ? fetch(i) : -1;
+    for (; i < a.n_ids; i += step) {
+        char *     yp  = a.y + (int64_t) i * a.ynb1;
+        const bool bad = r < 0 || r >= a.n_rows;
+        if (!bad) {
+#pragma unroll
+            for (int k = 0; k < MAXC; ++k) {
+                const int c = lane + 64 * k;
+                if (c < nc) {
+                    stage[c] = v[k];
+                }
+            }
+        }
+        const uint32_t in = i + step;
+        const int64_t  rn = in < a.n_ids ? fetch(in) : -1;  // in flight during this id's stores
+        if (bad) {
             if (lane == 0 && a.d_err) {
                 atomicAdd(a.d_err, 1);
             }
@@ -102,46 +139,31 @@ __global__ void __launch_bounds__(256) k_get_rows_q8_0_lds(const GetRowsArgs a, 
             for (int o = lane * OPS; o < a.n; o += 64 * OPS) {
                 store_vec<TO, OPS>(yp + (size_t) o * EO, z);
             }
-            continue;
-        }
-        const char * row = a.table + r * a.tnb1;
-        uint4         v[MAXC];
+        } else {
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            // OPS outputs (one 16-byte store) per lane per step: each store
+            // instruction writes 1 KB contiguous, whole cache lines
+            for (int o = lane * OPS; o < a.n; o += 64 * OPS) {
+                const uint16_t * bp = s16 + (o >> 5) * 17;  // a 34-byte block is 17 halfwords
+                const uint16_t * qp = bp + 1 + ((o & 31) >> 1);
+                const float      d  = (float) __builtin_bit_cast(_Float16, bp[0]);
+                float            f[OPS];
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) {
-            const int c = lane + 64 * k;
-            if (c < nc) {
-                v[k] = ld16(row + (size_t) c * 16);
-            }
-        }
+                for (int h = 0; h < OPS / 4; ++h) {
+                    const uint32_t w = (uint32_t) qp[2 * h] | ((uint32_t) qp[2 * h + 1] << 16);
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k) {
-            const int c = lane + 64 * k;
-            if (c < nc) {
-                stage[c] = v[k];
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        // OPS outputs (one 16-byte store) per lane per step: each store
-        // instruction writes 1 KB contiguous, whole cache lines
-        for (int o = lane * OPS; o < a.n; o += 64 * OPS) {
-            const uint16_t * bp = s16 + (o >> 5) * 17;  // a 34-byte block is 17 halfwords
-            const uint16_t * qp = bp + 1 + ((o & 31) >> 1);
-            const float      d  = (float) __builtin_bit_cast(_Float16, bp[0]);
-            float            f[OPS];
-#pragma unroll
-            for (int h = 0; h < OPS / 4; ++h) {
-                const uint32_t w = (uint32_t) qp[2 * h] | ((uint32_t) qp[2 * h + 1] << 16);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    f[4 * h + k] = i8f(w, k) * d;
+                    for (int k = 0; k < 4; ++k) {
+                        f[4 * h + k] = i8f(w, k) * d;
+                    }
                 }
+                store_vec<TO, OPS>(yp + (size_t) o * EO, f);
             }
-            store_vec<TO, OPS>(yp + (size_t) o * EO, f);
         }
         // the next id overwrites this wave's LDS rows
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
+        r = rn;
     }
 }
 
@@ -311,9 +333,21 @@ static int launch_to(const GetRowsArgs & a, int ttype, bool fast, bool lds, hipS
                     return MI_OK;
                 }
                 if (lds) {
-                    const int nc = a.n / 32 * 34 / 16;
-                    hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO>), dim3(grid), dim3(256), (size_t) 4 * nc * 16, s, a,
-                                       nc);
+                    const int      nc   = a.n / 32 * 34 / 16;
+                    const uint32_t gcap = (uint32_t) num_cus() * MI_GR_LDS_WG_PER_CU;
+                    const dim3     g(grid > gcap ? gcap : grid);
+                    const size_t   lb = (size_t) 4 * nc * 16;
+                    switch ((nc + 63) / 64) {  // nc <= 9 * 64 (ne0 <= 8192)
+                        case 1: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 1>), g, dim3(256), lb, s, a, nc); break;
+                        case 2: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 2>), g, dim3(256), lb, s, a, nc); break;
+                        case 3: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 3>), g, dim3(256), lb, s, a, nc); break;
+                        case 4: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 4>), g, dim3(256), lb, s, a, nc); break;
+                        case 5: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 5>), g, dim3(256), lb, s, a, nc); break;
+                        case 6: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 6>), g, dim3(256), lb, s, a, nc); break;
+                        case 7: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 7>), g, dim3(256), lb, s, a, nc); break;
+                        case 8: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 8>), g, dim3(256), lb, s, a, nc); break;
+                        default: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 9>), g, dim3(256), lb, s, a, nc); break;
+                    }
                 } else {
                     hipLaunchKernelGGL((k_get_rows_q8_0<TO>), dim3(grid), dim3(256), 0, s, a);
                 }

@@ -70,6 +70,25 @@ def test_get_rows_plain_tables(dev, ttype):
     assert np.array_equal(y, orc.get_rows(host, code, n, ids))
 
 
+def test_get_rows_q8_0_waves_walk_several_ids(dev):
+    """More ids than the LDS kernel's grid has waves (256 CUs x 16 workgroups x 4
+    waves on this device): each wave walks several ids a grid stride apart, the
+    next row in flight under the current stores; invalid ids among them count
+    and give zero rows, and the valid ones stay bit-exact."""
+    n_rows, n, n_ids = 512, 256, 70001
+    tab = _q8_table(n_rows, n, seed=3)
+    ids = rng(5).integers(0, n_rows, n_ids).astype(np.int32)
+    bad = rng(6).choice(n_ids, 97, replace=False)
+    ids[bad] = np.where(np.arange(bad.size) % 2 == 0, -3, n_rows + 7)
+    err = DTensor.zeros((1,), "i32")
+    y = to_np(ops.get_rows(ops.Q8(to_dev(tab, dev)), to_dev(ids, dev), err=err))
+    assert int(err.item()) == bad.size
+    good = np.ones(n_ids, bool)
+    good[bad] = False
+    assert np.array_equal(y[good], orc.get_rows(tab, orc.Q8_0, n, ids[good]))
+    assert not y[bad].any()
+
+
 def test_get_rows_out_of_range_ids(dev):
     tab = _q8_table(64, 256, seed=1)
     ids = np.array([0, 64, -1, 5, 1 << 30], np.int32)
