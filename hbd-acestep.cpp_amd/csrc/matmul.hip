@@ -373,6 +373,7 @@ __global__ void __launch_bounds__(256) k_mmv_reduce(const MmvArgs a) {
 typedef int mm_i32x4 __attribute__((ext_vector_type(4)));
 typedef int mm_i32x16 __attribute__((ext_vector_type(16)));
 typedef float mm_f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 mm_f16x8 __attribute__((ext_vector_type(8)));
 
 __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
     const int      tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
@@ -417,19 +418,24 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
         }
     };
     // the block's scales d_x[m] d_w[n] as a 32 x 32 outer product on the matrix
-    // core (k = 0 carries the scales, k = 1 zeros: exact), in the D layout of the
-    // int32 dots, so each output costs one conversion and one fma
+    // core, in the D layout of the int32 dots, so each output costs one
+    // conversion and one fma. Both scales are fp16 values (d_x was rounded to
+    // fp16 when x was quantized), so an fp16 MFMA with k-slot 0 carrying them and
+    // the other 15 slots zero forms every product exactly, at half the matrix-core
+    // time of an fp32 outer product.
     auto run = [&](const Blk & k) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const mm_i32x4 av = { (int) k.x[i].x, (int) k.x[i].y, (int) k.x[i].z, (int) k.x[i].w };
-            const float    sx = hh == 0 ? k.dx[i] : 0.0f;
+            mm_f16x8       sx = {};
+            sx[0]             = hh == 0 ? (_Float16) k.dx[i] : (_Float16) 0.0f;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const mm_i32x4  bv = { (int) k.w[j].x, (int) k.w[j].y, (int) k.w[j].z, (int) k.w[j].w };
                 const mm_i32x16 d  = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, mm_i32x16{}, 0, 0, 0);
-                const float     sw = hh == 0 ? (float) __builtin_bit_cast(_Float16, k.dw[j]) : 0.0f;
-                const mm_f32x16 sc = __builtin_amdgcn_mfma_f32_32x32x2f32(sx, sw, mm_f32x16{}, 0, 0, 0);
+                mm_f16x8        sw = {};
+                sw[0]              = hh == 0 ? __builtin_bit_cast(_Float16, k.dw[j]) : (_Float16) 0.0f;
+                const mm_f32x16 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(sx, sw, mm_f32x16{}, 0, 0, 0);
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     acc[i][j][e] = __builtin_fmaf((float) d[e], sc[e], acc[i][j][e]);

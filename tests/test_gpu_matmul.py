@@ -108,6 +108,20 @@ def test_matrix_kernel_shapes(dev, n, k, m):
     _run(n, k, m, seed=n * 7 + k + m)
 
 
+@pytest.mark.parametrize("m", [8, 300])
+def test_subnormal_fp16_scales(dev, m):
+    """Weights and x small enough that both block scales are fp16 subnormals
+    (|d| < 2^-14; d_x = amax/127 ~ 3e-6, d_w ~ 2e-6), through the matrix-vector
+    kernel (8 rows) and the matrix kernel (300 rows), whose scale products come
+    from an fp16 MFMA: subnormal inputs must not be flushed."""
+    print(f"mul_mat q8_0 subnormal scales m={m}", flush=True)
+    w, x, _ = _run(640, 256, m, seed=29 + m, wscale=1e-4, xscale=1e-4)
+    dx = np.abs(x.reshape(m, -1, 32)).max(axis=-1) / 127.0
+    assert (dx < 2.0 ** -14).all()  # every x scale is an fp16 subnormal
+    dw = w.reshape(w.shape[0], -1, 34)[:, :, :2].copy().view(np.float16).astype(np.float32)
+    assert (np.abs(dw) < 2.0 ** -14).all()
+
+
 def test_matrix_kernel_strided_x_and_y(dev):
     print("mul_mat q8_0 matrix strided x/y", flush=True)
     r = np.random.default_rng(17)
