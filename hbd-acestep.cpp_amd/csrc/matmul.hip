@@ -63,14 +63,16 @@ __device__ __forceinline__ float mm_div127(float amax) {
 // x rows -> Q8_0 (x86 rounding), block-major: quants xq[b][m][32] and widened
 // scales xd[b][m] at a row stride mp >= m (the matrix-vector kernel reads all
 // rows of a block in one 32 * m + 4 * m byte run with a few wide scalar loads;
-// the matrix kernel reads 32-row tiles); 8 lanes per 32-element block.
+// the matrix kernel reads 32-row tiles); 8 lanes per 32-element block, and the
+// blocks of a wave are one block of 8 consecutive rows: each row's 128 input
+// bytes are a whole line, and the wave's quants one contiguous 256-byte run.
 __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
     const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
     const uint32_t blk = gid / 8, sub = gid % 8;
     if (blk >= a.m * a.nbk) {
         return;  // whole groups of 8 lanes
     }
-    const uint32_t m = blk / a.nbk, b = blk - m * a.nbk;
+    const uint32_t b = blk / a.m, m = blk - b * a.m;
     float          f[4];
     auto           ld4 = [&](const char * p, float (&v)[4]) {
         if (a.xvec) {
