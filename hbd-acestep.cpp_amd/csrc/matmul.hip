@@ -66,15 +66,16 @@ __device__ __forceinline__ float mm_div127(float amax) {
 // the matrix kernel reads 32-row tiles); 8 lanes per 32-element block, and the
 // blocks of a wave are one block of 8 consecutive rows: each row's 128 input
 // bytes are a whole line, and the wave's quants one contiguous 256-byte run.
+#ifndef MI_QX_U
+#define MI_QX_U 4  // blocks per 8-lane group, a grid stride apart, all loads issued first
+#endif
 __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
-    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-    const uint32_t blk = gid / 8, sub = gid % 8;
-    if (blk >= a.m * a.nbk) {
-        return;  // whole groups of 8 lanes
-    }
-    const uint32_t b = blk / a.m, m = blk - b * a.m;
-    float          f[4];
-    auto           ld4 = [&](const char * p, float (&v)[4]) {
+    constexpr int  U     = MI_QX_U;
+    const uint32_t gid   = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t grp   = gid / 8, sub = gid % 8;
+    const uint32_t total = a.m * a.nbk;
+    const uint32_t ngrp  = gridDim.x * 32u;  // 8-lane groups in the grid
+    auto           ld4   = [&](const char * p, float (&v)[4]) {
         if (a.xvec) {
             const float4 q = *(const float4 *) p;
             v[0]           = q.x;
@@ -88,31 +89,48 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
             }
         }
     };
-    if (a.glu) {  // x = silu(g) * u, as mi_swiglu computes it
-        const int64_t off = (int64_t) m * a.gu1 + (int64_t) (b * 32 + sub * 4) * 4;
-        float         g[4], u[4];
-        ld4(a.g + off, g);
-        ld4(a.u + off, u);
+    // the U blocks' inputs (g and u for the SwiGLU prologue), all in flight at once
+    float f[U][4], h[U][4];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint32_t blk = grp + (uint32_t) k * ngrp;
+        if (blk < total) {  // uniform over the 8 lanes of a block
+            const uint32_t b = blk / a.m, m = blk - b * a.m;
+            if (a.glu) {
+                const int64_t off = (int64_t) m * a.gu1 + (int64_t) (b * 32 + sub * 4) * 4;
+                ld4(a.g + off, f[k]);
+                ld4(a.u + off, h[k]);
+            } else {
+                ld4(a.x + (int64_t) m * a.x1 + (int64_t) (b * 32 + sub * 4) * 4, f[k]);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint32_t blk = grp + (uint32_t) k * ngrp;
+        if (blk >= total) {
+            break;  // whole groups of 8 lanes; later blocks are further out
+        }
+        const uint32_t b = blk / a.m, m = blk - b * a.m;
+        float          x[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            f[e] = silu_f(g[e]) * u[e];
+            x[e] = a.glu ? silu_f(f[k][e]) * h[k][e] : f[k][e];  // x = silu(g) * u, as mi_swiglu computes it
         }
-    } else {
-        ld4(a.x + (int64_t) m * a.x1 + (int64_t) (b * 32 + sub * 4) * 4, f);
-    }
-    float amax = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
-    amax       = group_max<8>(amax);
-    const float d  = mm_div127(amax);
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    uint32_t    w  = 0;
+        float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+        amax       = group_max<8>(amax);
+        const float d  = mm_div127(amax);
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        uint32_t    w  = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(f[e] * id), -128.0f, 127.0f);
-        w |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
-    }
-    *(uint32_t *) (a.xq + ((int64_t) b * a.mp + m) * 32 + sub * 4) = w;
-    if (sub == 0) {
-        a.xd[(int64_t) b * a.mp + m] = (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
+        for (int e = 0; e < 4; ++e) {
+            const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(x[e] * id), -128.0f, 127.0f);
+            w |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
+        }
+        *(uint32_t *) (a.xq + ((int64_t) b * a.mp + m) * 32 + sub * 4) = w;
+        if (sub == 0) {
+            a.xd[(int64_t) b * a.mp + m] = (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
+        }
     }
 }
 
@@ -560,7 +578,7 @@ int launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s) {
     if (a.nw) {
         hipLaunchKernelGGL(k_mmv_quant_x_norm, dim3(a.m), dim3(256), 0, s, a);
     } else {
-        const uint64_t threads = (uint64_t) a.m * a.nbk * 8;
+        const uint64_t threads = ((uint64_t) a.m * a.nbk + MI_QX_U - 1) / MI_QX_U * 8;
         hipLaunchKernelGGL(k_mmv_quant_x, dim3((uint32_t) ((threads + 255) / 256)), dim3(256), 0, s, a);
     }
     if (a.m > 8) {
