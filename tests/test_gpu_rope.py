@@ -57,6 +57,28 @@ def test_qk_norm_rope_fused_qkv(dev, T, nh, nkv, D, theta, maxpos, dt):
     _check(ko, lambda a: orc.qk_norm_rope(a, kw, pos, EPS, D, theta), kh, bf16)
 
 
+@pytest.mark.parametrize("nh,nkv,dt", [
+    (16, 16, "bf16"),  # 4 batches of 8 rows, 2 per work item
+    (16, 8, "bf16"),   # DiT self-attention (16 Q, 8 KV heads): 3 batches, a whole token per item
+    (24, 16, "bf16"),  # 5 batches, items of 3 + 2
+    (14, 6, "bf16"),   # heads not a multiple of the batch: rows past the last head
+    (6, 2, "f32"),     # f32 rows (batches of 4): 2 + 1 batches, ragged Q rows
+])
+def test_qk_norm_rope_long_sequences_group_batches(dev, nh, nkv, dt):
+    """2100 tokens: enough to fill the chip with whole tokens, so each wave item
+    holds several head batches (2 or 3), including ragged last items and rows."""
+    T, D, theta = 2100, 128, 1e4
+    print(f"qk_norm_rope long T={T} nh={nh} nkv={nkv} {dt}", flush=True)
+    bf16 = dt == "bf16"
+    q, k, qh, kh = _fused_qkv(T, nh, nkv, D, seed=nh * 100 + nkv, bf16=bf16, dev=dev)
+    pos = np.arange(T, dtype=np.int32)[::-1].copy()
+    qw = randn((D,), seed=3, scale=0.1, mean=1.0)
+    kw = randn((D,), seed=4, scale=0.1, mean=1.0)
+    qo, ko = ops.qk_norm_rope(q, to_dev(qw, dev), to_dev(pos, dev), EPS, D, theta, k=k, k_w=to_dev(kw, dev))
+    _check(qo, lambda a: orc.qk_norm_rope(a, qw, pos, EPS, D, theta), qh, bf16)
+    _check(ko, lambda a: orc.qk_norm_rope(a, kw, pos, EPS, D, theta), kh, bf16)
+
+
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_rope_only_and_4d_batch(dev, dt):
     """ggml_rope_ext on [D, H, S, N] (positions index S, reused for each N)."""
@@ -134,6 +156,19 @@ def test_qk_norm_no_rope_cross_attn(dev):
     w = randn((D,), seed=8, scale=0.1, mean=1.0)
     y = ops.rms_norm(x, EPS, w=to_dev(w, dev))
     assert_f32_close(to_np(y), orc.rms_norm_mul(to_np(x), w, EPS))
+
+
+@pytest.mark.parametrize("H", [16, 20])
+def test_qk_norm_no_rope_long_rows(dev, H):
+    """Per-head Q-norm on 4400 x H x 128 bf16 (the cross-attention query shape):
+    2 or 3 head batches per work item, and with 20 heads rows past the last
+    head of a batch."""
+    rows, D = 4400, 128
+    print(f"q-norm long rows={rows} H={H}", flush=True)
+    xb = orc.f32_to_bf16(randn((rows, H, D), seed=H))
+    w = randn((D,), seed=11, scale=0.1, mean=1.0)
+    y = ops.rms_norm(to_dev(xb, dev, bf16=True), EPS, w=to_dev(w, dev))
+    assert_bf16_ulp(to_np(y), orc.bf16_chain(lambda a: orc.rms_norm_mul(a, w, EPS), xb), row_floor=True)
 
 
 def test_rope_unsupported_modes_rejected(dev):
