@@ -223,7 +223,12 @@ int mi_rms_norm(const mi_tensor * x, const mi_tensor * w, float eps, const mi_te
     }
     hipStream_t s = (hipStream_t) stream;
     if (x->ne[0] == 64 || x->ne[0] == 128 || x->ne[0] == 256) {
-        // head-sized rows: sub-wave groups per row
+        // head-sized rows: whole rows per lane group when the view allows it,
+        // else the per-head kernel's sub-wave groups
+        const int rc = launch_rms_norm_short(*x, w ? (const float *) w->data : nullptr, eps, *y, s);
+        if (rc != MI_ERR_UNSUPPORTED) {
+            return finish(rc);
+        }
         HeadArgs a;
         a.seg[0] = make_seg(*x, *y, w);
         a.nseg   = 1;

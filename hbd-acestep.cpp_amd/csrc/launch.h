@@ -39,6 +39,10 @@ struct AddNorm {
     const mi_tensor * ysum;
 };
 
+// Head-sized rows (ne0 = 64/128/256) of a row-uniform view, same type in and
+// out, 16-byte aligned: RMSNorm (* w) by whole rows per lane group.
+// MI_ERR_UNSUPPORTED for any other view (the caller takes another kernel).
+int launch_rms_norm_short(const mi_tensor & x, const float * w, float eps, const mi_tensor & y, hipStream_t s);
 int launch_rms_norm(const mi_tensor & x, const float * w, const float * sc, const float * sh, float eps,
                     const mi_tensor & y, hipStream_t s, const AddNorm * add = nullptr);
 

@@ -292,6 +292,134 @@ __global__ void __launch_bounds__(256) k_rms_rows_generic(const NormArgs a) {
     }
 }
 
+#ifndef MI_NORM_WPC
+#define MI_NORM_WPC 16  // resident waves per CU the grid is sized for
+#endif
+
+// Head-sized rows (D = 64, 128 or 256 elements) of a row-uniform view, RMSNorm
+// (* w), nothing else: the per-head Q/K norm with no rope (cross attention).
+// A row spans L = D/VI lanes, one 16-byte vector each, so one load instruction
+// of a wave covers 64/L whole consecutive rows (1 KB); each wave issues U of
+// them (U*64/L rows) before it reduces any, and walks such chunks with a
+// stride over a grid balanced so that every wave takes the same number of
+// chunks (+-1). The row sums are DPP group sums within the L lanes.
+//
+// Rows past the end of the view load and store the last row again (the same
+// values to the same bytes), so no load or store sits behind a branch.
+template <int TI, int D, bool W, int U>
+__global__ void __launch_bounds__(256) k_rms_short(const char * x, char * y, int64_t xs, int64_t ys, uint32_t rows,
+                                                   const float * w, float eps) {
+    constexpr int VI  = TT<TI>::VEC;
+    constexpr int L   = D / VI;   // lanes per row
+    constexpr int RPI = 64 / L;   // rows per load instruction
+    constexpr int CH  = U * RPI;  // rows per chunk
+    const int     lane = threadIdx.x & 63;
+    const int     j    = lane % L;
+    const int     g    = lane / L;
+    float         wl[VI];
+#pragma unroll
+    for (int e = 0; e < VI; ++e) {
+        wl[e] = W ? w[j * VI + e] : 1.0f;
+    }
+    // rows < 2^31 (the entry point's bound) and the stride is far below 2^31,
+    // so the 32-bit row indices do not wrap
+    const uint32_t step = gridDim.x * 4 * CH;
+    for (uint32_t base = (blockIdx.x * 4 + (threadIdx.x >> 6)) * CH; base < rows; base += step) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            uint32_t r = base + u * RPI + g;
+            r          = r < rows ? r : rows - 1;
+            v[u]       = ld16(x + (int64_t) r * xs + j * 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // all U loads issued before the first is used
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float f[VI];
+            unpack16<TI>(v[u], f);
+            sq_t<TI> ss = 0;
+#pragma unroll
+            for (int e = 0; e < VI; ++e) {
+                ss = sq_acc<TI>(ss, f[e]);
+            }
+            ss                = group_sum<L>(ss);
+            const float scale = rms_scale(ss, D, eps);
+#pragma unroll
+            for (int e = 0; e < VI; ++e) {
+                f[e] = W ? f[e] * scale * wl[e] : f[e] * scale;
+            }
+            uint32_t r = base + u * RPI + g;
+            r          = r < rows ? r : rows - 1;
+            store_vec<TI, VI>(y + (int64_t) r * ys + j * 16, f);
+        }
+    }
+}
+
+#ifndef MI_SHORT_U
+#define MI_SHORT_U 4  // load instructions per wave in flight
+#endif
+
+template <int TI, int D>
+static void launch_short_d(const char * x, char * y, int64_t xs, int64_t ys, uint32_t rows, const float * w, float eps,
+                           hipStream_t s) {
+    constexpr int  RPI    = 64 / (D / TT<TI>::VEC);
+    const uint64_t chunks = ((uint64_t) rows + MI_SHORT_U * RPI - 1) / (MI_SHORT_U * RPI);
+    const uint64_t maxw   = (uint64_t) num_cus() * MI_NORM_WPC;
+    const uint64_t per    = (chunks + maxw - 1) / maxw;
+    const uint64_t waves  = (chunks + per - 1) / per;
+    const dim3     grid((uint32_t) ((waves + 3) / 4));
+    if (w) {
+        hipLaunchKernelGGL((k_rms_short<TI, D, true, MI_SHORT_U>), grid, dim3(256), 0, s, x, y, xs, ys, rows, w, eps);
+    } else {
+        hipLaunchKernelGGL((k_rms_short<TI, D, false, MI_SHORT_U>), grid, dim3(256), 0, s, x, y, xs, ys, rows, w,
+                           eps);
+    }
+}
+
+template <int TI>
+static int launch_short_t(const char * x, char * y, int64_t xs, int64_t ys, uint32_t rows, int d, const float * w,
+                          float eps, hipStream_t s) {
+    switch (d) {
+        case 64:
+            launch_short_d<TI, 64>(x, y, xs, ys, rows, w, eps, s);
+            return MI_OK;
+        case 128:
+            launch_short_d<TI, 128>(x, y, xs, ys, rows, w, eps, s);
+            return MI_OK;
+        case 256:
+            launch_short_d<TI, 256>(x, y, xs, ys, rows, w, eps, s);
+            return MI_OK;
+        default:
+            return MI_ERR_UNSUPPORTED;
+    }
+}
+
+int launch_rms_norm_short(const mi_tensor & x, const float * w, float eps, const mi_tensor & y, hipStream_t s) {
+    const Rows3 xr = make_rows3(x), yr = make_rows3(y);
+    const bool  ok = x.type == y.type && xr.uni && yr.uni && aligned(x.data, 16) && aligned(y.data, 16) &&
+                    x.nb[1] % 16 == 0 && y.nb[1] % 16 == 0 && (!w || aligned(w, 16)) &&
+                    x.nb[0] == (uint64_t) type_size(x.type) && y.nb[0] == (uint64_t) type_size(y.type);
+    if (!ok) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    const uint32_t rows = (uint32_t) nrows(x);
+    if (rows == 0) {
+        return MI_OK;
+    }
+    const char * xp = (const char *) x.data;
+    char *       yp = (char *) y.data;
+    switch (x.type) {
+        case MI_TYPE_F32:
+            return launch_short_t<MI_TYPE_F32>(xp, yp, x.nb[1], y.nb[1], rows, (int) x.ne[0], w, eps, s);
+        case MI_TYPE_BF16:
+            return launch_short_t<MI_TYPE_BF16>(xp, yp, x.nb[1], y.nb[1], rows, (int) x.ne[0], w, eps, s);
+        case MI_TYPE_F16:
+            return launch_short_t<MI_TYPE_F16>(xp, yp, x.nb[1], y.nb[1], rows, (int) x.ne[0], w, eps, s);
+        default:
+            return MI_ERR_UNSUPPORTED;
+    }
+}
+
 // Workgroups for a grid-stride loop over ceil(rows/R) row groups, capped at
 // about MI_NORM_WPC resident waves per CU, with the groups spread evenly (every
 // workgroup runs the same number of iterations, +-1).
@@ -299,9 +427,6 @@ __global__ void __launch_bounds__(256) k_rms_rows_generic(const NormArgs a) {
 #define MI_NORM_MAXW 8  // most waves sharing one row (more waves: fewer columns per lane)
 #endif
 
-#ifndef MI_NORM_WPC
-#define MI_NORM_WPC 16  // resident waves per CU the grid is sized for
-#endif
 
 static uint32_t balanced_grid(uint32_t rows, int R, int nw) {
     const uint32_t iters  = (rows + R - 1) / R;

@@ -65,6 +65,44 @@ def test_rms_norm_strided_rows(dev, dt):
     assert_f32_close(to_np(y4), orc.rms_norm(to_np(x4), EPS))
 
 
+@pytest.mark.parametrize("n", [64, 128, 256])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_rms_norm_head_rows(dev, n, dt):
+    """Head-sized rows (the per-head Q/K norm) of row-uniform views take the
+    whole-row kernel: 70001 contiguous rows (several chunks per wave, a ragged
+    last chunk) with w, then rows of a wider buffer (nb1 > ne0*es) without w,
+    then a [n, 5, 7, 3] 4-D view. f16 outputs within 1 f16 ulp of the oracle's
+    RNE-rounded fp32 chain, f32 at 1e-5 and >= 99.9 % bit-identical."""
+    print(f"rms_norm head rows n={n} {dt}", flush=True)
+    f32 = dt == "f32"
+    enc = {"bf16": orc.f32_to_bf16, "f16": orc.f32_to_f16}.get(dt)
+    dec = {"bf16": orc.bf16_to_f32, "f16": orc.f16_to_f32}.get(dt)
+
+    def dev_of(a):
+        return to_dev(a, dev) if f32 else to_dev(a, dev, bf16=dt == "bf16", f16=dt == "f16")
+
+    def check(y, xh, w):
+        fn = (lambda a: orc.rms_norm_mul(a, w, EPS)) if w is not None else (lambda a: orc.rms_norm(a, EPS))
+        if f32:
+            ref = fn(xh)
+            assert_f32_close(y, ref)
+            assert frac_bitexact(y, ref) >= 0.999
+        else:
+            assert_bf16_ulp(y, enc(fn(dec(xh))))  # sign-magnitude ordinal: an f16 ulp as well
+
+    w = randn((n,), seed=n, scale=0.1, mean=1.0)
+    x = randn((70001, n), seed=n + 1)
+    xh = x if f32 else enc(x)
+    check(to_np(ops.rms_norm(dev_of(xh), EPS, w=to_dev(w, dev))), xh, w)
+    pad = 48
+    big = randn((301, n + pad), seed=n + 2)
+    bh = big if f32 else enc(big)
+    check(to_np(ops.rms_norm(dev_of(bh)[:, pad:], EPS)), np.ascontiguousarray(bh[:, pad:]), None)
+    x4 = randn((3, 7, 5, n), seed=n + 3)
+    x4h = x4 if f32 else enc(x4)
+    check(to_np(ops.rms_norm(dev_of(x4h), EPS, w=to_dev(w, dev))), x4h, w)
+
+
 def test_rms_norm_unaligned_generic_path(dev):
     """A 4-byte (not 16-byte) aligned view falls back to the scalar path."""
     n, rows = 1024, 9
