@@ -213,6 +213,40 @@ def test_kv_store_q8_0(dev, rounding, variant, B, T, decode):
     assert np.array_equal(y, orc.dequantize_q8_0(kch.reshape(-1, rb)[ids]))
 
 
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+def test_kv_store_q8_0_tiles_with_bad_slots(dev, src):
+    """Q8_0 caches whose 32-block store tiles (8 consecutive slots of one head)
+    are written whole, next to tiles with out-of-range slots (stored block by
+    block, the bad rows counted and skipped) and a sequence in a missing set."""
+    print(f"kv_store q8_0 tiles + bad slots {src}", flush=True)
+    D, Nkv, max_seq, B, T = 128, 8, 96, 3, 24
+    k = randn((B, T, Nkv, D), seed=13)
+    v = randn((B, T, Nkv, D), seed=14)
+    if src == "bf16":
+        kb, vb = orc.f32_to_bf16(k), orc.f32_to_bf16(v)
+        k, v = orc.bf16_to_f32(kb), orc.bf16_to_f32(vb)
+        kd, vd = to_dev(kb, dev, bf16=True), to_dev(vb, dev, bf16=True)
+    else:
+        kd, vd = to_dev(k, dev), to_dev(v, dev)
+    rb = D // 32 * 34
+    pos0 = np.array([5, max_seq - 20, 40], np.int32)  # sequence 1: slots past the end from t = 20
+    sets = np.array([0, 2, 9], np.int32)              # set 9 does not exist
+    kc = DTensor.full_byte((3, Nkv, max_seq, rb), 0xA5)
+    vc = DTensor.full_byte((3, Nkv, max_seq, rb), 0x5A)
+    err = DTensor.zeros((1,), "i32")
+    ops.kv_store(kd, ops.Q8(kc), to_dev(pos0, dev), v=vd, v_cache=ops.Q8(vc), sets=to_dev(sets, dev), err=err)
+    assert int(err.item()) == 2 * ((T - 20) * Nkv + T * Nkv)
+    kch, vch = to_np(kc), to_np(vc)
+    written = np.zeros((3, Nkv, max_seq), bool)
+    for b, n in ((0, T), (1, 20)):
+        s, p = sets[b], pos0[b]
+        written[s, :, p:p + n] = True
+        for src_, cache in ((k, kch), (v, vch)):
+            want = orc.quantize_q8_0(src_[b, :n].transpose(1, 0, 2), "x86")
+            assert np.array_equal(cache[s, :, p:p + n], want), f"b={b}"
+    assert (kch[~written] == 0xA5).all() and (vch[~written] == 0x5A).all()
+
+
 def test_kv_store_f16_cache_and_bad_slots(dev):
     """F16 cache (the Qwen3 LM's cache type) and out-of-range slots/sets."""
     D, Nkv, max_seq, B, T = 128, 8, 64, 3, 4
