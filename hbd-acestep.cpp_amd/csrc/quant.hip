@@ -178,15 +178,7 @@ __global__ void __launch_bounds__(256) k_row_q8(const RowCopy K, const RowCopy V
 // chunks, lane-contiguous (every load instruction covers whole cache lines,
 // whatever rows the tile spans), into LDS; then lane pairs quantize one block
 // each (16 elements per lane) from LDS and store the quants and the scale.
-//
-// CT: the host has shown that every tile's 32 blocks are 1088 contiguous,
-// 8-byte aligned destination bytes (KV rows of whole cache slots, a tile never
-// crossing a (sequence, head) run: slots pos0 + i2 .. + 32/nbpr - 1 of one head).
-// The quantized tile is then assembled in LDS (over the consumed source tile)
-// and written with three 8-byte store instructions per wave, rather than nine
-// 2-byte ones per lane scattered over 34-byte blocks. A tile with an invalid
-// slot in any of its rows stores block by block as without CT.
-template <int TI, int ROUND, bool CT>
+template <int TI, int ROUND>
 __global__ void __launch_bounds__(256) k_row_q8_lds(const RowCopy K, const RowCopy V, uint32_t nbk, uint32_t nbv,
                                                     uint32_t wg_k, uint32_t nbpr, FastDiv dnbpr) {
     constexpr int  EI  = TT<TI>::ES;
@@ -236,76 +228,6 @@ __global__ void __launch_bounds__(256) k_row_q8_lds(const RowCopy K, const RowCo
     __builtin_amdgcn_wave_barrier();
 
     // 2. one block per lane pair
-    if constexpr (CT) {
-        // every tile is whole (the host checked); the wave's slots are all valid or it stores per block
-        if (__builtin_amdgcn_ballot_w64(bad) == 0) {
-            float f[16];
-#pragma unroll
-            for (int k = 0; k < 16 / VEC; ++k) {
-                unpack16<TI>(tile[wv][j * CPB + sub * (CPB / 2) + k], f + VEC * k);
-            }
-            float amax = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                amax = fmaxf(amax, fabsf(f[e]));
-            }
-            amax          = group_max<2>(amax);
-            const float d = div127(amax);
-            float       id;
-            if constexpr (ROUND == MI_Q8_0_REF) {
-                id = d != 0.0f ? 1.0f / d : 0.0f;
-            } else {
-                id = amax != 0.0f ? 127.0f / amax : 0.0f;
-            }
-            uint32_t wq[4];
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                uint32_t acc = 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float x = f[4 * q4 + e] * id;
-                    float       q;
-                    if constexpr (ROUND == MI_Q8_0_REF) {
-                        q = round_half_away(x);
-                    } else {
-                        q = __builtin_amdgcn_fmed3f(__builtin_rintf(x), -128.0f, 127.0f);  // saturate like packs
-                    }
-                    acc |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
-                }
-                wq[q4] = acc;
-            }
-            // the tile's first destination byte: lane pair 0's block is block 0 of its row
-            // (an offset from the cache base, so the stores stay global ones)
-            const uint64_t o0 = (uint64_t) (drow + (size_t) bi * 34 - R.dst);
-            char * const   dt = R.dst + (int64_t) (((uint64_t) __builtin_amdgcn_readfirstlane((uint32_t) (o0 >> 32))
-                                                   << 32) |
-                                                  (uint32_t) __builtin_amdgcn_readfirstlane((uint32_t) o0));
-            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // source reads before the tile is overwritten
-            __builtin_amdgcn_wave_barrier();
-            char *     ob = (char *) tile[wv] + j * 34;
-            uint16_t * oq = (uint16_t *) (ob + 2 + sub * 16);
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                oq[2 * q4]     = (uint16_t) (wq[q4] & 0xffffu);
-                oq[2 * q4 + 1] = (uint16_t) (wq[q4] >> 16);
-            }
-            if (sub == 0) {
-                *(uint16_t *) ob = f32_to_f16_bits(d);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            // 136 words of 8 bytes; the third read stays inside the tile for every
-            // lane (at least 2048 bytes), only its store is limited to 8 lanes
-            const uint2 * ow = (const uint2 *) tile[wv];
-            const uint2   o1 = ow[lane], o2 = ow[64 + lane], o3 = ow[128 + lane];
-            st8(dt + 8 * lane, o1);
-            st8(dt + 8 * (64 + lane), o2);
-            if (lane < 8) {
-                st8(dt + 8 * (128 + lane), o3);
-            }
-            return;
-        }
-    }
     if (g >= total) {
         return;  // whole pairs; nothing below synchronizes
     }
@@ -450,21 +372,6 @@ __global__ void __launch_bounds__(256) k_row_copy_generic(const RowCopy K, const
     }
 }
 
-// Every 32-block tile of the staged Q8_0 KV store is 32*34 = 1088 contiguous,
-// 8-byte aligned destination bytes: work rows walk a head's tokens in order
-// (head-major), a row of nbpr blocks fills one cache slot exactly (slot
-// stride = nbpr*34), a tile holds whole rows of one (sequence, head) run
-// (32/nbpr rows, dividing the tokens per sequence), and every base and stride
-// is a multiple of 8.
-static bool tiles_contiguous(const RowCopy & R, uint32_t nbpr) {
-    if (!R.kv || !MI_KV_HEAD_MAJOR || nbpr == 0 || 32 % nbpr != 0) {
-        return false;
-    }
-    const uint32_t rpt = 32 / nbpr;
-    return R.cnb1 == (int64_t) nbpr * 34 && R.ne2 % rpt == 0 && aligned(R.dst, 8) && R.cnb1 % 8 == 0 &&
-           R.cnb2 % 8 == 0 && R.cnb3 % 8 == 0;
-}
-
 template <int TI, int TO, int ROUND>
 static int launch_k(const RowCopy & K, const RowCopy * V, bool fast, hipStream_t s) {
     const RowCopy & Vr = V ? *V : K;
@@ -477,13 +384,8 @@ static int launch_k(const RowCopy & K, const RowCopy * V, bool fast, hipStream_t
             const uint32_t nbv  = total - nbk;
             const uint32_t wg_k = (nbk + 127) / 128;  // 4 waves x 32 blocks per workgroup
             const uint32_t grid = wg_k + (nbv + 127) / 128;
-            if (tiles_contiguous(K, nbpr) && (!V || tiles_contiguous(*V, nbpr))) {
-                hipLaunchKernelGGL((k_row_q8_lds<TI, ROUND, true>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, nbv,
-                                   wg_k, nbpr, FastDiv(nbpr));
-            } else {
-                hipLaunchKernelGGL((k_row_q8_lds<TI, ROUND, false>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, nbv,
-                                   wg_k, nbpr, FastDiv(nbpr));
-            }
+            hipLaunchKernelGGL((k_row_q8_lds<TI, ROUND>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, nbv, wg_k, nbpr,
+                               FastDiv(nbpr));
 #else
             const uint32_t grid = (total * MI_Q8_LPB + 255) / 256;
             hipLaunchKernelGGL((k_row_q8<TI, ROUND>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, total, nbpr,

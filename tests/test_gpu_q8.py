@@ -215,9 +215,9 @@ def test_kv_store_q8_0(dev, rounding, variant, B, T, decode):
 
 @pytest.mark.parametrize("src", ["f32", "bf16"])
 def test_kv_store_q8_0_tiles_with_bad_slots(dev, src):
-    """Q8_0 caches whose 32-block store tiles (8 consecutive slots of one head)
-    are written whole, next to tiles with out-of-range slots (stored block by
-    block, the bad rows counted and skipped) and a sequence in a missing set."""
+    """Q8_0 caches written 8 consecutive slots of one head per wave tile, next
+    to tiles that mix valid and out-of-range slots (the bad rows counted and
+    skipped, the valid ones stored) and a sequence in a missing set."""
     print(f"kv_store q8_0 tiles + bad slots {src}", flush=True)
     D, Nkv, max_seq, B, T = 128, 8, 96, 3, 24
     k = randn((B, T, Nkv, D), seed=13)
