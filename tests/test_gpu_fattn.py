@@ -119,6 +119,31 @@ def _decode_mask(N, n_kv, lens):
 
 
 @pytest.mark.parametrize("kt", ["q8_0", "f16", "bf16", "f32"])
+def test_decode_poisoned_slots_past_each_length(dev, kt):
+    """Decode over caches whose slots past each sequence's length hold NaN bytes
+    (stale or unwritten cache rows), inside tiles that also hold live keys and in
+    whole dead tiles: ggml never reads masked keys, so the output stays finite."""
+    N, Nh, Nkv, n_kv, D = 3, 32, 8, 1024, 128
+    print(f"fa decode poisoned slots kt={kt}", flush=True)
+    lens = [1, 513, 1000]
+    r = _rng(21)
+    q = r.standard_normal((N, Nh, 1, D)).astype(np.float32)
+    k = r.standard_normal((N, Nkv, n_kv, D)).astype(np.float32)
+    v = r.standard_normal((N, Nkv, n_kv, D)).astype(np.float32)
+    for b, L in enumerate(lens):
+        k[b, :, L:] = np.nan
+        v[b, :, L:] = np.nan
+    dk, kf = _kv(k, kt)
+    dv, vf = _kv(v, kt)
+    dm, mf = _mask_dev(_decode_mask(N, n_kv, lens))
+    y = to_np(ops.flash_attn_ext(to_dev(q), dk, dv, dm, 0.125))
+    ref = orc.flash_attn_ext(q, kf, vf, mf, 0.125, kt)
+    assert np.isfinite(y).all() and np.isfinite(ref).all()
+    _check(y, ref, fa_bound(q, np.nan_to_num(kf), np.nan_to_num(vf), mf, 0.125, kt,
+                            _uses_mfma(kt, D, 1, Nh, Nkv, n_kv)))
+
+
+@pytest.mark.parametrize("kt", ["q8_0", "f16", "bf16", "f32"])
 @pytest.mark.parametrize("qt", ["f32", "bf16"])
 def test_decode_gqa_per_sequence_lengths(dev, kt, qt):
     """Qwen3-4B decode shape (32/8 heads x 128), 4 sequences of different lengths over a
