@@ -621,6 +621,9 @@ __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
 // Keys whose mask is -inf get p = 0 (their K/V bytes are multiplied, so they
 // must be finite, as every activation the reference feeds here is).
 // ---------------------------------------------------------------------------
+#ifndef MI_FA_DEC
+#define MI_FA_DEC 1  // decode (one query position, <= 16 heads per KV head) on the 16x16 matrix cores
+#endif
 #ifndef MI_FA_MFMA_MIN_ROWS
 #define MI_FA_MFMA_MIN_ROWS 64  // (query position, head) rows per KV head from which the MFMA path is used
 #endif
@@ -647,6 +650,276 @@ __device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, cons
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     } else {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+}
+
+// Decode on the matrix cores (F16/BF16 K and V, D = 128, one query position,
+// at most 16 query heads per KV head, a mask row shared by every head). A wave
+// owns (key split, sequence, KV head) as k_fa_split does and walks 32-key tiles,
+// the mask's dead tiles skipped before any K/V byte is read, the next tile's
+// loads in flight under the current one's math. With v_mfma_f32_16x16x32
+// (lane l: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16], C[4(l/16)+r][l%16]):
+//   S^T = K Q^T: A = K rows from LDS, B = the query heads (padded to 16) in K's
+//   type; lane l then holds the scores of head l%16 for keys 16 mt + 4 (l/16) + r.
+//   O^T += V^T P^T: B = those 8 probabilities as they sit (a high and a low
+//   16-bit part, two MFMAs), so V^T is stored to LDS with its keys in the same
+//   order: key 16 mt + 4 q + r at column 8 q + 4 mt + r.
+// Keys no head reads (masked, past the end) have p = 0 and zero K/V bytes in
+// LDS, whatever the cache holds there. Partials and the merge are k_fa_split's.
+template <int KT>
+__global__ void __launch_bounds__(64) k_fa_dec(const FaArgs a) {
+    using M          = FaM<KT>;
+    using x8         = typename M::x8;
+    constexpr int D   = 128;
+    constexpr int T   = FA_TILE;       // keys per tile
+    constexpr int KS  = D * 2 + 16;    // K row stride in LDS (bytes)
+    constexpr int VS  = T * 2 + 16;    // V^T row stride (bytes, 16-byte multiple)
+    constexpr int NKS = D / 32;        // k-steps of S (32 dims each)
+    constexpr int NDT = D / 16;        // 16-dim tiles of O^T
+    constexpr int KC  = T * D * 2 / 16 / 64;  // 16-byte K chunks per lane per tile (8)
+    constexpr int VC  = KC / 2;               // V key-pair chunks per lane per tile (4)
+    typedef float f4 __attribute__((ext_vector_type(4)));
+
+    __shared__ __align__(16) char kt[T * KS];
+    __shared__ __align__(16) char vt[D * VS];
+    __shared__ float              mt[FA_MAXT * T];  // the split's mask values
+    __shared__ uint32_t           lt[FA_MAXT];      // per tile: keys some head reads
+
+    const int      lane  = threadIdx.x;
+    const int      c16   = lane & 15, q4 = lane >> 4;
+    const uint32_t split = blockIdx.x;
+    const uint32_t bg    = blockIdx.y;
+    const uint32_t b     = bg / (uint32_t) a.nkv;
+    const uint32_t g     = bg - b * (uint32_t) a.nkv;
+    const bool     rv    = c16 < a.rows;
+    const int      h     = (int) g * a.rk + (rv ? c16 : 0);
+    const uint32_t kb    = b / (uint32_t) a.rk3;
+    const char *   kg    = a.k + (int64_t) kb * a.k3 + (int64_t) g * a.k2;
+    const char *   vg    = a.v + (int64_t) kb * a.v3 + (int64_t) g * a.v2;
+    const char *   mrow  = a.mask ? a.mask + (int64_t) (b % (uint32_t) a.mne3) * a.m3 : nullptr;
+    const int      kbeg  = (int) split * a.chunk;
+    const int      kend  = kbeg + a.chunk < a.n_kv ? kbeg + a.chunk : a.n_kv;
+    const int      nt    = (kend - kbeg + T - 1) / T;
+    const int      key   = lane & 31;
+
+    // the split's mask values (one per key), issued first
+    float ms[FA_MAXT];
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        const int kc = kbeg + t * T + key < kend ? kbeg + t * T + key : kend - 1;
+        ms[t]        = mrow != nullptr && t < nt ? load_elem<MI_TYPE_F16>(mrow + (size_t) kc * 2) : 0.0f;
+    }
+    // Q^T operands: k-step ks holds q[head c16][32 ks + 8 q4 + e] in K's type (RNE)
+    x8 qb[NKS];
+    {
+        const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2;
+        const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const char * p = qp + (size_t) (32 * ks + 8 * q4) * es;
+            float        f[8];
+            if (a.tq == MI_TYPE_F32) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    f[e] = ((const float *) p)[e];
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint16_t hv = ((const uint16_t *) p)[e];
+                    f[e] = a.tq == MI_TYPE_BF16 ? __uint_as_float((uint32_t) hv << 16)
+                                                : (float) __builtin_bit_cast(_Float16, hv);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                qb[ks][e] = __builtin_bit_cast(typename M::e, M::bits(rv ? f[e] : 0.0f));
+            }
+        }
+    }
+    // mask values into LDS and per tile the keys some head reads (the mask row is
+    // every head's, so a masked key is masked for all of them)
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        if (t < nt) {
+            const int   k0 = kbeg + t * T + key;
+            const float x  = k0 < kend ? ms[t] : -INFINITY;
+            if (lane < 32) {
+                mt[t * T + key] = x;
+            }
+            const uint64_t lv = __builtin_amdgcn_ballot_w64(lane < 32 && x != -INFINITY);
+            if (lane == 0) {
+                lt[t] = (uint32_t) lv;
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+
+    // K chunk i: key 4 i + lane / 16, 16-byte part lane % 16 (4 whole rows per
+    // load instruction). V chunk i: keys 2 m and 2 m + 1, m = 4 i + lane / 16, the
+    // same part of both. Keys are clamped into the split; unread keys' bytes are
+    // replaced by zeros.
+    uint4 kc[KC], vc[2 * VC];
+    auto  load_kv = [&](int t0, uint32_t live) {
+        const int nk = kend - t0 < T ? kend - t0 : T;
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+            const int kk = 4 * i + q4;
+            const int kr = kk < nk ? kk : nk - 1;
+            kc[i]        = ld16(kg + (int64_t) (t0 + kr) * a.k1 + c16 * 16);
+            if (!((live >> kk) & 1u)) {
+                kc[i] = make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VC; ++i) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int kk = 2 * (4 * i + q4) + j;
+                const int kr = kk < nk ? kk : nk - 1;
+                vc[2 * i + j] = ld16(vg + (int64_t) (t0 + kr) * a.v1 + c16 * 16);
+                if (!((live >> kk) & 1u)) {
+                    vc[2 * i + j] = make_uint4(0, 0, 0, 0);
+                }
+            }
+        }
+    };
+    // LDS column of key k in V^T (the order of the P operand)
+    auto vcol = [](int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); };
+
+    f4 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        o[dt] = f4{ 0.0f, 0.0f, 0.0f, 0.0f };
+    }
+    float    mrun = -INFINITY, lrun = 0.0f;
+    uint32_t live = nt > 0 ? lt[0] : 0u;
+    if (live) {
+        load_kv(kbeg, live);
+    }
+    for (int t = 0; t < nt; ++t) {
+        const int      t0   = kbeg + t * T;
+        const uint32_t next = t + 1 < nt ? lt[t + 1] : 0u;
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < KC; ++i) {
+                *(uint4 *) (kt + (4 * i + q4) * KS + c16 * 16) = kc[i];
+            }
+#pragma unroll
+            for (int i = 0; i < VC; ++i) {
+                const int      k0   = 2 * (4 * i + q4);
+                const int      col  = vcol(k0);  // even: keys k0, k0 + 1 in one word
+                const uint32_t w0[4] = { vc[2 * i].x, vc[2 * i].y, vc[2 * i].z, vc[2 * i].w };
+                const uint32_t w1[4] = { vc[2 * i + 1].x, vc[2 * i + 1].y, vc[2 * i + 1].z, vc[2 * i + 1].w };
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {  // V^T[8 c16 + e][col], [col + 1]
+                    const uint32_t lo = (w0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                    const uint32_t hi = (w1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                    *(uint32_t *) (vt + (8 * c16 + e) * VS + col * 2) = lo | (hi << 16);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (next) {
+            load_kv(t0 + T, next);  // in flight during this tile's math
+        }
+        if (live) {
+            // S^T for keys 16 mt + [0, 16) x the 16 (padded) heads
+            f4 s[2] = { f4{ 0.0f, 0.0f, 0.0f, 0.0f }, f4{ 0.0f, 0.0f, 0.0f, 0.0f } };
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+                for (int mt2 = 0; mt2 < 2; ++mt2) {
+                    const x8 kv = *(const x8 *) (kt + (16 * mt2 + c16) * KS + (32 * ks + 8 * q4) * 2);
+                    if constexpr (KT == MI_TYPE_BF16) {
+                        s[mt2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qb[ks], s[mt2], 0, 0, 0);
+                    } else {
+                        s[mt2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qb[ks], s[mt2], 0, 0, 0);
+                    }
+                }
+            }
+            // softmax: this lane's 8 keys of head c16, then the other 24 in lanes ^ 16, ^ 32
+            float x[8];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int   kk = 16 * (e >> 2) + 4 * q4 + (e & 3);
+                const float mv = mt[t * T + kk];
+                x[e]           = mv == -INFINITY ? -INFINITY : s[e >> 2][e & 3] * a.scale + mv;
+                tmax           = fmaxf(tmax, x[e]);
+            }
+            tmax           = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+            tmax           = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            const float mn = fmaxf(mrun, tmax);
+            float       alpha = 1.0f;
+            x8          phi, plo;
+            float       psum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float    p  = mn == -INFINITY || x[e] == -INFINITY ? 0.0f : __expf(x[e] - mn);
+                const uint16_t hb = M::bits(p);
+                psum += p;
+                phi[e] = __builtin_bit_cast(typename M::e, hb);
+                plo[e] = __builtin_bit_cast(typename M::e, M::bits(p - M::val(hb)));
+            }
+            if (mn != -INFINITY) {
+                alpha = __expf(mrun - mn);  // exp(-inf) = 0 on the first live tile
+            }
+            mrun = mn;
+            lrun = lrun * alpha + psum;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                o[dt] *= alpha;
+            }
+            // O^T += V^T P^T: A = V^T rows 16 dt + c16 at columns 8 q4 .. + 7
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const x8 va = *(const x8 *) (vt + (16 * dt + c16) * VS + 16 * q4);
+                if constexpr (KT == MI_TYPE_BF16) {
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi, o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo, o[dt], 0, 0, 0);
+                } else {
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, phi, o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, plo, o[dt], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();  // the next tile overwrites kt, vt
+        }
+        live = next;
+    }
+
+    // the head's sum over its 4 lanes; lane (c16, q4) holds O^T[16 dt + 4 q4 + r][c16]
+    lrun += __shfl_xor(lrun, 16, 64);
+    lrun += __shfl_xor(lrun, 32, 64);
+    if (!rv) {
+        return;
+    }
+    if (a.splits == 1) {
+        const float inv = 1.0f / lrun;  // all keys masked: 0 * inf = NaN, as ggml
+        float *     yp  = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) h * a.y1);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                yp[16 * dt + 4 * q4 + r] = o[dt][r] * inv;
+            }
+        }
+    } else {
+        float * wp = a.ws + (((int64_t) split * a.nb * a.nkv + bg) * a.rows + c16) * (D + 2);
+        if (q4 == 0) {
+            wp[0] = mrun;
+            wp[1] = lrun;
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                wp[2 + 16 * dt + 4 * q4 + r] = o[dt][r];
+            }
+        }
     }
 }
 
@@ -1199,6 +1472,12 @@ void flash_attn_plan(FaArgs & a, int D) {
         a.splits = 1;
         return;
     }
+    // decode on the matrix cores: one wave holds every query head of a KV head
+    a.dec = MI_FA_DEC && (a.kt == MI_TYPE_F16 || a.kt == MI_TYPE_BF16) && D == 128 && a.n_q == 1 &&
+            a.rows <= 16 && (a.mask == nullptr || a.mne2 == 1);
+    if (a.dec) {
+        a.rblocks = 1;
+    }
     const int64_t pairs  = (int64_t) a.nb * a.nkv * a.rblocks;
     const int64_t want   = (int64_t) num_cus() * MI_FA_WAVES_PER_CU;
     const int64_t tiles  = (a.n_kv + FA_TILE - 1) / FA_TILE;
@@ -1229,6 +1508,15 @@ size_t flash_attn_workspace(const FaArgs & a, int D) {
 template <int KT, int D>
 static void launch_kd(const FaArgs & a, hipStream_t s) {
     const dim3 grid((uint32_t) a.splits, (uint32_t) (a.nb * a.nkv), (uint32_t) a.rblocks);
+    if constexpr (D == 128 && (KT == MI_TYPE_F16 || KT == MI_TYPE_BF16)) {
+        if (a.dec) {
+            hipLaunchKernelGGL((k_fa_dec<KT>), grid, dim3(64), 0, s, a);
+            if (a.splits > 1) {
+                hipLaunchKernelGGL((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(256), 0, s, a);
+            }
+            return;
+        }
+    }
     if constexpr (D == 64 && KT != MI_TYPE_F32) {
         if (fa_rb(a.rows, D, KT) == 8) {
             hipLaunchKernelGGL((k_fa_split<KT, D, 8>), grid, dim3(64), 0, s, a);

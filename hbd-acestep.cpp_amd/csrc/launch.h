@@ -152,6 +152,7 @@ struct FaArgs {
     int          mne2, mne3;
     int          mshared;  // every row of a wave uses one mask row (set by flash_attn_plan)
     int          mfma;     // the matrix-core prefill path (set by flash_attn_plan)
+    int          dec;      // the matrix-core decode kernel (set by flash_attn_plan)
     int          yvec;     // y rows 16-byte aligned
     int          mvec;     // mask rows 8-byte aligned (4 fp16 per load)
     int          ngq;      // matrix-core path: groups of 16 query positions in the mask summary

@@ -71,9 +71,15 @@ def _check(y, ref, bound):
         assert np.all(err <= b), f"{int((err > b).sum())} elements beyond the bound (worst {err[worst]:.3e} > {b[worst]:.3e})"
 
 
-def _uses_mfma(kt, D, n_q, Nh, Nkv, n_kv):
-    """The launch plan's choice of the matrix-core path (flash_attn_plan)."""
-    return kt in ("f16", "bf16") and D == 128 and n_q * (Nh // Nkv) >= 64 and n_kv > 0
+def _uses_mfma(kt, D, n_q, Nh, Nkv, n_kv, mask=None):
+    """The launch plan's choice of a matrix-core kernel (flash_attn_plan): F16/BF16
+    K/V at D = 128, with 64 or more query rows per KV head (prefill), or one query
+    position, at most 16 heads per KV head and a mask row shared by every head
+    (decode). Both keep P as two 16-bit parts."""
+    if kt not in ("f16", "bf16") or D != 128 or n_kv <= 0:
+        return False
+    dec = n_q == 1 and Nh // Nkv <= 16 and (mask is None or mask.shape[1] == 1)
+    return n_q * (Nh // Nkv) >= 64 or dec
 
 
 def _run(N, Nh, Nkv, n_q, n_kv, D, kt, qt="f32", mask=None, scale=None, seed=0, Nk3=None, kview=None):
@@ -99,7 +105,7 @@ def _run(N, Nh, Nkv, n_q, n_kv, D, kt, qt="f32", mask=None, scale=None, seed=0, 
     y = to_np(ops.flash_attn_ext(dq, dk, dv, dm, float(scale)))
     rep = N // Nk3  # the oracle takes one KV batch per q batch (ggml: KV batch b // rep)
     ref = orc.flash_attn_ext(qf, np.repeat(kf, rep, axis=0), np.repeat(vf, rep, axis=0), mf, float(scale), kt)
-    bound = fa_bound(qf, kf, vf, mf, float(scale), kt, _uses_mfma(kt, D, n_q, Nh, Nkv, n_kv))
+    bound = fa_bound(qf, kf, vf, mf, float(scale), kt, _uses_mfma(kt, D, n_q, Nh, Nkv, n_kv, mf))
     _check(y, ref, bound)
     if kt == "f16":  # ggml-cpu's own F16-V result: within its carried fp16 errors plus our bound
         y16, bud = orc.flash_attn_ext_f16acc(qf, np.repeat(kf, rep, axis=0),
@@ -140,7 +146,7 @@ def test_decode_poisoned_slots_past_each_length(dev, kt):
     ref = orc.flash_attn_ext(q, kf, vf, mf, 0.125, kt)
     assert np.isfinite(y).all() and np.isfinite(ref).all()
     _check(y, ref, fa_bound(q, np.nan_to_num(kf), np.nan_to_num(vf), mf, 0.125, kt,
-                            _uses_mfma(kt, D, 1, Nh, Nkv, n_kv)))
+                            _uses_mfma(kt, D, 1, Nh, Nkv, n_kv, mf)))
 
 
 @pytest.mark.parametrize("kt", ["q8_0", "f16", "bf16", "f32"])
@@ -152,6 +158,17 @@ def test_decode_gqa_per_sequence_lengths(dev, kt, qt):
     print(f"fa decode kt={kt} qt={qt}", flush=True)
     lens = [1, 300, 1025, 1280]
     _run(N, 32, 8, 1, n_kv, 128, kt, qt, mask=_decode_mask(N, n_kv, lens), seed=1, kview=2048)
+
+
+@pytest.mark.parametrize("rk,masked,kt,qt", [(16, False, "f16", "f32"), (1, True, "bf16", "bf16"),
+                                               (2, False, "bf16", "f32"), (8, True, "f16", "bf16")])
+def test_decode_heads_per_kv_head(dev, rk, masked, kt, qt):
+    """One query position with 1 to 16 query heads per KV head (the decode
+    kernel pads them to 16), with and without a mask, over a ragged 777 keys."""
+    print(f"fa decode rk={rk} masked={masked} kt={kt} qt={qt}", flush=True)
+    N, Nkv, n_kv = 3, 2, 777
+    mask = _decode_mask(N, n_kv, [777, 40, 500]) if masked else None
+    _run(N, Nkv * rk, Nkv, 1, n_kv, 128, kt, qt, mask=mask, seed=31 + rk)
 
 
 @pytest.mark.parametrize("kt", ["q8_0", "f16"])
@@ -213,7 +230,7 @@ def test_fully_masked_rows_and_poisoned_masked_keys(dev):
     assert np.isnan(y[0, 1]).all() and np.isnan(ref[0, 1]).all()
     assert np.isfinite(y[1]).all()
     _check(y, ref, fa_bound(q, np.nan_to_num(kf), np.nan_to_num(vf), mf, 0.125, "f16",
-                            _uses_mfma("f16", D, n_q, Nh, Nkv, n_kv)))
+                            _uses_mfma("f16", D, n_q, Nh, Nkv, n_kv, mf)))
 
 
 def test_empty_key_range_is_nan(dev):
