@@ -666,8 +666,16 @@ __device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, cons
 //   order: key 16 mt + 4 q + r at column 8 q + 4 mt + r.
 // Keys no head reads (masked, past the end) have p = 0 and zero K/V bytes in
 // LDS, whatever the cache holds there. Partials and the merge are k_fa_split's.
+#ifndef MI_FA_DEC_WPE
+#define MI_FA_DEC_WPE 0  // > 0: ask the compiler for at least this many waves per SIMD
+#endif
+#if MI_FA_DEC_WPE > 0
+#define MI_FA_DEC_OCC __attribute__((amdgpu_waves_per_eu(MI_FA_DEC_WPE, 8)))
+#else
+#define MI_FA_DEC_OCC
+#endif
 template <int KT>
-__global__ void __launch_bounds__(64) k_fa_dec(const FaArgs a) {
+__global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
     using M          = FaM<KT>;
     using x8         = typename M::x8;
     constexpr int D   = 128;
