@@ -858,7 +858,7 @@ def main():
                     help="time the Q8_0 mul_mat of the Qwen3-4B decode projections and LM head at batch 8")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); every op of the path is "
+        print(f"bench.py: measures one GPU only (asked for --gpus {args.gpus}); every op of the path is "
               "row-parallel and shards by rows with no communication, so per-GPU throughput is the N=1 figure.",
               file=sys.stderr)
         sys.exit(2)

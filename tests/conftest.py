@@ -18,7 +18,7 @@ def _have_gpu() -> bool:
 
 
 def pytest_collection_modifyitems(config, items):
-    # Without a GPU device node (this build container) GPU tests are skipped;
+    # Without a GPU device node (a machine with no GPU) GPU tests are skipped;
     # on a machine with a GPU they always run, so a broken device fails instead of skipping.
     if _have_gpu():
         return
