@@ -680,7 +680,6 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
     using x8         = typename M::x8;
     constexpr int D   = 128;
     constexpr int T   = FA_TILE;       // keys per tile
-    constexpr int KS  = D * 2 + 16;    // K row stride in LDS (bytes)
     constexpr int VS  = T * 2 + 16;    // V^T row stride (bytes, 16-byte multiple)
     constexpr int NKS = D / 32;        // k-steps of S (32 dims each)
     constexpr int NDT = D / 16;        // 16-dim tiles of O^T
@@ -688,7 +687,6 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
     constexpr int VC  = KC / 2;               // V key-pair chunks per lane per tile (4)
     typedef float f4 __attribute__((ext_vector_type(4)));
 
-    __shared__ __align__(16) char kt[T * KS];
     __shared__ __align__(16) char vt[D * VS];
     __shared__ float              mt[FA_MAXT * T];  // the split's mask values
     __shared__ uint32_t           lt[FA_MAXT];      // per tile: keys some head reads
@@ -764,22 +762,27 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 
-    // K chunk i: key 4 i + lane / 16, 16-byte part lane % 16 (4 whole rows per
-    // load instruction). V chunk i: keys 2 m and 2 m + 1, m = 4 i + lane / 16, the
-    // same part of both. Keys are clamped into the split; unread keys' bytes are
-    // replaced by zeros.
-    uint4 kc[KC], vc[2 * VC];
-    auto  load_kv = [&](int t0, uint32_t live) {
+    // K goes straight into the S MFMAs' A operands: lane (c16, q4) of k-step ks
+    // holds K[key 16 mt + c16][32 ks + 8 q4 .. + 7] (a masked key's score is
+    // replaced by -inf, whatever its bytes). V chunk i: keys 2 m and 2 m + 1,
+    // m = 4 i + lane / 16, the same 16-byte part of both; unread keys' V bytes
+    // are replaced by zeros. Keys are clamped into the split.
+    x8    ka[2][NKS];
+    uint4 vc[2 * VC];
+    auto  load_k = [&](int t0) {
         const int nk = kend - t0 < T ? kend - t0 : T;
 #pragma unroll
-        for (int i = 0; i < KC; ++i) {
-            const int kk = 4 * i + q4;
+        for (int mt2 = 0; mt2 < 2; ++mt2) {
+            const int kk = 16 * mt2 + c16;
             const int kr = kk < nk ? kk : nk - 1;
-            kc[i]        = ld16(kg + (int64_t) (t0 + kr) * a.k1 + c16 * 16);
-            if (!((live >> kk) & 1u)) {
-                kc[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                ka[mt2][ks] = __builtin_bit_cast(x8, ld16(kg + (int64_t) (t0 + kr) * a.k1 + (32 * ks + 8 * q4) * 2));
             }
         }
+    };
+    auto load_v = [&](int t0, uint32_t live) {
+        const int nk = kend - t0 < T ? kend - t0 : T;
 #pragma unroll
         for (int i = 0; i < VC; ++i) {
 #pragma unroll
@@ -804,16 +807,13 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
     float    mrun = -INFINITY, lrun = 0.0f;
     uint32_t live = nt > 0 ? lt[0] : 0u;
     if (live) {
-        load_kv(kbeg, live);
+        load_k(kbeg);
+        load_v(kbeg, live);
     }
     for (int t = 0; t < nt; ++t) {
         const int      t0   = kbeg + t * T;
         const uint32_t next = t + 1 < nt ? lt[t + 1] : 0u;
         if (live) {
-#pragma unroll
-            for (int i = 0; i < KC; ++i) {
-                *(uint4 *) (kt + (4 * i + q4) * KS + c16 * 16) = kc[i];
-            }
 #pragma unroll
             for (int i = 0; i < VC; ++i) {
                 const int      k0   = 2 * (4 * i + q4);
@@ -831,23 +831,27 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
             __builtin_amdgcn_wave_barrier();
         }
         if (next) {
-            load_kv(t0 + T, next);  // in flight during this tile's math
+            load_v(t0 + T, next);  // in flight during this tile's math
         }
+        f4 s[2] = { f4{ 0.0f, 0.0f, 0.0f, 0.0f }, f4{ 0.0f, 0.0f, 0.0f, 0.0f } };
         if (live) {
             // S^T for keys 16 mt + [0, 16) x the 16 (padded) heads
-            f4 s[2] = { f4{ 0.0f, 0.0f, 0.0f, 0.0f }, f4{ 0.0f, 0.0f, 0.0f, 0.0f } };
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) {
 #pragma unroll
                 for (int mt2 = 0; mt2 < 2; ++mt2) {
-                    const x8 kv = *(const x8 *) (kt + (16 * mt2 + c16) * KS + (32 * ks + 8 * q4) * 2);
                     if constexpr (KT == MI_TYPE_BF16) {
-                        s[mt2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qb[ks], s[mt2], 0, 0, 0);
+                        s[mt2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[mt2][ks], qb[ks], s[mt2], 0, 0, 0);
                     } else {
-                        s[mt2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qb[ks], s[mt2], 0, 0, 0);
+                        s[mt2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[mt2][ks], qb[ks], s[mt2], 0, 0, 0);
                     }
                 }
             }
+        }
+        if (next) {
+            load_k(t0 + T);  // the A operands are free once this tile's S is issued
+        }
+        if (live) {
             // softmax: this lane's 8 keys of head c16, then the other 24 in lanes ^ 16, ^ 32
             float x[8];
             float tmax = -INFINITY;
@@ -894,7 +898,7 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-            __builtin_amdgcn_wave_barrier();  // the next tile overwrites kt, vt
+            __builtin_amdgcn_wave_barrier();  // the next tile overwrites vt
         }
         live = next;
     }
