@@ -511,6 +511,9 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
     }
 }
 
+#ifndef MI_MMV_NORED_MIN
+#define MI_MMV_NORED_MIN 8  // waves per CU from which key splits stop at one workgroup per row group (0: never)
+#endif
 #ifndef MI_MMV_WAVES_PER_CU
 #define MI_MMV_WAVES_PER_CU 16  // waves to spread one product over, per CU
 #endif
@@ -530,6 +533,11 @@ void mul_mat_q8_0_plan(MmvArgs & a, int cus) {
     }
     const uint32_t want = (uint32_t) (cus > 0 ? cus : 256) * MI_MMV_WAVES_PER_CU;
     uint32_t       s    = a.ng == 0 || a.ng >= want ? 1 : (want + a.ng - 1) / a.ng;
+    // when one workgroup per row group (its splits added in LDS) still gives the
+    // grid enough waves, stop there: no partials, no second launch to add them
+    if (MI_MMV_NORED_MIN > 0 && s > 8 && (uint64_t) a.ng * 8 >= (uint64_t) (cus > 0 ? cus : 256) * MI_MMV_NORED_MIN) {
+        s = 8;
+    }
     if (s > a.nbk) {
         s = a.nbk;
     }
