@@ -115,14 +115,13 @@ class Qwen3DecodeLayer:
             h1, gu = ops.mul_mat_q8_0_add_rms_norm(self.w["gu"], hidden, ao, self.post_norm_w, self.eps,
                                                    out_sum=self._buf("h1", (N, H)), out=self._buf("gu", (N, 2 * I)),
                                                    workspace=self._ws("gu", hidden), stream=st)
-        # swiglu and the down projection in one call: the SwiGLU values are made
-        # inside the quantization of the product's x (bit-identical to the two ops)
-        mlp = ops.mul_mat_q8_0_swiglu(self.w["down"], gu, out=self._buf("mlp", (N, H)),
-                                      workspace=self._ws_glu("down", gu), stream=st)
+        # swiglu, the down projection and the residual add in one call: the SwiGLU
+        # values are made inside the quantization of the product's x, and h1 is
+        # added (then clamped under clamp_fp16) where the product's sum is formed
+        # (bit-identical to the three ops)
         y = out if out is not None else self._buf("out", (N, H))
-        if self.clamp_fp16:
-            return ops.add_clamp(h1, mlp, -FP16_MAX, FP16_MAX, out=y, stream=st)
-        return ops.add(h1, mlp, out=y, stream=st)
+        return ops.mul_mat_q8_0_swiglu_add(self.w["down"], gu, h1, clamp=(-FP16_MAX, FP16_MAX) if self.clamp_fp16 else None,
+                                           out=y, workspace=self._ws_glu("down", gu), stream=st)
 
     def _ws(self, name, x):
         need = ops.mul_mat_q8_0_workspace(self.w[name], x)

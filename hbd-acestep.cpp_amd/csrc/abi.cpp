@@ -1105,6 +1105,48 @@ int mi_mul_mat_q8_0_swiglu(const void * w, int64_t k, int64_t n, const mi_tensor
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 
+int mi_mul_mat_q8_0_swiglu_add(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
+                               const mi_tensor * r, int clamp, float lo, float hi, const mi_tensor * y, void * workspace,
+                               size_t workspace_bytes, mi_stream stream) {
+    if (!y || !r) {
+        return MI_ERR_NULL;
+    }
+    MmvArgs a;
+    MI_TRY(mm_glu_desc(w, k, n, gu, swapped, y, a));
+    MI_TRY(check(r));
+    if (r->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (!same_shape(*r, *y) || !uniform_rows(*r) || r->nb[0] != 4) {
+        return MI_ERR_SHAPE;
+    }
+    if (clamp && !(lo <= hi)) {
+        return MI_ERR_PARAM;
+    }
+    if (a.m == 0 || a.n == 0) {
+        return MI_OK;
+    }
+    if (!w) {
+        return MI_ERR_NULL;
+    }
+    if (!aligned(w, 16)) {
+        return MI_ERR_ALIGN;
+    }
+    if (!workspace || workspace_bytes < mul_mat_q8_0_workspace(a)) {
+        return MI_ERR_PARAM;
+    }
+    if (!aligned(workspace, 256)) {
+        return MI_ERR_ALIGN;
+    }
+    a.res    = (const char *) r->data;
+    a.res1   = (int64_t) r->nb[1];
+    a.rclamp = clamp != 0;
+    a.rlo    = lo;
+    a.rhi    = hi;
+    mul_mat_q8_0_bind(a, (char *) workspace);
+    return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
+}
+
 static int mm_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * b,
                    const mi_tensor * norm_w, float eps, const mi_tensor * sum, const mi_tensor * y, void * workspace,
                    size_t workspace_bytes, mi_stream stream) {

@@ -30,11 +30,6 @@ struct BinArgs {
     float         lo, hi;
 };
 
-__device__ __forceinline__ float clamp_ggml(float v, float lo, float hi) {
-    const float t = v < hi ? v : hi;
-    return t > lo ? t : lo;
-}
-
 template <int OP, bool BROW>
 __device__ __forceinline__ float bin_apply(float a, float b, float v0, float v1) {
     if constexpr (OP == OP_ADD) {

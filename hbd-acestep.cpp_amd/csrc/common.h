@@ -393,6 +393,12 @@ __device__ __forceinline__ float log_f32(float x) {
 // mean = (float)(sum / n), scale = 1.0f / sqrtf(mean + eps). For n a power of
 // two, sum / n == sum * (1/n) exactly (a sum of float squares is never a
 // double subnormal), so the division becomes a multiply.
+// ggml_clamp: MAX(MIN(v, hi), lo) with C's comparison macros (a NaN becomes hi)
+__device__ __forceinline__ float clamp_ggml(float v, float lo, float hi) {
+    const float t = v < hi ? v : hi;
+    return t > lo ? t : lo;
+}
+
 // RMSNorm sum of squares. F32 activations: ggml's arithmetic, the float
 // square summed in double. BF16/F16 activations: fp32 accumulation (one fma
 // per element), the arithmetic the bf16 bar is stated for; it keeps the

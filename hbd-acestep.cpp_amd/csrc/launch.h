@@ -202,6 +202,10 @@ struct MmvArgs {
     const char * g;
     const char * u;
     int64_t      gu1;
+    const char * res;          // non-null: y = y + res (ggml_add after the product), rows at stride res1,
+    int64_t      res1;         // then clamped to [rlo, rhi] when rclamp (ggml_clamp)
+    int          rclamp;
+    float        rlo, rhi;
     char *       xq;           // workspace: quantized x [m][k]
     float *      xd;           //            scales [m][nbk]
     float *      part;         //            partials [splits][m][npad] (splits > 1)

@@ -233,6 +233,19 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
 #define MI_MMV_UNROLL 4  // blocks whose weight loads are issued together
 #endif
 
+// y element (m, n) as stored: the product, or ggml_add(product, res) then, with
+// rclamp, ggml_clamp -- the residual add fused after the product (one rounding,
+// as the separate add; the add is commutative, so the operand order is ggml's)
+__device__ __forceinline__ float mm_epilogue(const MmvArgs & a, uint32_t m, uint32_t n, float v) {
+    if (a.res != nullptr) {
+        v = v + *(const float *) (a.res + (int64_t) m * a.res1 + (int64_t) n * 4);
+        if (a.rclamp) {
+            v = clamp_ggml(v, a.rlo, a.rhi);
+        }
+    }
+    return v;
+}
+
 template <int M>
 __global__ void __launch_bounds__(512) k_mmv_q8_0(const MmvArgs a) {
     extern __shared__ float red[];  // [wave][m][lane], W * M * 64 floats when W > 1
@@ -317,7 +330,7 @@ __global__ void __launch_bounds__(512) k_mmv_q8_0(const MmvArgs a) {
     const uint32_t row = g * 64 + l;
     auto store_y = [&](int m, float v) {
         if (row < a.n) {
-            *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = v;
+            *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = mm_epilogue(a, (uint32_t) m, row, v);
         }
     };
     if (W == 1 && a.splits == 1) {
@@ -375,7 +388,7 @@ __global__ void __launch_bounds__(256) k_mmv_reduce(const MmvArgs a) {
     for (; s2 < a.splits; ++s2) {
         v += pp[s2 * st];
     }
-    *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = v;
+    *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = mm_epilogue(a, m, row, v);
 }
 
 
@@ -503,7 +516,7 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t m = m0 + 32 * i + 8 * q + 4 * hh + e;
                     if (m < a.m) {
-                        *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) n * 4) = acc[i][j][4 * q + e];
+                        *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) n * 4) = mm_epilogue(a, m, n, acc[i][j][4 * q + e]);
                     }
                 }
             }

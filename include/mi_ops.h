@@ -303,6 +303,19 @@ int mi_mul_mat_q8_0_swiglu_workspace(int64_t k, int64_t n, const mi_tensor * gu,
 int mi_mul_mat_q8_0_swiglu(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
                            const mi_tensor * y, void * workspace, size_t workspace_bytes, mi_stream stream);
 
+/* The down projection with the residual add after it, as one call:
+ * y = ggml_add(ggml_mul_mat(w, ggml_swiglu(gu)), r), then ggml_clamp(y, lo, hi)
+ * when clamp != 0 (qwen3-lm.h:736-741: the MLP output added to the
+ * post-attention residual, clamped to the fp16 range under clamp_fp16). r F32
+ * of y's shape (rows uniformly strided; y may be r). The residual is added
+ * where the product's sum is formed, so y is bit-identical to
+ * mi_mul_mat_q8_0_swiglu followed by mi_add (or mi_add_clamp), without the
+ * product's round trip through memory or the extra launch. Workspace as
+ * mi_mul_mat_q8_0_swiglu. */
+int mi_mul_mat_q8_0_swiglu_add(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
+                               const mi_tensor * r, int clamp, float lo, float hi, const mi_tensor * y, void * workspace,
+                               size_t workspace_bytes, mi_stream stream);
+
 /* The RMSNorm -> product pair as one call: y = ggml_mul_mat(w,
  * ggml_mul(ggml_rms_norm(x, eps), norm_w)) (qwen3-lm.h:632-639, the input norm
  * feeding the fused QKV projection; qwen3_rms_norm, qwen3-enc.h:114-120). x F32

@@ -286,6 +286,17 @@ def test_mul_mat_q8_0_validation():
     assert mg(W, k, n, R(gu), 0, None, None, 0, NULL_S) == -1
     assert mg(W, k, n, R(gu), 1, R(y), ctypes.c_void_p(1 << 20), wsn - 1, NULL_S) == -6
     assert mg(W, k, n, R(gu), 1, R(y), ctypes.c_void_p((1 << 20) + 16), wsn, NULL_S) == -5
+    # with the residual add after it: r F32 of y's shape; clamp bounds ordered
+    mr = L.mi_mul_mat_q8_0_swiglu_add
+    lo, hi = ctypes.c_float(-65504.0), ctypes.c_float(65504.0)
+    r = _t([n, m])
+    assert mr(W, k, n, R(gu), 0, None, 0, lo, hi, R(y), None, 0, NULL_S) == -1
+    assert mr(W, k, n, R(gu), 0, R(r), 0, lo, hi, None, None, 0, NULL_S) == -1
+    assert mr(W, k, n, R(gu), 0, R(_t([n, m], BF16)), 0, lo, hi, R(y), None, 0, NULL_S) == -2
+    assert mr(W, k, n, R(gu), 0, R(_t([n, m + 1])), 0, lo, hi, R(y), None, 0, NULL_S) == -3
+    assert mr(W, k, n, R(gu), 0, R(r), 1, hi, lo, R(y), None, 0, NULL_S) == -6     # lo > hi
+    assert mr(W, k, n, R(gu), 0, R(r), 1, lo, hi, R(y), ctypes.c_void_p(1 << 20), wsn - 1, NULL_S) == -6
+    assert mr(W, k, n, R(gu), 0, R(r), 1, lo, hi, R(y), ctypes.c_void_p((1 << 20) + 16), wsn, NULL_S) == -5
 
 
 def test_sampler_validation():

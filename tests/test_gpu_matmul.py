@@ -158,6 +158,34 @@ def test_swiglu_prologue_matches_swiglu_then_mul_mat(dev, n, k, m, swapped):
     _check(y_f, w, to_np(ff))
 
 
+@pytest.mark.parametrize("n,k,m,clamp,inplace", [
+    (2560, 9728, 8, False, False),   # Qwen3-4B down projection: key splits summed by the second launch
+    (2560, 9728, 8, True, True),     # clamp_fp16, the residual buffer updated in place
+    (16448, 256, 4, True, False),    # 257 row groups: splits added in LDS, one launch
+    (640, 256, 129, False, False),   # the matrix kernel
+    (640, 256, 129, True, True),
+])
+def test_swiglu_down_with_residual_add(dev, n, k, m, clamp, inplace):
+    """mi_mul_mat_q8_0_swiglu_add against mi_mul_mat_q8_0_swiglu then mi_add /
+    mi_add_clamp: bit-identical on every path that forms the product's sum. The
+    residual is scaled past the fp16 range in the clamped cases."""
+    print(f"mul_mat q8_0 swiglu + add n={n} k={k} m={m} clamp={clamp} inplace={inplace}", flush=True)
+    r = np.random.default_rng(n + k + m + int(clamp))
+    w = orc.quantize_q8_0((r.standard_normal((n, k)) * 0.05).astype(np.float32))
+    gu = (r.standard_normal((m, 2 * k)) * 2.0).astype(np.float32)
+    res = (r.standard_normal((m, n)) * (1e5 if clamp else 1.0)).astype(np.float32)
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    dgu, dres = to_dev(gu), to_dev(res)
+    lim = (-65504.0, 65504.0) if clamp else None
+    y_f = to_np(ops.mul_mat_q8_0_swiglu_add(wr, dgu, dres, clamp=lim, out=dres if inplace else None))
+    mlp = ops.mul_mat_q8_0_swiglu(wr, dgu)
+    dres2 = to_dev(res)
+    y_u = to_np(ops.add_clamp(dres2, mlp, *lim) if clamp else ops.add(dres2, mlp))
+    assert np.array_equal(y_f, y_u)
+    if clamp:
+        assert (np.abs(res) > 65504.0).any() and np.abs(y_f).max() <= 65504.0
+
+
 def test_swiglu_prologue_strided_rows(dev):
     """gu rows at a stride that is not a multiple of 16 bytes (element loads)."""
     print("mul_mat q8_0 swiglu strided", flush=True)

@@ -126,8 +126,12 @@ def test_decode_layer_stage_by_stage(dev, kv_type, clamp):
         assert_mul_mat_q8_0(b["gu"], Wgu, b["n2"])
     else:
         assert_mul_mat_q8_0(b["gu"], Wgu, orc.rms_norm_mul(h1, nw_post, eps))
-    # 7. SwiGLU -> down product; the last residual sum bit-exact
-    assert_mul_mat_q8_0(b["mlp"], Wd, orc.swiglu(b["gu"]))
-    out = orc.add_clamp(h1, b["mlp"]) if clamp else orc.add(h1, b["mlp"])
+    # 7. SwiGLU -> down product; the last residual sum bit-exact. The layer adds
+    # h1 inside the down product's call (mi_mul_mat_q8_0_swiglu_add), which equals
+    # mi_mul_mat_q8_0_swiglu then the add: the device's product alone is that
+    # call on the layer's own gate/up output
+    mlp = to_np(ops.mul_mat_q8_0_swiglu(layer.w["down"], layer._bufs["gu"]))
+    assert_mul_mat_q8_0(mlp, Wd, orc.swiglu(b["gu"]))
+    out = orc.add_clamp(h1, mlp) if clamp else orc.add(h1, mlp)
     assert np.array_equal(y, out)
     assert np.all(np.isfinite(y))
