@@ -777,10 +777,16 @@ def gemv_bench(steps: int):
 
 # ---------------------------------------------------------------------------
 # One whole Qwen3-4B decoder layer on the device (reported with --decode-layer):
-# batch 8, Q8_0 weights, Q8_0 KV cache of 8192 slots per sequence, lengths
-# U[1, 8192] and the 256-bucketed read (qw3lm_forward_batch, qwen3-lm.h:626-741).
+# batch 8, Q8_0 weights, an F16 KV cache (the LM's own, qwen3-lm.h:190-191) and a
+# Q8_0 one, 8192 slots per sequence, lengths U[1, 8192] and the 256-bucketed read
+# (qw3lm_forward_batch, qwen3-lm.h:626-741). One JSON line per cache type.
 # ---------------------------------------------------------------------------
 def decode_layer_bench(steps: int):
+    for kv_type in ("f16", "q8_0"):
+        decode_layer_bench_kv(steps, kv_type)
+
+
+def decode_layer_bench_kv(steps: int, kv_type: str):
     from acestep_ops import device, ops
     from acestep_ops.device import DTensor, Event, Graph, Stream
     from acestep_ops.qwen3 import Qwen3DecodeLayer, decode_mask
@@ -802,12 +808,20 @@ def decode_layer_bench(steps: int):
 
     ones = lambda n: DTensor.from_numpy(np.ones(n, np.float32))  # noqa: E731
     layer = Qwen3DecodeLayer(q8w((Nh + 2 * Nkv) * D, H), q8w(H, Nh * D), q8w(2 * I, H), q8w(H, I), ones(H), ones(H),
-                             ones(D), ones(D), H, Nh, Nkv, D, I, SLOTS, N, "q8_0", stream=sh)
-    kb = np.zeros((N, Nkv, SLOTS, D // 32 * 34), np.uint8)
-    kb[..., 2:] = rng.integers(-127, 128, kb[..., 2:].shape, dtype=np.int8).view(np.uint8)
-    kb.reshape(-1, 34)[:, :2] = np.full((kb.size // 34, 1), 1e-2, np.float16).view(np.uint8)
-    layer.k_cache = ops.Q8(DTensor.from_numpy(kb))
-    layer.v_cache = ops.Q8(DTensor.from_numpy(kb))
+                             ones(D), ones(D), H, Nh, Nkv, D, I, SLOTS, N, kv_type, stream=sh)
+    if kv_type == "q8_0":
+        kb = np.zeros((N, Nkv, SLOTS, D // 32 * 34), np.uint8)
+        kb[..., 2:] = rng.integers(-127, 128, kb[..., 2:].shape, dtype=np.int8).view(np.uint8)
+        kb.reshape(-1, 34)[:, :2] = np.full((kb.size // 34, 1), 1e-2, np.float16).view(np.uint8)
+        layer.k_cache = ops.Q8(DTensor.from_numpy(kb))
+        layer.v_cache = ops.Q8(DTensor.from_numpy(kb))
+        row_bytes = D // 32 * 34
+    else:
+        kh = rng.standard_normal((N, Nkv, SLOTS, D), dtype=np.float32).astype(np.float16)
+        layer.k_cache = DTensor.from_numpy(kh.view(np.uint16), "f16")
+        layer.v_cache = DTensor.from_numpy(kh.view(np.uint16), "f16")
+        row_bytes = D * 2
+        del kh
     hidden = DTensor.from_numpy(rng.standard_normal((N, H), dtype=np.float32))
     out = DTensor.empty((N, H), "f32")
     dpos, dsets = DTensor.from_numpy(pos), DTensor.from_numpy(np.arange(N, dtype=np.int32))
@@ -827,10 +841,12 @@ def decode_layer_bench(steps: int):
     e1.synchronize()
     us = 1000.0 * e0.elapsed_ms(e1) / steps
     wbytes = sum(w.n * (w.k // 32) * 34 for w in layer.w.values())
-    kvb = N * Nkv * read * (D // 32 * 34) * 2
-    print(json.dumps({"config": f"Qwen3-4B decode layer, batch {N}, Q8_0 weights and KV cache ({SLOTS} slots, lengths "
-                                f"U[1,{SLOTS}], read {read}), every op on the device",
-                      "us_per_layer": round(us, 2), "weight_bytes": wbytes, "kv_bytes_read": kvb,
+    # K/V bytes the step must read: each sequence's live keys (the mask's -inf tail
+    # of the 256-bucketed read is skipped before any byte of it is loaded).
+    kvb = int(lens.sum()) * Nkv * row_bytes * 2
+    print(json.dumps({"config": f"Qwen3-4B decode layer, batch {N}, Q8_0 weights, {kv_type.upper()} KV cache ({SLOTS} "
+                                f"slots, lengths U[1,{SLOTS}], read {read}), every op on the device",
+                      "us_per_layer": round(us, 2), "weight_bytes": wbytes, "kv_bytes_live": kvb,
                       "GB/s": round((wbytes + kvb) / (us * 1e-6) / 1e9, 1),
                       "frac": round((wbytes + kvb) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
                       "tokens_per_s_36_layers": round(N / (36 * us * 1e-6), 1)}), flush=True)
@@ -853,7 +869,7 @@ def main():
     ap.add_argument("--attention", action="store_true",
                     help="time flash attention over the KV cache at the C2 decode shape (one JSON line per cache type)")
     ap.add_argument("--decode-layer", action="store_true",
-                    help="time one whole Qwen3-4B decoder layer at batch 8 (Q8_0 weights and KV cache), all on the device")
+                    help="time one whole Qwen3-4B decoder layer at batch 8 (Q8_0 weights; F16 and Q8_0 KV caches), all on the device")
     ap.add_argument("--gemv", action="store_true",
                     help="time the Q8_0 mul_mat of the Qwen3-4B decode projections and LM head at batch 8")
     args = ap.parse_args()
