@@ -1162,10 +1162,9 @@ k_fa_mfma(const FaArgs a) {
             const uint32_t a0[4] = { vr[2 * i].x, vr[2 * i].y, vr[2 * i].z, vr[2 * i].w };
             const uint32_t a1[4] = { vr[2 * i + 1].x, vr[2 * i + 1].y, vr[2 * i + 1].z, vr[2 * i + 1].w };
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {  // V^T[8 pp + e][2 m2], [2 m2 + 1]
-                const uint32_t lo = (a0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                const uint32_t hi = (a1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                *(uint32_t *) (vt[buf] + (pp * 8 + e) * VS + m2 * 4) = lo | (hi << 16);
+            for (int e = 0; e < 8; ++e) {  // V^T[8 pp + e][2 m2], [2 m2 + 1]: one byte permute per word
+                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+                *(uint32_t *) (vt[buf] + (pp * 8 + e) * VS + m2 * 4) = __builtin_amdgcn_perm(a1[e >> 1], a0[e >> 1], sel);
             }
         }
     };
