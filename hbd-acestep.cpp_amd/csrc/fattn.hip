@@ -607,7 +607,7 @@ __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
 // A workgroup of 4 waves owns 128 query rows of one (sequence, KV head) -- the
 // rows are (query position, head) pairs, so the query heads sharing the KV
 // head share the workgroup -- and walks all keys in tiles of 64, K and V
-// double-buffered in LDS (V transposed on the way in). Per wave and tile:
+// double-buffered in LDS (both row-major; V read transposed). Per wave and tile:
 //   S^T = K Q^T   (v_mfma_f32_32x32x16: keys x 32 rows, q converted to K's
 //                  type as ggml converts it; products exact, fp32 sums)
 //   softmax       (lane-local: a lane holds 32 keys of one row, the other
@@ -1018,6 +1018,10 @@ __device__ __forceinline__ float fa_xhalf_sum(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// transposed LDS reads of 16-bit elements (gfx950 ds_read_b64_tr_b16)
+typedef short fa_v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) fa_v4s fa_lds_v4s;
+
 // raw buffer loads (32-bit offsets, range-checked: reads past the end return 0)
 typedef __amdgpu_buffer_rsrc_t fa_rsrc;
 __device__ __forceinline__ fa_rsrc fa_make_rsrc(const char * base, uint32_t bytes) {
@@ -1040,15 +1044,16 @@ k_fa_mfma(const FaArgs a) {
     using x8         = typename M::x8;
     constexpr int BQ = 128, BK = 64;
     constexpr int KS = D * 2 + 16;   // K row stride in LDS (bytes): 16-byte bank spread
-    constexpr int VS = BK * 2 + 8;   // V^T row stride (bytes): 34 words, conflict-free reads
+    constexpr int VR = D * 2 + 64;   // V row stride (bytes): rows 16 banks apart, conflict-free transposed reads
     constexpr int KC = D * 2 / 16;   // 16-byte chunks per K/V row
     constexpr int NC = BK * KC / 256;  // chunks per thread per tile (K and V each; even)
     constexpr int NKS = D / 16;      // k-steps of the S MFMA
     constexpr int NDB = D / 32;      // 32-row blocks of O^T
     static_assert(NC * 256 == BK * KC, "tile chunks");
+    static_assert(D * 2 % 256 == 0, "the V row stride's bank spread assumes whole 256-byte rows");
 
     __shared__ __align__(16) char kt[2][BK * KS];
-    __shared__ __align__(16) char vt[2][D * VS];
+    __shared__ __align__(16) char vt[2][BK * VR];
 
     const int      tid  = threadIdx.x;
     const int      wave = tid >> 6;
@@ -1121,18 +1126,16 @@ k_fa_mfma(const FaArgs a) {
         }
     }
 
-    // K tile loads: chunk c = tid + 256 i -> key c / KC, 16-byte part c % KC (a row
-    // is read by KC consecutive threads). V: thread t loads the same 16-byte part
-    // of two consecutive keys, c = tid + 256 i -> key pair c % 32, part c / 32, and
-    // writes V^T[d][2m..2m+1] as 4-byte words: a wave writes two 128-byte runs of
-    // V^T rows, conflict-free. Buffer loads: a fixed 32-bit offset per thread plus
-    // the tile's uniform offset (the planner keeps the key range below 4 GB).
+    // K and V tile loads: chunk c = tid + 256 i -> key c / KC, 16-byte part c % KC
+    // (a row is read by KC consecutive threads) and stored row-major in LDS; the
+    // P.V operands are read from V with transposed LDS reads. Buffer loads: a fixed
+    // 32-bit offset per thread plus the tile's uniform offset (the planner keeps
+    // the key range below 4 GB).
     constexpr int KR = 256 / KC;  // K rows per load round
     static_assert(KC <= 32 && 256 % KC == 0, "tile chunks");
     uint4          kr[NC], vr[NC];
     const uint32_t ko0 = (uint32_t) (tid / KC) * (uint32_t) a.k1 + (uint32_t) (tid % KC) * 16;
-    const uint32_t vo0 = (uint32_t) (2 * (tid % 32)) * (uint32_t) a.v1 + (uint32_t) (tid / 32) * 16;
-    const uint32_t vo1 = vo0 + (uint32_t) a.v1;
+    const uint32_t vo0 = (uint32_t) (tid / KC) * (uint32_t) a.v1 + (uint32_t) (tid % KC) * 16;
     // buffers end at the last key's row: keys past the end read as zeros
     const fa_rsrc  krs = fa_make_rsrc(kg, (uint32_t) ((int64_t) (a.n_kv - 1) * a.k1 + D * 2));
     const fa_rsrc  vrs = fa_make_rsrc(vg, (uint32_t) ((int64_t) (a.n_kv - 1) * a.v1 + D * 2));
@@ -1144,9 +1147,8 @@ k_fa_mfma(const FaArgs a) {
             kr[i] = fa_bld16(krs, ko0, ks0 + (uint32_t) (KR * i) * (uint32_t) a.k1);
         }
 #pragma unroll
-        for (int i = 0; i < NC / 2; ++i) {  // part c / 32 = tid / 32 + 8 i
-            vr[2 * i]     = fa_bld16(vrs, vo0 + 128 * i, vs0);
-            vr[2 * i + 1] = fa_bld16(vrs, vo1 + 128 * i, vs0);
+        for (int i = 0; i < NC; ++i) {
+            vr[i] = fa_bld16(vrs, vo0, vs0 + (uint32_t) (KR * i) * (uint32_t) a.v1);
         }
     };
     auto store_tile = [&](int buf) {
@@ -1156,16 +1158,9 @@ k_fa_mfma(const FaArgs a) {
             *(uint4 *) (kt[buf] + (c / KC) * KS + (c % KC) * 16) = kr[i];
         }
 #pragma unroll
-        for (int i = 0; i < NC / 2; ++i) {
-            const int      c  = tid + 256 * i;
-            const int      m2 = c % 32, pp = c / 32;
-            const uint32_t a0[4] = { vr[2 * i].x, vr[2 * i].y, vr[2 * i].z, vr[2 * i].w };
-            const uint32_t a1[4] = { vr[2 * i + 1].x, vr[2 * i + 1].y, vr[2 * i + 1].z, vr[2 * i + 1].w };
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {  // V^T[8 pp + e][2 m2], [2 m2 + 1]: one byte permute per word
-                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-                *(uint32_t *) (vt[buf] + (pp * 8 + e) * VS + m2 * 4) = __builtin_amdgcn_perm(a1[e >> 1], a0[e >> 1], sel);
-            }
+        for (int i = 0; i < NC; ++i) {
+            const int c = tid + 256 * i;
+            *(uint4 *) (vt[buf] + (c / KC) * VR + (c % KC) * 16) = vr[i];
         }
     };
     // mask values of this lane's 32 keys of a tile (key 32 bk + 8 j + 4 hh + i:
@@ -1321,13 +1316,17 @@ k_fa_mfma(const FaArgs a) {
                     phi[slot] = __builtin_bit_cast(typename M::e, hb);
                     plo[slot] = __builtin_bit_cast(typename M::e, M::bits(p - M::val(hb)));
                 }
+                // A = V^T rows 32 db + l % 32 at those keys, by transposed reads of the
+                // row-major V tile: lane m of a 16-lane group addresses V[K0 + m / 4][D0 +
+                // 4 (m % 4)], and lane j of the group receives V[K0 .. K0 + 3][D0 + j]
                 x8 va[NDB];
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
-                    const char * vp = vt[cur] + (32 * db + n) * VS + (32 * bk + 16 * jj + 4 * hh) * 2;
-                    const uint2  v0 = *(const uint2 *) vp;         // keys +0..3
-                    const uint2  v1 = *(const uint2 *) (vp + 16);  // keys +8..11
-                    va[db]          = __builtin_bit_cast(x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+                    const char * vp = vt[cur] + (32 * bk + 16 * jj + 4 * hh + (lane & 15) / 4) * VR +
+                                      (32 * db + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
+                    const fa_v4s v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_v4s *) vp);           // keys +0..3
+                    const fa_v4s v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_v4s *) (vp + 8 * VR));  // keys +8..11
+                    va[db] = __builtin_bit_cast(x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
                 }
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
