@@ -628,6 +628,10 @@ __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
 #define MI_FA_MFMA_MIN_ROWS 64  // (query position, head) rows per KV head from which the MFMA path is used
 #endif
 
+// transposed LDS reads of 16-bit elements (gfx950 ds_read_b64_tr_b16)
+typedef short fa_v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) fa_v4s fa_lds_v4s;
+
 template <int KT> struct FaM;
 template <> struct FaM<MI_TYPE_BF16> {
     typedef __bf16 e;
@@ -662,8 +666,8 @@ __device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, cons
 //   S^T = K Q^T: A = K rows from LDS, B = the query heads (padded to 16) in K's
 //   type; lane l then holds the scores of head l%16 for keys 16 mt + 4 (l/16) + r.
 //   O^T += V^T P^T: B = those 8 probabilities as they sit (a high and a low
-//   16-bit part, two MFMAs), so V^T is stored to LDS with its keys in the same
-//   order: key 16 mt + 4 q + r at column 8 q + 4 mt + r.
+//   16-bit part, two MFMAs); A = V^T in that key order, read from the row-major V
+//   tile in LDS with two transposed reads (keys 4 q + r, then 16 + 4 q + r).
 // Keys no head reads (masked, past the end) have p = 0 and zero K/V bytes in
 // LDS, whatever the cache holds there. Partials and the merge are k_fa_split's.
 #ifndef MI_FA_DEC_WPE
@@ -680,14 +684,14 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
     using x8         = typename M::x8;
     constexpr int D   = 128;
     constexpr int T   = FA_TILE;       // keys per tile
-    constexpr int VS  = T * 2 + 16;    // V^T row stride (bytes, 16-byte multiple)
+    constexpr int VR  = D * 2 + 32;    // V row stride (bytes): 8 rows on distinct banks for transposed reads
     constexpr int NKS = D / 32;        // k-steps of S (32 dims each)
     constexpr int NDT = D / 16;        // 16-dim tiles of O^T
     constexpr int KC  = T * D * 2 / 16 / 64;  // 16-byte K chunks per lane per tile (8)
     constexpr int VC  = KC / 2;               // V key-pair chunks per lane per tile (4)
     typedef float f4 __attribute__((ext_vector_type(4)));
 
-    __shared__ __align__(16) char vt[D * VS];
+    __shared__ __align__(16) char vt[T * VR];       // the tile's V rows (row-major)
     __shared__ float              mt[FA_MAXT * T];  // the split's mask values
     __shared__ uint32_t           lt[FA_MAXT];      // per tile: keys some head reads
 
@@ -796,8 +800,6 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
             }
         }
     };
-    // LDS column of key k in V^T (the order of the P operand)
-    auto vcol = [](int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); };
 
     f4 o[NDT];
 #pragma unroll
@@ -816,15 +818,9 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
         if (live) {
 #pragma unroll
             for (int i = 0; i < VC; ++i) {
-                const int      k0   = 2 * (4 * i + q4);
-                const int      col  = vcol(k0);  // even: keys k0, k0 + 1 in one word
-                const uint32_t w0[4] = { vc[2 * i].x, vc[2 * i].y, vc[2 * i].z, vc[2 * i].w };
-                const uint32_t w1[4] = { vc[2 * i + 1].x, vc[2 * i + 1].y, vc[2 * i + 1].z, vc[2 * i + 1].w };
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {  // V^T[8 c16 + e][col], [col + 1]
-                    const uint32_t lo = (w0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                    const uint32_t hi = (w1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                    *(uint32_t *) (vt + (8 * c16 + e) * VS + col * 2) = lo | (hi << 16);
+                for (int j = 0; j < 2; ++j) {
+                    *(uint4 *) (vt + (2 * (4 * i + q4) + j) * VR + c16 * 16) = vc[2 * i + j];
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -885,10 +881,16 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
             for (int dt = 0; dt < NDT; ++dt) {
                 o[dt] *= alpha;
             }
-            // O^T += V^T P^T: A = V^T rows 16 dt + c16 at columns 8 q4 .. + 7
+            // O^T += V^T P^T: A = V^T row 16 dt + c16 at keys 4 q4 + r and 16 + 4 q4 + r
+            // (P's order), by two transposed reads of the row-major tile: lane m of a
+            // 16-lane group addresses V[K0 + m / 4][D0 + 4 (m % 4)], and lane j receives
+            // V[K0 .. K0 + 3][D0 + j]
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
-                const x8 va = *(const x8 *) (vt + (16 * dt + c16) * VS + 16 * q4);
+                const char *  vp = vt + (4 * q4 + c16 / 4) * VR + (16 * dt + 4 * (c16 & 3)) * 2;
+                const fa_v4s  v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_v4s *) vp);             // keys 4 q4 + r
+                const fa_v4s  v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_v4s *) (vp + 16 * VR));  // keys 16 + 4 q4 + r
+                const x8      va = __builtin_bit_cast(x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
                 if constexpr (KT == MI_TYPE_BF16) {
                     o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi, o[dt], 0, 0, 0);
                     o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo, o[dt], 0, 0, 0);
@@ -1017,10 +1019,6 @@ __device__ __forceinline__ float fa_xhalf_sum(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-
-// transposed LDS reads of 16-bit elements (gfx950 ds_read_b64_tr_b16)
-typedef short fa_v4s __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) fa_v4s fa_lds_v4s;
 
 // raw buffer loads (32-bit offsets, range-checked: reads past the end return 0)
 typedef __amdgpu_buffer_rsrc_t fa_rsrc;
