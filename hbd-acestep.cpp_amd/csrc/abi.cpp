@@ -31,6 +31,18 @@ int num_cus() {
     return v;
 }
 
+namespace {
+thread_local bool t_dry_run = false;
+}
+
+bool dry_run() {
+    return t_dry_run;
+}
+
+void set_dry_run(bool on) {
+    t_dry_run = on;
+}
+
 }  // namespace mi
 
 using namespace mi;
@@ -58,6 +70,27 @@ int check(const mi_tensor * t, bool inner = true) {
     }
     if (t->type == MI_TYPE_Q8_0 && t->ne[0] % 32 != 0) {
         return MI_ERR_SHAPE;
+    }
+    // the row count, element count and byte extent must each fit in int64:
+    // nrows() / nelements() and the launchers multiply the ne[] unchecked
+    int64_t rows = 1, elems = 0;
+    if (__builtin_mul_overflow(t->ne[1], t->ne[2], &rows) || __builtin_mul_overflow(rows, t->ne[3], &rows) ||
+        __builtin_mul_overflow(rows, t->ne[0], &elems)) {
+        return MI_ERR_UNSUPPORTED;
+    }
+    if (elems > 0) {
+        // last addressed byte: sum of (ne[d] - 1) * nb[d] plus one element
+        uint64_t ext = (uint64_t) es;
+        for (int d = 0; d < 4; ++d) {
+            const uint64_t n = (uint64_t) (d == 0 ? t->ne[0] / blck_size(t->type) : t->ne[d]) - 1;
+            uint64_t       part = 0;
+            if (__builtin_mul_overflow(n, t->nb[d], &part) || __builtin_add_overflow(ext, part, &ext)) {
+                return MI_ERR_UNSUPPORTED;
+            }
+        }
+        if (ext > (uint64_t) INT64_MAX) {
+            return MI_ERR_UNSUPPORTED;
+        }
     }
     if (nelements(*t) > 0 && !t->data) {
         return MI_ERR_NULL;
@@ -119,8 +152,8 @@ bool can_repeat(const mi_tensor & b, const mi_tensor & a) {
 }
 
 int finish(int rc) {
-    if (rc != MI_OK) {
-        return rc;
+    if (rc != MI_OK || dry_run()) {
+        return rc;  // a validate-only call leaves the HIP error state alone
     }
     return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_HIP;
 }

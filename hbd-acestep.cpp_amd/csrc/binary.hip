@@ -301,13 +301,13 @@ static int launch_rows_c(const BinArgs & a, int T, int C, hipStream_t s) {
     const int nw = T / 64;
     switch (C) {
         case 1:
-            hipLaunchKernelGGL((k_bin_rows<T_, OP, BROW, 1, 4>), dim3(balanced_grid(a.rows, 4, nw)), dim3(T), 0, s, a);
+            MI_LAUNCH((k_bin_rows<T_, OP, BROW, 1, 4>), dim3(balanced_grid(a.rows, 4, nw)), dim3(T), 0, s, a);
             return MI_OK;
         case 2:
-            hipLaunchKernelGGL((k_bin_rows<T_, OP, BROW, 2, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0, s, a);
+            MI_LAUNCH((k_bin_rows<T_, OP, BROW, 2, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0, s, a);
             return MI_OK;
         case 4:
-            hipLaunchKernelGGL((k_bin_rows<T_, OP, BROW, 4, 1>), dim3(balanced_grid(a.rows, 1, nw)), dim3(T), 0, s, a);
+            MI_LAUNCH((k_bin_rows<T_, OP, BROW, 4, 1>), dim3(balanced_grid(a.rows, 1, nw)), dim3(T), 0, s, a);
             return MI_OK;
         default:
             return MI_ERR_UNSUPPORTED;
@@ -322,12 +322,12 @@ static int launch_flat_op(const BinArgs & a, hipStream_t s) {
     const uint32_t grid  = (uint32_t) ((total + 256u * MI_BIN_U - 1) / (256u * MI_BIN_U));
     if constexpr (OP == OP_ADD || OP == OP_NONE) {
         if (a.clamp) {
-            hipLaunchKernelGGL((k_bin_flat<T_, OP, BROW, MI_BIN_U, true>), dim3(grid), dim3(256), 0, s, a, nvr,
+            MI_LAUNCH((k_bin_flat<T_, OP, BROW, MI_BIN_U, true>), dim3(grid), dim3(256), 0, s, a, nvr,
                                FastDiv(nvr), (uint32_t) total);
             return MI_OK;
         }
     }
-    hipLaunchKernelGGL((k_bin_flat<T_, OP, BROW, MI_BIN_U, false>), dim3(grid), dim3(256), 0, s, a, nvr,
+    MI_LAUNCH((k_bin_flat<T_, OP, BROW, MI_BIN_U, false>), dim3(grid), dim3(256), 0, s, a, nvr,
                        FastDiv(nvr), (uint32_t) total);
     return MI_OK;
 }
@@ -393,7 +393,7 @@ static int launch_generic(int op, const mi_tensor & a, const mi_tensor * b, cons
     uint64_t       grid = (total + 255) / 256;
     const uint64_t cap  = (uint64_t) num_cus() * 32;
     grid                = grid > cap ? cap : grid;
-    hipLaunchKernelGGL(k_bin_generic, dim3((uint32_t) grid), dim3(256), 0, s, g);
+    MI_LAUNCH(k_bin_generic, dim3((uint32_t) grid), dim3(256), 0, s, g);
     return MI_OK;
 }
 

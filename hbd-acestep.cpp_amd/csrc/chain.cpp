@@ -4,6 +4,7 @@
 // one stream. The GEMM / attention outputs those builders produce between
 // the fused ops are inputs here (this library does not compute them).
 #include "mi_ops.h"
+#include "validate.h"
 
 #define MI_TRY(expr)            \
     do {                        \
@@ -38,10 +39,7 @@ mi_tensor seq_view(const mi_tensor & x, int64_t B) {
 
 }  // namespace
 
-extern "C" int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream s) {
-    if (!io) {
-        return MI_ERR_NULL;
-    }
+static int dit_block(const mi_dit_block_io * io, mi_stream s) {
     const int64_t H = io->hidden.ne[0];
     const mi_tensor & ad = io->adaln;
     if (ad.type != MI_TYPE_F32 || ad.ne[0] != 6 * H || ad.ne[1] != 1 || ad.ne[2] != 1 || ad.ne[3] != 1 ||
@@ -84,6 +82,20 @@ extern "C" int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream s) {
     return MI_OK;
 }
 
+// Every operand of the chain is validated (a launch-free pass through the
+// same entry points) before the first kernel runs, so an error leaves the
+// caller's buffers untouched.
+extern "C" int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream s) {
+    if (!io) {
+        return MI_ERR_NULL;
+    }
+    {
+        mi::DryRunScope validate_only;
+        MI_TRY(dit_block(io, s));
+    }
+    return dit_block(io, s);
+}
+
 // QK-norm -> rope (qwen3-lm.h:660-667) to q_out / k_out, the V clamp before
 // the cache cast (674-677, in place), then the KV store of every sequence, K
 // and V, in one launch (682-703)
@@ -109,10 +121,7 @@ static int qwen3_rope_and_store(const mi_qwen3_layer_io * io, mi_stream s) {
     return MI_OK;
 }
 
-extern "C" int mi_qwen3_layer_ops(const mi_qwen3_layer_io * io, mi_stream s) {
-    if (!io) {
-        return MI_ERR_NULL;
-    }
+static int qwen3_layer(const mi_qwen3_layer_io * io, mi_stream s) {
     const float lim = 65504.0f;
     // pre-attention RMSNorm (qwen3-lm.h:632)
     MI_TRY(mi_rms_norm(&io->hidden, &io->in_norm_w, io->eps, &io->norm, s));
@@ -142,4 +151,16 @@ extern "C" int mi_qwen3_layer_ops(const mi_qwen3_layer_io * io, mi_stream s) {
         MI_TRY(mi_add(&io->hidden, &io->mlp_out, &io->hidden, s));
     }
     return MI_OK;
+}
+
+// validated whole before the first launch, as mi_dit_block_ops
+extern "C" int mi_qwen3_layer_ops(const mi_qwen3_layer_io * io, mi_stream s) {
+    if (!io) {
+        return MI_ERR_NULL;
+    }
+    {
+        mi::DryRunScope validate_only;
+        MI_TRY(qwen3_layer(io, s));
+    }
+    return qwen3_layer(io, s);
 }

@@ -16,6 +16,7 @@
 #include <stdint.h>
 
 #include "mi_ops.h"
+#include "validate.h"
 
 namespace mi {
 

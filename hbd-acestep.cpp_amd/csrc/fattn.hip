@@ -1518,24 +1518,24 @@ static void launch_kd(const FaArgs & a, hipStream_t s) {
     const dim3 grid((uint32_t) a.splits, (uint32_t) (a.nb * a.nkv), (uint32_t) a.rblocks);
     if constexpr (D == 128 && (KT == MI_TYPE_F16 || KT == MI_TYPE_BF16)) {
         if (a.dec) {
-            hipLaunchKernelGGL((k_fa_dec<KT>), grid, dim3(64), 0, s, a);
+            MI_LAUNCH((k_fa_dec<KT>), grid, dim3(64), 0, s, a);
             if (a.splits > 1) {
-                hipLaunchKernelGGL((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(256), 0, s, a);
+                MI_LAUNCH((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(256), 0, s, a);
             }
             return;
         }
     }
     if constexpr (D == 64 && KT != MI_TYPE_F32) {
         if (fa_rb(a.rows, D, KT) == 8) {
-            hipLaunchKernelGGL((k_fa_split<KT, D, 8>), grid, dim3(64), 0, s, a);
+            MI_LAUNCH((k_fa_split<KT, D, 8>), grid, dim3(64), 0, s, a);
         } else {
-            hipLaunchKernelGGL((k_fa_split<KT, D, 4>), grid, dim3(64), 0, s, a);
+            MI_LAUNCH((k_fa_split<KT, D, 4>), grid, dim3(64), 0, s, a);
         }
     } else {
-        hipLaunchKernelGGL((k_fa_split<KT, D, 4>), grid, dim3(64), 0, s, a);
+        MI_LAUNCH((k_fa_split<KT, D, 4>), grid, dim3(64), 0, s, a);
     }
     if (a.splits > 1) {
-        hipLaunchKernelGGL((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(256), 0, s, a);
+        MI_LAUNCH((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(256), 0, s, a);
     }
 }
 
@@ -1565,7 +1565,7 @@ int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
     }
     if (a.mfma) {
         if (a.msum != nullptr) {
-            hipLaunchKernelGGL(k_fa_mask_summary, dim3((uint32_t) (((a.n_kv + 63) / 64 + FA_SUM_T - 1) / FA_SUM_T),
+            MI_LAUNCH(k_fa_mask_summary, dim3((uint32_t) (((a.n_kv + 63) / 64 + FA_SUM_T - 1) / FA_SUM_T),
                                                        (uint32_t) a.ngq,
                                                        (uint32_t) (a.mne3 * a.mne2)),
                                dim3(64), 0, s, a);
@@ -1573,19 +1573,19 @@ int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
         const dim3 grid((uint32_t) (a.tfull + 2 * a.tsplit));
         if (kt == MI_TYPE_BF16) {
             if (a.msum) {
-                hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_BF16, 128, true>), grid, dim3(256), 0, s, a);
+                MI_LAUNCH((k_fa_mfma<MI_TYPE_BF16, 128, true>), grid, dim3(256), 0, s, a);
             } else {
-                hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_BF16, 128, false>), grid, dim3(256), 0, s, a);
+                MI_LAUNCH((k_fa_mfma<MI_TYPE_BF16, 128, false>), grid, dim3(256), 0, s, a);
             }
         } else {
             if (a.msum) {
-                hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_F16, 128, true>), grid, dim3(256), 0, s, a);
+                MI_LAUNCH((k_fa_mfma<MI_TYPE_F16, 128, true>), grid, dim3(256), 0, s, a);
             } else {
-                hipLaunchKernelGGL((k_fa_mfma<MI_TYPE_F16, 128, false>), grid, dim3(256), 0, s, a);
+                MI_LAUNCH((k_fa_mfma<MI_TYPE_F16, 128, false>), grid, dim3(256), 0, s, a);
             }
         }
         if (a.tsplit > 0) {
-            hipLaunchKernelGGL(k_fa_mfma_combine, dim3((uint32_t) a.tsplit * 16), dim3(256), 0, s, a);
+            MI_LAUNCH(k_fa_mfma_combine, dim3((uint32_t) a.tsplit * 16), dim3(256), 0, s, a);
         }
         return MI_OK;
     }

@@ -327,7 +327,7 @@ static int launch_to(const GetRowsArgs & a, int ttype, bool fast, bool lds, hipS
                 // rows shorter than one wave-wide store; an invalid id loads from row 0
                 if (a.n / OPS < 64 && a.n_rows > 0 && nchunks < (1ull << 31)) {
                     constexpr uint32_t per_wg = 256 * MI_GR_FLAT_U;
-                    hipLaunchKernelGGL((k_get_rows_q8_0_flat<TO, MI_GR_FLAT_U>),
+                    MI_LAUNCH((k_get_rows_q8_0_flat<TO, MI_GR_FLAT_U>),
                                        dim3((uint32_t) ((nchunks + per_wg - 1) / per_wg)), dim3(256), 0, s, a,
                                        FastDiv((uint32_t) (a.n / OPS)), (uint32_t) nchunks);
                     return MI_OK;
@@ -338,33 +338,33 @@ static int launch_to(const GetRowsArgs & a, int ttype, bool fast, bool lds, hipS
                     const dim3     g(grid > gcap ? gcap : grid);
                     const size_t   lb = (size_t) 4 * nc * 16;
                     switch ((nc + 63) / 64) {  // nc <= 9 * 64 (ne0 <= 8192)
-                        case 1: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 1>), g, dim3(256), lb, s, a, nc); break;
-                        case 2: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 2>), g, dim3(256), lb, s, a, nc); break;
-                        case 3: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 3>), g, dim3(256), lb, s, a, nc); break;
-                        case 4: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 4>), g, dim3(256), lb, s, a, nc); break;
-                        case 5: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 5>), g, dim3(256), lb, s, a, nc); break;
-                        case 6: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 6>), g, dim3(256), lb, s, a, nc); break;
-                        case 7: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 7>), g, dim3(256), lb, s, a, nc); break;
-                        case 8: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 8>), g, dim3(256), lb, s, a, nc); break;
-                        default: hipLaunchKernelGGL((k_get_rows_q8_0_lds<TO, 9>), g, dim3(256), lb, s, a, nc); break;
+                        case 1: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 1>), g, dim3(256), lb, s, a, nc); break;
+                        case 2: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 2>), g, dim3(256), lb, s, a, nc); break;
+                        case 3: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 3>), g, dim3(256), lb, s, a, nc); break;
+                        case 4: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 4>), g, dim3(256), lb, s, a, nc); break;
+                        case 5: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 5>), g, dim3(256), lb, s, a, nc); break;
+                        case 6: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 6>), g, dim3(256), lb, s, a, nc); break;
+                        case 7: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 7>), g, dim3(256), lb, s, a, nc); break;
+                        case 8: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 8>), g, dim3(256), lb, s, a, nc); break;
+                        default: MI_LAUNCH((k_get_rows_q8_0_lds<TO, 9>), g, dim3(256), lb, s, a, nc); break;
                     }
                 } else {
-                    hipLaunchKernelGGL((k_get_rows_q8_0<TO>), dim3(grid), dim3(256), 0, s, a);
+                    MI_LAUNCH((k_get_rows_q8_0<TO>), dim3(grid), dim3(256), 0, s, a);
                 }
                 return MI_OK;
             }
             case MI_TYPE_F32:
-                hipLaunchKernelGGL((k_get_rows_vec<MI_TYPE_F32, TO>), dim3(grid), dim3(256), 0, s, a);
+                MI_LAUNCH((k_get_rows_vec<MI_TYPE_F32, TO>), dim3(grid), dim3(256), 0, s, a);
                 return MI_OK;
             case MI_TYPE_BF16:
-                hipLaunchKernelGGL((k_get_rows_vec<MI_TYPE_BF16, TO>), dim3(grid), dim3(256), 0, s, a);
+                MI_LAUNCH((k_get_rows_vec<MI_TYPE_BF16, TO>), dim3(grid), dim3(256), 0, s, a);
                 return MI_OK;
             default:
-                hipLaunchKernelGGL((k_get_rows_vec<MI_TYPE_F16, TO>), dim3(grid), dim3(256), 0, s, a);
+                MI_LAUNCH((k_get_rows_vec<MI_TYPE_F16, TO>), dim3(grid), dim3(256), 0, s, a);
                 return MI_OK;
         }
     }
-    hipLaunchKernelGGL((k_get_rows_generic<TO>), dim3(grid), dim3(256), 0, s, a, ttype);
+    MI_LAUNCH((k_get_rows_generic<TO>), dim3(grid), dim3(256), 0, s, a, ttype);
     return MI_OK;
 }
 

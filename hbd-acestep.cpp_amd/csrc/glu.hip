@@ -86,13 +86,13 @@ static int launch_t(const GluArgs & a, bool fast, int64_t rows, int64_t n, hipSt
     if (fast) {
         constexpr int  U    = MI_GLU_U;
         const uint32_t grid = (a.total + 256u * U - 1) / (256u * U);
-        hipLaunchKernelGGL((k_swiglu<TI, TO, U>), dim3(grid), dim3(256), 0, s, a);
+        MI_LAUNCH((k_swiglu<TI, TO, U>), dim3(grid), dim3(256), 0, s, a);
         return MI_OK;
     }
     uint64_t       grid = ((uint64_t) rows * n + 255) / 256;
     const uint64_t cap  = (uint64_t) num_cus() * 32;
     grid                = grid > cap ? cap : (grid ? grid : 1);
-    hipLaunchKernelGGL((k_swiglu_generic<TI, TO>), dim3((uint32_t) grid), dim3(256), 0, s, a.g, a.u, a.gs, a.us,
+    MI_LAUNCH((k_swiglu_generic<TI, TO>), dim3((uint32_t) grid), dim3(256), 0, s, a.g, a.u, a.gs, a.us,
                        a.y, a.ys, rows, n);
     return MI_OK;
 }

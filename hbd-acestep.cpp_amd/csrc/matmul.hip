@@ -587,7 +587,7 @@ int launch_q8_0_repack(const char * src, int64_t nb1, uint32_t k, uint32_t n, ch
     if (total == 0) {
         return MI_OK;
     }
-    hipLaunchKernelGGL(k_q8_0_repack, dim3((uint32_t) ((total + 255) / 256)), dim3(256), 0, s, src, nb1, n, nbk, ng,
+    MI_LAUNCH(k_q8_0_repack, dim3((uint32_t) ((total + 255) / 256)), dim3(256), 0, s, src, nb1, n, nbk, ng,
                        dst);
     return MI_OK;
 }
@@ -597,39 +597,39 @@ int launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s) {
         return MI_OK;
     }
     if (a.nw) {
-        hipLaunchKernelGGL(k_mmv_quant_x_norm, dim3(a.m), dim3(256), 0, s, a);
+        MI_LAUNCH(k_mmv_quant_x_norm, dim3(a.m), dim3(256), 0, s, a);
     } else {
         const uint64_t threads = ((uint64_t) a.m * a.nbk + MI_QX_U - 1) / MI_QX_U * 8;
-        hipLaunchKernelGGL(k_mmv_quant_x, dim3((uint32_t) ((threads + 255) / 256)), dim3(256), 0, s, a);
+        MI_LAUNCH(k_mmv_quant_x, dim3((uint32_t) ((threads + 255) / 256)), dim3(256), 0, s, a);
     }
     if (a.m > 8) {
-        hipLaunchKernelGGL(k_mmq_q8_0, dim3((a.n + 127) / 128, a.mp / 128), dim3(256), 0, s, a);
+        MI_LAUNCH(k_mmq_q8_0, dim3((a.n + 127) / 128, a.mp / 128), dim3(256), 0, s, a);
         return MI_OK;
     }
     const dim3   grid(a.ng, a.splits), blk(64 * a.wpg);
     const size_t lds = a.wpg > 1 ? (size_t) a.wpg * a.m * 64 * 4 : 0;
     switch (a.m) {
-        case 1: hipLaunchKernelGGL(k_mmv_q8_0<1>, grid, blk, lds, s, a); break;
-        case 2: hipLaunchKernelGGL(k_mmv_q8_0<2>, grid, blk, lds, s, a); break;
-        case 3: hipLaunchKernelGGL(k_mmv_q8_0<3>, grid, blk, lds, s, a); break;
-        case 4: hipLaunchKernelGGL(k_mmv_q8_0<4>, grid, blk, lds, s, a); break;
-        case 5: hipLaunchKernelGGL(k_mmv_q8_0<5>, grid, blk, lds, s, a); break;
-        case 6: hipLaunchKernelGGL(k_mmv_q8_0<6>, grid, blk, lds, s, a); break;
-        case 7: hipLaunchKernelGGL(k_mmv_q8_0<7>, grid, blk, lds, s, a); break;
-        case 8: hipLaunchKernelGGL(k_mmv_q8_0<8>, grid, blk, lds, s, a); break;
+        case 1: MI_LAUNCH(k_mmv_q8_0<1>, grid, blk, lds, s, a); break;
+        case 2: MI_LAUNCH(k_mmv_q8_0<2>, grid, blk, lds, s, a); break;
+        case 3: MI_LAUNCH(k_mmv_q8_0<3>, grid, blk, lds, s, a); break;
+        case 4: MI_LAUNCH(k_mmv_q8_0<4>, grid, blk, lds, s, a); break;
+        case 5: MI_LAUNCH(k_mmv_q8_0<5>, grid, blk, lds, s, a); break;
+        case 6: MI_LAUNCH(k_mmv_q8_0<6>, grid, blk, lds, s, a); break;
+        case 7: MI_LAUNCH(k_mmv_q8_0<7>, grid, blk, lds, s, a); break;
+        case 8: MI_LAUNCH(k_mmv_q8_0<8>, grid, blk, lds, s, a); break;
         default: return MI_ERR_UNSUPPORTED;
     }
     if (a.splits > 1) {
         const dim3 rg((a.m * a.npad + 255) / 256);
         switch (a.m) {
-            case 1: hipLaunchKernelGGL(k_mmv_reduce<1>, rg, dim3(256), 0, s, a); break;
-            case 2: hipLaunchKernelGGL(k_mmv_reduce<2>, rg, dim3(256), 0, s, a); break;
-            case 3: hipLaunchKernelGGL(k_mmv_reduce<3>, rg, dim3(256), 0, s, a); break;
-            case 4: hipLaunchKernelGGL(k_mmv_reduce<4>, rg, dim3(256), 0, s, a); break;
-            case 5: hipLaunchKernelGGL(k_mmv_reduce<5>, rg, dim3(256), 0, s, a); break;
-            case 6: hipLaunchKernelGGL(k_mmv_reduce<6>, rg, dim3(256), 0, s, a); break;
-            case 7: hipLaunchKernelGGL(k_mmv_reduce<7>, rg, dim3(256), 0, s, a); break;
-            default: hipLaunchKernelGGL(k_mmv_reduce<8>, rg, dim3(256), 0, s, a); break;
+            case 1: MI_LAUNCH(k_mmv_reduce<1>, rg, dim3(256), 0, s, a); break;
+            case 2: MI_LAUNCH(k_mmv_reduce<2>, rg, dim3(256), 0, s, a); break;
+            case 3: MI_LAUNCH(k_mmv_reduce<3>, rg, dim3(256), 0, s, a); break;
+            case 4: MI_LAUNCH(k_mmv_reduce<4>, rg, dim3(256), 0, s, a); break;
+            case 5: MI_LAUNCH(k_mmv_reduce<5>, rg, dim3(256), 0, s, a); break;
+            case 6: MI_LAUNCH(k_mmv_reduce<6>, rg, dim3(256), 0, s, a); break;
+            case 7: MI_LAUNCH(k_mmv_reduce<7>, rg, dim3(256), 0, s, a); break;
+            default: MI_LAUNCH(k_mmv_reduce<8>, rg, dim3(256), 0, s, a); break;
         }
     }
     return MI_OK;

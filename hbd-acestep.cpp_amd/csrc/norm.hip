@@ -369,9 +369,9 @@ static void launch_short_d(const char * x, char * y, int64_t xs, int64_t ys, uin
     const uint64_t waves  = (chunks + per - 1) / per;
     const dim3     grid((uint32_t) ((waves + 3) / 4));
     if (w) {
-        hipLaunchKernelGGL((k_rms_short<TI, D, true, MI_SHORT_U>), grid, dim3(256), 0, s, x, y, xs, ys, rows, w, eps);
+        MI_LAUNCH((k_rms_short<TI, D, true, MI_SHORT_U>), grid, dim3(256), 0, s, x, y, xs, ys, rows, w, eps);
     } else {
-        hipLaunchKernelGGL((k_rms_short<TI, D, false, MI_SHORT_U>), grid, dim3(256), 0, s, x, y, xs, ys, rows, w,
+        MI_LAUNCH((k_rms_short<TI, D, false, MI_SHORT_U>), grid, dim3(256), 0, s, x, y, xs, ys, rows, w,
                            eps);
     }
 }
@@ -440,19 +440,19 @@ static int dispatch_fast_add(const NormArgs & a, int T, int C, hipStream_t s) {
     const int nw = T / 64;
     switch (C) {
         case 1:
-            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, ADD, 1, MI_NORM_R>),
+            MI_LAUNCH((k_rms_rows<TI, TO, MODE, ADD, 1, MI_NORM_R>),
                                dim3(balanced_grid(a.rows, MI_NORM_R, nw)), dim3(T), 0, s, a);
             break;
         case 2:
-            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, ADD, 2, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
+            MI_LAUNCH((k_rms_rows<TI, TO, MODE, ADD, 2, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
                                s, a);
             break;
         case 3:
-            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, ADD, 3, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
+            MI_LAUNCH((k_rms_rows<TI, TO, MODE, ADD, 3, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
                                s, a);
             break;
         case 4:
-            hipLaunchKernelGGL((k_rms_rows<TI, TO, MODE, ADD, 4, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
+            MI_LAUNCH((k_rms_rows<TI, TO, MODE, ADD, 4, 2>), dim3(balanced_grid(a.rows, 2, nw)), dim3(T), 0,
                                s, a);
             break;
         default:
@@ -493,13 +493,13 @@ static int dispatch_types(const NormArgs & a, int mode, bool fast, int T, int C,
     grid                = grid > cap ? cap : grid;
     switch (mode) {
         case 0:
-            hipLaunchKernelGGL((k_rms_rows_generic<TI, TO, 0>), dim3(grid), dim3(256), 0, s, a);
+            MI_LAUNCH((k_rms_rows_generic<TI, TO, 0>), dim3(grid), dim3(256), 0, s, a);
             break;
         case 1:
-            hipLaunchKernelGGL((k_rms_rows_generic<TI, TO, 1>), dim3(grid), dim3(256), 0, s, a);
+            MI_LAUNCH((k_rms_rows_generic<TI, TO, 1>), dim3(grid), dim3(256), 0, s, a);
             break;
         default:
-            hipLaunchKernelGGL((k_rms_rows_generic<TI, TO, 2>), dim3(grid), dim3(256), 0, s, a);
+            MI_LAUNCH((k_rms_rows_generic<TI, TO, 2>), dim3(grid), dim3(256), 0, s, a);
             break;
     }
     return MI_OK;

@@ -384,16 +384,16 @@ static int launch_k(const RowCopy & K, const RowCopy * V, bool fast, hipStream_t
             const uint32_t nbv  = total - nbk;
             const uint32_t wg_k = (nbk + 127) / 128;  // 4 waves x 32 blocks per workgroup
             const uint32_t grid = wg_k + (nbv + 127) / 128;
-            hipLaunchKernelGGL((k_row_q8_lds<TI, ROUND>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, nbv, wg_k, nbpr,
+            MI_LAUNCH((k_row_q8_lds<TI, ROUND>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, nbv, wg_k, nbpr,
                                FastDiv(nbpr));
 #else
             const uint32_t grid = (total * MI_Q8_LPB + 255) / 256;
-            hipLaunchKernelGGL((k_row_q8<TI, ROUND>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, total, nbpr,
+            MI_LAUNCH((k_row_q8<TI, ROUND>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, total, nbpr,
                                FastDiv(nbpr));
 #endif
         } else {
             const uint32_t grid = (total * 4 + 255) / 256;
-            hipLaunchKernelGGL((k_row_copy<TI, TO>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, total, nbpr,
+            MI_LAUNCH((k_row_copy<TI, TO>), dim3(grid), dim3(256), 0, s, K, Vr, nbk, total, nbpr,
                                FastDiv(nbpr));
         }
         return MI_OK;
@@ -404,7 +404,7 @@ static int launch_k(const RowCopy & K, const RowCopy * V, bool fast, hipStream_t
     uint64_t       grid    = (total + 255) / 256;
     const uint64_t cap     = (uint64_t) num_cus() * 32;
     grid                   = grid > cap ? cap : (grid ? grid : 1);
-    hipLaunchKernelGGL((k_row_copy_generic<TI, TO, ROUND>), dim3((uint32_t) grid), dim3(256), 0, s, K, Vr, nk, total,
+    MI_LAUNCH((k_row_copy_generic<TI, TO, ROUND>), dim3((uint32_t) grid), dim3(256), 0, s, K, Vr, nk, total,
                        per_row);
     return MI_OK;
 }

@@ -386,7 +386,7 @@ static void launch_persistent(uint64_t items, hipStream_t s, Args... args) {
     uint64_t       grid = (items + 3) / 4;
     const uint64_t cap  = (uint64_t) num_cus() * (uint64_t) per_cu;
     grid                = grid > cap ? cap : grid;
-    hipLaunchKernelGGL(kernel, dim3((uint32_t) grid), dim3(256), 0, s, args...);
+    MI_LAUNCH(kernel, dim3((uint32_t) grid), dim3(256), 0, s, args...);
 }
 
 template <int TI, int TC, int D, int ROUND, bool TOCACHE>
@@ -406,7 +406,7 @@ static void launch_fast(const HeadArgs & a, hipStream_t s) {
         if (nbq + nbk > (uint32_t) MI_ROPE_PF) {
             const uint64_t waves = (uint64_t) a.ntok * (nbq + nbk);
             HeadKV         kv{};
-            hipLaunchKernelGGL((k_heads_kv<TI, TI, D, 0, false>), dim3((uint32_t) ((waves + 3) / 4)), dim3(256), 0,
+            MI_LAUNCH((k_heads_kv<TI, TI, D, 0, false>), dim3((uint32_t) ((waves + 3) / 4)), dim3(256), 0,
                                s, a, kv, nbq, nbk, FastDiv(nbq + nbk));
             return;
         }
@@ -467,7 +467,7 @@ static int launch_t(HeadArgs & a, bool fast, hipStream_t s) {
     uint64_t grid = (rows + 3) / 4;
     const uint64_t cap = (uint64_t) num_cus() * 16;
     grid = grid > cap ? cap : (grid ? grid : 1);
-    hipLaunchKernelGGL((k_heads_generic<TI, TO>), dim3((uint32_t) grid), dim3(256), 0, s, a);
+    MI_LAUNCH((k_heads_generic<TI, TO>), dim3((uint32_t) grid), dim3(256), 0, s, a);
     return MI_OK;
 }
 
@@ -749,12 +749,12 @@ static void launch_kv_d(const HeadArgs & a, const HeadKV & kv, int rounding, uin
     const dim3     grid((uint32_t) ((waves + 3) / 4));
     if constexpr (TC == MI_TYPE_Q8_0) {
         if (rounding == MI_Q8_0_REF) {
-            hipLaunchKernelGGL((k_heads_kv<TI, TC, D, MI_Q8_0_REF>), grid, dim3(256), 0, s, a, kv, nbq, nbk,
+            MI_LAUNCH((k_heads_kv<TI, TC, D, MI_Q8_0_REF>), grid, dim3(256), 0, s, a, kv, nbq, nbk,
                                FastDiv(nbt));
             return;
         }
     }
-    hipLaunchKernelGGL((k_heads_kv<TI, TC, D, MI_Q8_0_CPU_X86>), grid, dim3(256), 0, s, a, kv, nbq, nbk, FastDiv(nbt));
+    MI_LAUNCH((k_heads_kv<TI, TC, D, MI_Q8_0_CPU_X86>), grid, dim3(256), 0, s, a, kv, nbq, nbk, FastDiv(nbt));
 }
 
 template <int TI, int TC>

@@ -287,12 +287,12 @@ int launch_stork4(const StorkArgs & a, const StorkPlan * plans, hipStream_t s) {
     const uint32_t blocks = (uint32_t) std::min<uint64_t>((a.n + 1023) / 1024, 2048);
     if (a.hist > 0) {
         const uint32_t nblk = (uint32_t) std::min<uint64_t>((a.n + 1023) / 1024, STORK_STAT_BLOCKS);
-        hipLaunchKernelGGL(k_stork_stats, dim3(nblk), dim3(256), 0, s, a);
+        MI_LAUNCH(k_stork_stats, dim3(nblk), dim3(256), 0, s, a);
         for (int q = 0; q < a.n_attempts; ++q) {
-            hipLaunchKernelGGL(k_stork_attempt, dim3(blocks), dim3(256), 0, s, a, plans[q], nblk);
+            MI_LAUNCH(k_stork_attempt, dim3(blocks), dim3(256), 0, s, a, plans[q], nblk);
         }
     }
-    hipLaunchKernelGGL(k_stork_commit, dim3(blocks), dim3(256), 0, s, a);
+    MI_LAUNCH(k_stork_commit, dim3(blocks), dim3(256), 0, s, a);
     return MI_OK;
 }
 
@@ -354,7 +354,7 @@ int launch_dcw(const DcwArgs & a, hipStream_t s) {
     if (work == 0) {
         return MI_OK;
     }
-    hipLaunchKernelGGL(k_dcw, dim3((uint32_t) ((work + 255) / 256)), dim3(256), 0, s, a);
+    MI_LAUNCH(k_dcw, dim3((uint32_t) ((work + 255) / 256)), dim3(256), 0, s, a);
     return MI_OK;
 }
 
@@ -364,7 +364,7 @@ int launch_apg(const ApgArgs & a, hipStream_t s) {
     }
     const uint32_t nph = 1024 / a.oc;
     const size_t   lds = (size_t) (3 * nph * a.oc + 3 * a.oc) * sizeof(double);
-    hipLaunchKernelGGL(k_apg, dim3(a.n), dim3(nph * a.oc), lds, s, a);
+    MI_LAUNCH(k_apg, dim3(a.n), dim3(nph * a.oc), lds, s, a);
     return MI_OK;
 }
 
@@ -372,7 +372,7 @@ int launch_flow_step(const FlowArgs & a, hipStream_t s) {
     if (a.n == 0) {
         return MI_OK;
     }
-    hipLaunchKernelGGL(k_flow_step, dim3((uint32_t) ((a.n + 255) / 256)), dim3(256), 0, s, a);
+    MI_LAUNCH(k_flow_step, dim3((uint32_t) ((a.n + 255) / 256)), dim3(256), 0, s, a);
     return MI_OK;
 }
 

@@ -57,15 +57,15 @@ static void scale_out(const mi_tensor & x, float sc, const mi_tensor & y, uint32
     const uint32_t rows = (uint32_t) nrows(x), n = (uint32_t) x.ne[0];
     switch (y.type) {
         case MI_TYPE_F32:
-            hipLaunchKernelGGL((k_scale<TI, MI_TYPE_F32>), dim3(grid), dim3(256), 0, s, (const char *) x.data, xr,
+            MI_LAUNCH((k_scale<TI, MI_TYPE_F32>), dim3(grid), dim3(256), 0, s, (const char *) x.data, xr,
                                (char *) y.data, yr, rows, n, sc);
             break;
         case MI_TYPE_BF16:
-            hipLaunchKernelGGL((k_scale<TI, MI_TYPE_BF16>), dim3(grid), dim3(256), 0, s, (const char *) x.data, xr,
+            MI_LAUNCH((k_scale<TI, MI_TYPE_BF16>), dim3(grid), dim3(256), 0, s, (const char *) x.data, xr,
                                (char *) y.data, yr, rows, n, sc);
             break;
         default:
-            hipLaunchKernelGGL((k_scale<TI, MI_TYPE_F16>), dim3(grid), dim3(256), 0, s, (const char *) x.data, xr,
+            MI_LAUNCH((k_scale<TI, MI_TYPE_F16>), dim3(grid), dim3(256), 0, s, (const char *) x.data, xr,
                                (char *) y.data, yr, rows, n, sc);
             break;
     }
@@ -100,7 +100,7 @@ int launch_timestep_embedding(const float * t, int64_t n, int64_t ts, int dim, i
     }
     int64_t grid = (total + 255) / 256;
     grid         = grid > 1024 ? 1024 : grid;
-    hipLaunchKernelGGL(k_tsembd, dim3((uint32_t) grid), dim3(256), 0, s, t, n, ts, dim, max_period, y, ys);
+    MI_LAUNCH(k_tsembd, dim3((uint32_t) grid), dim3(256), 0, s, t, n, ts, dim, max_period, y, ys);
     return MI_OK;
 }
 

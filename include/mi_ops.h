@@ -285,8 +285,11 @@ int mi_mul_mat_q8_0(const void * w, int64_t k, int64_t n, const mi_tensor * x, c
  * to 8 and prefill chunks up to about m * k = 28M fit) returns MI_ERR_SCRATCH
  * before any launch. Every call on one GPU uses the same array, so calls that
  * overlap on one GPU (other streams, other host threads) race; stream-ordered
- * calls do not. Nothing in it has to start at zero: a call writes every
- * scratch value it reads. y is bit-identical to mi_mul_mat_q8_0's. */
+ * calls do not. Nothing in it has to start at zero: every scratch value that
+ * feeds a stored y element is written by the same call. (The matrix kernel,
+ * m > 8, reads the quantized x of the padding rows m .. 128*ceil(m/128)-1,
+ * which an earlier call may have left there; those rows only produce y rows
+ * that are never stored.) y is bit-identical to mi_mul_mat_q8_0's. */
 #define MI_MUL_MAT_NOALLOC_SCRATCH_BYTES ((size_t) 32 << 20)
 int mi_mul_mat_q8_0_noalloc(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * y,
                             mi_stream stream);
@@ -459,6 +462,8 @@ int mi_gguf_upload_rows(const mi_gguf * g, const char * const * names, int n, vo
 /* Layer-chain drivers: launch the fused-op sequence of one DiT block or   */
 /* one Qwen3 layer in the order of the reference's layer composers, taking */
 /* the GEMM / attention outputs (not computed by this library) as inputs.  */
+/* Every operand of the whole chain is validated before the first launch:  */
+/* a non-zero return means nothing was launched and no buffer was written. */
 
 /* One ACE-Step DiT block's non-GEMM ops, in dit_ggml_build_layer order
  * (dit-graph.h:367-448). hidden is updated in place. Each residual add is
@@ -504,7 +509,11 @@ int mi_dit_block_ops(const mi_dit_block_io * io, mi_stream stream);
  *   (clamp v in place when clamp_fp16), kv_store(k_out, v -> caches at pos0/sets)
  *     (with a cache and k_out.data NULL these are one mi_qk_norm_rope_kv_store
  *     launch instead: K goes only to the cache, and v is left unclamped in
- *     place; the cache gets the clamped values either way)
+ *     place; the cache gets the clamped values either way. That launch has
+ *     mi_qk_norm_rope_kv_store's limits: for partial rotation (n_dims < D),
+ *     D outside {64, 128, 256} or q/k/v views that are not 16-byte aligned,
+ *     pass a k_out buffer, which selects the three-call path; without one
+ *     such a layer returns MI_ERR_UNSUPPORTED before any launch)
  *   hidden = hidden + attn_out   (clamped to +-65504 when clamp_fp16), fused with
  *   norm2  = rms_norm(hidden) * post_norm_w
  *   ff     = swiglu(gate_up)

@@ -382,6 +382,58 @@ def test_chain_validation():
     assert L.mi_qwen3_layer_ops(None, NULL_S) == -1
 
 
+def test_descriptor_extent_overflow_is_refused():
+    """ne1*ne2*ne3 (or the byte extent) past int64 is refused before launch:
+    an unchecked product would wrap to a small or negative row count."""
+    y = _t([4, 8])
+    wrap = _t([4, 2**32 + 1, 2**32 - 1, 1], nb=[4, 16, 16, 16])   # rows wrap to -1 in int64
+    assert L.mi_rms_norm(R(wrap), None, 1e-6, R(y), NULL_S) in (-3, -7)
+    big = _t([4, 2**20, 2**20, 2**20], nb=[4, 16, 16, 16])          # 2^60 rows x 4: elements overflow
+    assert L.mi_rms_norm(R(big), None, 1e-6, R(y), NULL_S) in (-3, -7)
+    ext = _t([4, 2, 1, 1], nb=[4, 2**63 - 8, 16, 16])               # byte extent past 2^63
+    assert L.mi_rms_norm(R(ext), None, 1e-6, R(_t([4, 2])), NULL_S) == -7
+    assert L.mi_rms_norm(R(_t([4, 2**31, 1, 1])), None, 1e-6, R(y), NULL_S) == -7
+
+
+def _qwen3_io(**bad):
+    """A decode-layer io (H=256, 4/2 heads x 64, I=512, 2 tokens, F32, Q8_0
+    caches) over fake, never dereferenced addresses; `bad` replaces fields."""
+    H, NH, NKV, D, I, N, SLOTS = 256, 4, 2, 64, 512, 2, 16
+    addr = [1 << 40]
+
+    def t(shape, typ=F32, nb=None):
+        addr[0] += 1 << 30
+        return _t(shape, typ, data=addr[0], nb=nb)
+
+    qkv_row = (NH + 2 * NKV) * D * 4
+    qkv = t([(NH + 2 * NKV) * D, N])
+    view = lambda off, heads: _t([D, heads, N], data=qkv.data + off, nb=[4, D * 4, qkv_row, qkv_row * N])  # noqa
+    io = _lib.MiQwen3LayerIO()
+    io.hidden, io.in_norm_w, io.post_norm_w = t([H, N]), t([H]), t([H])
+    io.norm, io.norm2 = t([H, N]), t([H, N])
+    io.q, io.k, io.v = view(0, NH), view(NH * D * 4, NKV), view((NH + NKV) * D * 4, NKV)
+    io.q_w, io.k_w, io.q_out, io.k_out, io.pos = t([D]), t([D]), t([D, NH, N]), t([D, NKV, N]), t([N], I32)
+    io.k_cache, io.v_cache = t([D, SLOTS, NKV, N], Q8_0), t([D, SLOTS, NKV, N], Q8_0)
+    io.pos0, io.sets = t([N], I32), t([N], I32)
+    io.attn_out, io.gate_up, io.ff, io.mlp_out = t([H, N]), t([2 * I, N]), t([I, N]), t([H, N])
+    io.eps, io.rope_freq_base, io.n_dims, io.clamp_fp16, io.kv_rounding = 1e-6, 1e6, D, 1, _lib.Q8_0_CPU_X86
+    for k, v in bad.items():
+        setattr(io, k, v)
+    return io
+
+
+def test_chain_drivers_validate_before_any_launch():
+    """A bad operand late in the chain is reported as such (-3), not as the
+    HIP error (-8) the first launch gives on this GPU-less host: the whole
+    chain is validated before anything is launched (and so before `hidden`
+    could be updated in place)."""
+    assert L.mi_qwen3_layer_ops(R(_qwen3_io(mlp_out=_t([255, 2], data=1 << 50))), NULL_S) == -3
+    assert L.mi_qwen3_layer_ops(R(_qwen3_io(ff=_t([511, 2], data=1 << 50))), NULL_S) == -3
+    assert L.mi_qwen3_layer_ops(R(_qwen3_io(attn_out=_t([256, 3], data=1 << 50))), NULL_S) == -3
+    no_kout = _qwen3_io(k_out=_t([64, 2, 2], data=0), n_dims=32)     # fused path: partial rotation refused
+    assert L.mi_qwen3_layer_ops(R(no_kout), NULL_S) == -7
+
+
 def test_product_path_has_no_fallback(tmp_path):
     """The ops fail loudly when the HIP library is absent (no CPU fallback)."""
     import subprocess

@@ -114,3 +114,20 @@ def test_view_outside_its_allocation_is_refused():
     with pytest.raises(ValueError, match="outside"):
         ops.desc(bad)
     ops.desc(t[1:, 2:])
+
+
+@pytest.mark.parametrize("cross", [False, True])
+def test_dit_block_bad_late_operand_returns_before_any_launch(cross):
+    """The block's descriptors with the SwiGLU input (the 5th or 7th op of the
+    chain) one column short: mi_dit_block_ops reports the shape error (-3)
+    rather than the HIP error (-8) the first launch gives on this GPU-less
+    host, so nothing ran (and `hidden` was not updated in place)."""
+    import ctypes
+    ALLOCS.clear()
+    io, _, _, _ = dit_block_case.build("bf16", cross, _HostStorage)
+    io.gate_up.ne[0] -= 2
+    lib = _lib.load()
+    assert lib.mi_dit_block_ops(ctypes.byref(io), None) == -3
+    io.gate_up.ne[0] += 2
+    io.ffn_out.ne[1] -= 1
+    assert lib.mi_dit_block_ops(ctypes.byref(io), None) == -3
