@@ -520,12 +520,23 @@ def _qwen3_configs():
                         "f32", 16384, 2560, 32, 8, 9728, kv=(8, 2048, 8192, s0), pos=ppos)
 
 
-def configs_bench(steps: int, warmup: int):
-    """One JSON line per Qwen3 configuration: µs per layer and GB/s per op."""
+def configs_bench(steps: int, warmup: int, emit: bool = True) -> list:
+    """Per Qwen3 configuration: µs per layer (one replay of a graph of `steps`
+    consecutive layers), and per op two timings that bracket the kernel's own
+    duration:
+      us      HIP event pairs around its launch inside the layer sequence; they
+              include ~2.5-3 us of event and dispatch time per launch (most of
+              the figure for the decode-sized ops);
+      us_b2b  one replay of a graph of `steps` back-to-back launches of the op
+              alone, per launch; no event time, but a repeated launch can
+              re-read inputs that fit the 256 MB last-level cache.
+    GB/s and frac use `us` (the conservative one), GB/s_b2b and frac_b2b
+    us_b2b. One JSON line each when `emit`."""
     from acestep_ops import device
     from acestep_ops.device import Event, Graph
 
-    for make in _qwen3_configs():
+    out = []
+    for key, make in zip(("C1", "C2", "C4", "C5"), _qwen3_configs()):
         c = make()
         st, sh = c["stream"], c["stream"].handle
         fns = [f for _, f in c["launches"]]
@@ -558,17 +569,35 @@ def configs_bench(steps: int, warmup: int):
                 ev[i][j + 1].record(sh)
         st.synchronize()
         per = {}
-        for j, (label, _) in enumerate(c["launches"]):
+        for j, (label, f) in enumerate(c["launches"]):
             us = 1000.0 * float(np.mean([ev[i][j].elapsed_ms(ev[i][j + 1]) for i in range(steps)]))
+            gb = Graph()
+            with gb.capture(st):
+                for _ in range(steps):
+                    f()
+            gb.launch()
+            st.synchronize()
+            a.record(sh)
+            gb.launch()
+            b.record(sh)
+            b.synchronize()
+            us_b2b = 1000.0 * a.elapsed_ms(b) / steps
             gbs = c["bytes"][label] / (us * 1e-6) / 1e9
-            per[label] = {"us": round(us, 2), "MB": round(c["bytes"][label] / 1e6, 3), "GB/s": round(gbs, 1),
-                          "frac": round(gbs / HBM_PEAK_GBS, 3)}
+            gbs_b = c["bytes"][label] / (us_b2b * 1e-6) / 1e9
+            per[label] = {"us": round(us, 2), "us_b2b": round(us_b2b, 2), "MB": round(c["bytes"][label] / 1e6, 3),
+                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3),
+                          "GB/s_b2b": round(gbs_b, 1), "frac_b2b": round(gbs_b / HBM_PEAK_GBS, 3)}
+            del gb
         tot = sum(c["bytes"].values())
-        print(json.dumps({"config": c["name"], "us_per_layer": round(us_layer, 2), "launches": len(fns),
-                          "bytes_per_layer": tot, "GB/s": round(tot / (us_layer * 1e-6) / 1e9, 1),
-                          "per_op": per}), flush=True)
+        r = {"key": key, "config": c["name"], "us_per_layer": round(us_layer, 2), "launches": len(fns),
+             "bytes_per_layer": tot, "GB/s": round(tot / (us_layer * 1e-6) / 1e9, 1),
+             "frac": round(tot / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 3), "per_op": per}
+        out.append(r)
+        if emit:
+            print(json.dumps(r), flush=True)
         del c, g, g1
         device.synchronize()
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -862,6 +891,7 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=ROWS, help="rows of the block the CPU baseline runs")
     ap.add_argument("--cpu-reps", type=int, default=64, help="timed CPU repetitions (about 10 s on 8 threads)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="leave the Qwen3 layer chains out of the default line")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="launch each block kernel once plus a copy of known size, for counter collection")
     ap.add_argument("--configs", action="store_true",
@@ -908,6 +938,10 @@ def main():
     value = graph_bytes / (args.steps * ms_step * 1e-3) / 1e9
     dom = "swiglu"
     dom_gbs = kb[dom] / (per_k[dom] * 1e-6) / 1e9
+    # the Qwen3 layer chains (C1 0.6B T=512, C2 4B decode batch 8, C4 1.7B
+    # prefill 4x4096, C5 4B prefill 8x2048 into a Q8_0 KV cache), timed in the
+    # same run; they do not enter value
+    cfg = None if args.no_configs else configs_bench(min(args.steps, 20), args.warmup, emit=False)
 
     # HBM bytes per launch of the dominant kernel from the committed counter
     # summary (FETCH_SIZE and WRITE_SIZE, each scaled by a copy of known size)
@@ -939,6 +973,9 @@ def main():
             "value": round(total_bytes / cpu_block_s / 1e9, 3),
             "unit": "GB/s",
             "cores": threads,
+            "cores_note": (f"{threads} OpenMP threads (unpinned), so at most {threads} of the host's "
+                           f"{hc['physical_cores']} physical cores ({hc['threads_per_core']} hardware thread(s) "
+                           f"per core) busy at once"),
             "threads": threads,
             "kind": "port",
             "us_per_block": round(cpu_block_s * 1e6, 1),
@@ -990,7 +1027,11 @@ def main():
             "per_kernel_gbs": {k: round(kb_ca[k] / (per_k_ca[k] * 1e-6) / 1e9, 1) for k in kb_ca}},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_swiglu (bf16)",
-                     "bytes_per_launch": kb[dom]},
+                     "bytes_per_launch": kb[dom], "us_per_launch": round(per_k[dom], 2),
+                     "timing": "mean of HIP event pairs around the kernel's launch inside the steady-state block "
+                               "sequence on the bench stream (includes ~2.5-3 us of event and dispatch time that "
+                               "rocprof's kernel duration leaves out)"},
+        "configs": cfg,
         "cpu_baseline": cpu,
         "wall_s": round(wall, 4),
     }

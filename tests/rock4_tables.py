@@ -13,6 +13,8 @@ the same shape and layout built here:
 velocity integrates exactly (the weights of v sum to -dt), as a real ROCK4
 table does.
 """
+import os
+
 import numpy as np
 
 DEGREES = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16, 18, 20, 24, 28, 32, 40, 48, 64, 80, 100, 128, 148]
@@ -59,3 +61,40 @@ def degree_of(ms, s):
     row = int(np.searchsorted(ms, s, side="left"))
     off = int(np.sum(2 * ms[:row] - 1))
     return int(ms[row]), row, off
+
+
+REFERENCE_NPZ = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "rock4_reference.npz")
+
+
+def reference_tables():
+    """(ms, fpa, fpb, recf): the reference's own ROCK4 tables
+    (solver-stork4-constants.h), from the fixture tests/golden/make_rock4_tables.py wrote."""
+    d = np.load(REFERENCE_NPZ)
+    return d["ms"], d["fpa"], d["fpb"], d["recf"]
+
+
+def stability_polynomial(ms, fpa, fpb, recf, row):
+    """Coefficients (float64, ascending powers of z = h*lambda) of the polynomial
+    R with y_1 = R(z) y_0 when the degree-`row` scheme -- the recurrence
+    Y_1 = Y_0 + mu_1 z Y_0, Y_j = mu_j z Y_{j-1} + (1 + kappa_j) Y_{j-1} - kappa_j Y_{j-2},
+    then the four finishing stages and the fpb blend, as solver-stork.h:193-267
+    applies them -- integrates y' = lambda y over one step h."""
+    from numpy.polynomial import polynomial as P
+
+    m = int(ms[row])
+    off = int(np.sum(2 * np.asarray(ms[:row], np.int64) - 1))
+    b = np.asarray(recf[off:off + 2 * m - 1], np.float64)
+    z = [0.0, 1.0]
+    y2, y1 = np.array([1.0]), np.array([1.0, b[0]])
+    for j in range(2, m + 1):
+        mu, kap = b[2 * (j - 2) + 1], b[2 * (j - 2) + 2]
+        y2, y1 = y1, P.polyadd(P.polyadd(P.polymul([0.0, mu], y1), (1.0 + kap) * y1), -kap * y2)
+    a, w = fpa[row], fpb[row]
+    f1 = P.polymul(z, y1)
+    f2 = P.polymul(z, P.polyadd(y1, a[0] * f1))
+    f3 = P.polymul(z, P.polyadd(P.polyadd(y1, a[1] * f1), a[2] * f2))
+    f4 = P.polymul(z, P.polyadd(P.polyadd(P.polyadd(y1, a[3] * f1), a[4] * f2), a[5] * f3))
+    r = y1
+    for c, f in zip(w, (f1, f2, f3, f4)):
+        r = P.polyadd(r, c * f)
+    return r

@@ -171,6 +171,28 @@ def test_decode_heads_per_kv_head(dev, rk, masked, kt, qt):
     _run(N, Nkv * rk, Nkv, 1, n_kv, 128, kt, qt, mask=mask, seed=31 + rk)
 
 
+@pytest.mark.parametrize("kt,qt,rk,n_kv", [("f16", "f32", 4, 20), ("bf16", "bf16", 16, 32), ("f16", "bf16", 1, 7)])
+def test_decode_single_split_and_fully_masked_sequence(dev, kt, qt, rk, n_kv):
+    """The matrix-core decode kernel over at most 32 keys: one key split, so
+    the kernel writes the output itself (no partials, no merge launch). The
+    last sequence has every key masked: its rows are NaN (1/0 row sum)."""
+    print(f"fa decode one split kt={kt} qt={qt} rk={rk} n_kv={n_kv}", flush=True)
+    N, Nkv = 3, 2
+    assert _uses_mfma(kt, 128, 1, Nkv * rk, Nkv, n_kv, _decode_mask(N, n_kv, [n_kv, 3, 0]))
+    y, _ = _run(N, Nkv * rk, Nkv, 1, n_kv, 128, kt, qt, mask=_decode_mask(N, n_kv, [n_kv, 3, 0]), seed=41 + rk)
+    assert np.isnan(y[2]).all() and np.isfinite(y[:2]).all()
+
+
+@pytest.mark.parametrize("kt,n_kv", [("f16", 24), ("bf16", 700)])
+def test_decode_kv_and_mask_batch_broadcast(dev, kt, n_kv):
+    """Decode with K/V shared by pairs of query batches (batch b reads KV batch
+    b / 2) and a mask of 2 batches broadcast over 4 (batch b reads mask b % 2),
+    with one and with several key splits."""
+    print(f"fa decode broadcasts kt={kt} n_kv={n_kv}", flush=True)
+    m = _decode_mask(2, n_kv, [n_kv, n_kv // 3])
+    _run(4, 8, 2, 1, n_kv, 128, kt, "f32", mask=m, seed=51, Nk3=2)
+
+
 @pytest.mark.parametrize("kt", ["q8_0", "f16"])
 def test_decode_long_kv_splits(dev, kt):
     """8192 keys: the key range is split over many waves and merged."""

@@ -2,7 +2,9 @@
 norm, Q8_0 QKV product, QK-norm + rope, KV-cache write, flash attention over
 the cache, O product, fused residual add + norm, gate/up product, SwiGLU, down
 product, residual add) against the oracle, stage by stage
-(qw3lm_forward_batch, qwen3-lm.h:626-741).
+(qw3lm_forward_batch, qwen3-lm.h:626-741), at a small size and at the
+Qwen3-4B batch-8 decode shape (H 2560, 32/8 heads x 128, I 9728, 8192-slot
+caches, positions up to 8191).
 
 Every stage is checked against the oracle applied to the device's own inputs
 of that stage (read back from the layer's buffers), at that op's own bar:
@@ -36,11 +38,20 @@ def _w(r, n, k, s=0.05):
     return orc.quantize_q8_0((r.standard_normal((n, k)) * s).astype(np.float32))
 
 
-@pytest.mark.parametrize("kv_type,clamp", [("q8_0", False), ("f16", False), ("q8_0", True)])
-def test_decode_layer_stage_by_stage(dev, kv_type, clamp):
-    print(f"qwen3 decode layer kv={kv_type} clamp_fp16={clamp}", flush=True)
+# (H, Nh, Nkv, D, I, N, max_seq, n_sets, s0): a small layer, and the
+# Qwen3-4B decode layer at batch 8 over 8192-slot caches (one set more than
+# the batch, so one set stays untouched)
+SIZES = {"small": (256, 4, 2, 128, 512, 4, 512, 6, 1),
+         "qwen3_4b_b8": (2560, 32, 8, 128, 9728, 8, 8192, 9, 1)}
+
+
+@pytest.mark.parametrize("size,kv_type,clamp", [("small", "q8_0", False), ("small", "f16", False),
+                                                ("small", "q8_0", True), ("qwen3_4b_b8", "q8_0", False),
+                                                ("qwen3_4b_b8", "f16", False), ("qwen3_4b_b8", "q8_0", True)])
+def test_decode_layer_stage_by_stage(dev, size, kv_type, clamp):
+    print(f"qwen3 decode layer {size} kv={kv_type} clamp_fp16={clamp}", flush=True)
     r = np.random.default_rng(31)
-    H, Nh, Nkv, D, I, N, max_seq, n_sets, s0 = 256, 4, 2, 128, 512, 4, 512, 6, 1
+    H, Nh, Nkv, D, I, N, max_seq, n_sets, s0 = SIZES[size]
     eps, theta = 1e-6, 1e6
     Wqkv, Wo, Wgu, Wd = _w(r, (Nh + 2 * Nkv) * D, H), _w(r, H, Nh * D), _w(r, 2 * I, H), _w(r, H, I)
     nw_in, nw_post = (1 + 0.1 * r.standard_normal(H)).astype(np.float32), (1 + 0.1 * r.standard_normal(H)).astype(
@@ -56,10 +67,13 @@ def test_decode_layer_stage_by_stage(dev, kv_type, clamp):
                              to_dev(nw_in), to_dev(nw_post), to_dev(qn), to_dev(kn), H, Nh, Nkv, D, I, max_seq,
                              n_sets, kv_type, eps, theta, clamp_fp16=clamp)
     # earlier tokens already in the caches (random but finite), then this step's
-    pos = np.array([0, 37, 200, 255], np.int32)
-    read_len = 256
-    kc0 = (r.standard_normal((n_sets, Nkv, max_seq, D)) * 0.5).astype(np.float32)
-    vc0 = (r.standard_normal((n_sets, Nkv, max_seq, D)) * 0.5).astype(np.float32)
+    if size == "small":
+        pos = np.array([0, 37, 200, 255], np.int32)
+    else:  # positions U[0, 8191] with the extremes included
+        pos = np.concatenate([[0, max_seq - 1], r.integers(0, max_seq, N - 2)]).astype(np.int32)
+    read_len = int(min(max_seq, (pos.max() + 1 + 255) // 256 * 256))  # the 256-bucketed read (qwen3-lm.h:582-596)
+    kc0 = r.standard_normal((n_sets, Nkv, max_seq, D), dtype=np.float32) * np.float32(0.5)
+    vc0 = r.standard_normal((n_sets, Nkv, max_seq, D), dtype=np.float32) * np.float32(0.5)
     if kv_type == "q8_0":
         kq, vq = orc.quantize_q8_0(kc0, "x86"), orc.quantize_q8_0(vc0, "x86")
         layer.k_cache, layer.v_cache = ops.Q8(to_dev(kq)), ops.Q8(to_dev(vq))
@@ -114,7 +128,8 @@ def test_decode_layer_stage_by_stage(dev, kv_type, clamp):
     kr, vr = kcache[s0:s0 + N, :, :read_len], vcache[s0:s0 + N, :, :read_len]
     attn = b["attn"]
     ref = orc.flash_attn_ext(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type)
-    bound = fa_bound(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type)
+    # F16/BF16 caches run the matrix-core decode kernel (P in two 16-bit parts)
+    bound = fa_bound(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type, mfma=kv_type in ("f16", "bf16"))
     assert np.all(np.abs(attn - ref) <= bound)
     # 5. O product; the residual sum (clamped with clamp_fp16) bit-exact
     assert_mul_mat_q8_0(b["ao"], Wo, attn.reshape(N, Nh * D))

@@ -7,13 +7,16 @@ so results are bit-exact. The one reduction, STORK4's sums of squares for the
 derivative guards, is summed in a different order than the oracle's; it only
 decides the derivative order, and the inputs here sit far from the guard
 thresholds, so the decisions agree and the results stay bit-exact.
-STORK4's ROCK4 tables are synthetic ones of the reference's layout
-(tests/rock4_tables.py): the step's arithmetic does not depend on their values."""
+STORK4 runs with synthetic ROCK4 tables of the reference's layout
+(tests/rock4_tables.py), which steer every path, and with the reference's own
+tables (solver-stork4-constants.h, kept as the fixture
+tests/golden/rock4_reference.npz and pinned by the fourth-order conditions in
+tests/test_rock4_reference_cpu.py)."""
 import numpy as np
 import pytest
 from helpers import to_dev, to_np
 from oracle import oracle as orc
-from rock4_tables import make_tables
+from rock4_tables import degree_of, make_tables, reference_tables
 
 from acestep_ops import ops
 from acestep_ops import sampler as smp
@@ -75,6 +78,39 @@ def test_stork4_sequence_bit_exact(dev, shape, substeps):
         assert np.array_equal(to_np(xd), x), f"step {k}"
         assert np.array_equal(to_np(pd), p1) and np.array_equal(to_np(p2d), p2)
         assert (order, deg, fb) == (info[0], info[1], int(info[2])), f"step {k}: {(order, deg, fb)} vs {info}"
+        hist = min(hist + 1, 2)
+        h2, h1 = h1, float(np.float32(ts[k]) - np.float32(ts[k + 1]))
+
+
+@pytest.mark.parametrize("substeps", [1, 10, 21, 100, 148, 400])
+def test_stork4_reference_tables_bit_exact(dev, substeps):
+    """Five steps from the bootstrap with the reference's ROCK4 tables: the
+    degree each substep count selects (1 -> 2, 21 -> 22, 100 -> 105, 400 -> 148
+    the largest), its real recurrence and finishing coefficients, bit-exact against
+    the oracle, and the accepted degree as the reference's table lookup gives it."""
+    print(f"stork4 reference tables s={substeps}", flush=True)
+    r = np.random.default_rng(15)
+    tab = reference_tables()
+    tables = smp.Rock4Tables(*tab)
+    shape = (2, 250, 64)
+    x = r.standard_normal(shape).astype(np.float32)
+    xd = to_dev(x)
+    p1, p2 = np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+    pd, p2d = DTensor.zeros(shape, "f32"), DTensor.zeros(shape, "f32")
+    ws = smp.stork4_workspace(xd)
+    ts = [1.0, 0.93, 0.8, 0.62, 0.41, 0.2]
+    hist, h1, h2 = 0, 0.0, 0.0
+    for k in range(len(ts) - 1):
+        v, _, _ = _stork_case(r, shape, "order2")
+        smp.stork4_step(to_dev(v), xd, ts[k], ts[k + 1], hist, h1, h2, pd, p2d, tables, ws, substeps)
+        info = orc.stork4_step(x, v, ts[k], ts[k + 1], hist, h1, h2, p1, p2, substeps, tab)
+        fb, order, deg = smp.stork4_status(ws)
+        assert np.array_equal(to_np(xd), x), f"step {k}"
+        assert np.array_equal(to_np(pd), p1) and np.array_equal(to_np(p2d), p2)
+        assert (order, deg, fb) == (info[0], info[1], int(info[2])), f"step {k}: {(order, deg, fb)} vs {info}"
+        if k > 0:   # the bootstrap step is Euler (degree 0); later ones take the table's degree for
+            # max(substeps, 2) (solver-stork.h:296)
+            assert deg == degree_of(tab[0], max(substeps, 2))[0] and fb == 0
         hist = min(hist + 1, 2)
         h2, h1 = h1, float(np.float32(ts[k]) - np.float32(ts[k + 1]))
 
