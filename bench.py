@@ -686,9 +686,18 @@ def attention_bench(steps: int):
         vv = qkv.view(NB, S, NHD + 2 * NKVD, Dh)[:, :, NHD + NKVD:].permute(0, 2, 1, 3)
         yd = DTensor.empty((NB, S, NHD, Dh), "f32")
         zmask = DTensor.zeros((NB, 1, S, S), "f16")
+        # the sliding-window layers' mask (dit-sampler.h:253-274, every even
+        # layer, dit.h:399): |qi - ki| <= 128, no padding
+        win = 128
+        ii = np.arange(S)[:, None]
+        wm = np.where(np.abs(ii - np.arange(S)[None, :]) <= win, 0.0, -np.inf).astype(np.float16)
+        wmask = DTensor.from_numpy(np.ascontiguousarray(np.broadcast_to(wm, (NB, 1, S, S))).view(np.uint16), "f16")
+        live = float(np.isfinite(wm).sum())  # (query, key) pairs the window keeps
+        del wm, ii
         flops = 4.0 * S * S * Dh * NHD * NB
         wsd = DTensor.empty((max(ops.flash_attn_workspace(qv, kv, vv), 1),), "u8")
-        for label, mk in (("F16 padding mask (all zero)", zmask), ("no mask", None)):
+        for label, mk in ((f"F16 sliding-window mask (window {win})", wmask), ("F16 padding mask (all zero)", zmask),
+                          ("no mask", None)):
             call = lambda: ops.flash_attn_ext(qv, kv, vv, mk, 1.0 / float(np.sqrt(Dh)), out=yd,  # noqa
                                               workspace=wsd, stream=sh)
             # 30 untimed calls first: the first series after the uploads above runs
@@ -705,11 +714,16 @@ def attention_bench(steps: int):
             st.synchronize()
             us = 1000.0 * ev[0].elapsed_ms(ev[steps]) / steps
             tf = flops / (us * 1e-6) / 1e12
-            print(json.dumps({"config": f"DiT self-attention, bf16 q/k/v views, S={S} x {NB}, {NHD}/{NKVD} heads "
-                                        f"x {Dh}, {label}",
-                              "us_per_call": round(us, 2), "TFLOP/s": round(tf, 1), "flop_per_call": flops,
-                              "frac_of_bf16_dense": round(tf / 2500.0, 3)}), flush=True)
-        del qd, kd, qkv, qv, kv, vv, yd, zmask, wsd
+            rec = {"config": f"DiT self-attention, bf16 q/k/v views, S={S} x {NB}, {NHD}/{NKVD} heads x {Dh}, {label}",
+                   "us_per_call": round(us, 2), "TFLOP/s": round(tf, 1), "flop_per_call": flops,
+                   "frac_of_bf16_dense": round(tf / 2500.0, 3)}
+            if mk is wmask:
+                # dense-equivalent figures above; the window keeps `live` of S*S pairs
+                lf = 4.0 * live * Dh * NHD * NB
+                rec.update({"live_pairs_frac": round(live / (S * S), 4), "live_flop_per_call": lf,
+                            "live_TFLOP/s": round(lf / (us * 1e-6) / 1e12, 1)})
+            print(json.dumps(rec), flush=True)
+        del qd, kd, qkv, qv, kv, vv, yd, zmask, wmask, wsd
         device.synchronize()
 
 # ---------------------------------------------------------------------------

@@ -317,3 +317,51 @@ def test_mfma_tail_split(dev, kt, n_kv, masked):
         mask = np.where(np.abs(i * (n_kv / n_q) - j) <= 40, 0.0, -np.inf).astype(np.float32)[None, None]
         mask[..., 7, :] = -np.inf
     _run(2, 16, 8, n_q, n_kv, 128, kt, "bf16", mask=mask, seed=11)
+
+
+def _dit_window_mask(S, win, real):
+    """The DiT self-attention mask of a sliding-window layer (dit-sampler.h:253-274):
+    0 where both positions are real (< real) and |qi - ki| <= win, else -inf;
+    [ki, qi] per batch element."""
+    i = np.arange(S)[:, None]
+    j = np.arange(S)[None, :]
+    ok = (i < real) & (j < real) & ((win <= 0) | (S <= win) | (np.abs(i - j) <= win))
+    return np.where(ok, 0.0, -np.inf).astype(np.float32)
+
+
+@pytest.mark.parametrize("S,win,real", [(3000, 128, 2950), (3000, 0, 3000)])
+def test_dit_self_attention_full_size(dev, S, win, real):
+    """The DiT's self attention as the reference runs it (dit-graph.h:201-231):
+    S = T / 2 = 3000 tokens per element of the CFG pair (T = 6000 frames at
+    patch size 2), 16/8 heads x 128, F32 q as a permuted view of the rope
+    output [D, Nh, S, N] -> [D, S, Nh, N], K/V cast to F16, and the F16 mask of
+    a sliding-window layer (window 128, the last 50 positions padding: their
+    query rows have every key masked and are NaN) or of a full-attention layer
+    without padding (all zero). The whole problem runs on the device; 40 query
+    positions (window edges, padding edges, both ends) x both CFG elements x
+    all 16 heads are checked against the oracle under the kernel's bound."""
+    print(f"fa dit self attention S={S} win={win} real={real}", flush=True)
+    N, Nh, Nkv, D = 2, 16, 8, 128
+    r = _rng(61)
+    q = r.standard_normal((N, S, Nh, D), dtype=np.float32)      # rope output rows [D, Nh, S, N]
+    k = r.standard_normal((N, Nkv, S, D), dtype=np.float32)
+    v = r.standard_normal((N, Nkv, S, D), dtype=np.float32)
+    m = np.broadcast_to(_dit_window_mask(S, win, real), (N, 1, S, S))
+    dq = to_dev(q).permute(0, 2, 1, 3)                            # (N, Nh, S, D) view
+    dk, kf = _kv(k, "f16")
+    dv, vf = _kv(v, "f16")
+    dm, mf = _mask_dev(np.ascontiguousarray(m))
+    scale = 1.0 / np.sqrt(D)
+    y = to_np(ops.flash_attn_ext(dq, dk, dv, dm, float(scale)))   # (N, S, Nh, D)
+    qs = np.unique(np.r_[0, 1, 63, 64, 127, 128, 129, 255, 256, 1000, 1499, 1500, 2047, 2048,
+                         real - 130, real - 129, real - 128, real - 2, real - 1, real, real + 1, S - 2, S - 1,
+                         r.integers(0, S, 17)])
+    qs = qs[(qs >= 0) & (qs < S)]
+    qf = np.ascontiguousarray(q[:, qs].transpose(0, 2, 1, 3))     # (N, Nh, len(qs), D)
+    ms = np.ascontiguousarray(mf[:, :, qs])
+    ref = orc.flash_attn_ext(qf, kf, vf, ms, float(scale), "f16")
+    bound = fa_bound(qf, kf, vf, ms, float(scale), "f16", mfma=True)
+    assert _uses_mfma("f16", D, S, Nh, Nkv, S, mf)
+    _check(y[:, qs], ref, bound)
+    if real < S:
+        assert np.isnan(y[:, real:]).all() and np.isfinite(y[:, :real]).all()
