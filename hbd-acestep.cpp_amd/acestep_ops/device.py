@@ -64,7 +64,6 @@ def hip():
             "hipEventCreate": [ctypes.POINTER(vp)],
             "hipEventDestroy": [vp],
             "hipEventRecord": [vp, vp],
-            "hipEventRecordWithFlags": [vp, vp, ctypes.c_uint],
             "hipEventSynchronize": [vp],
             "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp],
             "hipGetDeviceCount": [ctypes.POINTER(i)],
@@ -382,12 +381,6 @@ class Event:
 
     def record(self, stream=None):
         check(hip().hipEventRecord(self.h, stream), "hipEventRecord")
-
-    def record_node(self, stream):
-        """Record on a capturing stream as an event-record node of the graph
-        (hipEventRecordExternal): each replay of the graph records the event
-        on the device, between the neighbouring nodes."""
-        check(hip().hipEventRecordWithFlags(self.h, stream, 1), "hipEventRecordWithFlags")
 
     def synchronize(self):
         check(hip().hipEventSynchronize(self.h), "hipEventSynchronize")
