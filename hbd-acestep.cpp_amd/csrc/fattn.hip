@@ -1194,8 +1194,8 @@ k_fa_mfma(const FaArgs a) {
     const float sl2  = a.scale * 1.4426950408889634f;  // scale * log2(e)
     const int   ntl  = (a.n_kv + BK - 1) / BK;
     const bool  allr = (int) (rbk * BQ + BQ) <= a.rows;  // every row of the workgroup valid
-    const int   tb   = part == 2 ? a.tmid : 0;             // this workgroup's key tiles [tb, te)
-    const int   te   = part == 1 ? a.tmid : ntl;
+    int         tb   = part == 2 ? a.tmid : 0;             // this workgroup's key tiles [tb, te)
+    int         te   = part == 1 ? a.tmid : ntl;
     // per tile, from the mask summary of this lane's row (one tile ahead): does
     // the wave read the tile's mask values, does it have a live key at all
     const uint8_t * sp =
@@ -1214,6 +1214,9 @@ k_fa_mfma(const FaArgs a) {
             return t < te ? 1 : 0;
         }
     };
+    if (tb >= te) {
+        return;  // no tile with a live key for any row of the workgroup
+    }
     int  fcur = flag(tb);
     load_tile(tb * BK);
     store_tile(0);
@@ -1347,15 +1350,41 @@ k_fa_mfma(const FaArgs a) {
     };
     bool clean = !MSK;
     if constexpr (MSK) {
-        // independent loads (no short-circuit): a chain of dependent byte loads
-        // would cost a memory latency per tile
-        uint32_t c = 1;
+        // One pass over this lane's summary bytes: are they all "live, zero"
+        // (then the workgroup may skip the per-tile reads), and which tiles hold
+        // a live key for the row. The workgroup then walks only the tiles from
+        // the first to the last live one of any of its rows (a sliding-window
+        // mask leaves a few of them), with the same tiles and order for every
+        // wave. Independent loads (no short-circuit): a chain of dependent byte
+        // loads would cost a memory latency per tile.
+        uint32_t c  = 1;
+        int      lo = te, hi = tb - 1;
         if (rvld) {
             for (int t = tb; t < te; ++t) {
-                c &= (uint32_t) (sp[t] == 1);
+                const uint32_t f = sp[t];
+                c &= (uint32_t) (f == 1);
+                lo = (f & 1) && t < lo ? t : lo;
+                hi = (f & 1) ? t : hi;
             }
         }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            lo = min(lo, __shfl_xor(lo, off, 64));
+            hi = max(hi, __shfl_xor(hi, off, 64));
+        }
+        __shared__ int wrange[4][2];
+        if (lane == 0) {
+            wrange[wave][0] = lo;
+            wrange[wave][1] = hi;
+        }
         clean = __syncthreads_and((int) c) != 0;  // workgroup-uniform: the waves share the K/V tiles
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            lo = min(lo, wrange[w][0]);
+            hi = max(hi, wrange[w][1]);
+        }
+        tb = lo;
+        te = hi + 1;
     }
     if (clean) {
         tiles(std::false_type{});
