@@ -937,6 +937,350 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
     }
 }
 
+// Decode on the matrix cores over a Q8_0 cache (D = 128, one query position,
+// at most 16 query heads per KV head, a mask row shared by every head): the
+// decomposition of k_fa_dec (a wave per key split, sequence and KV head; dead
+// tiles skipped before any K/V byte is read; the next tile's loads in flight)
+// with the Q8_0 arithmetic of k_fa_split:
+//   S^T = K Q^T block by block with v_mfma_i32_16x16x32_i8 (lane l: A[l%16]
+//   [8(l/16)+e], B[8(l/16)+e][l%16], C[4(l/16)+r][l%16]; checked on the
+//   device): A = 8 quants of key 16 mt + c16 read from the tile's raw rows in
+//   LDS (2-byte aligned 8-byte reads), B = q converted to Q8_0 with the x86
+//   quantizer as it sits in the lane (head c16, elements 32 kb + 8 q4 + e). The
+//   exact int32 block dots are scaled as k_fa_split scales them (fma(d_k *
+//   d_q, dot, s), blocks 0-1 and 2-3 summed apart, then added), so the scores
+//   equal its scores.
+//   O^T += V^T P^T per 32-column block b of V: B = p * d_v[key][b] (rounded
+//   once) as a high and a low bf16 part; A = the V tile's quants as bf16
+//   (exact), row-major in LDS and read transposed as in k_fa_dec. l sums p.
+// Keys no head reads get p = 0 and d_v = 0, so their bytes (integers, or a
+// NaN scale) never reach the output.
+#ifndef MI_FA_DEC_Q8
+#define MI_FA_DEC_Q8 1  // Q8_0 caches take k_fa_dec_q8 (else the split path)
+#endif
+__global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec_q8(const FaArgs a) {
+    typedef __bf16 x8 __attribute__((ext_vector_type(8)));
+    typedef float  f4 __attribute__((ext_vector_type(4)));
+    typedef int    i4 __attribute__((ext_vector_type(4)));
+    constexpr int D   = 128;
+    constexpr int T   = FA_TILE;                // keys per tile
+    constexpr int NB  = D / 32;                 // Q8_0 blocks per row
+    constexpr int RB  = NB * 34;                // bytes per cache row (136)
+    constexpr int VR  = D * 2 + 32;             // bf16 V row stride (bytes), as k_fa_dec
+    constexpr int NDT = D / 16;                 // 16-dim tiles of O^T
+
+    __shared__ __align__(16) char  kraw[T * RB];  // the tile's K rows as stored (136-byte rows)
+    __shared__ __align__(16) char  vt[T * VR];    // V quants as bf16, row-major
+    __shared__ __align__(16) float dks[NB][T];    // K block scales [block][key]
+    __shared__ __align__(16) float dvs[NB][T];    // V block scales, 0 for keys no head reads
+    __shared__ float               mt[FA_MAXT * T];
+    __shared__ uint32_t            lt[FA_MAXT];
+
+    const int      lane  = threadIdx.x;
+    const int      c16   = lane & 15, q4 = lane >> 4;
+    const uint32_t split = blockIdx.x;
+    const uint32_t bg    = blockIdx.y;
+    const uint32_t b     = bg / (uint32_t) a.nkv;
+    const uint32_t g     = bg - b * (uint32_t) a.nkv;
+    const bool     rv    = c16 < a.rows;
+    const int      h     = (int) g * a.rk + (rv ? c16 : 0);
+    const uint32_t kb3   = b / (uint32_t) a.rk3;
+    const char *   kg    = a.k + (int64_t) kb3 * a.k3 + (int64_t) g * a.k2;
+    const char *   vg    = a.v + (int64_t) kb3 * a.v3 + (int64_t) g * a.v2;
+    const char *   mrow  = a.mask ? a.mask + (int64_t) (b % (uint32_t) a.mne3) * a.m3 : nullptr;
+    const int      kbeg  = (int) split * a.chunk;
+    const int      kend  = kbeg + a.chunk < a.n_kv ? kbeg + a.chunk : a.n_kv;
+    const int      nt    = (kend - kbeg + T - 1) / T;
+    const int      key   = lane & 31;
+
+    // the split's mask values (one per key), issued first
+    float ms[FA_MAXT];
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        const int kc = kbeg + t * T + key < kend ? kbeg + t * T + key : kend - 1;
+        ms[t]        = mrow != nullptr && t < nt ? load_elem<MI_TYPE_F16>(mrow + (size_t) kc * 2) : 0.0f;
+    }
+    // q converted to Q8_0 (x86 from_float, as fa_q8_block): lane (c16, q4) holds
+    // elements 32 kb + 8 q4 + e of head c16, so each block's amax is a max over
+    // lanes c16 + 16 q4; B operand of block kb = its 8 quants, d_q its scale
+    long  qb8[NB];
+    float dq[NB];
+    {
+        const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2;
+        const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            const char * p = qp + (size_t) (32 * kb + 8 * q4) * es;
+            float        f[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float x;
+                if (a.tq == MI_TYPE_F32) {
+                    x = ((const float *) p)[e];
+                } else {
+                    const uint16_t hv = ((const uint16_t *) p)[e];
+                    x = a.tq == MI_TYPE_BF16 ? __uint_as_float((uint32_t) hv << 16) : (float) __builtin_bit_cast(_Float16, hv);
+                }
+                f[e] = rv ? x : 0.0f;
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                amax = fmaxf(amax, fabsf(f[e]));
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            constexpr float C  = 1.0f / 127.0f;
+            const float     q0 = amax * C;
+            const float     d  = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, amax), C, q0);  // IEEE amax / 127
+            const float     id = amax != 0.0f ? 127.0f / amax : 0.0f;
+            uint64_t        w  = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(f[e] * id), -128.0f, 127.0f);
+                w |= (uint64_t) ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
+            }
+            qb8[kb] = (long) w;
+            dq[kb]  = (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
+        }
+    }
+    // mask values into LDS and per tile the keys some head reads
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        if (t < nt) {
+            const int   k0 = kbeg + t * T + key;
+            const float x  = k0 < kend ? ms[t] : -INFINITY;
+            if (lane < 32) {
+                mt[t * T + key] = x;
+            }
+            const uint64_t lv = __builtin_amdgcn_ballot_w64(lane < 32 && x != -INFINITY);
+            if (lane == 0) {
+                lt[t] = (uint32_t) lv;
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+
+    // Tile loads: lane (key kk = lane / 2, half hf = lane % 2) loads bytes
+    // [68 hf, 68 hf + 68) of its key's K and V rows -- blocks 2 hf and 2 hf + 1
+    // -- as 17 words w[0..16]: eight 8-byte loads (row bytes 0..63, or
+    // 72..135) and one 4-byte load (64..67, or 68..71), rows 8-byte aligned
+    // (the planner checks the strides and bases). Keys past the split are
+    // clamped into it. Offsets inside a tile fit 32 bits (the planner keeps
+    // 32 rows below 4 GB).
+    const int      kk  = lane >> 1, hf = lane & 1;
+    const uint32_t o8  = hf ? 72u : 0u;     // the 8-byte loads' first byte
+    const uint32_t o4  = hf ? 68u : 64u;    // the 4-byte load's byte
+    uint2          kq8[8], vq8[8];
+    uint32_t       kq4, vq4;
+    auto           load_tile = [&](int t0) {
+        const int      nk  = kend - t0 < T ? kend - t0 : T;
+        const uint32_t kr  = (uint32_t) (kk < nk ? kk : nk - 1);
+        const char *   kt0 = kg + (int64_t) t0 * a.k1;
+        const char *   vt0 = vg + (int64_t) t0 * a.v1;
+        const uint32_t ko  = kr * (uint32_t) a.k1, vo = kr * (uint32_t) a.v1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            kq8[j] = *(const uint2 *) (kt0 + ko + o8 + 8 * j);
+            vq8[j] = *(const uint2 *) (vt0 + vo + o8 + 8 * j);
+        }
+        kq4 = *(const uint32_t *) (kt0 + ko + o4);
+        vq4 = *(const uint32_t *) (vt0 + vo + o4);
+    };
+    // the 17 words in row order: w[i] = bytes 68 hf + 4 i .. + 3
+    auto words = [&](const uint2 * q8, uint32_t q4, uint32_t * w) {
+#pragma unroll
+        for (int i = 0; i < 17; ++i) {
+            const int      j0 = i / 2, j1 = (i - 1) / 2;               // the 8-byte load holding word i (hf 0 / 1)
+            const uint32_t w0 = i < 16 ? (i % 2 ? q8[j0].y : q8[j0].x) : q4;
+            const uint32_t w1 = i > 0 ? ((i - 1) % 2 ? q8[j1].y : q8[j1].x) : q4;
+            w[i]              = hf ? w1 : w0;
+        }
+    };
+
+    f4 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        o[dt] = f4{ 0.0f, 0.0f, 0.0f, 0.0f };
+    }
+    float    mrun = -INFINITY, lrun = 0.0f;
+    uint32_t live = nt > 0 ? lt[0] : 0u;
+    if (live) {
+        load_tile(kbeg);
+    }
+    for (int t = 0; t < nt; ++t) {
+        const int      t0   = kbeg + t * T;
+        const uint32_t next = t + 1 < nt ? lt[t + 1] : 0u;
+        if (live) {
+            // K: the half-row into the raw tile, its block scales into dks. V:
+            // its block scales into dvs (0 for a key no head reads) and its
+            // quants as bf16 (exact) into the row-major tile.
+            const bool rd = (live >> kk) & 1u;
+            uint32_t   w[17];
+            words(kq8, kq4, w);
+            {
+                char * kp = kraw + kk * RB + 68 * hf;  // 4-byte aligned
+#pragma unroll
+                for (int i = 0; i < 17; ++i) {
+                    *(uint32_t *) (kp + 4 * i) = w[i];
+                }
+                dks[2 * hf][kk]     = (float) __builtin_bit_cast(_Float16, (uint16_t) (w[0] & 0xffffu));
+                dks[2 * hf + 1][kk] = (float) __builtin_bit_cast(_Float16, (uint16_t) (w[8] >> 16));
+            }
+            words(vq8, vq4, w);
+            {
+                dvs[2 * hf][kk]     = rd ? (float) __builtin_bit_cast(_Float16, (uint16_t) (w[0] & 0xffffu)) : 0.0f;
+                dvs[2 * hf + 1][kk] = rd ? (float) __builtin_bit_cast(_Float16, (uint16_t) (w[8] >> 16)) : 0.0f;
+                // quants: first block at half-row bytes 2..33, second at 36..67
+                uint32_t qa[8], qb[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    qa[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+                    qb[i] = w[9 + i];
+                }
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb) {
+                    const uint32_t * qw = bb ? qb : qa;
+                    uint32_t         bw[16];
+#pragma unroll
+                    for (int w4 = 0; w4 < 8; ++w4) {
+                        const int32_t x = (int32_t) qw[w4];
+                        bw[2 * w4]      = pack_bf16x2((float) (int8_t) (x & 0xff), (float) (int8_t) ((x >> 8) & 0xff));
+                        bw[2 * w4 + 1]  = pack_bf16x2((float) (int8_t) ((x >> 16) & 0xff), (float) (int8_t) (x >> 24));
+                    }
+                    uint4 * dst = (uint4 *) (vt + kk * VR + 64 * (2 * hf + bb));
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        dst[c] = make_uint4(bw[4 * c], bw[4 * c + 1], bw[4 * c + 2], bw[4 * c + 3]);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (next) {
+            load_tile(t0 + T);  // in flight during this tile's math
+        }
+        if (live) {
+            // S^T for keys 16 mt + [0, 16) x the 16 (padded) heads, block by block
+            f4 s[2];
+#pragma unroll
+            for (int mt2 = 0; mt2 < 2; ++mt2) {
+                i4 acc[NB];
+#pragma unroll
+                for (int kb = 0; kb < NB; ++kb) {
+                    const long ka = *(const long *) (kraw + (16 * mt2 + c16) * RB + 34 * kb + 2 + 8 * q4);
+                    acc[kb]       = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka, qb8[kb], i4{ 0, 0, 0, 0 }, 0, 0, 0);
+                }
+                // the scales of keys 16 mt + 4 q4 + r, r < 4, per block
+                f4 dk[NB];
+#pragma unroll
+                for (int kb = 0; kb < NB; ++kb) {
+                    dk[kb] = *(const f4 *) &dks[kb][16 * mt2 + 4 * q4];
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float sa = 0.0f, sb = 0.0f;
+                    sa        = __builtin_fmaf(dk[0][r] * dq[0], (float) acc[0][r], sa);
+                    sa        = __builtin_fmaf(dk[1][r] * dq[1], (float) acc[1][r], sa);
+                    sb        = __builtin_fmaf(dk[2][r] * dq[2], (float) acc[2][r], sb);
+                    sb        = __builtin_fmaf(dk[3][r] * dq[3], (float) acc[3][r], sb);
+                    s[mt2][r] = sa + sb;
+                }
+            }
+            // softmax as k_fa_dec: this lane's 8 keys of head c16, then the other 24 in lanes ^ 16, ^ 32
+            float x[8];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int   kk = 16 * (e >> 2) + 4 * q4 + (e & 3);
+                const float mv = mt[t * T + kk];
+                x[e]           = mv == -INFINITY ? -INFINITY : s[e >> 2][e & 3] * a.scale + mv;
+                tmax           = fmaxf(tmax, x[e]);
+            }
+            tmax           = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+            tmax           = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            const float mn = fmaxf(mrun, tmax);
+            float       alpha = 1.0f, p[8], psum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                p[e] = mn == -INFINITY || x[e] == -INFINITY ? 0.0f : __expf(x[e] - mn);
+                psum += p[e];
+            }
+            if (mn != -INFINITY) {
+                alpha = __expf(mrun - mn);  // exp(-inf) = 0 on the first live tile
+            }
+            mrun = mn;
+            lrun = lrun * alpha + psum;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                o[dt] *= alpha;
+            }
+            // O^T += V^T P'^T per V block: B = p * d_v[key][block] (high and low
+            // bf16 parts) for keys 4 q4 + r and 16 + 4 q4 + r; A = V^T row 16 dt + c16
+            // at those keys by two transposed reads of the bf16 tile (as k_fa_dec)
+#pragma unroll
+            for (int bk = 0; bk < NB; ++bk) {
+                const f4 d0 = *(const f4 *) &dvs[bk][4 * q4];
+                const f4 d1 = *(const f4 *) &dvs[bk][16 + 4 * q4];
+                x8       phi, plo;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float    pp = p[e] * (e < 4 ? d0[e & 3] : d1[e & 3]);
+                    const uint16_t hb = f32_to_bf16_bits(pp);
+                    phi[e]            = __builtin_bit_cast(__bf16, hb);
+                    plo[e]            = __builtin_bit_cast(__bf16, f32_to_bf16_bits(pp - __uint_as_float((uint32_t) hb << 16)));
+                }
+#pragma unroll
+                for (int dh = 0; dh < 2; ++dh) {
+                    const int     dt = 2 * bk + dh;
+                    const char *  vp = vt + (4 * q4 + c16 / 4) * VR + (16 * dt + 4 * (c16 & 3)) * 2;
+                    const fa_v4s  v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_v4s *) vp);             // keys 4 q4 + r
+                    const fa_v4s  v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_v4s *) (vp + 16 * VR));  // keys 16 + 4 q4 + r
+                    const x8      va = __builtin_bit_cast(x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi, o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo, o[dt], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();  // the next tile overwrites the LDS tiles
+        }
+        live = next;
+    }
+
+    // the head's sum over its 4 lanes; lane (c16, q4) holds O^T[16 dt + 4 q4 + r][c16]
+    lrun += __shfl_xor(lrun, 16, 64);
+    lrun += __shfl_xor(lrun, 32, 64);
+    if (!rv) {
+        return;
+    }
+    if (a.splits == 1) {
+        const float inv = 1.0f / lrun;  // all keys masked: 0 * inf = NaN, as ggml
+        float *     yp  = (float *) (a.y + (int64_t) b * a.y3 + (int64_t) h * a.y1);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                yp[16 * dt + 4 * q4 + r] = o[dt][r] * inv;
+            }
+        }
+    } else {
+        float * wp = a.ws + (((int64_t) split * a.nb * a.nkv + bg) * a.rows + c16) * (D + 2);
+        if (q4 == 0) {
+            wp[0] = mrun;
+            wp[1] = lrun;
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                wp[2 + 16 * dt + 4 * q4 + r] = o[dt][r];
+            }
+        }
+    }
+}
+
 // Mask summary for the matrix-core path, one wave per (mask batch and head,
 // group of 16 query positions, FA_SUM_T consecutive 64-key tiles): lane = 4
 // keys (4 * (lane % 16)) of rows lane / 16 + 4 i of each tile, as 8-byte loads
@@ -1512,6 +1856,13 @@ void flash_attn_plan(FaArgs & a, int D) {
     // decode on the matrix cores: one wave holds every query head of a KV head
     a.dec = MI_FA_DEC && (a.kt == MI_TYPE_F16 || a.kt == MI_TYPE_BF16) && D == 128 && a.n_q == 1 &&
             a.rows <= 16 && (a.mask == nullptr || a.mne2 == 1);
+    // Q8_0 caches: rows are loaded as 8-byte words, so every row start must be
+    // 8-byte aligned (136-byte rows: strides and bases multiples of 8), and a
+    // tile's 32 rows must span less than 4 GB (32-bit offsets)
+    a.dec = a.dec || (MI_FA_DEC_Q8 && a.kt == MI_TYPE_Q8_0 && D == 128 && a.n_q == 1 && a.rows <= 16 &&
+                      (a.mask == nullptr || a.mne2 == 1) && a.k1 % 8 == 0 && a.k2 % 8 == 0 && a.k3 % 8 == 0 &&
+                      a.v1 % 8 == 0 && a.v2 % 8 == 0 && a.v3 % 8 == 0 && aligned(a.k, 8) && aligned(a.v, 8) &&
+                      a.k1 < ((int64_t) 1 << 26) && a.v1 < ((int64_t) 1 << 26));
     if (a.dec) {
         a.rblocks = 1;
     }
@@ -1548,6 +1899,15 @@ static void launch_kd(const FaArgs & a, hipStream_t s) {
     if constexpr (D == 128 && (KT == MI_TYPE_F16 || KT == MI_TYPE_BF16)) {
         if (a.dec) {
             MI_LAUNCH((k_fa_dec<KT>), grid, dim3(64), 0, s, a);
+            if (a.splits > 1) {
+                MI_LAUNCH((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(256), 0, s, a);
+            }
+            return;
+        }
+    }
+    if constexpr (D == 128 && KT == MI_TYPE_Q8_0) {
+        if (a.dec) {
+            MI_LAUNCH(k_fa_dec_q8, grid, dim3(64), 0, s, a);
             if (a.splits > 1) {
                 MI_LAUNCH((k_fa_combine<D>), dim3((uint32_t) (a.nb * a.nkv * a.rows)), dim3(256), 0, s, a);
             }

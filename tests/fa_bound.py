@@ -25,7 +25,9 @@ rescales (each exp(m_old - m_new) carries the error above; their arguments add
 up to at most the score range) and the split merge weights.
 e_j: the matrix-core path multiplies V by P split into a high and a low 16-bit
 part while l sums the fp32 p: |e_j| <= 2^-18 p_j for bf16 parts, 2^-22 p_j +
-2^-25 for fp16 parts (the low part may be subnormal).
+2^-25 for fp16 parts (the low part may be subnormal). Over a Q8_0 cache the
+decode kernel splits p_j d_v (rounded once) into bf16 parts and multiplies the
+quants: relative to p_j |v_j| that is 2^-18 + 2^-24.
 The accumulation of o and l over n = n_kv (+ 2 n_kv for the two MFMA passes)
 roundings uses the probabilistic bound of Higham and Mary (SIAM J. Sci.
 Comput. 41(5), 2019): with rounding errors independent and mean zero, the
@@ -98,7 +100,12 @@ def fa_bound(q, k, v, mask, scale: float, kt: str, mfma: bool = False):
             t3 = LAMBDA * np.sqrt(n_round) * U * ((p @ aV) / L + np.abs(ref))
             bound = t1 + t3 + 2 * U * np.abs(ref) + 1e-37
             if mfma:
-                e = p * 2.0 ** -18 if kt == "bf16" else p * 2.0 ** -22 + np.where(live, 2.0 ** -25, 0.0)
+                if kt == "bf16":
+                    e = p * 2.0 ** -18
+                elif kt == "q8_0":
+                    e = p * (2.0 ** -18 + U)
+                else:
+                    e = p * 2.0 ** -22 + np.where(live, 2.0 ** -25, 0.0)
                 bound = bound + (e @ aV) / L
             bound = np.where(ok, bound, np.nan)
             for i, h in enumerate(hs):

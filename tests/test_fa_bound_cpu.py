@@ -53,6 +53,81 @@ def _emulate(q, k, v, mask, scale, kt, mfma=False, tile=32, drop_rescale=False):
     return y
 
 
+def _q8_parts(x):
+    """Q8_0 (x86) of rows x (..., D): block scales (..., D/32) and quants (..., D), as floats."""
+    D = x.shape[-1]
+    b = orc.quantize_q8_0(np.ascontiguousarray(x, F).reshape(-1, D), "x86").reshape(-1, D // 32, 34)
+    d = b[:, :, :2].copy().view(np.float16)[..., 0].astype(F)
+    qs = b[:, :, 2:].view(np.int8).astype(F)
+    return d.reshape(x.shape[:-1] + (D // 32,)), qs.reshape(x.shape)
+
+
+def _emulate_q8_dec(q, k, v, mask, scale, tile=32):
+    """The Q8_0 matrix-core decode kernel's arithmetic: q and K, V as Q8_0 (k, v
+    hold the float rows the quantizer sees), exact int block dots scaled by
+    fma(d_k * d_q, dot, s) with blocks 0-1 and 2-3 summed apart, p.V as
+    (p * d_v) split into bf16 high + low parts times the quants."""
+    dq, qq = _q8_parts(q[0])                    # (Nh, n_q, 4), (Nh, n_q, D)
+    dk, kq = _q8_parts(k[0, 0])                 # (n_kv, 4), (n_kv, D)
+    dv, vq = _q8_parts(v[0, 0])
+    Nh, n_q, D = qq.shape
+    n_kv = kq.shape[0]
+    y = np.empty((1, n_q, Nh, D), F)
+    for h in range(Nh):
+        for iq in range(n_q):
+            m, l, o = F(-np.inf), F(0), np.zeros(D, F)
+            for t0 in range(0, n_kv, tile):
+                kk = slice(t0, min(n_kv, t0 + tile))
+                dots = [(kq[kk, 32 * j:32 * j + 32] @ qq[h, iq, 32 * j:32 * j + 32]).astype(F) for j in range(4)]
+                w = [(dk[kk, j] * dq[h, iq, j]).astype(F) for j in range(4)]
+                sa = (w[1] * dots[1] + (w[0] * dots[0]).astype(F)).astype(F)
+                sb = (w[3] * dots[3] + (w[2] * dots[2]).astype(F)).astype(F)
+                s = (sa + sb).astype(F)
+                mv = mask[0, 0, iq, kk] if mask is not None else np.zeros_like(s)
+                x = np.where(mv == -np.inf, F(-np.inf), F(F(s * F(scale)) + mv)).astype(F)
+                mn = F(max(m, x.max()))
+                if mn == -np.inf:
+                    continue
+                alpha = F(np.exp(F(m - mn)))
+                p = np.exp((x - mn).astype(F)).astype(F)
+                m = mn
+                l = F(l * alpha)
+                o = (o * alpha).astype(F)
+                for j in range(p.size):
+                    l = F(l + p[j])
+                    for bk in range(4):
+                        pp = F(p[j] * dv[kk.start + j, bk])
+                        hi = orc.bf16_to_f32(orc.f32_to_bf16(np.array([pp], F)))[0]
+                        lo = orc.bf16_to_f32(orc.f32_to_bf16(np.array([F(pp - hi)], F)))[0]
+                        cols = slice(32 * bk, 32 * bk + 32)
+                        o[cols] = (o[cols] + (F(hi) + F(lo)) * vq[kk.start + j, cols]).astype(F)
+            y[0, iq, h] = (o * F(F(1) / l)).astype(F)
+    return y
+
+
+def test_emulated_q8_0_decode_kernel_within_bound():
+    """The Q8_0 decode kernel's arithmetic (one query position, 4 heads of one KV
+    head, scores of several magnitudes) stays inside the q8_0 matrix-core bound,
+    which it uses visibly."""
+    D, n_kv = 128, 300
+    r = np.random.default_rng(9)
+    for qscale in (1.0, 6.0):
+        q = (r.standard_normal((1, 4, 1, D)) * qscale).astype(F)
+        kx = r.standard_normal((1, 1, n_kv, D)).astype(F)
+        vx = r.standard_normal((1, 1, n_kv, D)).astype(F)
+        m = np.zeros((1, 1, 1, n_kv), F)
+        m[..., 250:] = -np.inf
+        kf = orc.dequantize_q8_0(orc.quantize_q8_0(kx.reshape(-1, D), "x86")).reshape(kx.shape)
+        vf = orc.dequantize_q8_0(orc.quantize_q8_0(vx.reshape(-1, D), "x86")).reshape(vx.shape)
+        scale = 1.0 / np.sqrt(D)
+        ref = orc.flash_attn_ext(q, kf, vf, m, scale, "q8_0")
+        bound = fa_bound(q, kf, vf, m, scale, "q8_0", mfma=True)
+        y = _emulate_q8_dec(q, kx, vx, m, scale)
+        err = np.abs(y.astype(np.float64) - ref)
+        assert np.all(err <= bound), (err / bound).max()
+        assert (err / bound).max() > 1e-3
+
+
 def _case(seed, n_kv, D, qscale, kt):
     r = np.random.default_rng(seed)
     q = (r.standard_normal((1, 2, 3, D)) * qscale).astype(F)

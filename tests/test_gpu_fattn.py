@@ -75,11 +75,12 @@ def _uses_mfma(kt, D, n_q, Nh, Nkv, n_kv, mask=None):
     """The launch plan's choice of a matrix-core kernel (flash_attn_plan): F16/BF16
     K/V at D = 128, with 64 or more query rows per KV head (prefill), or one query
     position, at most 16 heads per KV head and a mask row shared by every head
-    (decode). Both keep P as two 16-bit parts."""
-    if kt not in ("f16", "bf16") or D != 128 or n_kv <= 0:
+    (decode; Q8_0 K/V too, with 8-byte aligned rows as every cache here has).
+    They keep P (or P times V's block scale) as two 16-bit parts."""
+    if kt not in ("f16", "bf16", "q8_0") or D != 128 or n_kv <= 0:
         return False
     dec = n_q == 1 and Nh // Nkv <= 16 and (mask is None or mask.shape[1] == 1)
-    return n_q * (Nh // Nkv) >= 64 or dec
+    return dec or (kt != "q8_0" and n_q * (Nh // Nkv) >= 64)
 
 
 def _run(N, Nh, Nkv, n_q, n_kv, D, kt, qt="f32", mask=None, scale=None, seed=0, Nk3=None, kview=None):

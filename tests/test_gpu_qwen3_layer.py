@@ -128,8 +128,9 @@ def test_decode_layer_stage_by_stage(dev, size, kv_type, clamp):
     kr, vr = kcache[s0:s0 + N, :, :read_len], vcache[s0:s0 + N, :, :read_len]
     attn = b["attn"]
     ref = orc.flash_attn_ext(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type)
-    # F16/BF16 caches run the matrix-core decode kernel (P in two 16-bit parts)
-    bound = fa_bound(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type, mfma=kv_type in ("f16", "bf16"))
+    # every cache type runs a matrix-core decode kernel (P, or P times V's block
+    # scale, in two 16-bit parts)
+    bound = fa_bound(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type, mfma=True)
     assert np.all(np.abs(attn - ref) <= bound)
     # 5. O product; the residual sum (clamped with clamp_fp16) bit-exact
     assert_mul_mat_q8_0(b["ao"], Wo, attn.reshape(N, Nh * D))
