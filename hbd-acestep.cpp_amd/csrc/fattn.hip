@@ -1199,24 +1199,29 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec_q8(const FaArgs a) 
                 x[e]           = mv == -INFINITY ? -INFINITY : s[e >> 2][e & 3] * a.scale + mv;
                 tmax           = fmaxf(tmax, x[e]);
             }
-            tmax           = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-            tmax           = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-            const float mn = fmaxf(mrun, tmax);
-            float       alpha = 1.0f, p[8], psum = 0.0f;
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            // Lazy rescale (as k_fa_mfma): the reference max moves only when some
+            // head's max passes it by more than ln 256, so p <= 256 and O, l are
+            // rescaled only then
+            if (__builtin_amdgcn_ballot_w64(tmax > mrun + 5.5451774f) != 0) {
+                __asm__ volatile("");  // a real branch: the 32 multiplies are not speculated
+                const float mn    = fmaxf(mrun, tmax);
+                const float alpha = mn == -INFINITY ? 1.0f : __expf(mrun - mn);  // exp(-inf) = 0 on the first live tile
+                mrun              = mn;
+                lrun *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    o[dt] *= alpha;
+                }
+            }
+            float p[8], psum = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                p[e] = mn == -INFINITY || x[e] == -INFINITY ? 0.0f : __expf(x[e] - mn);
+                p[e] = mrun == -INFINITY || x[e] == -INFINITY ? 0.0f : __expf(x[e] - mrun);
                 psum += p[e];
             }
-            if (mn != -INFINITY) {
-                alpha = __expf(mrun - mn);  // exp(-inf) = 0 on the first live tile
-            }
-            mrun = mn;
-            lrun = lrun * alpha + psum;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                o[dt] *= alpha;
-            }
+            lrun += psum;
             // O^T += V^T P'^T per V block: B = p * d_v[key][block] (high and low
             // bf16 parts) for keys 4 q4 + r and 16 + 4 q4 + r; A = V^T row 16 dt + c16
             // at those keys by two transposed reads of the bf16 tile (as k_fa_dec)
@@ -1224,14 +1229,18 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec_q8(const FaArgs a) 
             for (int bk = 0; bk < NB; ++bk) {
                 const f4 d0 = *(const f4 *) &dvs[bk][4 * q4];
                 const f4 d1 = *(const f4 *) &dvs[bk][16 + 4 * q4];
-                x8       phi, plo;
+                // pairs through the packed conversion (RNE): the high parts, their
+                // values back as floats, the remainders, the low parts
+                uint32_t hw[4], lw[4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float    pp = p[e] * (e < 4 ? d0[e & 3] : d1[e & 3]);
-                    const uint16_t hb = f32_to_bf16_bits(pp);
-                    phi[e]            = __builtin_bit_cast(__bf16, hb);
-                    plo[e]            = __builtin_bit_cast(__bf16, f32_to_bf16_bits(pp - __uint_as_float((uint32_t) hb << 16)));
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    const float pa = p[2 * e2] * (e2 < 2 ? d0[2 * e2] : d1[2 * e2 - 4]);
+                    const float pb = p[2 * e2 + 1] * (e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3]);
+                    hw[e2]         = pack_bf16x2(pa, pb);
+                    lw[e2]         = pack_bf16x2(pa - __uint_as_float(hw[e2] << 16), pb - __uint_as_float(hw[e2] & 0xffff0000u));
                 }
+                const x8 phi = __builtin_bit_cast(x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+                const x8 plo = __builtin_bit_cast(x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
 #pragma unroll
                 for (int dh = 0; dh < 2; ++dh) {
                     const int     dt = 2 * bk + dh;
