@@ -1710,14 +1710,27 @@ k_fa_mfma(const FaArgs a) {
         // mask leaves a few of them), with the same tiles and order for every
         // wave. Independent loads (no short-circuit): a chain of dependent byte
         // loads would cost a memory latency per tile.
+        // The bytes are read 16 at a time, all 16 loads issued before any is
+        // used: one memory latency per 16 tiles, where a loop of single loads
+        // waits once per tile.
         uint32_t c  = 1;
         int      lo = te, hi = tb - 1;
         if (rvld) {
-            for (int t = tb; t < te; ++t) {
-                const uint32_t f = sp[t];
-                c &= (uint32_t) (f == 1);
-                lo = (f & 1) && t < lo ? t : lo;
-                hi = (f & 1) ? t : hi;
+            for (int t16 = tb; t16 < te; t16 += 16) {
+                uint32_t f[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    f[j] = sp[t16 + j < te ? t16 + j : te - 1];  // past the range: a repeat of the last byte
+                }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int t = t16 + j;
+                    if (t < te) {
+                        c &= (uint32_t) (f[j] == 1);
+                        lo = (f[j] & 1) && t < lo ? t : lo;
+                        hi = (f[j] & 1) ? t : hi;
+                    }
+                }
             }
         }
 #pragma unroll
