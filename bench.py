@@ -220,6 +220,30 @@ def pmc_pass():
           "read, 147456000 B written)", flush=True)
 
 
+def pmc_pass_configs():
+    """The C4 and C5 layers' QK-norm/rope, Q8_0 get_rows, Q8_0 KV store and
+    dequant-back launched once each, eagerly, then the same calibration copy as
+    pmc_pass (for rocprofv3 --pmc)."""
+    from acestep_ops import device, ops
+    from acestep_ops.device import DTensor, Stream
+
+    gens = list(_qwen3_configs())
+    for idx in (2, 3):  # C4, C5
+        c = gens[idx]()
+        for label, f in c["launches"]:
+            if label in ("get_rows_q8_0", "kv_store_q8_0", "get_rows_kv_back", "qk_norm_rope"):
+                f()
+        c["stream"].synchronize()
+        del c
+        device.synchronize()
+    st = Stream()
+    a, b = DTensor.empty((BATCH, T_FRAMES, I_FF), "bf16"), DTensor.empty((BATCH, T_FRAMES, I_FF), "bf16")
+    ops.cpy(a, b, stream=st.handle)
+    st.synchronize()
+    print("pmc pass (configs): C4 and C5 QK-norm/rope, get_rows, KV store, dequant back + 1 calibration copy "
+          "(bf16, 147456000 B read, 147456000 B written)", flush=True)
+
+
 def gpu_bench(steps: int, warmup: int):
     from acestep_ops import device
     from acestep_ops.device import Event, Graph
@@ -911,6 +935,8 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="leave the Qwen3 layer chains out of the default line")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="launch each block kernel once plus a copy of known size, for counter collection")
+    ap.add_argument("--pmc-configs", action="store_true",
+                    help="launch the C4/C5 Q8_0 and QK-norm/rope kernels once plus a copy of known size, for counters")
     ap.add_argument("--configs", action="store_true",
                     help="time the Qwen3 layer op chains at the C1/C2/C4/C5 shapes instead (one JSON line each)")
     ap.add_argument("--attention", action="store_true",
@@ -931,6 +957,9 @@ def main():
 
     if args.pmc_pass:
         pmc_pass()
+        return
+    if args.pmc_configs:
+        pmc_pass_configs()
         return
     if args.configs:
         configs_bench(args.steps, args.warmup)
