@@ -34,6 +34,9 @@ namespace mi {
 #ifndef MI_FA_WAVES_PER_CU
 #define MI_FA_WAVES_PER_CU 8  // splits are chosen so the grid holds about this many waves per CU
 #endif
+#ifndef MI_FA_DEC_Q8_WAVES_PER_CU
+#define MI_FA_DEC_Q8_WAVES_PER_CU 12  // the same for the Q8_0 decode kernel (shorter key splits pay there)
+#endif
 
 constexpr int FA_TILE = 32;  // keys per tile
 constexpr int FA_MAXT = 16;  // tiles per split at most (the split's mask is staged in LDS)
@@ -513,9 +516,13 @@ __global__ void __launch_bounds__(64) MI_FA_OCC k_fa_split(const FaArgs a) {
 // Merge the splits of one (sequence, KV head, row): y = sum_s w_s o_s / sum_s w_s l_s,
 // w_s = exp(m_s - max_s m_s) (0 for a split whose keys were all masked). A
 // workgroup of 256 threads per row: every split's (m, l) loaded at once, the
-// weights in LDS; then thread t accumulates one 16-byte column chunk over the
+// weights in LDS; thread t accumulates one 16-byte column chunk over the
 // splits s = t / (D/4) (mod 256 / (D/4)), and the partial sums are added
-// through LDS. Every load of a pass is independent of the others.
+// through LDS. With at most FA_CMB_PRE splits per thread (the usual case) the
+// column chunks are loaded together with the (m, l) pairs, before the weights
+// are known, so the merge waits for one round of loads; indexes past the last
+// split are clamped to it and their weight is 0.
+constexpr int FA_CMB_PRE = 8;
 template <int D>
 __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
     constexpr int  C4  = D / 4;    // float4 chunks per output row
@@ -534,16 +541,30 @@ __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
     const int      h    = (int) g * a.rk + (row - iq * a.rk);
     const int64_t  sstr = (int64_t) a.nb * a.nkv * a.rows * (D + 2);  // one split's records
     const float *  w0   = a.ws + (int64_t) rec * (D + 2);
+    const int      c    = tid % C4;
+    const int      sg   = tid / C4;
+    const int      last = a.splits - 1;
 
+    const bool pre = a.splits <= SG * FA_CMB_PRE;
+    float4     pv[FA_CMB_PRE];
+    if (pre) {
+#pragma unroll
+        for (int j = 0; j < FA_CMB_PRE; ++j) {
+            const int s = sg + SG * j;
+            pv[j]       = *(const float4 *) (w0 + (int64_t) (s < last ? s : last) * sstr + 2 + 4 * c);
+        }
+    }
     // pass 1: max over the splits, weights, weighted sum of the row sums
     float ml[FA_MAX_SPLITS / 256], ll[FA_MAX_SPLITS / 256];
     float mloc = -INFINITY;
 #pragma unroll
     for (int i = 0; i < FA_MAX_SPLITS / 256; ++i) {
-        const int s = tid + 256 * i;
-        ml[i]       = s < a.splits ? w0[s * sstr] : -INFINITY;
-        ll[i]       = s < a.splits ? w0[s * sstr + 1] : 0.0f;
-        mloc        = fmaxf(mloc, ml[i]);
+        const int     s  = tid + 256 * i;
+        const float * mp = w0 + (int64_t) (s < last ? s : last) * sstr;
+        ml[i]            = mp[0];
+        ll[i]            = mp[1];
+        ml[i]            = s <= last ? ml[i] : -INFINITY;
+        mloc             = fmaxf(mloc, ml[i]);
     }
     mloc = group_max<64>(mloc);
     if ((tid & 63) == 0) {
@@ -556,7 +577,7 @@ __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
     for (int i = 0; i < FA_MAX_SPLITS / 256; ++i) {
         const int   s = tid + 256 * i;
         const float w = ml[i] == -INFINITY ? 0.0f : __expf(ml[i] - mx);
-        if (s < a.splits) {
+        if (s <= last) {
             wsh[s] = w;
         }
         lw = __builtin_fmaf(w, ll[i], lw);
@@ -569,17 +590,30 @@ __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
     const float L = (red[4] + red[5]) + (red[6] + red[7]);
 
     // pass 2: weighted outputs
-    const int c  = tid % C4;
-    const int sg = tid / C4;
-    float4    acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (pre) {
+#pragma unroll
+        for (int j = 0; j < FA_CMB_PRE; ++j) {
+            const int s = sg + SG * j;
+            if (s <= last) {
+                const float  w = wsh[s];
+                const float4 v = pv[j];
+                acc.x          = __builtin_fmaf(w, v.x, acc.x);
+                acc.y          = __builtin_fmaf(w, v.y, acc.y);
+                acc.z          = __builtin_fmaf(w, v.z, acc.z);
+                acc.w          = __builtin_fmaf(w, v.w, acc.w);
+            }
+        }
+    } else {
 #pragma unroll 8
-    for (int s = sg; s < a.splits; s += SG) {
-        const float  w = wsh[s];
-        const float4 v = *(const float4 *) (w0 + s * sstr + 2 + 4 * c);
-        acc.x          = __builtin_fmaf(w, v.x, acc.x);
-        acc.y          = __builtin_fmaf(w, v.y, acc.y);
-        acc.z          = __builtin_fmaf(w, v.z, acc.z);
-        acc.w          = __builtin_fmaf(w, v.w, acc.w);
+        for (int s = sg; s < a.splits; s += SG) {
+            const float  w = wsh[s];
+            const float4 v = *(const float4 *) (w0 + s * sstr + 2 + 4 * c);
+            acc.x          = __builtin_fmaf(w, v.x, acc.x);
+            acc.y          = __builtin_fmaf(w, v.y, acc.y);
+            acc.z          = __builtin_fmaf(w, v.z, acc.z);
+            acc.w          = __builtin_fmaf(w, v.w, acc.w);
+        }
     }
     part[sg][c] = acc;
     __syncthreads();
@@ -657,6 +691,69 @@ __device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, cons
     }
 }
 
+// Decode prologue loads. Every load is issued before any value is used (a
+// load under a per-element condition would be waited on where it stands).
+// The split's mask values, one per key (lane % 32) of each of FA_MAXT tiles,
+// keys clamped into the split (tiles past the split's last are never read).
+__device__ __forceinline__ void fa_dec_mask(const char * mrow, int kbeg, int kend, int key, float (&ms)[FA_MAXT]) {
+    if (mrow == nullptr) {
+#pragma unroll
+        for (int t = 0; t < FA_MAXT; ++t) {
+            ms[t] = 0.0f;
+        }
+        return;
+    }
+    uint16_t hv[FA_MAXT];
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        const int k = kbeg + t * FA_TILE + key;
+        hv[t]       = *(const uint16_t *) (mrow + (size_t) (k < kend ? k : kend - 1) * 2);
+    }
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        ms[t] = (float) __builtin_bit_cast(_Float16, hv[t]);
+    }
+}
+
+// The query row's elements 32 ks + 8 q4 + e (ks < NKS, e < 8) as floats, 0 in
+// lanes past the rows (rv false; qp then points at a valid row).
+template <int NKS>
+__device__ __forceinline__ void fa_dec_q(const char * qp, int tq, int q4, bool rv, float (&f)[NKS][8]) {
+    if (tq == MI_TYPE_F32) {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                f[ks][e] = ((const float *) (qp + (size_t) (32 * ks + 8 * q4) * 4))[e];
+            }
+        }
+    } else {
+        uint16_t hv[NKS][8];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hv[ks][e] = ((const uint16_t *) (qp + (size_t) (32 * ks + 8 * q4) * 2))[e];
+            }
+        }
+        const bool bf = tq == MI_TYPE_BF16;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                f[ks][e] = bf ? __uint_as_float((uint32_t) hv[ks][e] << 16) : (float) __builtin_bit_cast(_Float16, hv[ks][e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            f[ks][e] = rv ? f[ks][e] : 0.0f;
+        }
+    }
+}
+
 // Decode on the matrix cores (F16/BF16 K and V, D = 128, one query position,
 // at most 16 query heads per KV head, a mask row shared by every head). A wave
 // owns (key split, sequence, KV head) as k_fa_split does and walks 32-key tiles,
@@ -712,39 +809,18 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec(const FaArgs a) {
     const int      nt    = (kend - kbeg + T - 1) / T;
     const int      key   = lane & 31;
 
-    // the split's mask values (one per key), issued first
+    // the split's mask values (one per key) and the query row, issued first
     float ms[FA_MAXT];
-#pragma unroll
-    for (int t = 0; t < FA_MAXT; ++t) {
-        const int kc = kbeg + t * T + key < kend ? kbeg + t * T + key : kend - 1;
-        ms[t]        = mrow != nullptr && t < nt ? load_elem<MI_TYPE_F16>(mrow + (size_t) kc * 2) : 0.0f;
-    }
+    fa_dec_mask(mrow, kbeg, kend, key, ms);
+    float qf[NKS][8];
+    fa_dec_q<NKS>(a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2, a.tq, q4, rv, qf);
     // Q^T operands: k-step ks holds q[head c16][32 ks + 8 q4 + e] in K's type (RNE)
     x8 qb[NKS];
-    {
-        const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2;
-        const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            const char * p = qp + (size_t) (32 * ks + 8 * q4) * es;
-            float        f[8];
-            if (a.tq == MI_TYPE_F32) {
+    for (int ks = 0; ks < NKS; ++ks) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    f[e] = ((const float *) p)[e];
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint16_t hv = ((const uint16_t *) p)[e];
-                    f[e] = a.tq == MI_TYPE_BF16 ? __uint_as_float((uint32_t) hv << 16)
-                                                : (float) __builtin_bit_cast(_Float16, hv);
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                qb[ks][e] = __builtin_bit_cast(typename M::e, M::bits(rv ? f[e] : 0.0f));
-            }
+        for (int e = 0; e < 8; ++e) {
+            qb[ks][e] = __builtin_bit_cast(typename M::e, M::bits(qf[ks][e]));
         }
     }
     // mask values into LDS and per tile the keys some head reads (the mask row is
@@ -993,37 +1069,21 @@ __global__ void __launch_bounds__(64) MI_FA_DEC_OCC k_fa_dec_q8(const FaArgs a) 
     const int      nt    = (kend - kbeg + T - 1) / T;
     const int      key   = lane & 31;
 
-    // the split's mask values (one per key), issued first
+    // the split's mask values (one per key) and the query row, issued first
     float ms[FA_MAXT];
-#pragma unroll
-    for (int t = 0; t < FA_MAXT; ++t) {
-        const int kc = kbeg + t * T + key < kend ? kbeg + t * T + key : kend - 1;
-        ms[t]        = mrow != nullptr && t < nt ? load_elem<MI_TYPE_F16>(mrow + (size_t) kc * 2) : 0.0f;
-    }
+    fa_dec_mask(mrow, kbeg, kend, key, ms);
+    float qf[NB][8];
+    fa_dec_q<NB>(a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2, a.tq, q4, rv, qf);
     // q converted to Q8_0 (x86 from_float, as fa_q8_block): lane (c16, q4) holds
     // elements 32 kb + 8 q4 + e of head c16, so each block's amax is a max over
     // lanes c16 + 16 q4; B operand of block kb = its 8 quants, d_q its scale
     long  qb8[NB];
     float dq[NB];
     {
-        const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2;
-        const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
 #pragma unroll
         for (int kb = 0; kb < NB; ++kb) {
-            const char * p = qp + (size_t) (32 * kb + 8 * q4) * es;
-            float        f[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float x;
-                if (a.tq == MI_TYPE_F32) {
-                    x = ((const float *) p)[e];
-                } else {
-                    const uint16_t hv = ((const uint16_t *) p)[e];
-                    x = a.tq == MI_TYPE_BF16 ? __uint_as_float((uint32_t) hv << 16) : (float) __builtin_bit_cast(_Float16, hv);
-                }
-                f[e] = rv ? x : 0.0f;
-            }
-            float amax = 0.0f;
+            const float * f    = qf[kb];
+            float         amax = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 amax = fmaxf(amax, fabsf(f[e]));
@@ -1889,7 +1949,7 @@ void flash_attn_plan(FaArgs & a, int D) {
         a.rblocks = 1;
     }
     const int64_t pairs  = (int64_t) a.nb * a.nkv * a.rblocks;
-    const int64_t want   = (int64_t) num_cus() * MI_FA_WAVES_PER_CU;
+    const int64_t want   = (int64_t) num_cus() * (a.dec && a.kt == MI_TYPE_Q8_0 ? MI_FA_DEC_Q8_WAVES_PER_CU : MI_FA_WAVES_PER_CU);
     const int64_t tiles  = (a.n_kv + FA_TILE - 1) / FA_TILE;
     int64_t       splits = (want + pairs - 1) / pairs;
     splits               = splits < 1 ? 1 : (splits > tiles ? tiles : splits);

@@ -194,6 +194,35 @@ def test_decode_kv_and_mask_batch_broadcast(dev, kt, n_kv):
     _run(4, 8, 2, 1, n_kv, 128, kt, "f32", mask=m, seed=51, Nk3=2)
 
 
+@pytest.mark.parametrize("layout", ["contiguous", "slot_major"])
+def test_decode_q8_row_layouts_ragged(dev, layout):
+    """Q8_0 decode over 777 keys (the last 32-key tile holds 9: an odd number of
+    136-byte rows) in two cache layouts: each KV head's rows contiguous, and the
+    KV heads of a slot side by side (K/V views with a 1088-byte key stride)."""
+    print(f"fa decode q8_0 layout={layout}", flush=True)
+    N, Nh, Nkv, n_kv, D = 3, 32, 8, 777, 128
+    r = _rng(61)
+    q = r.standard_normal((N, Nh, 1, D)).astype(np.float32)
+    k = r.standard_normal((N, Nkv, n_kv, D)).astype(np.float32)
+    v = r.standard_normal((N, Nkv, n_kv, D)).astype(np.float32)
+    if layout == "contiguous":
+        dk, kf = _kv(k, "q8_0")
+        dv, vf = _kv(v, "q8_0")
+    else:
+        kq = orc.quantize_q8_0(np.ascontiguousarray(k.transpose(0, 2, 1, 3)), "x86")  # (N, n_kv, Nkv, 136)
+        vq = orc.quantize_q8_0(np.ascontiguousarray(v.transpose(0, 2, 1, 3)), "x86")
+        dk = ops.Q8(to_dev(kq).permute(0, 2, 1, 3))
+        dv = ops.Q8(to_dev(vq).permute(0, 2, 1, 3))
+        assert dk.data.strides[2] == Nkv * 136
+        kf = orc.dequantize_q8_0(kq).transpose(0, 2, 1, 3)
+        vf = orc.dequantize_q8_0(vq).transpose(0, 2, 1, 3)
+    m = _decode_mask(N, n_kv, [777, 9, 300])
+    dm, mf = _mask_dev(m)
+    y = to_np(ops.flash_attn_ext(to_dev(q), dk, dv, dm, 0.125))
+    ref = orc.flash_attn_ext(q, kf, vf, mf, 0.125, "q8_0")
+    _check(y, ref, fa_bound(q, kf, vf, mf, 0.125, "q8_0", _uses_mfma("q8_0", D, 1, Nh, Nkv, n_kv, mf)))
+
+
 @pytest.mark.parametrize("kt", ["q8_0", "f16"])
 def test_decode_long_kv_splits(dev, kt):
     """8192 keys: the key range is split over many waves and merged."""
