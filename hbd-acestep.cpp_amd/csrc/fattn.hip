@@ -97,6 +97,70 @@ __device__ __forceinline__ float fa_q8_block(const float * x, uint32_t * qw) {
 #define MI_FA_OCC
 #endif
 
+// Start-up loads of the split-key kernels. Every load is issued before any
+// value is used (a load under a per-element condition is waited on where it
+// stands). The split's mask values in a shared mask row, one per key (lane %
+// 32) of each of FA_MAXT tiles, keys clamped into the split (values of tiles
+// past the split's last are never read).
+__device__ __forceinline__ void fa_dec_mask(const char * mrow, int kbeg, int kend, int key, float (&ms)[FA_MAXT]) {
+    if (mrow == nullptr) {
+#pragma unroll
+        for (int t = 0; t < FA_MAXT; ++t) {
+            ms[t] = 0.0f;
+        }
+        return;
+    }
+    uint16_t hv[FA_MAXT];
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        const int k = kbeg + t * FA_TILE + key;
+        hv[t]       = *(const uint16_t *) (mrow + (size_t) (k < kend ? k : kend - 1) * 2);
+    }
+#pragma unroll
+    for (int t = 0; t < FA_MAXT; ++t) {
+        ms[t] = (float) __builtin_bit_cast(_Float16, hv[t]);
+    }
+}
+
+// The query row's elements 32 ks + 8 q4 + e (ks < NKS, e < 8) as floats, 0 in
+// lanes past the rows (rv false; qp then points at a valid row).
+template <int NKS>
+__device__ __forceinline__ void fa_dec_q(const char * qp, int tq, int q4, bool rv, float (&f)[NKS][8]) {
+    if (tq == MI_TYPE_F32) {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                f[ks][e] = ((const float *) (qp + (size_t) (32 * ks + 8 * q4) * 4))[e];
+            }
+        }
+    } else {
+        uint16_t hv[NKS][8];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hv[ks][e] = ((const uint16_t *) (qp + (size_t) (32 * ks + 8 * q4) * 2))[e];
+            }
+        }
+        const bool bf = tq == MI_TYPE_BF16;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                f[ks][e] = bf ? __uint_as_float((uint32_t) hv[ks][e] << 16) : (float) __builtin_bit_cast(_Float16, hv[ks][e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            f[ks][e] = rv ? f[ks][e] : 0.0f;
+        }
+    }
+}
+
 template <int KT, int D, int RB>
 __global__ void __launch_bounds__(64) MI_FA_OCC k_fa_split(const FaArgs a) {
     constexpr int RBYTES = FaT<KT>::row(D);
@@ -157,13 +221,7 @@ __global__ void __launch_bounds__(64) MI_FA_OCC k_fa_split(const FaArgs a) {
 
     // the shared mask row's values for every tile of the split, issued first
     float ms[FA_MAXT];
-#pragma unroll
-    for (int t = 0; t < FA_MAXT; ++t) {
-        const int t0 = kbeg + t * FA_TILE;
-        const int kc = t0 + key < kend ? t0 + key : kend - 1;
-        ms[t]        = a.mask != nullptr && a.mshared && t < nt ? load_elem<MI_TYPE_F16>(mrow[0] + (size_t) kc * 2)
-                                                              : 0.0f;
-    }
+    fa_dec_mask(a.mask != nullptr && a.mshared ? mrow[0] : nullptr, kbeg, kend, key, ms);
 
     // 1. q rows into LDS as floats: 16-byte loads when q's rows are 16-byte
     //    aligned (elementwise otherwise), all issued before any is used; then
@@ -174,20 +232,31 @@ __global__ void __launch_bounds__(64) MI_FA_OCC k_fa_split(const FaArgs a) {
         const int     epc = 16 / es;    // elements per chunk
         const int     cpr = D / epc;    // chunks per row
         uint4         qv[NQC];
+        const char *  qp[NQC];
 #pragma unroll
         for (int i = 0; i < NQC; ++i) {
             const int c  = lane + 64 * i;
             const int cc = c < RB * cpr ? c : RB * cpr - 1;
             const int r  = cc / cpr;
-            const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h_of[r] * a.q2 + (int64_t) iq_of[r] * a.q1 +
-                              (int64_t) (cc - r * cpr) * 16;
-            if (a.qvec) {
-                qv[i] = ld16(qp);
-            } else if (es == 4) {
-                const uint32_t * w = (const uint32_t *) qp;
+            qp[i]        = a.q + (int64_t) b * a.q3 + (int64_t) h_of[r] * a.q2 + (int64_t) iq_of[r] * a.q1 +
+                    (int64_t) (cc - r * cpr) * 16;
+        }
+        // the access width is tested once, outside the loads
+        if (a.qvec) {
+#pragma unroll
+            for (int i = 0; i < NQC; ++i) {
+                qv[i] = ld16(qp[i]);
+            }
+        } else if (es == 4) {
+#pragma unroll
+            for (int i = 0; i < NQC; ++i) {
+                const uint32_t * w = (const uint32_t *) qp[i];
                 qv[i]              = make_uint4(w[0], w[1], w[2], w[3]);
-            } else {
-                const uint16_t * h = (const uint16_t *) qp;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NQC; ++i) {
+                const uint16_t * h = (const uint16_t *) qp[i];
                 qv[i]              = make_uint4((uint32_t) h[0] | ((uint32_t) h[1] << 16),
                                                 (uint32_t) h[2] | ((uint32_t) h[3] << 16),
                                                 (uint32_t) h[4] | ((uint32_t) h[5] << 16),
@@ -254,28 +323,61 @@ __global__ void __launch_bounds__(64) MI_FA_OCC k_fa_split(const FaArgs a) {
     //    q conversion above so that the two round trips overlap.
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    // Per-row mask rows: the values of FA_MG tiles x RB rows are loaded together
+    // (keys clamped into the split: every load is in bounds), then used.
+    constexpr int FA_MG = 4;
+    static_assert(FA_MAXT % FA_MG == 0, "mask tiles are loaded in groups of FA_MG");
 #pragma unroll
-    for (int t = 0; t < FA_MAXT; ++t) {
-        if (t < nt) {
-            const int  t0  = kbeg + t * FA_TILE;
-            const int  kc  = t0 + key < kend ? t0 + key : kend - 1;  // clamped: every load is in bounds
-            const bool ok  = t0 + key < kend;
-            bool       any = false;
+    for (int t4 = 0; t4 < FA_MAXT; t4 += FA_MG) {
+        if (t4 < nt) {
+            float xs[FA_MG][RB];
+            if (a.mask != nullptr && !a.mshared) {
+                uint16_t hv[FA_MG][RB];
 #pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                float x = 0.0f;
-                if (a.mask != nullptr) {
-                    x = a.mshared ? ms[t] : load_elem<MI_TYPE_F16>(mrow[r] + (size_t) kc * 2);
+                for (int u = 0; u < FA_MG; ++u) {
+                    const int k  = kbeg + (t4 + u) * FA_TILE + key;
+                    const int kc = k < kend ? k : kend - 1;
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        hv[u][r] = *(const uint16_t *) (mrow[r] + (size_t) kc * 2);
+                    }
                 }
-                x = ok && rv[r] ? x : -INFINITY;
-                if (half == 0) {
-                    mt[t * FA_TILE + key][r] = x;
+#pragma unroll
+                for (int u = 0; u < FA_MG; ++u) {
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        xs[u][r] = (float) __builtin_bit_cast(_Float16, hv[u][r]);
+                    }
                 }
-                any = any || x != -INFINITY;
+            } else {
+#pragma unroll
+                for (int u = 0; u < FA_MG; ++u) {
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        xs[u][r] = a.mask != nullptr ? ms[t4 + u] : 0.0f;
+                    }
+                }
             }
-            const uint64_t lv = __builtin_amdgcn_ballot_w64(any && half == 0);  // bit k: key k is read
-            if (lane == 0) {
-                lt[t] = lv;
+#pragma unroll
+            for (int u = 0; u < FA_MG; ++u) {
+                const int t = t4 + u;
+                if (t < nt) {
+                    const int  t0  = kbeg + t * FA_TILE;
+                    const bool ok  = t0 + key < kend;
+                    bool       any = false;
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        const float x = ok && rv[r] ? xs[u][r] : -INFINITY;
+                        if (half == 0) {
+                            mt[t * FA_TILE + key][r] = x;
+                        }
+                        any = any || x != -INFINITY;
+                    }
+                    const uint64_t lv = __builtin_amdgcn_ballot_w64(any && half == 0);  // bit k: key k is read
+                    if (lane == 0) {
+                        lt[t] = lv;
+                    }
+                }
             }
         }
     }
@@ -688,69 +790,6 @@ __device__ __forceinline__ fa_f32x16 fa_mma(const typename FaM<KT>::x8 & a, cons
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     } else {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
-}
-
-// Decode prologue loads. Every load is issued before any value is used (a
-// load under a per-element condition would be waited on where it stands).
-// The split's mask values, one per key (lane % 32) of each of FA_MAXT tiles,
-// keys clamped into the split (tiles past the split's last are never read).
-__device__ __forceinline__ void fa_dec_mask(const char * mrow, int kbeg, int kend, int key, float (&ms)[FA_MAXT]) {
-    if (mrow == nullptr) {
-#pragma unroll
-        for (int t = 0; t < FA_MAXT; ++t) {
-            ms[t] = 0.0f;
-        }
-        return;
-    }
-    uint16_t hv[FA_MAXT];
-#pragma unroll
-    for (int t = 0; t < FA_MAXT; ++t) {
-        const int k = kbeg + t * FA_TILE + key;
-        hv[t]       = *(const uint16_t *) (mrow + (size_t) (k < kend ? k : kend - 1) * 2);
-    }
-#pragma unroll
-    for (int t = 0; t < FA_MAXT; ++t) {
-        ms[t] = (float) __builtin_bit_cast(_Float16, hv[t]);
-    }
-}
-
-// The query row's elements 32 ks + 8 q4 + e (ks < NKS, e < 8) as floats, 0 in
-// lanes past the rows (rv false; qp then points at a valid row).
-template <int NKS>
-__device__ __forceinline__ void fa_dec_q(const char * qp, int tq, int q4, bool rv, float (&f)[NKS][8]) {
-    if (tq == MI_TYPE_F32) {
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                f[ks][e] = ((const float *) (qp + (size_t) (32 * ks + 8 * q4) * 4))[e];
-            }
-        }
-    } else {
-        uint16_t hv[NKS][8];
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                hv[ks][e] = ((const uint16_t *) (qp + (size_t) (32 * ks + 8 * q4) * 2))[e];
-            }
-        }
-        const bool bf = tq == MI_TYPE_BF16;
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                f[ks][e] = bf ? __uint_as_float((uint32_t) hv[ks][e] << 16) : (float) __builtin_bit_cast(_Float16, hv[ks][e]);
-            }
-        }
-    }
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            f[ks][e] = rv ? f[ks][e] : 0.0f;
-        }
     }
 }
 
@@ -1365,34 +1404,59 @@ __global__ void __launch_bounds__(64) k_fa_mask_summary(const FaArgs a) {
     const char *   mp  = a.mask + (int64_t) m3 * a.m3 + (int64_t) m2 * a.m2;
     const int      ntl = (a.n_kv + 63) / 64;
     const int      kl  = 4 * (lane & 15);  // this lane's 4 keys within a tile
+    // Loads are unconditional, rows and keys clamped into the mask (values
+    // outside it are never used below), so that all of them are in flight
+    // before the first is used; only a lane whose 4 keys straddle the end of
+    // a row loads them one by one afterwards.
     uint16_t       hv[FA_SUM_T][4][4];
+    if (a.mvec && a.n_kv >= 4) {
+        uint2 w[FA_SUM_T][4];
 #pragma unroll
-    for (int tt = 0; tt < FA_SUM_T; ++tt) {
-        const int tile = (int) blockIdx.x * FA_SUM_T + tt;
-        const int k4   = tile * 64 + kl;
+        for (int tt = 0; tt < FA_SUM_T; ++tt) {
+            const int k4 = ((int) blockIdx.x * FA_SUM_T + tt) * 64 + kl;
+            const int ks = k4 + 3 < a.n_kv ? k4 : 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int iq = (int) grp * 16 + (lane >> 4) + 4 * i;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hv[tt][i][e] = 0;
+            for (int i = 0; i < 4; ++i) {
+                const int iq = (int) grp * 16 + (lane >> 4) + 4 * i;
+                w[tt][i]     = *(const uint2 *) (mp + (int64_t) (iq < a.n_q ? iq : a.n_q - 1) * a.m1 + (int64_t) ks * 2);
             }
-            if (tile >= ntl || iq >= a.n_q || k4 >= a.n_kv) {
-                continue;
+        }
+#pragma unroll
+        for (int tt = 0; tt < FA_SUM_T; ++tt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                hv[tt][i][0] = (uint16_t) w[tt][i].x;
+                hv[tt][i][1] = (uint16_t) (w[tt][i].x >> 16);
+                hv[tt][i][2] = (uint16_t) w[tt][i].y;
+                hv[tt][i][3] = (uint16_t) (w[tt][i].y >> 16);
             }
-            const char * rp = mp + (int64_t) iq * a.m1;
-            if (a.mvec && k4 + 3 < a.n_kv) {
-                const uint2 w = *(const uint2 *) (rp + (int64_t) k4 * 2);
-                hv[tt][i][0]  = (uint16_t) w.x;
-                hv[tt][i][1]  = (uint16_t) (w.x >> 16);
-                hv[tt][i][2]  = (uint16_t) w.y;
-                hv[tt][i][3]  = (uint16_t) (w.y >> 16);
-            } else {
+        }
+#pragma unroll
+        for (int tt = 0; tt < FA_SUM_T; ++tt) {
+            const int k4 = ((int) blockIdx.x * FA_SUM_T + tt) * 64 + kl;
+            if (k4 < a.n_kv && k4 + 3 >= a.n_kv) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int    iq = (int) grp * 16 + (lane >> 4) + 4 * i;
+                    const char * rp = mp + (int64_t) (iq < a.n_q ? iq : a.n_q - 1) * a.m1;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        hv[tt][i][e] = *(const uint16_t *) (rp + (int64_t) (k4 + e < a.n_kv ? k4 + e : a.n_kv - 1) * 2);
+                    }
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int tt = 0; tt < FA_SUM_T; ++tt) {
+            const int k4 = ((int) blockIdx.x * FA_SUM_T + tt) * 64 + kl;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int    iq = (int) grp * 16 + (lane >> 4) + 4 * i;
+                const char * rp = mp + (int64_t) (iq < a.n_q ? iq : a.n_q - 1) * a.m1;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    if (k4 + e < a.n_kv) {
-                        hv[tt][i][e] = *(const uint16_t *) (rp + (int64_t) (k4 + e) * 2);
-                    }
+                    hv[tt][i][e] = *(const uint16_t *) (rp + (int64_t) (k4 + e < a.n_kv ? k4 + e : a.n_kv - 1) * 2);
                 }
             }
         }
@@ -1497,42 +1561,67 @@ k_fa_mfma(const FaArgs a) {
                                  : nullptr;
 
     // Q^T operands: k-step ks needs q[row][16 ks + 8 hh + i], converted to K's type (RNE)
+    // (q's type and access width are tested once, outside the loads, so that
+    // every load is in flight before the first is used)
     x8 qb[NKS];
     {
         const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2 + (int64_t) iq * a.q1;
-        const int    es = a.tq == MI_TYPE_F32 ? 4 : 2;
+        float        f[NKS][8];
+        if (a.tq == MI_TYPE_F32) {
+            if (a.qvec) {
+                uint4 u[NKS][2];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            const char * p = qp + (size_t) (16 * ks + 8 * hh) * es;
-            float        f[8];
-            if (a.tq == MI_TYPE_F32) {
-                if (a.qvec) {
-                    unpack16<MI_TYPE_F32>(ld16(p), f);
-                    unpack16<MI_TYPE_F32>(ld16(p + 16), f + 4);
-                } else {
+                for (int ks = 0; ks < NKS; ++ks) {
+                    const char * p = qp + (size_t) (16 * ks + 8 * hh) * 4;
+                    u[ks][0]       = ld16(p);
+                    u[ks][1]       = ld16(p + 16);
+                }
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        f[e] = ((const float *) p)[e];
-                    }
+                for (int ks = 0; ks < NKS; ++ks) {
+                    unpack16<MI_TYPE_F32>(u[ks][0], f[ks]);
+                    unpack16<MI_TYPE_F32>(u[ks][1], f[ks] + 4);
                 }
             } else {
-                uint4 v;
-                if (a.qvec) {
-                    v = ld16(p);
-                } else {
-                    const uint16_t * q16 = (const uint16_t *) p;
-                    v = make_uint4((uint32_t) q16[0] | ((uint32_t) q16[1] << 16), (uint32_t) q16[2] | ((uint32_t) q16[3] << 16),
-                                   (uint32_t) q16[4] | ((uint32_t) q16[5] << 16), (uint32_t) q16[6] | ((uint32_t) q16[7] << 16));
-                }
-                if (a.tq == MI_TYPE_BF16) {
-                    unpack16<MI_TYPE_BF16>(v, f);
-                } else {
-                    unpack16<MI_TYPE_F16>(v, f);
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        f[ks][e] = ((const float *) (qp + (size_t) (16 * ks + 8 * hh) * 4))[e];
+                    }
                 }
             }
+        } else {
+            uint4 v[NKS];
+            if (a.qvec) {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    v[ks] = ld16(qp + (size_t) (16 * ks + 8 * hh) * 2);
+                }
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    const uint16_t * q16 = (const uint16_t *) (qp + (size_t) (16 * ks + 8 * hh) * 2);
+                    v[ks] = make_uint4((uint32_t) q16[0] | ((uint32_t) q16[1] << 16), (uint32_t) q16[2] | ((uint32_t) q16[3] << 16),
+                                       (uint32_t) q16[4] | ((uint32_t) q16[5] << 16), (uint32_t) q16[6] | ((uint32_t) q16[7] << 16));
+                }
+            }
+            if (a.tq == MI_TYPE_BF16) {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    unpack16<MI_TYPE_BF16>(v[ks], f[ks]);
+                }
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    unpack16<MI_TYPE_F16>(v[ks], f[ks]);
+                }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                qb[ks][e] = __builtin_bit_cast(typename M::e, M::bits(rvld ? f[e] : 0.0f));
+                qb[ks][e] = __builtin_bit_cast(typename M::e, M::bits(rvld ? f[ks][e] : 0.0f));
             }
         }
     }
@@ -1575,24 +1664,38 @@ k_fa_mfma(const FaArgs a) {
         }
     };
     // mask values of this lane's 32 keys of a tile (key 32 bk + 8 j + 4 hh + i:
-    // groups of 4), as 4 fp16 per 8-byte load when the mask rows allow it
+    // groups of 4), as 4 fp16 per 8-byte load when the mask rows allow it and
+    // the tile lies inside the row; the choice is uniform, and within it every
+    // load is unconditional (keys clamped), so all 8 groups are in flight at once
     auto load_mask = [&](int t0, uint2 (&mr)[2][4]) {
+        if (a.mvec && t0 + BK <= a.n_kv) {
 #pragma unroll
-        for (int bk = 0; bk < 2; ++bk) {
+            for (int bk = 0; bk < 2; ++bk) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int k4 = t0 + 32 * bk + 8 * j + 4 * hh;
-                if (a.mvec && k4 + 3 < a.n_kv) {
-                    mr[bk][j] = *(const uint2 *) (mrow + (size_t) k4 * 2);
-                } else {
-                    uint16_t hv[4];
+                for (int j = 0; j < 4; ++j) {
+                    mr[bk][j] = *(const uint2 *) (mrow + (size_t) (t0 + 32 * bk + 8 * j + 4 * hh) * 2);
+                }
+            }
+        } else {
+            uint16_t hv[2][4][4];
+#pragma unroll
+            for (int bk = 0; bk < 2; ++bk) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int k4 = t0 + 32 * bk + 8 * j + 4 * hh;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int kc = k4 + i < a.n_kv ? k4 + i : a.n_kv - 1;
-                        hv[i]        = *(const uint16_t *) (mrow + (size_t) kc * 2);
+                        hv[bk][j][i] = *(const uint16_t *) (mrow + (size_t) kc * 2);
                     }
-                    mr[bk][j] = make_uint2((uint32_t) hv[0] | ((uint32_t) hv[1] << 16),
-                                           (uint32_t) hv[2] | ((uint32_t) hv[3] << 16));
+                }
+            }
+#pragma unroll
+            for (int bk = 0; bk < 2; ++bk) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    mr[bk][j] = make_uint2((uint32_t) hv[bk][j][0] | ((uint32_t) hv[bk][j][1] << 16),
+                                           (uint32_t) hv[bk][j][2] | ((uint32_t) hv[bk][j][3] << 16));
                 }
             }
         }

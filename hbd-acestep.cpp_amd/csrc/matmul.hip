@@ -246,6 +246,17 @@ __device__ __forceinline__ float mm_epilogue(const MmvArgs & a, uint32_t m, uint
     return v;
 }
 
+// The epilogue split in two for an output group: the residual values loaded
+// first (all of a group's loads in flight together; callers clamp m and n into
+// the output), then added (with the clamp) as mm_epilogue adds them.
+__device__ __forceinline__ float mm_res(const MmvArgs & a, uint32_t m, uint32_t n) {
+    return *(const float *) (a.res + (int64_t) m * a.res1 + (int64_t) n * 4);
+}
+__device__ __forceinline__ float mm_add_res(const MmvArgs & a, float v, float r) {
+    v = v + r;
+    return a.rclamp ? clamp_ggml(v, a.rlo, a.rhi) : v;
+}
+
 template <int M>
 __global__ void __launch_bounds__(512) k_mmv_q8_0(const MmvArgs a) {
     extern __shared__ float red[];  // [wave][m][lane], W * M * 64 floats when W > 1
@@ -334,6 +345,21 @@ __global__ void __launch_bounds__(512) k_mmv_q8_0(const MmvArgs a) {
         }
     };
     if (W == 1 && a.splits == 1) {
+        if (a.res != nullptr) {
+            const uint32_t rc = row < a.n ? row : a.n - 1;
+            float          r[M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                r[m] = mm_res(a, (uint32_t) m, rc);
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if (row < a.n) {
+                    *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = mm_add_res(a, acc[m], r[m]);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             store_y(m, acc[m]);
@@ -501,7 +527,8 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
             break;
         }
     }
-    // D lane l: column n0 + 32 j + c, rows m0 + 32 i + 8 q + 4 hh + e
+    // D lane l: column n0 + 32 j + c, rows m0 + 32 i + 8 q + 4 hh + e; with a
+    // residual, the 16 values of an (i, j) tile are loaded before any is added
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const uint32_t n = n0 + 32 * j + c;
@@ -510,13 +537,26 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
+            float r[16];
+            if (a.res != nullptr) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t m = m0 + 32 * i + 8 * q + 4 * hh + e;
+                        r[4 * q + e]     = mm_res(a, m < a.m ? m : a.m - 1, n);
+                    }
+                }
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t m = m0 + 32 * i + 8 * q + 4 * hh + e;
                     if (m < a.m) {
-                        *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) n * 4) = mm_epilogue(a, m, n, acc[i][j][4 * q + e]);
+                        const float v = acc[i][j][4 * q + e];
+                        *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) n * 4) =
+                            a.res != nullptr ? mm_add_res(a, v, r[4 * q + e]) : v;
                     }
                 }
             }
