@@ -66,6 +66,7 @@ namespace mi {
 struct HeadItem {
     uint32_t bbeg, bend;  // batch range
     uint32_t i2, i3;      // token coordinates
+    int32_t  pos;         // the token's position (rope only)
 };
 
 template <int TI, int TO, int D, bool NORM, bool ROPE>
@@ -140,9 +141,14 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
         const uint32_t nxt    = item + stride;
         const bool     one    = it.bend - it.bbeg <= (uint32_t) PF;  // a single load round
         HeadItem       nx     = it;
+        // the next item's position is a scalar load, so that waiting for it
+        // never waits for the rows in flight
         auto           ahead  = [&]() {
             if (nxt < nitems) {
                 nx = decode(nxt);
+                if constexpr (ROPE) {
+                    nx.pos = ld_scalar_i32(a.pos, nx.i2);
+                }
                 load_batch(nx, nx.bbeg, n0, n1);
             }
         };
@@ -154,7 +160,7 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
         if constexpr (ROPE) {
             float *     ct = tab[wv][0];
             float *     st = tab[wv][1];
-            const float p  = (float) a.pos[it.i2];  // wave-uniform: scalar load
+            const float p  = (float) it.pos;  // loaded with the item's rows (scalar)
             if (lane == 0) {
                 float th = p;
                 ct[0]    = th;
@@ -278,6 +284,9 @@ __global__ void __launch_bounds__(256) MI_ROPE_OCC k_heads(const HeadArgs a, uin
     HeadItem it{};
     if (item < nitems) {
         it = decode(item);
+        if constexpr (ROPE) {
+            it.pos = ld_scalar_i32(a.pos, it.i2);
+        }
         load_batch(it, it.bbeg, va0, va1);
     }
     if constexpr (NORM) {
@@ -564,6 +573,12 @@ __global__ void __launch_bounds__(256) k_heads_kv(const HeadArgs a, const HeadKV
     const HeadSeg & S  = a.seg[sg == 0 ? 0 : 1];
     const bool     ok  = h < S.heads;  // V has K's heads
 
+    // the position is a scalar load, so that the angle chain below waits for
+    // it alone, not for the rows
+    int32_t pos = 0;
+    if (sg < 2 && a.pos) {
+        pos = ld_scalar_i32(a.pos, i2);
+    }
     const char * xp = sg == 2 ? kv.v + (int64_t) i3 * kv.vs3 + (int64_t) i2 * kv.vs2 + (int64_t) h * kv.vs1
                               : S.x + (int64_t) i3 * S.xs3 + (int64_t) i2 * S.xs2 + (int64_t) h * S.xs1;
     uint4 c0 = make_uint4(0, 0, 0, 0), c1 = make_uint4(0, 0, 0, 0);
@@ -580,7 +595,7 @@ __global__ void __launch_bounds__(256) k_heads_kv(const HeadArgs a, const HeadKV
         if (a.pos) {
             float *     ct = tab[wv][0];
             float *     st = tab[wv][1];
-            const float p  = (float) a.pos[i2];
+            const float p  = (float) pos;
             if (lane == 0) {
                 float th = p;
                 ct[0]    = th;
