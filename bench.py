@@ -924,6 +924,67 @@ def decode_layer_bench_kv(steps: int, kv_type: str):
     device.synchronize()
 
 
+# ---------------------------------------------------------------------------
+# One whole Qwen3-4B decoder layer in prefill on the device (reported with
+# --prefill-layer): the two CFG sequences (conditional and unconditional KV
+# sets, qwen3-lm.h:429-431) of a 512-token prompt from slot 0, Q8_0 weights,
+# an F16 KV cache (the LM's own, qwen3-lm.h:190-191) and a Q8_0 one
+# (qw3lm_forward, qwen3-lm.h:429-549). One JSON line per cache type.
+# ---------------------------------------------------------------------------
+def prefill_layer_bench(steps: int):
+    for kv_type in ("f16", "q8_0"):
+        prefill_layer_bench_kv(steps, kv_type)
+
+
+def prefill_layer_bench_kv(steps: int, kv_type: str):
+    from acestep_ops import device, ops
+    from acestep_ops.device import DTensor, Event, Graph, Stream
+    from acestep_ops.qwen3 import Qwen3Layer
+
+    H, Nh, Nkv, D, I, N, S, SLOTS = 2560, 32, 8, 128, 9728, 2, 512, 4096
+    rng = np.random.default_rng(17)
+    st = Stream()
+    sh = st.handle
+
+    def q8w(n, k):
+        nbk = k // 32
+        b = np.empty((n, nbk, 34), np.uint8)
+        b[:, :, 2:] = rng.integers(-127, 128, (n, nbk, 32), dtype=np.int8).view(np.uint8)
+        b[:, :, :2] = (rng.uniform(0.5, 1.0, (n, nbk)) * 2e-3).astype(np.float16).view(np.uint8).reshape(n, nbk, 2)
+        return ops.Q8(DTensor.from_numpy(b.reshape(n, nbk * 34)))
+
+    ones = lambda n: DTensor.from_numpy(np.ones(n, np.float32))  # noqa: E731
+    layer = Qwen3Layer(q8w((Nh + 2 * Nkv) * D, H), q8w(H, Nh * D), q8w(2 * I, H), q8w(H, I), ones(H), ones(H),
+                       ones(D), ones(D), H, Nh, Nkv, D, I, SLOTS, N, kv_type, stream=sh)
+    hidden = DTensor.from_numpy(rng.standard_normal((N, S, H), dtype=np.float32))
+    out = DTensor.empty((N, S, H), "f32")
+    inp = layer.prefill_inputs([0] * N, S, 0)
+    layer.prefill_run(hidden, inp, out=out)  # allocates the layer's buffers outside the graph
+    st.synchronize()
+    g = Graph()
+    with g.capture(st):
+        for _ in range(steps):
+            layer.prefill_run(hidden, inp, out=out)
+    g.launch()
+    st.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(sh)
+    g.launch()
+    e1.record(sh)
+    e1.synchronize()
+    us = 1000.0 * e0.elapsed_ms(e1) / steps
+    T = N * S
+    gemm = 2 * T * sum(w.n * w.k for w in layer.w.values())
+    attn = 4 * D * Nh * N * (S * (S + 1) // 2)  # the causal pairs (masked tiles are skipped)
+    print(json.dumps({"config": f"Qwen3-4B prefill layer, {N} sequences (CFG sets) x {S} tokens from slot 0, Q8_0 "
+                                f"weights, {kv_type.upper()} KV cache, every op on the device",
+                      "us_per_layer": round(us, 1), "gemm_flop": gemm, "attn_flop_causal": attn,
+                      "TFLOP/s": round((gemm + attn) / (us * 1e-6) / 1e12, 1),
+                      "tokens_per_s_36_layers": round(T / (36 * us * 1e-6), 1)}), flush=True)
+    del layer, g
+    device.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -943,6 +1004,9 @@ def main():
                     help="time flash attention over the KV cache at the C2 decode shape (one JSON line per cache type)")
     ap.add_argument("--decode-layer", action="store_true",
                     help="time one whole Qwen3-4B decoder layer at batch 8 (Q8_0 weights; F16 and Q8_0 KV caches), all on the device")
+    ap.add_argument("--prefill-layer", action="store_true",
+                    help="time one whole Qwen3-4B decoder layer in prefill (2 CFG sequences x 512 tokens; F16 and "
+                         "Q8_0 KV caches), all on the device")
     ap.add_argument("--gemv", action="store_true",
                     help="time the Q8_0 mul_mat of the Qwen3-4B decode projections and LM head at batch 8")
     args = ap.parse_args()
@@ -972,6 +1036,9 @@ def main():
         return
     if args.decode_layer:
         decode_layer_bench(args.steps)
+        return
+    if args.prefill_layer:
+        prefill_layer_bench(args.steps)
         return
     kb = block_bytes(ROWS, cross=True)
     kb_f = block_bytes(ROWS, fused=True)

@@ -202,7 +202,7 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 // A wave-uniform load of data the kernel never writes, through the scalar
 // memory path: it is counted apart from the vector loads, so waiting for it
 // does not wait for the vector loads issued before it.
-__device__ __forceinline__ int32_t ld_scalar_i32(const int32_t * p, uint32_t i) {
+__device__ __forceinline__ int32_t ld_scalar_i32(const int32_t * p, int64_t i) {
     return ((const __attribute__((address_space(4))) int32_t *) p)[i];
 }
 

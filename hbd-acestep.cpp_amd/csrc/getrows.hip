@@ -100,9 +100,12 @@ __global__ void __launch_bounds__(256) k_get_rows_q8_0_lds(const GetRowsArgs a, 
     const uint16_t * s16   = (const uint16_t *) stage;
     const uint32_t   step  = gridDim.x * 4;
     uint4            v[MAXC];
-    // the row of id `id`; its loads are issued into v when it is valid
+    // the row of id `id`; its loads are issued into v when it is valid. The id
+    // (wave-uniform) comes through the scalar path: waiting for it does not
+    // wait for the previous row's stores, which the vector memory counter
+    // also tracks.
     auto fetch = [&](uint32_t id) -> int64_t {
-        const int64_t r = a.ids[(int64_t) id * a.ids_stride];
+        const int64_t r = ld_scalar_i32(a.ids, (int64_t) id * a.ids_stride);
         if (r >= 0 && r < a.n_rows) {
             const char * row = a.table + r * a.tnb1;
 #pragma unroll
