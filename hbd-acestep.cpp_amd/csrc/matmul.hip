@@ -429,6 +429,15 @@ __global__ void __launch_bounds__(256) k_mmv_reduce(const MmvArgs a) {
 // block-major quantized rows (lane l: row l % 32, bytes 16 (l / 32) of the
 // block), weights from the R64 layout (a 32-row half of a group is two 512-byte
 // runs), so no LDS staging is needed; one block ahead is in flight.
+#ifndef MI_MMQ_WG_PER_CU
+#define MI_MMQ_WG_PER_CU 2  // resident workgroups of the matrix kernel per CU (2 waves per SIMD)
+#endif
+#ifndef MI_MMQ_MAX_KSPLIT
+#define MI_MMQ_MAX_KSPLIT 4  // key splits of the matrix kernel at most
+#endif
+#ifndef MI_MMQ_MIN_BPS
+#define MI_MMQ_MIN_BPS 32  // blocks of 32 keys per split at least
+#endif
 typedef int mm_i32x4 __attribute__((ext_vector_type(4)));
 typedef int mm_i32x16 __attribute__((ext_vector_type(16)));
 typedef float mm_f32x16 __attribute__((ext_vector_type(16)));
@@ -502,13 +511,16 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
             }
         }
     };
-    Blk      k0, k1;
-    uint32_t b = 0;
-    if (a.nbk > 0) {
-        load(k0, 0);
+    // this workgroup's blocks: split blockIdx.z of the key range
+    const uint32_t bb = blockIdx.z * a.bps;
+    const uint32_t be = bb + a.bps < a.nbk ? bb + a.bps : a.nbk;
+    Blk            k0, k1;
+    uint32_t       b = bb;
+    if (b < be) {
+        load(k0, b);
     }
-    while (b < a.nbk) {
-        const bool n1 = b + 1 < a.nbk;
+    while (b < be) {
+        const bool n1 = b + 1 < be;
         if (n1) {
             load(k1, b + 1);
         }
@@ -517,7 +529,7 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
         if (!n1) {
             break;
         }
-        const bool n0b = b + 1 < a.nbk;
+        const bool n0b = b + 1 < be;
         if (n0b) {
             load(k0, b + 1);
         }
@@ -526,6 +538,26 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
         if (!n0b) {
             break;
         }
+    }
+    if (a.splits > 1) {
+        // the split's sums to the workspace [split][mp][npad] (every row and
+        // column of the tile lies inside the padded extent); k_mmq_reduce adds
+        // the splits in order and applies the epilogue
+        float * pp = a.part + (size_t) blockIdx.z * a.mp * a.npad;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        pp[(size_t) (m0 + 32 * i + 8 * q + 4 * hh + e) * a.npad + n0 + 32 * j + c] = acc[i][j][4 * q + e];
+                    }
+                }
+            }
+        }
+        return;
     }
     // D lane l: column n0 + 32 j + c, rows m0 + 32 i + 8 q + 4 hh + e; with a
     // residual, the 16 values of an (i, j) tile are loaded before any is added
@@ -564,6 +596,32 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
     }
 }
 
+// The matrix kernel's key splits added in split order, then the epilogue
+// (residual, clamp): one thread per output, consecutive threads along a row.
+__global__ void __launch_bounds__(256) k_mmq_reduce(const MmvArgs a) {
+    const uint64_t gid = (uint64_t) blockIdx.x * 256u + threadIdx.x;
+    const uint32_t m   = (uint32_t) (gid / a.n);
+    const uint32_t n   = (uint32_t) (gid - (uint64_t) m * a.n);
+    if (m >= a.m) {
+        return;
+    }
+    const float *  pp  = a.part + (size_t) m * a.npad + n;
+    const size_t   st  = (size_t) a.mp * a.npad;
+    float          v[MI_MMQ_MAX_KSPLIT];
+#pragma unroll
+    for (int s2 = 0; s2 < MI_MMQ_MAX_KSPLIT; ++s2) {
+        v[s2] = pp[(size_t) (s2 < (int) a.splits ? s2 : 0) * st];  // all loads before any add
+    }
+    float t = v[0];
+#pragma unroll
+    for (int s2 = 1; s2 < MI_MMQ_MAX_KSPLIT; ++s2) {
+        if (s2 < (int) a.splits) {
+            t += v[s2];
+        }
+    }
+    *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) n * 4) = mm_epilogue(a, m, n, t);
+}
+
 #ifndef MI_MMV_NORED_MIN
 #define MI_MMV_NORED_MIN 8  // waves per CU from which key splits stop at one workgroup per row group (0: never)
 #endif
@@ -579,9 +637,19 @@ void mul_mat_q8_0_plan(MmvArgs & a, int cus) {
     a.npad   = a.ng * 64;
     a.qbytes = (uint64_t) a.ng * a.nbk * 2048;
     a.mp     = a.m <= 8 ? a.m : (a.m + 127) / 128 * 128;
-    if (a.m > 8) {  // the matrix kernel: no key split
-        a.wpg = a.splits = 1;
-        a.bps = a.nbk;
+    if (a.m > 8) {
+        // the matrix kernel: key splits (workspace partials, added by
+        // k_mmq_reduce) only when its 128 x 128 tiles leave resident workgroup
+        // slots empty -- the narrow products (n = H) at prefill sizes
+        a.wpg             = 1;
+        const uint64_t tl = (uint64_t) ((a.n + 127) / 128) * (a.mp / 128);
+        const uint64_t sl = (uint64_t) (cus > 0 ? cus : 256) * MI_MMQ_WG_PER_CU;
+        uint64_t       ks = tl < sl ? sl / tl : 1;
+        ks                = ks > MI_MMQ_MAX_KSPLIT ? MI_MMQ_MAX_KSPLIT : ks;
+        ks                = ks > a.nbk / MI_MMQ_MIN_BPS ? a.nbk / MI_MMQ_MIN_BPS : ks;
+        ks                = ks < 1 ? 1 : ks;
+        a.bps             = a.nbk == 0 ? 1 : (uint32_t) ((a.nbk + ks - 1) / ks);
+        a.splits          = a.nbk == 0 ? 1 : (a.nbk + a.bps - 1) / a.bps;
         return;
     }
     const uint32_t want = (uint32_t) (cus > 0 ? cus : 256) * MI_MMV_WAVES_PER_CU;
@@ -608,8 +676,8 @@ static size_t al256(size_t v) {
 
 size_t mul_mat_q8_0_workspace(const MmvArgs & a) {
     size_t b = al256((size_t) a.mp * a.k) + al256((size_t) a.mp * a.nbk * 4);
-    if (a.splits > 1) {
-        b += al256((size_t) a.splits * a.m * a.npad * 4);
+    if (a.splits > 1) {  // partials: [splits][m][npad], or [splits][mp][npad] for the matrix kernel
+        b += al256((size_t) a.splits * (a.m > 8 ? a.mp : a.m) * a.npad * 4);
     }
     return b;
 }
@@ -643,7 +711,11 @@ int launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s) {
         MI_LAUNCH(k_mmv_quant_x, dim3((uint32_t) ((threads + 255) / 256)), dim3(256), 0, s, a);
     }
     if (a.m > 8) {
-        MI_LAUNCH(k_mmq_q8_0, dim3((a.n + 127) / 128, a.mp / 128), dim3(256), 0, s, a);
+        MI_LAUNCH(k_mmq_q8_0, dim3((a.n + 127) / 128, a.mp / 128, a.splits), dim3(256), 0, s, a);
+        if (a.splits > 1) {
+            const uint64_t outs = (uint64_t) a.m * a.n;
+            MI_LAUNCH(k_mmq_reduce, dim3((uint32_t) ((outs + 255) / 256)), dim3(256), 0, s, a);
+        }
         return MI_OK;
     }
     const dim3   grid(a.ng, a.splits), blk(64 * a.wpg);

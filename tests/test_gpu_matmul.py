@@ -100,10 +100,12 @@ def test_zero_x_rows_and_repeat_calls_are_identical(dev):
 
 
 @pytest.mark.parametrize("n,k,m", [(2048, 2048, 300), (640, 256, 129), (100, 96, 9), (6144, 512, 512),
-                                   (70, 32, 1000)])
+                                   (70, 32, 1000), (2560, 9728, 520), (2560, 4096, 300)])
 def test_matrix_kernel_shapes(dev, n, k, m):
     """More than 8 rows of x (DiT and prefill projections): ragged row tiles of x
-    and of the weights, one-block rows, many rows."""
+    and of the weights, one-block rows, many rows; the narrow Qwen3-4B prefill
+    products (n = 2560: O, down), whose few 128 x 128 tiles take key splits added
+    by a second launch (2048 x 2048 x 300 takes two)."""
     print(f"mul_mat q8_0 matrix n={n} k={k} m={m}", flush=True)
     _run(n, k, m, seed=n * 7 + k + m)
 
@@ -164,6 +166,7 @@ def test_swiglu_prologue_matches_swiglu_then_mul_mat(dev, n, k, m, swapped):
     (16448, 256, 4, True, False),    # 257 row groups: splits added in LDS, one launch
     (640, 256, 129, False, False),   # the matrix kernel
     (640, 256, 129, True, True),
+    (2560, 9728, 200, True, True),   # the matrix kernel with key splits: the residual added by the split sum
 ])
 def test_swiglu_down_with_residual_add(dev, n, k, m, clamp, inplace):
     """mi_mul_mat_q8_0_swiglu_add against mi_mul_mat_q8_0_swiglu then mi_add /
