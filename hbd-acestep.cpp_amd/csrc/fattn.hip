@@ -1507,6 +1507,9 @@ __device__ __forceinline__ uint4 fa_bld16(fa_rsrc r, uint32_t voff, uint32_t sof
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+#ifndef MI_FA_PRIO_PV
+#define MI_FA_PRIO_PV 1  // > 0: the wave's issue priority in its P.V section (MFMAs between the P conversions)
+#endif
 #ifndef MI_FA_MFMA_WPE
 #define MI_FA_MFMA_WPE 2  // waves per SIMD: 2 caps registers at 256 (two workgroups per CU, 144 KB of LDS)
 #endif
@@ -1817,6 +1820,9 @@ k_fa_mfma(const FaArgs a) {
         // a row with no live key yet has mrun = -inf and only -inf values: p = 0
         const float nmn  = mrun == -INFINITY ? 0.0f : -mrun;
         float       psum = 0.0f;
+        if constexpr (MI_FA_PRIO_PV > 0) {
+            __builtin_amdgcn_s_setprio(MI_FA_PRIO_PV);
+        }
         // O^T += V^T P^T. MFMA (bk, jj) covers keys 32 bk + 16 jj + [0, 16): k-slot
         // 8 hh + 4 jh + i is key 32 bk + 16 jj + 8 jh + 4 hh + i (S^T accumulator
         // 8 jj + 4 jh + i); A lane = V^T row 32 db + n at those keys
@@ -1856,6 +1862,9 @@ k_fa_mfma(const FaArgs a) {
             }
         }
         lrun += psum;
+        if constexpr (MI_FA_PRIO_PV > 0) {
+            __builtin_amdgcn_s_setprio(0);
+        }
         }  // live
         if (t + 1 < te) {
             store_tile(cur ^ 1);

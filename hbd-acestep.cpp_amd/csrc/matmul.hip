@@ -429,6 +429,9 @@ __global__ void __launch_bounds__(256) k_mmv_reduce(const MmvArgs a) {
 // block-major quantized rows (lane l: row l % 32, bytes 16 (l / 32) of the
 // block), weights from the R64 layout (a 32-row half of a group is two 512-byte
 // runs), so no LDS staging is needed; one block ahead is in flight.
+#ifndef MI_MMQ_PRIO
+#define MI_MMQ_PRIO 1  // > 0: the wave's issue priority while it issues a block's MFMAs
+#endif
 #ifndef MI_MMQ_WG_PER_CU
 #define MI_MMQ_WG_PER_CU 2  // resident workgroups of the matrix kernel per CU (2 waves per SIMD)
 #endif
@@ -500,10 +503,16 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const mm_i32x4  bv = { (int) k.w[j].x, (int) k.w[j].y, (int) k.w[j].z, (int) k.w[j].w };
+                if constexpr (MI_MMQ_PRIO > 0) {
+                    __builtin_amdgcn_s_setprio(MI_MMQ_PRIO);
+                }
                 const mm_i32x16 d  = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, mm_i32x16{}, 0, 0, 0);
                 mm_f16x8        sw = {};
                 sw[0]              = hh == 0 ? __builtin_bit_cast(_Float16, k.dw[j]) : (_Float16) 0.0f;
                 const mm_f32x16 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(sx, sw, mm_f32x16{}, 0, 0, 0);
+                if constexpr (MI_MMQ_PRIO > 0) {
+                    __builtin_amdgcn_s_setprio(0);
+                }
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     acc[i][j][e] = __builtin_fmaf((float) d[e], sc[e], acc[i][j][e]);
