@@ -19,7 +19,10 @@ of that stage, at that op's own bar:
                                  the matrix-core kernel over an F16 cache (P in two
                                  16-bit parts), the split kernel over Q8_0
   O product, gate/up, down       Q8_0 product bound
-  residual sums                  bit-exact"""
+  residual sums                  bit-exact (clamped to +-65504 with clamp_fp16)
+With clamp_fp16 (qwen3-lm.h:53) the layer clamps V before the cache store
+(qwen3-lm.h:392-393) and both residual sums (480-481, 488-489): the case drives V
+and the hidden state past the fp16 range."""
 import numpy as np
 import pytest
 from fa_bound import fa_bound
@@ -30,6 +33,7 @@ from acestep_ops import ops
 from acestep_ops.qwen3 import Qwen3Layer
 
 pytestmark = pytest.mark.gpu
+LIM = 65504.0
 
 
 def _w(r, n, k, s=0.05):
@@ -41,10 +45,11 @@ SIZES = {"small": (256, 4, 2, 128, 512, 37, (0, 100), 256, 4, 1),
          "qwen3_4b": (2560, 32, 8, 128, 9728, 96, (0, 300), 512, 3, 1)}
 
 
-@pytest.mark.parametrize("size,kv_type", [("small", "f16"), ("small", "q8_0"), ("qwen3_4b", "f16"),
-                                          ("qwen3_4b", "q8_0")])
-def test_prefill_layer_stage_by_stage(dev, size, kv_type):
-    print(f"qwen3 prefill layer {size} kv={kv_type}", flush=True)
+@pytest.mark.parametrize("size,kv_type,clamp", [("small", "f16", False), ("small", "q8_0", False),
+                                                ("small", "q8_0", True), ("qwen3_4b", "f16", False),
+                                                ("qwen3_4b", "q8_0", False)])
+def test_prefill_layer_stage_by_stage(dev, size, kv_type, clamp):
+    print(f"qwen3 prefill layer {size} kv={kv_type} clamp_fp16={clamp}", flush=True)
     r = np.random.default_rng(47)
     H, Nh, Nkv, D, I, S, kv_pos, max_seq, n_sets, s0 = SIZES[size]
     N = len(kv_pos)
@@ -55,9 +60,17 @@ def test_prefill_layer_stage_by_stage(dev, size, kv_type):
     nw_post = (1 + 0.1 * r.standard_normal(H)).astype(np.float32)
     qn, kn = (1 + 0.1 * r.standard_normal(D)).astype(np.float32), (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
     hidden = (r.standard_normal((N, S, H)) * 0.8).astype(np.float32)
+    if clamp:
+        # V of most tokens past the fp16 range (the cache gets it clamped, qwen3-lm.h:392-393), and
+        # residual sums past it (qwen3-lm.h:480-481, 488-489). Element 3 is fixed so that its
+        # normalized value (at most ~7.1e6) stays below 127 * 65504, where the Q8_0 block scale of x
+        # would overflow fp16 (in ggml as here).
+        nw_in[3] = 2.5e6
+        hidden[:, :, 3] = 2.0
+        hidden[0, 0, :3] = [7e4, -9e4, 6e4]
     layer = Qwen3Layer(ops.Q8(to_dev(Wqkv)), ops.Q8(to_dev(Wo)), ops.Q8(to_dev(Wgu)), ops.Q8(to_dev(Wd)),
                        to_dev(nw_in), to_dev(nw_post), to_dev(qn), to_dev(kn), H, Nh, Nkv, D, I, max_seq, n_sets,
-                       kv_type, eps, theta)
+                       kv_type, eps, theta, clamp_fp16=clamp)
     # earlier tokens of each sequence (and every other slot) already hold finite values
     kc0 = r.standard_normal((n_sets, Nkv, max_seq, D), dtype=np.float32) * np.float32(0.5)
     vc0 = r.standard_normal((n_sets, Nkv, max_seq, D), dtype=np.float32) * np.float32(0.5)
@@ -87,6 +100,9 @@ def test_prefill_layer_stage_by_stage(dev, size, kv_type):
     ko = to_np(ko)
     assert_f32_close(b["qo"], orc.qk_norm_rope(q, qn, pos, eps, D, theta), row_floor=True)
     assert_f32_close(ko, orc.qk_norm_rope(k, kn, pos, eps, D, theta), row_floor=True)
+    if clamp:
+        assert (np.abs(v) > LIM).sum() > v.size // 4
+        v = orc.clamp(v, -LIM, LIM)
     # 3. the cache: the new tokens' slots bit-exact, every other slot unchanged
     if kv_type == "q8_0":
         kdev, vdev = to_np(layer.k_cache.data), to_np(layer.v_cache.data)
@@ -116,18 +132,23 @@ def test_prefill_layer_stage_by_stage(dev, size, kv_type):
     bound = fa_bound(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type, mfma=mfma)
     assert np.all(np.isfinite(attn))
     assert np.all(np.abs(attn - ref) <= bound)
-    # 5. O product; the residual sum bit-exact
+    # 5. O product; the residual sum (clamped with clamp_fp16) bit-exact
     a2 = attn.reshape(T, Nh * D)
     assert_mul_mat_q8_0(b["ao"], Wo, a2)
-    h1 = orc.add(h2, b["ao"])
+    h1 = orc.add_clamp(h2, b["ao"]) if clamp else orc.add(h2, b["ao"])
     assert np.array_equal(b["h1"], h1)
-    # 6. post-attention norm -> gate/up product (one call)
-    assert_mul_mat_q8_0(b["gu"], Wgu, orc.rms_norm_mul(h1, nw_post, eps))
+    # 6. post-attention norm -> gate/up product
+    if clamp:
+        assert_f32_close(b["n2"], orc.rms_norm_mul(h1, nw_post, eps))
+        assert_mul_mat_q8_0(b["gu"], Wgu, b["n2"])
+    else:
+        assert_mul_mat_q8_0(b["gu"], Wgu, orc.rms_norm_mul(h1, nw_post, eps))
     # 7. SwiGLU -> down product; the last residual sum bit-exact (the layer adds h1
     # inside the down product's call, bit-identical to the product then the add)
     mlp = to_np(ops.mul_mat_q8_0_swiglu(layer.w["down"], layer._bufs["gu"]))
     assert_mul_mat_q8_0(mlp, Wd, orc.swiglu(b["gu"]))
-    assert np.array_equal(y.reshape(T, H), orc.add(h1, mlp))
+    out = orc.add_clamp(h1, mlp) if clamp else orc.add(h1, mlp)
+    assert np.array_equal(y.reshape(T, H), out)
     assert np.all(np.isfinite(y))
 
 
