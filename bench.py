@@ -753,6 +753,60 @@ def attention_bench(steps: int):
         del qd, kd, qkv, qv, kv, vv, yd, zmask, wmask, wsd
         device.synchronize()
 
+    # LM prefill attention over the KV cache (qw3lm_forward, qwen3-lm.h:429-549;
+    # the songgen LM reads an F16 or a Q8_0 cache, songgen-lelm-gen.h:50-61):
+    # Qwen3-4B 32/8 heads x 128, 8 sequences x 2048 new tokens from slot 0 of
+    # an 8192-slot cache (the batched prefill's shape), F32 q as the rope output,
+    # the causal F16 mask [kv_len, S] shared by the heads; flops count the
+    # causal (query, key) pairs
+    NP, SP, NHP, NKP = 8, 2048, 32, 8
+    qp = DTensor.from_numpy(rng.standard_normal((NP, SP, NHP, Dh), dtype=np.float32))
+    qpv = qp.permute(0, 2, 1, 3)
+    ii = np.arange(SP)[:, None]
+    cm = np.where(np.arange(SP)[None, :] <= ii, 0.0, -np.inf).astype(np.float16)
+    cmask = DTensor.from_numpy(np.ascontiguousarray(np.broadcast_to(cm, (NP, 1, SP, SP))).view(np.uint16), "f16")
+    del cm, ii
+    yp = DTensor.empty((NP, SP, NHP, Dh), "f32")
+    live = NP * NHP * SP * (SP + 1) / 2
+    for kt in ("q8_0", "f16"):
+        caches = []
+        for _ in range(2):  # K, V
+            src = DTensor.from_numpy(rng.standard_normal((NP, NKP, SP, Dh), dtype=np.float32))
+            if kt == "q8_0":
+                c = DTensor.empty((NP, NKP, SLOTS, Q8_ROW(Dh)), "u8")
+                ops.cpy(src, ops.Q8(c[:, :, :SP]), stream=sh)
+                caches.append(ops.Q8(c[:, :, :SP]))
+            else:
+                c = DTensor.empty((NP, NKP, SLOTS, Dh), "f16")
+                ops.cpy(src, c[:, :, :SP], stream=sh)
+                caches.append(c[:, :, :SP])
+            st.synchronize()
+            del src
+        kc, vc = caches
+        wsp = DTensor.empty((max(ops.flash_attn_workspace(qpv, kc, vc), 1),), "u8")
+        call = lambda: ops.flash_attn_ext(qpv, kc, vc, cmask, 1.0 / float(np.sqrt(Dh)), out=yp,  # noqa
+                                          workspace=wsp, stream=sh)
+        for _ in range(10):
+            call()
+        st.synchronize()
+        ev = [Event() for _ in range(steps + 1)]
+        ev[0].record(sh)
+        for i in range(steps):
+            call()
+            ev[i + 1].record(sh)
+        st.synchronize()
+        us = 1000.0 * ev[0].elapsed_ms(ev[steps]) / steps
+        lf = 4.0 * live * Dh
+        print(json.dumps({"config": f"Qwen3-4B prefill attention, {NP} x {SP} tokens from slot 0, {NHP}/{NKP} heads x "
+                                    f"{Dh}, F32 q, causal F16 mask, {kt} KV cache of {SLOTS} slots",
+                          "us_per_call": round(us, 2), "live_flop_per_call": lf,
+                          "TFLOP/s": round(lf / (us * 1e-6) / 1e12, 1),
+                          "frac_of_bf16_dense": round(lf / (us * 1e-6) / 1e12 / 2500.0, 3)}), flush=True)
+        del caches, kc, vc, wsp
+        device.synchronize()
+    del qp, qpv, cmask, yp
+    device.synchronize()
+
 # ---------------------------------------------------------------------------
 # Q8_0 matrix-vector products (reported with --gemv): ggml_mul_mat with Q8_0
 # weights at the Qwen3-4B batch-8 decode shape (qwen3-lm.h:639-651, 729, 737,

@@ -756,9 +756,24 @@ __global__ void __launch_bounds__(256) k_fa_combine(const FaArgs a) {
 // column l%32, same k; D lane l = column l%32, row 8j + 4*(l/32) + i at 4j+i.
 // Keys whose mask is -inf get p = 0 (their K/V bytes are multiplied, so they
 // must be finite, as every activation the reference feeds here is).
+// Q8_0 K and V (the same walk, tiles of 64 keys):
+//   S^T           per 32-element block: v_mfma_i32_32x32x32_i8 of the K quants
+//                 (LDS) and q converted to Q8_0 with the x86 quantizer (exact
+//                 int32 block dots), and the block's d_k d_q as an fp16 outer
+//                 product on the matrix core (exact); s = the four scaled dots
+//                 summed by a chain of fmas in block order
+//   V             dequantized once per tile into LDS: V' = q d_v exactly, as a
+//                 bf16 high part RN(V') and an f16 low part V' - RN(V') (exact:
+//                 at most 10 significant bits on the fp16 grid), so V' is held
+//                 exactly for every finite d_v
+//   O^T += V^T P^T as three MFMAs: bf16 high x (P high + P low), f16 low x P
+//                 rounded to f16; P keeps ~16 bits against V's high part
 // ---------------------------------------------------------------------------
 #ifndef MI_FA_DEC
 #define MI_FA_DEC 1  // decode (one query position, <= 16 heads per KV head) on the 16x16 matrix cores
+#endif
+#ifndef MI_FA_MFMA_Q8
+#define MI_FA_MFMA_Q8 1  // prefill over Q8_0 K/V on the matrix cores (else the split path)
 #endif
 #ifndef MI_FA_MFMA_MIN_ROWS
 #define MI_FA_MFMA_MIN_ROWS 64  // (query position, head) rows per KV head from which the MFMA path is used
@@ -1518,20 +1533,29 @@ __device__ __forceinline__ uint4 fa_bld16(fa_rsrc r, uint32_t voff, uint32_t sof
 template <int KT, int D, bool MSK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MI_FA_MFMA_WPE, MI_FA_MFMA_WPE)))
 k_fa_mfma(const FaArgs a) {
-    using M          = FaM<KT>;
-    using x8         = typename M::x8;
+    constexpr bool Q8 = KT == MI_TYPE_Q8_0;
+    using M           = FaM<Q8 ? MI_TYPE_BF16 : KT>;  // type of the P.V operands (Q8_0: V's bf16 high part)
+    using x8          = typename M::x8;
+    typedef int      i32x4 __attribute__((ext_vector_type(4)));
+    typedef int      i32x16 __attribute__((ext_vector_type(16)));
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
     constexpr int BQ = 128, BK = 64;
-    constexpr int KS = D * 2 + 16;   // K row stride in LDS (bytes): 16-byte bank spread
+    constexpr int KS = Q8 ? D + 16 : D * 2 + 16;  // K row stride in LDS (bytes; Q8_0: the quants): 16-byte bank spread
     constexpr int VR = D * 2 + 64;   // V row stride (bytes): rows 16 banks apart, conflict-free transposed reads
     constexpr int KC = D * 2 / 16;   // 16-byte chunks per K/V row
     constexpr int NC = BK * KC / 256;  // chunks per thread per tile (K and V each; even)
-    constexpr int NKS = D / 16;      // k-steps of the S MFMA
-    constexpr int NDB = D / 32;      // 32-row blocks of O^T
+    constexpr int NKS = D / 16;      // k-steps of the S MFMA (Q8_0: 8 elements of a lane's 16 per block)
+    constexpr int NDB = D / 32;      // 32-row blocks of O^T (Q8_0: also the blocks of a row)
+    constexpr int RBY = Q8 ? NDB * 34 : D * 2;  // bytes of a K/V row
     static_assert(NC * 256 == BK * KC, "tile chunks");
     static_assert(D * 2 % 256 == 0, "the V row stride's bank spread assumes whole 256-byte rows");
+    static_assert(!Q8 || BK * NDB == 256, "Q8_0 tiles: one thread per (key, block)");
 
-    __shared__ __align__(16) char kt[2][BK * KS];
-    __shared__ __align__(16) char vt[2][BK * VR];
+    // K tiles double-buffered; V tiles double-buffered, or for Q8_0 one tile
+    // as its bf16 high part (vt[0]) and f16 low part (vt[1])
+    __shared__ __align__(16) char     kt[2][BK * KS];
+    __shared__ __align__(16) char     vt[2][BK * VR];
+    __shared__ __align__(16) uint16_t kds[2][Q8 ? BK * NDB : 1];  // Q8_0: K block scales [key][block]
 
     const int      tid  = threadIdx.x;
     const int      wave = tid >> 6;
@@ -1563,10 +1587,15 @@ k_fa_mfma(const FaArgs a) {
                                       (int64_t) iq * a.m1
                                  : nullptr;
 
-    // Q^T operands: k-step ks needs q[row][16 ks + 8 hh + i], converted to K's type (RNE)
+    // Q^T operands: k-step ks needs q[row][16 ks + 8 hh + i], converted to K's type (RNE).
+    // Q8_0: block j needs q[row][32 j + 16 hh + i], i < 16 (ks = 2 j + i / 8), as
+    // its x86 Q8_0 quants; d_q of each block kept as fp16 bits.
     // (q's type and access width are tested once, outside the loads, so that
     // every load is in flight before the first is used)
-    x8 qb[NKS];
+    auto qe = [&](int ks) { return Q8 ? 32 * (ks >> 1) + 16 * hh + 8 * (ks & 1) : 16 * ks + 8 * hh; };
+    x8       qb[NKS];
+    i32x4    qa[NDB];
+    uint16_t dq16[NDB];
     {
         const char * qp = a.q + (int64_t) b * a.q3 + (int64_t) h * a.q2 + (int64_t) iq * a.q1;
         float        f[NKS][8];
@@ -1575,7 +1604,7 @@ k_fa_mfma(const FaArgs a) {
                 uint4 u[NKS][2];
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    const char * p = qp + (size_t) (16 * ks + 8 * hh) * 4;
+                    const char * p = qp + (size_t) qe(ks) * 4;
                     u[ks][0]       = ld16(p);
                     u[ks][1]       = ld16(p + 16);
                 }
@@ -1589,7 +1618,7 @@ k_fa_mfma(const FaArgs a) {
                 for (int ks = 0; ks < NKS; ++ks) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        f[ks][e] = ((const float *) (qp + (size_t) (16 * ks + 8 * hh) * 4))[e];
+                        f[ks][e] = ((const float *) (qp + (size_t) qe(ks) * 4))[e];
                     }
                 }
             }
@@ -1598,12 +1627,12 @@ k_fa_mfma(const FaArgs a) {
             if (a.qvec) {
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    v[ks] = ld16(qp + (size_t) (16 * ks + 8 * hh) * 2);
+                    v[ks] = ld16(qp + (size_t) qe(ks) * 2);
                 }
             } else {
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    const uint16_t * q16 = (const uint16_t *) (qp + (size_t) (16 * ks + 8 * hh) * 2);
+                    const uint16_t * q16 = (const uint16_t *) (qp + (size_t) qe(ks) * 2);
                     v[ks] = make_uint4((uint32_t) q16[0] | ((uint32_t) q16[1] << 16), (uint32_t) q16[2] | ((uint32_t) q16[3] << 16),
                                        (uint32_t) q16[4] | ((uint32_t) q16[5] << 16), (uint32_t) q16[6] | ((uint32_t) q16[7] << 16));
                 }
@@ -1620,11 +1649,44 @@ k_fa_mfma(const FaArgs a) {
                 }
             }
         }
+        if constexpr (Q8) {
+            // x86 from_float per block (as fa_q8_block): the block's 32 elements sit
+            // in lanes l and l ^ 32, so its amax is one exchange away
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
+            for (int j = 0; j < NDB; ++j) {
+                float x[16];
+                float amax = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                qb[ks][e] = __builtin_bit_cast(typename M::e, M::bits(rvld ? f[ks][e] : 0.0f));
+                for (int i = 0; i < 16; ++i) {
+                    x[i] = rvld ? f[2 * j + i / 8][i % 8] : 0.0f;
+                    amax = fmaxf(amax, fabsf(x[i]));
+                }
+                amax              = fa_xhalf_max(amax);
+                constexpr float C  = 1.0f / 127.0f;
+                const float     q0 = amax * C;
+                const float     d  = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, amax), C, q0);  // IEEE amax / 127
+                const float     id = amax != 0.0f ? 127.0f / amax : 0.0f;
+                uint32_t        w[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    uint32_t acc = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(x[4 * k + e] * id), -128.0f, 127.0f);
+                        acc |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
+                    }
+                    w[k] = acc;
+                }
+                qa[j]   = i32x4{ (int) w[0], (int) w[1], (int) w[2], (int) w[3] };
+                dq16[j] = f32_to_f16_bits(d);
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    qb[ks][e] = __builtin_bit_cast(typename M::e, M::bits(rvld ? f[ks][e] : 0.0f));
+                }
             }
         }
     }
@@ -1639,31 +1701,106 @@ k_fa_mfma(const FaArgs a) {
     uint4          kr[NC], vr[NC];
     const uint32_t ko0 = (uint32_t) (tid / KC) * (uint32_t) a.k1 + (uint32_t) (tid % KC) * 16;
     const uint32_t vo0 = (uint32_t) (tid / KC) * (uint32_t) a.v1 + (uint32_t) (tid % KC) * 16;
+    // Q8_0: thread (key qk, block qc) loads the 9 words of its key's 136-byte row
+    // that hold block qc: bytes [34 qc, 34 qc + 36), 2 bytes earlier for odd qc
+    // (4-byte aligned: the planner checks strides and bases), so the block's
+    // scale sits at byte 0 (even qc) or 2 (odd) of the words, its quants after it
+    const uint32_t qk = (uint32_t) tid >> 2, qc = (uint32_t) tid & 3u;
+    const bool     qodd = (qc & 1u) != 0;
+    const uint32_t qko  = qk * (uint32_t) a.k1 + 34u * qc - (qodd ? 2u : 0u);
+    const uint32_t qvo  = qk * (uint32_t) a.v1 + 34u * qc - (qodd ? 2u : 0u);
+    uint32_t       kw[9], vw[9];
     // buffers end at the last key's row: keys past the end read as zeros
-    const fa_rsrc  krs = fa_make_rsrc(kg, (uint32_t) ((int64_t) (a.n_kv - 1) * a.k1 + D * 2));
-    const fa_rsrc  vrs = fa_make_rsrc(vg, (uint32_t) ((int64_t) (a.n_kv - 1) * a.v1 + D * 2));
+    const fa_rsrc  krs = fa_make_rsrc(kg, (uint32_t) ((int64_t) (a.n_kv - 1) * a.k1 + RBY));
+    const fa_rsrc  vrs = fa_make_rsrc(vg, (uint32_t) ((int64_t) (a.n_kv - 1) * a.v1 + RBY));
     auto load_tile = [&](int t0) {
         const uint32_t ks0 = (uint32_t) t0 * (uint32_t) a.k1;
         const uint32_t vs0 = (uint32_t) t0 * (uint32_t) a.v1;
+        if constexpr (Q8) {
+            // the whole offset in the per-lane operand, which the range check covers
+            const uint32_t kb0 = qko + ks0, vb0 = qvo + vs0;
 #pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            kr[i] = fa_bld16(krs, ko0, ks0 + (uint32_t) (KR * i) * (uint32_t) a.k1);
-        }
+            for (int j = 0; j < 9; ++j) {
+                kw[j] = __builtin_amdgcn_raw_buffer_load_b32(krs, (int) (kb0 + 4 * j), 0, 0);
+            }
 #pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            vr[i] = fa_bld16(vrs, vo0, vs0 + (uint32_t) (KR * i) * (uint32_t) a.v1);
+            for (int j = 0; j < 9; ++j) {
+                vw[j] = __builtin_amdgcn_raw_buffer_load_b32(vrs, (int) (vb0 + 4 * j), 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                kr[i] = fa_bld16(krs, ko0, ks0 + (uint32_t) (KR * i) * (uint32_t) a.k1);
+            }
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                vr[i] = fa_bld16(vrs, vo0, vs0 + (uint32_t) (KR * i) * (uint32_t) a.v1);
+            }
         }
     };
-    auto store_tile = [&](int buf) {
+    // Q8_0: the block's 32 quants from the 9 words (shifted by 2 bytes for even qc)
+    auto q8_quants = [&](const uint32_t (&w)[9], uint32_t (&qw)[8]) {
 #pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            const int c = tid + 256 * i;
-            *(uint4 *) (kt[buf] + (c / KC) * KS + (c % KC) * 16) = kr[i];
+        for (int i = 0; i < 8; ++i) {
+            qw[i] = qodd ? w[i + 1] : __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
         }
+    };
+    // K (Q8_0: the quants and the block scale; V goes through store_v)
+    auto store_tile = [&](int buf) {
+        if constexpr (Q8) {
+            uint32_t qw[8];
+            q8_quants(kw, qw);
+            char * kp = kt[buf] + qk * KS + 32 * qc;
+            *(uint4 *) kp        = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+            *(uint4 *) (kp + 16) = make_uint4(qw[4], qw[5], qw[6], qw[7]);
+            kds[buf][qk * NDB + qc] = (uint16_t) (kw[0] >> (qodd ? 16 : 0));
+        } else {
 #pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            const int c = tid + 256 * i;
-            *(uint4 *) (vt[buf] + (c / KC) * VR + (c % KC) * 16) = vr[i];
+            for (int i = 0; i < NC; ++i) {
+                const int c = tid + 256 * i;
+                *(uint4 *) (kt[buf] + (c / KC) * KS + (c % KC) * 16) = kr[i];
+            }
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                const int c = tid + 256 * i;
+                *(uint4 *) (vt[buf] + (c / KC) * VR + (c % KC) * 16) = vr[i];
+            }
+        }
+    };
+    // Q8_0 V: V' = q d_v of the thread's block, exactly (fma(q + 128, d, -128 d)
+    // rounds the exact product, which fp32 holds), stored as its bf16 high part
+    // RN(V') into vt[0] and its low part V' - RN(V') into vt[1] as f16 (exact).
+    // The buffer is single: the caller separates this store from the previous
+    // tile's reads by a barrier.
+    auto store_v = [&]() {
+        if constexpr (Q8) {
+            uint32_t qw[8];
+            q8_quants(vw, qw);
+            const float dv = (float) __builtin_bit_cast(_Float16, (uint16_t) (vw[0] >> (qodd ? 16 : 0)));
+            const float nd = -128.0f * dv;
+            uint32_t    hw[16], lw[16];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t x = qw[i] ^ 0x80808080u;  // q + 128 per byte
+                float          v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = __builtin_fmaf((float) ((x >> (8 * e)) & 0xffu), dv, nd);
+                }
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    const uint32_t hp = pack_bf16x2(v[2 * h2], v[2 * h2 + 1]);
+                    hw[2 * i + h2]    = hp;
+                    lw[2 * i + h2]    = pack_f16x2(v[2 * h2] - bf16_lo(hp), v[2 * h2 + 1] - bf16_hi(hp));
+                }
+            }
+            uint4 * hp = (uint4 *) (vt[0] + qk * VR + 64 * qc);
+            uint4 * lp = (uint4 *) (vt[1] + qk * VR + 64 * qc);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                hp[c] = make_uint4(hw[4 * c], hw[4 * c + 1], hw[4 * c + 2], hw[4 * c + 3]);
+                lp[c] = make_uint4(lw[4 * c], lw[4 * c + 1], lw[4 * c + 2], lw[4 * c + 3]);
+            }
         }
     };
     // mask values of this lane's 32 keys of a tile (key 32 bk + 8 j + 4 hh + i:
@@ -1739,6 +1876,7 @@ k_fa_mfma(const FaArgs a) {
     int  fcur = flag(tb);
     load_tile(tb * BK);
     store_tile(0);
+    store_v();
     __syncthreads();
     for (int t = tb; t < te; ++t) {
         const int cur   = (t - tb) & 1;
@@ -1758,12 +1896,37 @@ k_fa_mfma(const FaArgs a) {
         }
         // S^T for keys [32 bk, 32 bk + 32) x this wave's 32 rows (two independent chains)
         fa_f32x16 sacc[2] = { fa_f32x16{}, fa_f32x16{} };
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
+        if constexpr (Q8) {
+            // per block j: the int32 dots (A = 16 quants of key 32 bk + n, B = q's),
+            // d_k d_q in the same layout from an fp16 MFMA whose k-slot 0 carries the
+            // two scales (slot 8, the other half-wave's, and the rest zero), then
+            // s = fma(d_k d_q, dot, s) in block order
 #pragma unroll
             for (int bk = 0; bk < 2; ++bk) {
-                const x8 kv = *(const x8 *) (kt[cur] + (32 * bk + n) * KS + (16 * ks + 8 * hh) * 2);
-                sacc[bk]    = fa_mma<KT>(kv, qb[ks], sacc[bk]);
+                const uint2 kd4 = *(const uint2 *) &kds[cur][(32 * bk + n) * NDB];  // the key's 4 scales
+#pragma unroll
+                for (int j = 0; j < NDB; ++j) {
+                    const i32x4  ka = *(const i32x4 *) (kt[cur] + (32 * bk + n) * KS + 32 * j + 16 * hh);
+                    const i32x16 dd = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka, qa[j], i32x16{}, 0, 0, 0);
+                    const uint32_t kdw = j < 2 ? kd4.x : kd4.y;
+                    h8 sk = {}, sq = {};
+                    sk[0] = __builtin_bit_cast(_Float16, (uint16_t) (hh == 0 ? (kdw >> (16 * (j & 1))) & 0xffffu : 0u));
+                    sq[0] = __builtin_bit_cast(_Float16, (uint16_t) (hh == 0 ? dq16[j] : 0u));
+                    const fa_f32x16 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(sk, sq, fa_f32x16{}, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        sacc[bk][e] = j == 0 ? sc[e] * (float) dd[e] : __builtin_fmaf(sc[e], (float) dd[e], sacc[bk][e]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+                for (int bk = 0; bk < 2; ++bk) {
+                    const x8 kv = *(const x8 *) (kt[cur] + (32 * bk + n) * KS + (16 * ks + 8 * hh) * 2);
+                    sacc[bk]    = fa_mma<KT>(kv, qb[ks], sacc[bk]);
+                }
             }
         }
         // softmax in base 2, x = (dot * scale + mask) * log2 e. General form: x is
@@ -1830,34 +1993,74 @@ k_fa_mfma(const FaArgs a) {
         for (int bk = 0; bk < 2; ++bk) {
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
-                x8 phi, plo;
-#pragma unroll
-                for (int slot = 0; slot < 8; ++slot) {
-                    const float    p  = __builtin_amdgcn_exp2f(fmaf(sacc[bk][8 * jj + slot], c1, nmn));
-                    const uint16_t hb = M::bits(p);
-                    psum += p;
-                    phi[slot] = __builtin_bit_cast(typename M::e, hb);
-                    plo[slot] = __builtin_bit_cast(typename M::e, M::bits(p - M::val(hb)));
-                }
                 // A = V^T rows 32 db + l % 32 at those keys, by transposed reads of the
                 // row-major V tile: lane m of a 16-lane group addresses V[K0 + m / 4][D0 +
                 // 4 (m % 4)], and lane j of the group receives V[K0 .. K0 + 3][D0 + j]
-                x8 va[NDB];
-#pragma unroll
-                for (int db = 0; db < NDB; ++db) {
-                    const char * vp = vt[cur] + (32 * bk + 16 * jj + 4 * hh + (lane & 15) / 4) * VR +
+                auto vread = [&](const char * tile, int db) {
+                    const char * vp = tile + (32 * bk + 16 * jj + 4 * hh + (lane & 15) / 4) * VR +
                                       (32 * db + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
                     const fa_v4s v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_v4s *) vp);           // keys +0..3
                     const fa_v4s v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_v4s *) (vp + 8 * VR));  // keys +8..11
-                    va[db] = __builtin_bit_cast(x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
-                }
+                    return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+                };
+                if constexpr (Q8) {
+                    // P as bf16 high + low parts against V's bf16 high part, and P as
+                    // f16 against its f16 low part (|low| <= 2^-8 |V'|)
+                    uint32_t ph[4], pl[4], pf[4];
 #pragma unroll
-                for (int db = 0; db < NDB; ++db) {
-                    o[db] = fa_mma<KT>(va[db], phi, o[db]);
-                }
+                    for (int pr = 0; pr < 4; ++pr) {
+                        const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[bk][8 * jj + 2 * pr], c1, nmn));
+                        const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[bk][8 * jj + 2 * pr + 1], c1, nmn));
+                        psum += p0;
+                        psum += p1;
+                        ph[pr] = pack_bf16x2(p0, p1);
+                        pl[pr] = pack_bf16x2(p0 - bf16_lo(ph[pr]), p1 - bf16_hi(ph[pr]));
+                        pf[pr] = pack_f16x2(p0, p1);
+                    }
+                    const x8 phi = __builtin_bit_cast(x8, ph), plo = __builtin_bit_cast(x8, pl);
+                    const h8 pfh = __builtin_bit_cast(h8, pf);
+                    x8       va[NDB];
+                    h8       vl[NDB];
 #pragma unroll
-                for (int db = 0; db < NDB; ++db) {
-                    o[db] = fa_mma<KT>(va[db], plo, o[db]);
+                    for (int db = 0; db < NDB; ++db) {
+                        va[db] = __builtin_bit_cast(x8, vread(vt[0], db));
+                        vl[db] = __builtin_bit_cast(h8, vread(vt[1], db));
+                    }
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        o[db] = fa_mma<MI_TYPE_BF16>(va[db], phi, o[db]);
+                    }
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        o[db] = fa_mma<MI_TYPE_BF16>(va[db], plo, o[db]);
+                    }
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl[db], pfh, o[db], 0, 0, 0);
+                    }
+                } else {
+                    x8 phi, plo;
+#pragma unroll
+                    for (int slot = 0; slot < 8; ++slot) {
+                        const float    p  = __builtin_amdgcn_exp2f(fmaf(sacc[bk][8 * jj + slot], c1, nmn));
+                        const uint16_t hb = M::bits(p);
+                        psum += p;
+                        phi[slot] = __builtin_bit_cast(typename M::e, hb);
+                        plo[slot] = __builtin_bit_cast(typename M::e, M::bits(p - M::val(hb)));
+                    }
+                    x8 va[NDB];
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        va[db] = __builtin_bit_cast(x8, vread(vt[cur], db));
+                    }
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        o[db] = fa_mma<KT>(va[db], phi, o[db]);
+                    }
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        o[db] = fa_mma<KT>(va[db], plo, o[db]);
+                    }
                 }
             }
         }
@@ -1871,6 +2074,12 @@ k_fa_mfma(const FaArgs a) {
         }
         fcur = fnext;
         __syncthreads();
+        if constexpr (Q8) {
+            if (t + 1 < te) {  // uniform: the next tile's V once every wave has read this one's
+                store_v();
+                __syncthreads();
+            }
+        }
     }
     };
     bool clean = !MSK;
@@ -2021,7 +2230,10 @@ void flash_attn_plan(FaArgs & a, int D) {
     // rows r0..r0+rb-1 of a wave share one query position when n_q == 1 or rb
     // divides Nh/Nkv, and one mask head when the mask does not vary by head
     a.mshared = a.mask != nullptr && a.mne2 == 1 && (a.n_q == 1 || a.rk % rb == 0);
-    a.mfma    = (a.kt == MI_TYPE_F16 || a.kt == MI_TYPE_BF16) && D == 128 && a.rows >= MI_FA_MFMA_MIN_ROWS &&
+    // Q8_0 K/V are loaded as 4-byte words: row starts 4-byte aligned (strides and bases)
+    const bool q8 = MI_FA_MFMA_Q8 && a.kt == MI_TYPE_Q8_0 && a.k1 % 4 == 0 && a.k2 % 4 == 0 && a.k3 % 4 == 0 &&
+                    a.v1 % 4 == 0 && a.v2 % 4 == 0 && a.v3 % 4 == 0 && aligned(a.k, 4) && aligned(a.v, 4);
+    a.mfma = (a.kt == MI_TYPE_F16 || a.kt == MI_TYPE_BF16 || q8) && D == 128 && a.rows >= MI_FA_MFMA_MIN_ROWS &&
              a.n_kv > 0 && (uint64_t) (a.n_kv + 64) * (uint64_t) (a.k1 > a.v1 ? a.k1 : a.v1) < (1ull << 32);
     if (a.mfma) {
         a.chunk  = a.n_kv;
@@ -2154,7 +2366,13 @@ int launch_flash_attn(const FaArgs & a, int kt, int D, hipStream_t s) {
                                dim3(64), 0, s, a);
         }
         const dim3 grid((uint32_t) (a.tfull + 2 * a.tsplit));
-        if (kt == MI_TYPE_BF16) {
+        if (kt == MI_TYPE_Q8_0) {
+            if (a.msum) {
+                MI_LAUNCH((k_fa_mfma<MI_TYPE_Q8_0, 128, true>), grid, dim3(256), 0, s, a);
+            } else {
+                MI_LAUNCH((k_fa_mfma<MI_TYPE_Q8_0, 128, false>), grid, dim3(256), 0, s, a);
+            }
+        } else if (kt == MI_TYPE_BF16) {
             if (a.msum) {
                 MI_LAUNCH((k_fa_mfma<MI_TYPE_BF16, 128, true>), grid, dim3(256), 0, s, a);
             } else {

@@ -24,11 +24,19 @@ and per row eta_r = 3 u (max x - min x) + 2 u (n_kv / 32 + 2): the running-max
 rescales (each exp(m_old - m_new) carries the error above; their arguments add
 up to at most the score range) and the split merge weights.
 e_j: the matrix-core path multiplies V by P split into a high and a low 16-bit
-part while l sums the fp32 p: |e_j| <= 2^-18 p_j for bf16 parts, 2^-22 p_j +
-2^-25 for fp16 parts (the low part may be subnormal). Over a Q8_0 cache the
-decode kernel splits p_j d_v (rounded once) into bf16 parts and multiplies the
-quants: relative to p_j |v_j| that is 2^-18 + 2^-24.
-The accumulation of o and l over n = n_kv (+ 2 n_kv for the two MFMA passes)
+part while l sums the fp32 p. With u_h the unit roundoff of the 16-bit type
+(2^-8 bf16, 2^-11 fp16), |p - hi| <= u_h p, and the low part rounds that
+remainder, which lies at least one binade lower: |e_j| <= 2^-17 p_j for bf16
+parts (reached: p = 1 + 2^-9 + 2^-17 keeps 1 + 2^-9), 2^-22 p_j + 2^-25 for
+fp16 parts (the low part may be subnormal). Over a Q8_0 cache the decode
+kernel splits p_j d_v (rounded once) into bf16 parts and multiplies the
+quants: relative to p_j |v_j| that is 2^-17 + 2^-24. The Q8_0 prefill kernel
+holds V' = q d_v exactly as a bf16 high part V_h and an fp16 low part V_l
+(|V_l| <= 2^-8 |V'|) and forms (P_hi + P_lo) V_h + RN_fp16(p) V_l: relative to
+p_j |v_j|, 2^-17 (1 + 2^-8) + 2^-11 2^-8, plus 2^-25 2^-8 |v_j| for a
+subnormal fp16 p.
+The accumulation of o and l over n = n_kv (+ 2 n_kv for the two MFMA passes,
+3 n_kv for the Q8_0 prefill kernel's three)
 roundings uses the probabilistic bound of Higham and Mary (SIAM J. Sci.
 Comput. 41(5), 2019): with rounding errors independent and mean zero, the
 error of an n-term sum is at most lambda sqrt(n) u sum |terms| with
@@ -57,16 +65,20 @@ def convert_q(q, kt: str):
     return q
 
 
-def fa_bound(q, k, v, mask, scale: float, kt: str, mfma: bool = False):
+def fa_bound(q, k, v, mask, scale: float, kt: str, mfma=False):
     """q (N, Nh, n_q, D) as handed to the kernel; k, v (Nk3, Nkv, n_kv, D) float
     values of the stored K/V; mask (mN, mH, mQ, n_kv) float values or None.
+    mfma: False for the split path, True or "dec" for a matrix-core kernel
+    (over a Q8_0 cache: the decode kernel), "prefill" for the matrix-core
+    prefill kernel (the two differ only over a Q8_0 cache).
     Returns the bound (N, n_q, Nh, D) (NaN where every key is masked)."""
     N, Nh, n_q, D = q.shape
     Nk3, Nkv, n_kv, _ = k.shape
     rk, rk3 = Nh // Nkv, N // Nk3
     qc = convert_q(np.asarray(q, np.float32), kt).astype(np.float64)
     c = D / 32 + 3 if kt == "q8_0" else D
-    n_round = (3 * n_kv if mfma else n_kv) + 64
+    q8_prefill = kt == "q8_0" and mfma == "prefill"
+    n_round = ((4 if q8_prefill else 3) * n_kv if mfma else n_kv) + 64
     out = np.empty((N, n_q, Nh, D))
     for b in range(N):
         for g in range(Nkv):
@@ -101,9 +113,11 @@ def fa_bound(q, k, v, mask, scale: float, kt: str, mfma: bool = False):
             bound = t1 + t3 + 2 * U * np.abs(ref) + 1e-37
             if mfma:
                 if kt == "bf16":
-                    e = p * 2.0 ** -18
+                    e = p * 2.0 ** -17
+                elif q8_prefill:
+                    e = p * (2.0 ** -17 + 2.0 ** -19 + 2.0 ** -24) + np.where(live, 2.0 ** -33, 0.0)
                 elif kt == "q8_0":
-                    e = p * (2.0 ** -18 + U)
+                    e = p * (2.0 ** -17 + U)
                 else:
                     e = p * 2.0 ** -22 + np.where(live, 2.0 ** -25, 0.0)
                 bound = bound + (e @ aV) / L

@@ -72,15 +72,17 @@ def _check(y, ref, bound):
 
 
 def _uses_mfma(kt, D, n_q, Nh, Nkv, n_kv, mask=None):
-    """The launch plan's choice of a matrix-core kernel (flash_attn_plan): F16/BF16
-    K/V at D = 128, with 64 or more query rows per KV head (prefill), or one query
-    position, at most 16 heads per KV head and a mask row shared by every head
-    (decode; Q8_0 K/V too, with 8-byte aligned rows as every cache here has).
-    They keep P (or P times V's block scale) as two 16-bit parts."""
+    """The launch plan's choice of a matrix-core kernel (flash_attn_plan), as
+    fa_bound's mfma argument: F16/BF16/Q8_0 K/V at D = 128 with 64 or more query
+    rows per KV head ("prefill"; Q8_0 rows 4-byte aligned, as every cache here
+    has), or one query position, at most 16 heads per KV head and a mask row
+    shared by every head ("dec"; Q8_0 rows 8-byte aligned). They keep P (or P
+    times V's block scale) as 16-bit parts."""
     if kt not in ("f16", "bf16", "q8_0") or D != 128 or n_kv <= 0:
         return False
-    dec = n_q == 1 and Nh // Nkv <= 16 and (mask is None or mask.shape[1] == 1)
-    return dec or (kt != "q8_0" and n_q * (Nh // Nkv) >= 64)
+    if n_q == 1 and Nh // Nkv <= 16 and (mask is None or mask.shape[1] == 1):
+        return "dec"
+    return "prefill" if n_q * (Nh // Nkv) >= 64 else False
 
 
 def _run(N, Nh, Nkv, n_q, n_kv, D, kt, qt="f32", mask=None, scale=None, seed=0, Nk3=None, kview=None):
@@ -295,13 +297,16 @@ def test_empty_key_range_is_nan(dev):
 
 @pytest.mark.parametrize("kt,qt,rk,masked", [("bf16", "bf16", 2, False), ("bf16", "f32", 2, "window"),
                                               ("f16", "f32", 4, "window"), ("f16", "bf16", 2, False),
-                                              ("bf16", "bf16", 2, "zero"), ("f16", "f32", 4, "one_key")])
+                                              ("bf16", "bf16", 2, "zero"), ("f16", "f32", 4, "one_key"),
+                                              ("q8_0", "f32", 4, "window"), ("q8_0", "bf16", 2, False),
+                                              ("q8_0", "f32", 2, "zero"), ("q8_0", "f32", 4, "one_key")])
 def test_mfma_prefill(dev, kt, qt, rk, masked):
     """The matrix-core path (128 query rows per workgroup, 64-key tiles): 203 query
     positions x rk heads per KV head (a ragged last row block), 333 keys (a ragged last
     tile), 2 batch elements, with no mask, a window mask, an all-zero mask (every
     workgroup takes the loop without mask reads), or a zero mask with one -inf key in
-    one query position (its workgroup reads the mask, the others do not)."""
+    one query position (its workgroup reads the mask, the others do not). Q8_0 K/V take
+    the kernel's int8 score and split-V form."""
     print(f"fa mfma prefill kt={kt} qt={qt} rk={rk} masked={masked}", flush=True)
     n_q, n_kv, nkv = 203, 333, 2
     mask = None
@@ -318,7 +323,7 @@ def test_mfma_prefill(dev, kt, qt, rk, masked):
     _run(2, nkv * rk, nkv, n_q, n_kv, 128, kt, qt, mask=mask, seed=7)
 
 
-@pytest.mark.parametrize("kt,n_kv,masked", [("bf16", 333, True), ("f16", 269, False)])
+@pytest.mark.parametrize("kt,n_kv,masked", [("bf16", 333, True), ("f16", 269, False), ("q8_0", 269, True)])
 def test_mfma_tail_split(dev, kt, n_kv, masked):
     """More 128-row work items than two rounds of resident workgroups fill, with a last
     round at most half full: those last items run as two halves of the key tiles and a
@@ -328,7 +333,7 @@ def test_mfma_tail_split(dev, kt, n_kv, masked):
     # the smallest such shape on this device: the workspace holds the partials of the
     # split items after the mask summary, so it grows past the summary exactly then
     qall = DTensor.empty((2, 16, 64 * 400, 128), "f32")
-    kv = DTensor.empty((2, 8, n_kv, 128), kt)
+    kv = ops.Q8(DTensor.empty((2, 8, n_kv, 136), "u8")) if kt == "q8_0" else DTensor.empty((2, 8, n_kv, 128), kt)
     n_q = None
     for rblk in range(2, 400):
         nq = 64 * rblk - 28  # rows = 2 n_q = 128 rblk - 56: a ragged last row block

@@ -16,8 +16,9 @@ of that stage, at that op's own bar:
                                  QKV buffer, which the fused launch equals) and V
   earlier slots, other sets      unchanged
   attention                      the kernels' derived bound (tests/fa_bound.py):
-                                 the matrix-core kernel over an F16 cache (P in two
-                                 16-bit parts), the split kernel over Q8_0
+                                 the matrix-core prefill kernel (over an F16
+                                 cache P in two 16-bit parts; over Q8_0 exact
+                                 int8 block dots and V held as bf16 + f16 parts)
   O product, gate/up, down       Q8_0 product bound
   residual sums                  bit-exact (clamped to +-65504 with clamp_fp16)
 With clamp_fp16 (qwen3-lm.h:53) the layer clamps V before the cache store
@@ -128,7 +129,7 @@ def test_prefill_layer_stage_by_stage(dev, size, kv_type, clamp):
     kr, vr = kcache[s0:s0 + N, :, :kv_len], vcache[s0:s0 + N, :, :kv_len]
     attn = b["attn"]
     ref = orc.flash_attn_ext(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type)
-    mfma = kv_type == "f16" and S * (Nh // Nkv) >= 64
+    mfma = "prefill" if S * (Nh // Nkv) >= 64 else False
     bound = fa_bound(qf, kr, vr, mask, 1.0 / np.sqrt(D), kv_type, mfma=mfma)
     assert np.all(np.isfinite(attn))
     assert np.all(np.abs(attn - ref) <= bound)
