@@ -1522,6 +1522,27 @@ __device__ __forceinline__ uint4 fa_bld16(fa_rsrc r, uint32_t voff, uint32_t sof
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+#ifndef MI_FA_ITEM_ORDER
+#define MI_FA_ITEM_ORDER 1  // 1: row blocks in descending order across the (sequence, KV head) pairs
+#endif
+// Work item -> (row block, sequence and KV head). Order 1: row blocks in
+// descending order, each over every (sequence, KV head) before the next. Under
+// a causal mask a later row block holds more live key tiles, so the longest
+// items start first and the shortest fill the last round (longest first); with
+// items of equal length the order changes nothing but which run together.
+// Order 0: every row block of one (sequence, KV head) in turn.
+__device__ __forceinline__ void fa_item(const FaArgs & a, uint32_t item, uint32_t & rbk, uint32_t & bg) {
+    if (MI_FA_ITEM_ORDER == 1) {
+        const uint32_t nbg = (uint32_t) (a.nb * a.nkv);
+        const uint32_t i   = item / nbg;
+        rbk                = (uint32_t) a.rblk - 1 - i;
+        bg                 = item - i * nbg;
+    } else {
+        rbk = item % (uint32_t) a.rblk;
+        bg  = item / (uint32_t) a.rblk;
+    }
+}
+
 #ifndef MI_FA_PRIO_PV
 #define MI_FA_PRIO_PV 1  // > 0: the wave's issue priority in its P.V section (MFMAs between the P conversions)
 #endif
@@ -1571,8 +1592,8 @@ k_fa_mfma(const FaArgs a) {
         item             = a.tfull + j / 2;
         part             = 1 + (j & 1);
     }
-    const uint32_t rbk  = item % (uint32_t) a.rblk;
-    const uint32_t bg   = item / (uint32_t) a.rblk;
+    uint32_t       rbk, bg;
+    fa_item(a, item, rbk, bg);
     const uint32_t b    = bg / (uint32_t) a.nkv;
     const uint32_t g    = bg - b * (uint32_t) a.nkv;
     const int      r    = (int) rbk * BQ + wave * 32 + n;
@@ -2188,9 +2209,8 @@ k_fa_mfma(const FaArgs a) {
 __global__ void __launch_bounds__(256) k_fa_mfma_combine(const FaArgs a) {
     const uint32_t row  = blockIdx.x * 8 + threadIdx.x / 32;  // split item * 128 + row of the block
     const uint32_t j    = row / 128, rr = row % 128;
-    const uint32_t item = a.tfull + j;
-    const uint32_t rbk  = item % (uint32_t) a.rblk;
-    const uint32_t bg   = item / (uint32_t) a.rblk;
+    uint32_t       rbk, bg;
+    fa_item(a, a.tfull + j, rbk, bg);
     const int      r    = (int) (rbk * 128 + rr);
     if (r >= a.rows) {
         return;
