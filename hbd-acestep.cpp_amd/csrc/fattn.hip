@@ -1714,9 +1714,9 @@ k_fa_mfma(const FaArgs a) {
 
     // K and V tile loads: chunk c = tid + 256 i -> key c / KC, 16-byte part c % KC
     // (a row is read by KC consecutive threads) and stored row-major in LDS; the
-    // P.V operands are read from V with transposed LDS reads. Buffer loads: a fixed
-    // 32-bit offset per thread plus the tile's uniform offset (the planner keeps
-    // the key range below 4 GB).
+    // P.V operands are read from V with transposed LDS reads. Buffer loads with
+    // the whole 32-bit offset in the per-lane operand, which the range check
+    // covers (the planner keeps the key range below 4 GB).
     constexpr int KR = 256 / KC;  // K rows per load round
     static_assert(KC <= 32 && 256 % KC == 0, "tile chunks");
     uint4          kr[NC], vr[NC];
@@ -1738,7 +1738,6 @@ k_fa_mfma(const FaArgs a) {
         const uint32_t ks0 = (uint32_t) t0 * (uint32_t) a.k1;
         const uint32_t vs0 = (uint32_t) t0 * (uint32_t) a.v1;
         if constexpr (Q8) {
-            // the whole offset in the per-lane operand, which the range check covers
             const uint32_t kb0 = qko + ks0, vb0 = qvo + vs0;
 #pragma unroll
             for (int j = 0; j < 9; ++j) {
@@ -1751,11 +1750,11 @@ k_fa_mfma(const FaArgs a) {
         } else {
 #pragma unroll
             for (int i = 0; i < NC; ++i) {
-                kr[i] = fa_bld16(krs, ko0, ks0 + (uint32_t) (KR * i) * (uint32_t) a.k1);
+                kr[i] = fa_bld16(krs, ko0 + ks0 + (uint32_t) (KR * i) * (uint32_t) a.k1, 0);
             }
 #pragma unroll
             for (int i = 0; i < NC; ++i) {
-                vr[i] = fa_bld16(vrs, vo0, vs0 + (uint32_t) (KR * i) * (uint32_t) a.v1);
+                vr[i] = fa_bld16(vrs, vo0 + vs0 + (uint32_t) (KR * i) * (uint32_t) a.v1, 0);
             }
         }
     };
