@@ -262,6 +262,17 @@ def test_no_mask_and_kv_batch_broadcast(dev):
     _run(4, 8, 8, 3, 100, 128, "q8_0", "f32", mask=None, seed=5, Nk3=2)
 
 
+@pytest.mark.parametrize("kt", ["q8_0", "f16"])
+def test_mfma_kv_batch_broadcast_and_cache_view(dev, kt):
+    """The matrix-core path with K/V shared by pairs of batch elements (rk3 = 2, GQA 4:1,
+    160 rows per KV head), and over views of the first 150 slots of 200-slot caches whose
+    other slots hold different values."""
+    print(f"fa mfma rk3 = 2 / cache view kt={kt}", flush=True)
+    assert _uses_mfma(kt, 128, 40, 8, 2, 150) == "prefill"
+    _run(4, 8, 2, 40, 150, 128, kt, "f32", mask=None, seed=12, Nk3=2)
+    _run(2, 8, 2, 40, 150, 128, kt, "bf16", mask=None, seed=13, kview=200)
+
+
 def test_fully_masked_rows_and_poisoned_masked_keys(dev):
     """Rows with every key masked are NaN; keys masked for every row are never read, so
     NaN bytes there do not reach the output."""
