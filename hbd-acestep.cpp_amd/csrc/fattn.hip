@@ -1796,7 +1796,11 @@ k_fa_mfma(const FaArgs a) {
         if constexpr (Q8) {
             uint32_t qw[8];
             q8_quants(vw, qw);
-            const float dv = (float) __builtin_bit_cast(_Float16, (uint16_t) (vw[0] >> (qodd ? 16 : 0)));
+            // a non-finite scale reads as 0: a key whose mask is -inf for a row enters
+            // the P.V products with p = 0, so the V' of a slot that holds garbage
+            // (never written, past a sequence's length) must be finite
+            const float d0 = (float) __builtin_bit_cast(_Float16, (uint16_t) (vw[0] >> (qodd ? 16 : 0)));
+            const float dv = __builtin_isfinite(d0) ? d0 : 0.0f;
             const float nd = -128.0f * dv;
             uint32_t    hw[16], lw[16];
 #pragma unroll

@@ -262,6 +262,35 @@ def test_no_mask_and_kv_batch_broadcast(dev):
     _run(4, 8, 8, 3, 100, 128, "q8_0", "f32", mask=None, seed=5, Nk3=2)
 
 
+def test_mfma_prefill_q8_poisoned_slots_past_each_length(dev):
+    """Prefill over a Q8_0 cache whose slots past each sequence's length hold NaN
+    scales (unwritten cache rows), inside a tile that also holds live keys and in
+    whole dead tiles: the matrix-core kernel reads a non-finite V scale as 0, so
+    keys masked for a row (p = 0) leave the output finite, as ggml never reads them."""
+    print("fa mfma prefill q8_0 poisoned slots", flush=True)
+    N, Nh, Nkv, n_q, n_kv, D = 2, 8, 2, 40, 200, 128
+    lens = [200, 90]
+    assert _uses_mfma("q8_0", D, n_q, Nh, Nkv, n_kv) == "prefill"
+    r = _rng(23)
+    q = r.standard_normal((N, Nh, n_q, D)).astype(np.float32)
+    k = r.standard_normal((N, Nkv, n_kv, D)).astype(np.float32)
+    v = r.standard_normal((N, Nkv, n_kv, D)).astype(np.float32)
+    m = np.full((N, 1, n_q, n_kv), -np.inf, np.float32)
+    for b, L in enumerate(lens):
+        k[b, :, L:] = np.nan
+        v[b, :, L:] = np.nan
+        for i in range(n_q):
+            m[b, 0, i, :L - n_q + i + 1] = 0.0   # causal: the new tokens are the last n_q of the sequence
+    dk, kf = _kv(k, "q8_0")
+    dv, vf = _kv(v, "q8_0")
+    assert np.isnan(kf[1, :, 90:]).all() and np.isnan(vf[1, :, 90:]).all()
+    dm, mf = _mask_dev(m)
+    y = to_np(ops.flash_attn_ext(to_dev(q), dk, dv, dm, 0.125))
+    ref = orc.flash_attn_ext(q, kf, vf, mf, 0.125, "q8_0")
+    assert np.isfinite(y).all() and np.isfinite(ref).all()
+    _check(y, ref, fa_bound(q, np.nan_to_num(kf), np.nan_to_num(vf), mf, 0.125, "q8_0", "prefill"))
+
+
 @pytest.mark.parametrize("kt", ["q8_0", "f16"])
 def test_mfma_kv_batch_broadcast_and_cache_view(dev, kt):
     """The matrix-core path with K/V shared by pairs of batch elements (rk3 = 2, GQA 4:1,
