@@ -229,8 +229,10 @@ int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi
 
 /* ggml_flash_attn_ext(q, k, v, mask, scale, max_bias, logit_softcap) with
  * GGML_PREC_F32. Replaces the DiT self and cross attention
- * (dit-graph.h:227-231, 348-349) and the batched decode attention over the KV
- * cache (qwen3-lm.h:718-723, 256-bucketed read length at 582-596).
+ * (dit-graph.h:227-231, 348-349), the LM prefill attention over the KV cache
+ * (qwen3-lm.h:414-417; songgen-lelm-gen.h:276-277, F16 or Q8_0 cache) and the
+ * batched decode attention over it (qwen3-lm.h:718-723, 256-bucketed read
+ * length at 582-596; songgen-lelm-gen.h:582-583).
  *   q:    [D, n_q, Nh, N]      F32/BF16/F16
  *   k, v: [D, n_kv, Nkv, Nk3]  both F16, both BF16, both Q8_0 or both F32
  *         (F32 only for D <= 128); Nh % Nkv == 0, N % Nk3 == 0; rows at a
@@ -242,8 +244,13 @@ int mi_timestep_embedding(const mi_tensor * t, int dim, int max_period, const mi
  * D (= ne0 of q, k and v) is 64, 128 or 256. max_bias and logit_softcap must
  * be 0 (the only values the reference passes); others return
  * MI_ERR_UNSUPPORTED. q is converted to K's dot type as ggml-cpu converts it
- * (fp16, bf16, or Q8_0 with the x86 rounding); keys whose mask is -inf are
- * skipped and never read; a row whose keys are all masked is NaN.
+ * (fp16, bf16, or Q8_0 with the x86 rounding); keys whose mask is -inf do not
+ * contribute; a row whose keys are all masked is NaN. The decode and split
+ * kernels never read masked keys; the matrix-core prefill kernel (64 or more
+ * (query, head) rows per KV head, D = 128) reads the K/V rows of keys masked
+ * for only some rows of a 64-key tile and multiplies them by 0, so F16/BF16
+ * rows there must be finite (the reference clears its caches at allocation);
+ * a Q8_0 V block with a non-finite scale counts as 0.
  * workspace: device memory of at least mi_flash_attn_ext_workspace() bytes
  * (for the partial results of a split key range; NULL when that is 0). The
  * size depends on the shapes and on the current device's CU count. */
