@@ -808,6 +808,90 @@ def attention_bench(steps: int):
     device.synchronize()
 
 # ---------------------------------------------------------------------------
+# Each kernel of the steady-state C3 block alone (reported with --kernels): a
+# graph of `steps` back-to-back launches cycling over 4 sets of its operands
+# (every set a fresh allocation, 4 x 147-442 MB, so no launch finds its inputs
+# in the 256 MB Infinity Cache), the same calls and shapes as the block.
+# ---------------------------------------------------------------------------
+def kernels_bench(steps: int):
+    from acestep_ops import device, ops
+    from acestep_ops.device import DTensor, Event, Graph, Stream
+
+    rng = np.random.default_rng(5)
+    NS = 4
+
+    def dev_bf16(shape):
+        return DTensor.from_numpy(bf16_bits(rng.standard_normal(shape, dtype=np.float32)), "bf16")
+
+    def dev_f32(shape, scale=1.0, mean=0.0):
+        return DTensor.from_numpy((rng.standard_normal(shape, dtype=np.float32) * scale + mean).astype(np.float32))
+
+    st = Stream()
+    sh = st.handle
+    adaln = dev_f32((6 * H,), 0.1)
+    shift_sa, scale_sa, gate_sa, shift_ff, scale_ff, gate_ff = (adaln[i * H:(i + 1) * H] for i in range(6))
+    sa_w, ff_w = dev_f32((H,), 0.1, 1.0), dev_f32((H,), 0.1, 1.0)
+    q_w, k_w = dev_f32((D,), 0.1, 1.0), dev_f32((D,), 0.1, 1.0)
+    pos = DTensor.from_numpy(np.tile(np.arange(T_FRAMES, dtype=np.int32), BATCH))
+    kb = block_bytes(ROWS, cross=True)
+
+    def qk_set():
+        qkv = dev_bf16((ROWS, (NH + 2 * NKV) * D))
+        q = qkv[:, :NH * D].unflatten(1, (NH, D))
+        k = qkv[:, NH * D:(NH + NKV) * D].unflatten(1, (NKV, D))
+        qo, ko = DTensor.empty((ROWS, NH, D), "bf16"), DTensor.empty((ROWS, NKV, D), "bf16")
+        return (qkv, qo, ko), lambda: ops.qk_norm_rope(q, q_w, pos, EPS, D, THETA, k=k, k_w=k_w, q_out=qo,
+                                                        k_out=ko, stream=sh)
+
+    def ffn_norm_set():
+        h, sa = dev_bf16((BATCH, T_FRAMES, H)), dev_bf16((BATCH, T_FRAMES, H))
+        h1, nf = DTensor.empty((BATCH, T_FRAMES, H), "bf16"), DTensor.empty((BATCH, T_FRAMES, H), "bf16")
+        return (h, sa, h1, nf), lambda: ops.add_rms_norm(h, sa, EPS, gate=gate_sa, w=ff_w, scale=scale_ff,
+                                                         shift=shift_ff, out_sum=h1, out_norm=nf, stream=sh)
+
+    def swiglu_set():
+        gu = dev_bf16((BATCH, T_FRAMES, 2 * I_FF))
+        ff = DTensor.empty((BATCH, T_FRAMES, I_FF), "bf16")
+        return (gu, ff), lambda: ops.swiglu(gu, out=ff, stream=sh)
+
+    def sa_norm_set():
+        h1, fo = dev_bf16((BATCH, T_FRAMES, H)), dev_bf16((BATCH, T_FRAMES, H))
+        hn, ns = DTensor.empty((BATCH, T_FRAMES, H), "bf16"), DTensor.empty((BATCH, T_FRAMES, H), "bf16")
+        return (h1, fo, hn, ns), lambda: ops.add_rms_norm(h1, fo, EPS, gate=gate_ff, w=sa_w, scale=scale_sa,
+                                                          shift=shift_sa, out_sum=hn, out_norm=ns, stream=sh)
+
+    for name, make in (("qk_norm_rope", qk_set), ("add_rms_norm_modulate_ffn", ffn_norm_set),
+                       ("swiglu", swiglu_set), ("gated_add_ffn_rms_norm_modulate_sa", sa_norm_set)):
+        sets = [make() for _ in range(NS)]
+        calls = [c for _, c in sets]
+        for c in calls:
+            c()
+        st.synchronize()
+        g = Graph()
+        with g.capture(st):
+            for i in range(steps):
+                calls[i % NS]()
+        g.launch()
+        st.synchronize()
+        res = []
+        for _ in range(3):
+            a, b_ = Event(), Event()
+            a.record(sh)
+            g.launch()
+            b_.record(sh)
+            b_.synchronize()
+            res.append(1000.0 * a.elapsed_ms(b_) / steps)
+        us = min(res)
+        gbs = kb[name] / (us * 1e-6) / 1e9
+        print(json.dumps({"config": f"C3 DiT block kernel alone: {name}, {steps} back-to-back launches in a graph over "
+                                    f"{NS} operand sets", "us_per_launch": round(us, 2),
+                          "us_per_launch_3_replays": [round(x, 2) for x in res], "bytes_per_launch": kb[name],
+                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}), flush=True)
+        del g, sets, calls
+        device.synchronize()
+
+
+# ---------------------------------------------------------------------------
 # Q8_0 matrix-vector products (reported with --gemv): ggml_mul_mat with Q8_0
 # weights at the Qwen3-4B batch-8 decode shape (qwen3-lm.h:639-651, 729, 737,
 # 755): the fused QKV, O, fused gate/up and down projections of one layer, and
@@ -1056,6 +1140,8 @@ def main():
                     help="time the Qwen3 layer op chains at the C1/C2/C4/C5 shapes instead (one JSON line each)")
     ap.add_argument("--attention", action="store_true",
                     help="time flash attention over the KV cache at the C2 decode shape (one JSON line per cache type)")
+    ap.add_argument("--kernels", action="store_true",
+                    help="each C3 block kernel alone, back to back over rotated operand sets")
     ap.add_argument("--decode-layer", action="store_true",
                     help="time one whole Qwen3-4B decoder layer at batch 8 (Q8_0 weights; F16 and Q8_0 KV caches), all on the device")
     ap.add_argument("--prefill-layer", action="store_true",
@@ -1087,6 +1173,9 @@ def main():
         return
     if args.gemv:
         gemv_bench(args.steps)
+        return
+    if args.kernels:
+        kernels_bench(args.steps)
         return
     if args.decode_layer:
         decode_layer_bench(args.steps)
