@@ -753,6 +753,43 @@ def attention_bench(steps: int):
         del qd, kd, qkv, qv, kv, vv, yd, zmask, wmask, wsd
         device.synchronize()
 
+    # DiT cross attention (dit-graph.h:296-351): q from the S=3000 latent rows of
+    # each CFG element, K/V from the condition encoder's enc_S rows (F16 casts),
+    # 16/8 heads x 128, the F16 mask [enc_S, S] blocking the encoder's padding
+    # (the last 40 positions here); flops count the live (query, key) pairs
+    S, ENC = 3000, 512
+    qc = DTensor.from_numpy(rng.standard_normal((NB, S, NHD, Dh), dtype=np.float32))
+    qcv = qc.permute(0, 2, 1, 3)
+    kc_ = DTensor.from_numpy(rng.standard_normal((NB, NKVD, ENC, Dh), dtype=np.float32).astype(np.float16).view(
+        np.uint16), "f16")
+    vc_ = DTensor.from_numpy(rng.standard_normal((NB, NKVD, ENC, Dh), dtype=np.float32).astype(np.float16).view(
+        np.uint16), "f16")
+    pm = np.zeros((NB, 1, S, ENC), np.float16)
+    pm[..., ENC - 40:] = -np.inf
+    pmask = DTensor.from_numpy(pm.view(np.uint16), "f16")
+    yc = DTensor.empty((NB, S, NHD, Dh), "f32")
+    wsc = DTensor.empty((max(ops.flash_attn_workspace(qcv, kc_, vc_), 1),), "u8")
+    call = lambda: ops.flash_attn_ext(qcv, kc_, vc_, pmask, 1.0 / float(np.sqrt(Dh)), out=yc,  # noqa
+                                      workspace=wsc, stream=sh)
+    for _ in range(10):
+        call()
+    st.synchronize()
+    ev = [Event() for _ in range(steps + 1)]
+    ev[0].record(sh)
+    for i in range(steps):
+        call()
+        ev[i + 1].record(sh)
+    st.synchronize()
+    us = 1000.0 * ev[0].elapsed_ms(ev[steps]) / steps
+    lf = 4.0 * NB * NHD * S * (ENC - 40) * Dh
+    print(json.dumps({"config": f"DiT cross attention, F32 q view S={S} x {NB}, {NHD}/{NKVD} heads x {Dh}, F16 K/V of "
+                                f"{ENC} encoder rows, F16 padding mask (last 40 masked)",
+                      "us_per_call": round(us, 2), "live_flop_per_call": lf,
+                      "TFLOP/s": round(lf / (us * 1e-6) / 1e12, 1),
+                      "frac_of_bf16_dense": round(lf / (us * 1e-6) / 1e12 / 2500.0, 3)}), flush=True)
+    del qc, qcv, kc_, vc_, pmask, yc, wsc
+    device.synchronize()
+
     # LM prefill attention over the KV cache (qw3lm_forward, qwen3-lm.h:429-549;
     # the songgen LM reads an F16 or a Q8_0 cache, songgen-lelm-gen.h:50-61):
     # Qwen3-4B 32/8 heads x 128, 8 sequences x 2048 new tokens from slot 0 of
