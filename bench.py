@@ -1107,16 +1107,19 @@ def decode_layer_bench_kv(steps: int, kv_type: str):
 # (qw3lm_forward, qwen3-lm.h:429-549). One JSON line per cache type.
 # ---------------------------------------------------------------------------
 def prefill_layer_bench(steps: int):
-    for kv_type in ("f16", "q8_0"):
-        prefill_layer_bench_kv(steps, kv_type)
+    # the CFG pair of a 512-token prompt, and the batched prefill of 8 sequences
+    # x 2048 tokens (the Qwen3-4B batch-8 prefill into a KV cache)
+    for n, s_, slots in ((2, 512, 4096), (8, 2048, 8192)):
+        for kv_type in ("f16", "q8_0"):
+            prefill_layer_bench_kv(steps, kv_type, n, s_, slots)
 
 
-def prefill_layer_bench_kv(steps: int, kv_type: str):
+def prefill_layer_bench_kv(steps: int, kv_type: str, N: int = 2, S: int = 512, SLOTS: int = 4096):
     from acestep_ops import device, ops
     from acestep_ops.device import DTensor, Event, Graph, Stream
     from acestep_ops.qwen3 import Qwen3Layer
 
-    H, Nh, Nkv, D, I, N, S, SLOTS = 2560, 32, 8, 128, 9728, 2, 512, 4096
+    H, Nh, Nkv, D, I = 2560, 32, 8, 128, 9728
     rng = np.random.default_rng(17)
     st = Stream()
     sh = st.handle
@@ -1151,8 +1154,8 @@ def prefill_layer_bench_kv(steps: int, kv_type: str):
     T = N * S
     gemm = 2 * T * sum(w.n * w.k for w in layer.w.values())
     attn = 4 * D * Nh * N * (S * (S + 1) // 2)  # the causal pairs (masked tiles are skipped)
-    print(json.dumps({"config": f"Qwen3-4B prefill layer, {N} sequences (CFG sets) x {S} tokens from slot 0, Q8_0 "
-                                f"weights, {kv_type.upper()} KV cache, every op on the device",
+    print(json.dumps({"config": f"Qwen3-4B prefill layer, {N} sequences x {S} tokens from slot 0 of {SLOTS}-slot "
+                                f"caches, Q8_0 weights, {kv_type.upper()} KV cache, every op on the device",
                       "us_per_layer": round(us, 1), "gemm_flop": gemm, "attn_flop_causal": attn,
                       "TFLOP/s": round((gemm + attn) / (us * 1e-6) / 1e12, 1),
                       "tokens_per_s_36_layers": round(T / (36 * us * 1e-6), 1)}), flush=True)

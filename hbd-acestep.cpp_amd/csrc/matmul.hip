@@ -229,6 +229,115 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
     }
 }
 
+// The same prologue for longer x (prefill): a workgroup per 8 consecutive rows.
+// Lane (row r0 + l / 8, part l % 8) of wave w holds 4 elements of each of its
+// row's blocks w, w + 4, ... in registers, all loaded at once: their float
+// squares summed in double, over the row's 8 lanes and over the 4 waves (LDS),
+// give the row's scale; the same registers are then scaled, multiplied by w,
+// quantized and stored, so that each store instruction writes the 8 rows'
+// quants of one block as one 256-byte run of the block-major layout (one
+// workgroup per row wrote 32-byte pieces 32 * mp bytes apart). With an addend
+// the residual sum is formed once and written in the first pass (ADD: a.ab is
+// given, so that the plain prologue holds no registers for it). Rows of x are
+// at most 4 * NBW blocks.
+template <int NBW, bool ADD>
+__global__ void __launch_bounds__(256) k_mmv_quant_x_norm8(const MmvArgs a) {
+    __shared__ double red[4][8];
+    __shared__ float  scl[8];
+    const int      tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t row = blockIdx.x * 8u + (uint32_t) (lane >> 3), sub = (uint32_t) lane & 7u;
+    const bool     rv  = row < a.m;  // uniform over a row's 8 lanes
+    const uint32_t rc  = rv ? row : a.m - 1;
+    const char *   xr  = a.x + (int64_t) rc * a.x1;
+    const char *   br  = ADD ? a.ab + (int64_t) rc * a.ab1 : nullptr;
+    auto           ld4 = [&](const char * p, float (&v)[4]) {
+        if (a.xvec) {
+            const float4 q = *(const float4 *) p;
+            v[0]           = q.x;
+            v[1]           = q.y;
+            v[2]           = q.z;
+            v[3]           = q.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = ((const float *) p)[e];
+            }
+        }
+    };
+    // every load unconditional (blocks past the row clamped to its last one), so
+    // all are in flight before the first is used
+    float v[NBW][4], u[ADD ? NBW : 1][4];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const uint32_t b  = (uint32_t) wv + 4u * (uint32_t) j;
+        const uint32_t bc = b < a.nbk ? b : a.nbk - 1;
+        ld4(xr + (size_t) (bc * 32u + sub * 4u) * 4, v[j]);
+        if constexpr (ADD) {
+            ld4(br + (size_t) (bc * 32u + sub * 4u) * 4, u[j]);
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const uint32_t b = (uint32_t) wv + 4u * (uint32_t) j;
+        if (b < a.nbk && rv) {
+            if constexpr (ADD) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[j][e] = v[j][e] + u[j][e];
+                }
+                if (a.sum) {
+                    *(float4 *) ((float *) (a.sum + (int64_t) row * a.sum1) + b * 32u + sub * 4u) =
+                        make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                ss += (double) (v[j][e] * v[j][e]);
+            }
+        }
+    }
+    ss = group_sum<8>(ss);
+    if (sub == 0) {
+        red[wv][lane >> 3] = ss;
+    }
+    __syncthreads();
+    if (tid < 8) {
+        scl[tid] = rms_scale(red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid], (int) a.k, a.eps);
+    }
+    __syncthreads();
+    const float scale = scl[lane >> 3];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const uint32_t b = (uint32_t) wv + 4u * (uint32_t) j;
+        if (b >= a.nbk) {
+            break;  // uniform over the wave
+        }
+        const uint32_t i0 = b * 32u + sub * 4u;
+        float          f[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            f[e] = (v[j][e] * scale) * a.nw[i0 + e];
+        }
+        float amax = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
+        amax       = group_max<8>(amax);
+        const float d  = mm_div127(amax);
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        uint32_t    wq = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(f[e] * id), -128.0f, 127.0f);
+            wq |= ((uint32_t) (int32_t) q & 0xffu) << (8 * e);
+        }
+        if (rv) {
+            *(uint32_t *) (a.xq + ((int64_t) b * a.mp + row) * 32 + sub * 4) = wq;
+            if (sub == 0) {
+                a.xd[(int64_t) b * a.mp + row] = (float) __builtin_bit_cast(_Float16, f32_to_f16_bits(d));
+            }
+        }
+    }
+}
+
 #ifndef MI_MMV_UNROLL
 #define MI_MMV_UNROLL 4  // blocks whose weight loads are issued together
 #endif
@@ -709,11 +818,35 @@ int launch_q8_0_repack(const char * src, int64_t nb1, uint32_t k, uint32_t n, ch
     return MI_OK;
 }
 
+#ifndef MI_QXN8_MIN_ROWS
+#define MI_QXN8_MIN_ROWS 4096  // rows of x from which the norm prologue takes 8 rows per workgroup
+#endif
+template <bool ADD>
+static void launch_quant_x_norm8(const MmvArgs & a, hipStream_t s) {
+    const dim3 grid((a.m + 7) / 8);
+    if (a.nbk <= 4 * 8) {
+        MI_LAUNCH((k_mmv_quant_x_norm8<8, ADD>), grid, dim3(256), 0, s, a);
+    } else if (a.nbk <= 4 * 16) {
+        MI_LAUNCH((k_mmv_quant_x_norm8<16, ADD>), grid, dim3(256), 0, s, a);
+    } else if (a.nbk <= 4 * 24) {
+        MI_LAUNCH((k_mmv_quant_x_norm8<24, ADD>), grid, dim3(256), 0, s, a);
+    } else {
+        MI_LAUNCH((k_mmv_quant_x_norm8<32, ADD>), grid, dim3(256), 0, s, a);
+    }
+}
+
 int launch_mul_mat_q8_0(const MmvArgs & a, hipStream_t s) {
     if (a.n == 0 || a.m == 0) {
         return MI_OK;
     }
-    if (a.nw) {
+    if (a.nw && a.m >= (uint32_t) MI_QXN8_MIN_ROWS && a.nbk <= 4 * 32) {
+        // long x: 8 rows per workgroup, x held in registers (4 * NBW blocks per row at most)
+        if (a.ab) {
+            launch_quant_x_norm8<true>(a, s);
+        } else {
+            launch_quant_x_norm8<false>(a, s);
+        }
+    } else if (a.nw) {
         MI_LAUNCH(k_mmv_quant_x_norm, dim3(a.m), dim3(256), 0, s, a);
     } else {
         const uint64_t threads = ((uint64_t) a.m * a.nbk + MI_QX_U - 1) / MI_QX_U * 8;

@@ -204,12 +204,14 @@ def test_swiglu_prologue_strided_rows(dev):
 
 
 @pytest.mark.parametrize("n,k,m,view", [(6144, 2560, 8, False), (300, 256, 3, True), (640, 256, 129, False),
-                                        (100, 96, 1000, True)])
+                                        (100, 96, 1000, True), (64, 2560, 4100, False), (64, 4096, 4099, True),
+                                        (96, 1536, 4096, False)])
 def test_rms_norm_prologue_matches_norm_then_mul_mat(dev, n, k, m, view):
     """mi_mul_mat_q8_0_rms_norm (RMSNorm*w computed inside the quantization of x)
     against mi_rms_norm followed by mi_mul_mat_q8_0: bit-identical, for the decode and
-    matrix kernels, with 16-byte aligned rows or rows 4 bytes off (element loads);
-    rows of very different scales. Then the product against the oracle on the
+    matrix kernels, with a workgroup per row and (4096 rows or more) per 8 rows, a
+    ragged last group among them, with 16-byte aligned rows or rows 4 bytes off
+    (element loads); rows of very different scales. Then the product against the oracle on the
     normalized rows the device produced."""
     print(f"mul_mat q8_0 rms_norm n={n} k={k} m={m} view={view}", flush=True)
     r = np.random.default_rng(n + k + m + 1)
@@ -227,7 +229,8 @@ def test_rms_norm_prologue_matches_norm_then_mul_mat(dev, n, k, m, view):
     _check(y_f, w, to_np(norm))
 
 
-@pytest.mark.parametrize("n,k,m", [(19456, 2560, 8), (300, 256, 3), (640, 256, 129)])
+@pytest.mark.parametrize("n,k,m", [(19456, 2560, 8), (300, 256, 3), (640, 256, 129), (64, 2560, 4103),
+                                   (64, 4096, 4096), (64, 256, 4104)])
 def test_add_rms_norm_prologue_matches_add_norm_then_mul_mat(dev, n, k, m):
     """mi_mul_mat_q8_0_add_rms_norm (sum = a + b written, RMSNorm*w of it made inside
     the quantization of x) against mi_add_rms_norm followed by mi_mul_mat_q8_0: the
