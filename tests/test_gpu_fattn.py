@@ -440,3 +440,40 @@ def test_dit_self_attention_full_size(dev, S, win, real):
     _check(y[:, qs], ref, bound)
     if real < S:
         assert np.isnan(y[:, real:]).all() and np.isfinite(y[:, :real]).all()
+
+
+@pytest.mark.parametrize("kt", ["q8_0", "f16"])
+def test_lm_prefill_attention_full_size(dev, kt):
+    """The LM's prefill attention over its KV cache at the Qwen3-4B batched-prefill
+    size (qwen3-lm.h:414-417; songgen-lelm-gen.h:276-277): 2 sequences x 2048 new
+    tokens from slot 0, 32/8 heads x 128, F32 q as the permuted rope output, K/V
+    as views of the first 2048 slots of 4096-slot caches (Q8_0 or F16), the
+    causal F16 mask. The whole call runs on the device (4096 work items of the
+    matrix-core kernel, longest first); 36 query positions (both ends, tile and
+    row-block edges) x both sequences x all 32 heads are checked against the
+    oracle under the kernel's bound."""
+    print(f"fa lm prefill full size kt={kt}", flush=True)
+    N, Nh, Nkv, D, S, SLOTS = 2, 32, 8, 128, 2048, 4096
+    r = _rng(71)
+    q = r.standard_normal((N, S, Nh, D), dtype=np.float32)
+    k = r.standard_normal((N, Nkv, SLOTS, D), dtype=np.float32)
+    v = r.standard_normal((N, Nkv, SLOTS, D), dtype=np.float32)
+    dkf, kf = _kv(k, kt)
+    dvf, vf = _kv(v, kt)
+    sl = (slice(None), slice(None), slice(0, S))
+    dk = ops.Q8(dkf.data[sl]) if kt == "q8_0" else dkf[sl]
+    dv = ops.Q8(dvf.data[sl]) if kt == "q8_0" else dvf[sl]
+    kf, vf = kf[:, :, :S], vf[:, :, :S]
+    i = np.arange(S)
+    m = np.broadcast_to(np.where(i[None, :] <= i[:, None], 0.0, -np.inf).astype(np.float32), (N, 1, S, S))
+    dm, mf = _mask_dev(np.ascontiguousarray(m))
+    dq = to_dev(q).permute(0, 2, 1, 3)                            # (N, Nh, S, D) view
+    y = to_np(ops.flash_attn_ext(dq, dk, dv, dm, 1.0 / np.sqrt(D)))  # (N, S, Nh, D)
+    assert _uses_mfma(kt, D, S, Nh, Nkv, S, mf) == "prefill"
+    qs = np.unique(np.r_[0, 1, 31, 32, 63, 64, 65, 127, 128, 129, 511, 512, 1023, 1024, 1500, 2015, 2016, 2046, 2047,
+                         r.integers(0, S, 17)])
+    qf = np.ascontiguousarray(q[:, qs].transpose(0, 2, 1, 3))     # (N, Nh, len(qs), D)
+    ms = np.ascontiguousarray(mf[:, :, qs])
+    ref = orc.flash_attn_ext(qf, kf, vf, ms, 1.0 / np.sqrt(D), kt)
+    _check(y[:, qs], ref, fa_bound(qf, kf, vf, ms, 1.0 / np.sqrt(D), kt, "prefill"))
+    assert np.isfinite(y).all()
