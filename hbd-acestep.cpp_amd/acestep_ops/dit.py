@@ -1,0 +1,158 @@
+"""One ACE-Step DiT layer, every op on the device, with Q8_0 weights and F32
+activations (dit_ggml_build_layer, dit-graph.h:367-448, with the self-attention
+of dit_ggml_build_self_attn, 136-245, the cross attention of
+dit_ggml_build_cross_attn, 274-354, and the MLP of dit_ggml_build_mlp, 249-268):
+
+  norm_sa  = modulate(rms_norm(hidden) * sa_norm, scale_sa, shift_sa)  (404-405)
+  qkv      = mul_mat(W_sa_qkv, norm_sa); q, k, v = views of qkv       (159-163)
+  q, k     = rope(rms_norm(q|k) * q_norm|k_norm), positions 0..S-1     (181-198)
+  k, v     = F16 casts                                                 (221-228)
+  attn     = flash_attn_ext(q, k, v, sa_mask, 1/sqrt(D)), F32 precision (230-234)
+  hidden   = hidden + mul_mat(W_sa_o, attn) * gate_sa                  (243, 415)
+  cross attention (with encoder states enc):
+    norm_ca = rms_norm(hidden) * ca_norm                               (424)
+    q       = mul_mat(W_ca_q, norm_ca); k, v = views of mul_mat(W_ca_kv, enc)  (302-307)
+    q, k    = rms_norm(q|k) * ca_q_norm|ca_k_norm (no rope)           (326-330)
+    attn    = flash_attn_ext(q, F16 k, F16 v, ca_mask, 1/sqrt(D))     (334-348)
+    hidden  = hidden + mul_mat(W_ca_o, attn)                          (353, 427)
+  norm_ffn = modulate(rms_norm(hidden) * mlp_norm, scale_ffn, shift_ffn)  (437-438)
+  hidden   = hidden + mul_mat(W_down, swiglu(mul_mat(W_gate_up, norm_ffn))) * gate_ffn  (439-440)
+
+Each gated (or plain) residual add runs in one launch with the norm after it
+(mi_add_rms_norm), and the SwiGLU inside the quantization of the down
+product's x (mi_mul_mat_q8_0_swiglu). The six AdaLN vectors come in as one F32
+(6, H) tensor: scale_shift_table + the timestep projection (dit-graph.h:384-399),
+rows shift_sa, scale_sa, gate_sa, shift_ffn, scale_ffn, gate_ffn.
+
+Shapes outermost first: hidden (N, S, H) F32; enc (N, enc_S, H) F32; sa_mask
+(N, 1, S, S) F16 or None; ca_mask (N, 1, S, enc_S) F16 or None."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import ops
+from .device import DTensor
+
+
+class DiTLayer:
+    def __init__(self, w_sa_qkv, w_sa_o, w_gate_up, w_down, sa_norm_w, mlp_norm_w, sa_q_norm_w, sa_k_norm_w,
+                 H: int, Nh: int, Nkv: int, D: int, I: int, eps: float = 1e-6, rope_theta: float = 1e6,
+                 w_ca_q=None, w_ca_kv=None, w_ca_o=None, ca_norm_w=None, ca_q_norm_w=None, ca_k_norm_w=None,
+                 stream=None):
+        """w_*: Q8 weights in the GGUF layout (repacked here once); norms: F32 DTensors.
+        The cross-attention weights are all given or all None."""
+        self.H, self.Nh, self.Nkv, self.D, self.I = H, Nh, Nkv, D, I
+        self.eps, self.theta, self.stream = eps, rope_theta, stream
+        ws = {"sa_qkv": w_sa_qkv, "sa_o": w_sa_o, "gu": w_gate_up, "down": w_down}
+        ca = (w_ca_q, w_ca_kv, w_ca_o, ca_norm_w, ca_q_norm_w, ca_k_norm_w)
+        if any(x is not None for x in ca) and any(x is None for x in ca):
+            raise ValueError("cross attention: give every weight or none")
+        self.cross = w_ca_q is not None
+        if self.cross:
+            ws.update({"ca_q": w_ca_q, "ca_kv": w_ca_kv, "ca_o": w_ca_o})
+        self.w = {name: ops.q8_0_repack(w, stream=stream) for name, w in ws.items()}
+        self.sa_norm_w, self.mlp_norm_w = sa_norm_w, mlp_norm_w
+        self.sa_q_norm_w, self.sa_k_norm_w = sa_q_norm_w, sa_k_norm_w
+        self.ca_norm_w, self.ca_q_norm_w, self.ca_k_norm_w = ca_norm_w, ca_q_norm_w, ca_k_norm_w
+        self._bufs = {}
+
+    def _buf(self, name, shape, dtype="f32"):
+        b = self._bufs.get(name)
+        if b is None or b.shape != tuple(shape):
+            b = DTensor.empty(tuple(shape), dtype)
+            self._bufs[name] = b
+        return b
+
+    def _ws(self, name, x):
+        need = ops.mul_mat_q8_0_workspace(self.w[name], x)
+        return self._buf("ws_" + name, (max(need, 1),), "u8")
+
+    def _fa(self, name, q, k, v, mask, out):
+        need = ops.flash_attn_workspace(q, k, v)
+        ws = self._buf("ws_fa_" + name, (max(need, 1),), "u8")
+        return ops.flash_attn_ext(q, k, v, mask, 1.0 / math.sqrt(self.D), out=out, workspace=ws, stream=self.stream)
+
+    @staticmethod
+    def positions(N: int, S: int) -> DTensor:
+        """The rope positions: 0..S-1 for each of the N sequences (dit-graph.h:186-195)."""
+        return DTensor.from_numpy(np.tile(np.arange(S, dtype=np.int32), N))
+
+    def forward(self, hidden, adaln, pos, sa_mask=None, enc=None, ca_mask=None, out=None):
+        """hidden (N, S, H) F32 -> new hidden (N, S, H); adaln (6, H) F32; pos from
+        positions(N, S); enc (N, enc_S, H) F32 when the layer has cross attention."""
+        N, S, H = hidden.shape
+        Nh, Nkv, D, I = self.Nh, self.Nkv, self.D, self.I
+        st = self.stream
+        if self.cross != (enc is not None):
+            raise ValueError("enc is given exactly when the layer has cross-attention weights")
+        T = N * S
+        h2 = hidden.view(T, H)
+        shift_sa, scale_sa, gate_sa, shift_ffn, scale_ffn, gate_ffn = (adaln[i] for i in range(6))
+
+        # self attention
+        norm_sa = ops.rms_norm_modulate(h2, self.sa_norm_w, scale_sa, shift_sa, self.eps,
+                                        out=self._buf("norm_sa", (T, H)), stream=st)
+        qkv_dim = (Nh + 2 * Nkv) * D
+        qkv = ops.mul_mat_q8_0(self.w["sa_qkv"], norm_sa, out=self._buf("qkv", (T, qkv_dim)),
+                               workspace=self._ws("sa_qkv", norm_sa), stream=st)
+        q = qkv[:, 0:Nh * D].unflatten(1, (Nh, D))
+        k = qkv[:, Nh * D:(Nh + Nkv) * D].unflatten(1, (Nkv, D))
+        v = qkv[:, (Nh + Nkv) * D:qkv_dim].unflatten(1, (Nkv, D))
+        qo, ko = ops.qk_norm_rope(q, self.sa_q_norm_w, pos, self.eps, D, self.theta, k=k, k_w=self.sa_k_norm_w,
+                                  q_out=self._buf("qo", (T, Nh, D)), k_out=self._buf("ko", (T, Nkv, D)), stream=st)
+        k16 = ops.cpy(ko, self._buf("k16", (T, Nkv, D), "f16"), stream=st)
+        v16 = ops.cpy(v, self._buf("v16", (T, Nkv, D), "f16"), stream=st)
+        # (N, heads, S, D) views, ggml's permute(x, 0, 2, 1, 3) (dit-graph.h:206-208)
+        attn = self._fa("sa", qo.view(N, S, Nh, D).permute(0, 2, 1, 3), k16.view(N, S, Nkv, D).permute(0, 2, 1, 3),
+                        v16.view(N, S, Nkv, D).permute(0, 2, 1, 3), sa_mask, self._buf("attn", (N, S, Nh, D)))
+        sa_out = ops.mul_mat_q8_0(self.w["sa_o"], attn.view(T, Nh * D), out=self._buf("sa_out", (T, H)),
+                                  workspace=self._ws("sa_o", attn.view(T, Nh * D)), stream=st)
+        if self.cross:
+            # the gated residual and the cross-attention norm in one launch
+            h1, norm_ca = ops.add_rms_norm(h2, sa_out, self.eps, gate=gate_sa, w=self.ca_norm_w,
+                                           out_sum=self._buf("h1", (T, H)), out_norm=self._buf("norm_ca", (T, H)),
+                                           stream=st)
+            ca_out = self._cross(norm_ca, enc, ca_mask, N, S)
+            # the cross-attention residual and the FFN norm -> modulate in one launch
+            h2b, norm_ffn = ops.add_rms_norm(h1, ca_out, self.eps, w=self.mlp_norm_w, scale=scale_ffn,
+                                             shift=shift_ffn, out_sum=self._buf("h2", (T, H)),
+                                             out_norm=self._buf("norm_ffn", (T, H)), stream=st)
+        else:
+            # the gated residual and the FFN norm -> modulate in one launch
+            h2b, norm_ffn = ops.add_rms_norm(h2, sa_out, self.eps, gate=gate_sa, w=self.mlp_norm_w, scale=scale_ffn,
+                                             shift=shift_ffn, out_sum=self._buf("h2", (T, H)),
+                                             out_norm=self._buf("norm_ffn", (T, H)), stream=st)
+        # the MLP: gate/up, then SwiGLU inside the down product's quantization
+        gu = ops.mul_mat_q8_0(self.w["gu"], norm_ffn, out=self._buf("gu", (T, 2 * I)),
+                              workspace=self._ws("gu", norm_ffn), stream=st)
+        need = ops.mul_mat_q8_0_swiglu_workspace(self.w["down"], gu)
+        ffn = ops.mul_mat_q8_0_swiglu(self.w["down"], gu, out=self._buf("ffn", (T, H)),
+                                      workspace=self._buf("ws_down", (max(need, 1),), "u8"), stream=st)
+        y = out.view(T, H) if out is not None else self._buf("out", (T, H))
+        ops.gated_add(h2b, ffn, gate_ffn, out=y, stream=st)
+        return y.view(N, S, H)
+
+    def _cross(self, norm_ca, enc, ca_mask, N: int, S: int):
+        """Cross attention of the layer's rows over the encoder states: its O product (T, H)."""
+        Nh, Nkv, D, H = self.Nh, self.Nkv, self.D, self.H
+        st = self.stream
+        T = N * S
+        E = enc.shape[1]
+        e2 = enc.view(N * E, H)
+        qc = ops.mul_mat_q8_0(self.w["ca_q"], norm_ca, out=self._buf("ca_q", (T, Nh * D)),
+                              workspace=self._ws("ca_q", norm_ca), stream=st)
+        kvc = ops.mul_mat_q8_0(self.w["ca_kv"], e2, out=self._buf("ca_kv", (N * E, 2 * Nkv * D)),
+                               workspace=self._ws("ca_kv", e2), stream=st)
+        qn = ops.rms_norm(qc.unflatten(1, (Nh, D)), self.eps, w=self.ca_q_norm_w,
+                          out=self._buf("ca_qn", (T, Nh, D)), stream=st)
+        kn = ops.rms_norm(kvc[:, 0:Nkv * D].unflatten(1, (Nkv, D)), self.eps, w=self.ca_k_norm_w,
+                          out=self._buf("ca_kn", (N * E, Nkv, D)), stream=st)
+        k16 = ops.cpy(kn, self._buf("ca_k16", (N * E, Nkv, D), "f16"), stream=st)
+        v16 = ops.cpy(kvc[:, Nkv * D:2 * Nkv * D].unflatten(1, (Nkv, D)), self._buf("ca_v16", (N * E, Nkv, D), "f16"),
+                      stream=st)
+        attn = self._fa("ca", qn.view(N, S, Nh, D).permute(0, 2, 1, 3), k16.view(N, E, Nkv, D).permute(0, 2, 1, 3),
+                        v16.view(N, E, Nkv, D).permute(0, 2, 1, 3), ca_mask, self._buf("ca_attn", (N, S, Nh, D)))
+        return ops.mul_mat_q8_0(self.w["ca_o"], attn.view(T, Nh * D), out=self._buf("ca_out", (T, H)),
+                                workspace=self._ws("ca_o", attn.view(T, Nh * D)), stream=st)

@@ -1,0 +1,152 @@
+"""A whole ACE-Step DiT layer on the device (acestep_ops.dit.DiTLayer: AdaLN
+norm -> modulate, Q8_0 QKV product, QK-norm + rope, F16 casts, flash attention
+under the sliding-window or padding mask, O product, gated residual fused with
+the next norm, the cross attention over encoder states, the MLP with the
+SwiGLU inside the down product, the last gated residual) against the oracle,
+stage by stage (dit_ggml_build_layer, dit-graph.h:367-448), at a small size and
+at the DiT's layer shape (H 2048, 16/8 heads x 128, I 6144).
+
+Every stage is checked against the oracle applied to the device's own inputs
+of that stage, at that op's own bar:
+  norm -> modulate, QK-norm -> rope, the cross-attention norms   1e-5 (row floor
+                                                                 where values cancel)
+  Q8_0 products (QKV, O, cross Q, cross K/V, gate/up, down)      Q8_0 product bound
+  F16 casts of K and V                                           bit-exact
+  attention                                                      the matrix-core
+                                                                 kernel's derived bound
+  gated and plain residual sums                                  bit-exact"""
+import numpy as np
+import pytest
+from fa_bound import fa_bound
+from helpers import assert_f32_close, assert_mul_mat_q8_0, to_dev, to_np
+from oracle import oracle as orc
+
+from acestep_ops import ops
+from acestep_ops.device import DTensor
+from acestep_ops.dit import DiTLayer
+
+pytestmark = pytest.mark.gpu
+
+
+def _w(r, n, k, s=0.05):
+    return orc.quantize_q8_0((r.standard_normal((n, k)) * s).astype(np.float32))
+
+
+def _f16_mask(m):
+    return DTensor.from_numpy(np.ascontiguousarray(m.astype(np.float16)).view(np.uint16), "f16")
+
+
+# (H, Nh, Nkv, D, I, S, N, enc_S)
+SIZES = {"small": (256, 4, 2, 128, 512, 70, 2, 40), "dit": (2048, 16, 8, 128, 6144, 96, 2, 40)}
+
+
+@pytest.mark.parametrize("size,cross,window", [("small", False, 32), ("small", True, 32), ("dit", True, 0),
+                                               ("dit", False, 64)])
+def test_dit_layer_stage_by_stage(dev, size, cross, window):
+    print(f"dit layer {size} cross={cross} window={window}", flush=True)
+    r = np.random.default_rng(59)
+    H, Nh, Nkv, D, I, S, N, E = SIZES[size]
+    eps, theta = 1e-6, 1e6
+    T = N * S
+    W = {"sa_qkv": _w(r, (Nh + 2 * Nkv) * D, H), "sa_o": _w(r, H, Nh * D), "gu": _w(r, 2 * I, H),
+         "down": _w(r, H, I), "ca_q": _w(r, Nh * D, H), "ca_kv": _w(r, 2 * Nkv * D, H), "ca_o": _w(r, H, Nh * D)}
+    nw = {k: (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+          for k, n in (("sa", H), ("mlp", H), ("ca", H), ("qn", D), ("kn", D), ("cqn", D), ("ckn", D))}
+    adaln = (0.3 * r.standard_normal((6, H))).astype(np.float32)
+    shift_sa, scale_sa, gate_sa, shift_ff, scale_ff, gate_ff = adaln
+    hidden = (r.standard_normal((N, S, H)) * 0.8).astype(np.float32)
+    enc = (r.standard_normal((N, E, H)) * 0.8).astype(np.float32)
+    ii = np.arange(S)
+    # the self-attention mask: a sliding window (window > 0), else all zero (no padding)
+    sa_m = np.where(np.abs(ii[None, :] - ii[:, None]) <= window, 0.0, -np.inf) if window else np.zeros((S, S))
+    sa_m = np.ascontiguousarray(np.broadcast_to(sa_m, (N, 1, S, S))).astype(np.float32)
+    # the cross-attention mask: sequence 1's last 7 encoder positions are padding
+    ca_m = np.zeros((N, 1, S, E), np.float32)
+    ca_m[1, :, :, E - 7:] = -np.inf
+    q8 = lambda a: ops.Q8(to_dev(a))  # noqa: E731
+    layer = DiTLayer(q8(W["sa_qkv"]), q8(W["sa_o"]), q8(W["gu"]), q8(W["down"]), to_dev(nw["sa"]), to_dev(nw["mlp"]),
+                     to_dev(nw["qn"]), to_dev(nw["kn"]), H, Nh, Nkv, D, I, eps, theta,
+                     **({"w_ca_q": q8(W["ca_q"]), "w_ca_kv": q8(W["ca_kv"]), "w_ca_o": q8(W["ca_o"]),
+                         "ca_norm_w": to_dev(nw["ca"]), "ca_q_norm_w": to_dev(nw["cqn"]),
+                         "ca_k_norm_w": to_dev(nw["ckn"])} if cross else {}))
+    pos = np.tile(np.arange(S, dtype=np.int32), N)
+    y = to_np(layer.forward(to_dev(hidden), to_dev(adaln), DiTLayer.positions(N, S), sa_mask=_f16_mask(sa_m),
+                            enc=to_dev(enc) if cross else None, ca_mask=_f16_mask(ca_m) if cross else None))
+    b = {k: to_np(v) for k, v in layer._bufs.items() if not k.startswith("ws")}
+    h2 = hidden.reshape(T, H)
+    scale = 1.0 / np.sqrt(D)
+    mfma = "prefill" if S * (Nh // Nkv) >= 64 else False
+
+    def attention(name, qo, k16, v16, n_kv, mask):
+        qf = np.ascontiguousarray(qo.reshape(N, S, Nh, D).transpose(0, 2, 1, 3))
+        kr = np.ascontiguousarray(orc.f16_to_f32(k16).reshape(N, n_kv, Nkv, D).transpose(0, 2, 1, 3))
+        vr = np.ascontiguousarray(orc.f16_to_f32(v16).reshape(N, n_kv, Nkv, D).transpose(0, 2, 1, 3))
+        ref = orc.flash_attn_ext(qf, kr, vr, mask, scale, "f16")
+        bound = fa_bound(qf, kr, vr, mask, scale, "f16", mfma=mfma)
+        got = b[name].reshape(N, S, Nh, D)  # y (N, S, Nh, D), as the oracle's
+        assert np.all(np.isfinite(got)), name
+        assert np.all(np.abs(got - ref) <= bound), name
+
+    # 1. norm -> modulate; the QKV product on the device's norm
+    assert_f32_close(b["norm_sa"], orc.rms_norm_modulate(h2, nw["sa"], scale_sa, shift_sa, eps), row_floor=True)
+    qkv = b["qkv"]
+    assert_mul_mat_q8_0(qkv, W["sa_qkv"], b["norm_sa"])
+    # 2. QK-norm -> rope; the F16 casts of K and V bit-exact
+    q = qkv[:, :Nh * D].reshape(T, Nh, D)
+    k = qkv[:, Nh * D:(Nh + Nkv) * D].reshape(T, Nkv, D)
+    v = qkv[:, (Nh + Nkv) * D:].reshape(T, Nkv, D)
+    assert_f32_close(b["qo"], orc.qk_norm_rope(q, nw["qn"], pos, eps, D, theta), row_floor=True)
+    assert_f32_close(b["ko"], orc.qk_norm_rope(k, nw["kn"], pos, eps, D, theta), row_floor=True)
+    assert np.array_equal(b["k16"], orc.f32_to_f16(b["ko"]))
+    assert np.array_equal(b["v16"], orc.f32_to_f16(v))
+    # 3. self attention under its mask; the O product
+    attention("attn", b["qo"], b["k16"], b["v16"], S, sa_m)
+    assert_mul_mat_q8_0(b["sa_out"], W["sa_o"], b["attn"].reshape(T, Nh * D))
+    if cross:
+        # 4. the gated residual (bit-exact) and the cross-attention norm
+        h1 = orc.gated_add(h2, b["sa_out"], gate_sa)
+        assert np.array_equal(b["h1"], h1)
+        assert_f32_close(b["norm_ca"], orc.rms_norm_mul(h1, nw["ca"], eps))
+        # 5. cross Q from the layer's rows, K/V from the encoder states; the
+        # per-head norms; the F16 casts; attention under the padding mask
+        assert_mul_mat_q8_0(b["ca_q"], W["ca_q"], b["norm_ca"])
+        assert_mul_mat_q8_0(b["ca_kv"], W["ca_kv"], enc.reshape(N * E, H))
+        kv = b["ca_kv"]
+        assert_f32_close(b["ca_qn"], orc.rms_norm_mul(b["ca_q"].reshape(T, Nh, D), nw["cqn"], eps))
+        assert_f32_close(b["ca_kn"], orc.rms_norm_mul(kv[:, :Nkv * D].reshape(N * E, Nkv, D), nw["ckn"], eps))
+        assert np.array_equal(b["ca_k16"], orc.f32_to_f16(b["ca_kn"]))
+        assert np.array_equal(b["ca_v16"], orc.f32_to_f16(kv[:, Nkv * D:].reshape(N * E, Nkv, D)))
+        attention("ca_attn", b["ca_qn"], b["ca_k16"], b["ca_v16"], E, ca_m)
+        assert_mul_mat_q8_0(b["ca_out"], W["ca_o"], b["ca_attn"].reshape(T, Nh * D))
+        # 6. the plain residual (bit-exact), then the FFN norm -> modulate
+        hf = orc.add(h1, b["ca_out"])
+    else:
+        hf = orc.gated_add(h2, b["sa_out"], gate_sa)
+    assert np.array_equal(b["h2"], hf)
+    assert_f32_close(b["norm_ffn"], orc.rms_norm_modulate(hf, nw["mlp"], scale_ff, shift_ff, eps), row_floor=True)
+    # 7. gate/up; the down product on the device's SwiGLU values (the prologue
+    # quantizes silu(g)*u as mi_swiglu computes it, within ~1 ulp of the oracle's)
+    assert_mul_mat_q8_0(b["gu"], W["gu"], b["norm_ffn"])
+    sw = to_np(ops.swiglu(layer._bufs["gu"]))
+    assert_f32_close(sw, orc.swiglu(b["gu"]))
+    assert_mul_mat_q8_0(b["ffn"], W["down"], sw)
+    # 8. the last gated residual, bit-exact
+    assert np.array_equal(y.reshape(T, H), orc.gated_add(hf, b["ffn"], gate_ff))
+    assert np.all(np.isfinite(y))
+
+
+def test_dit_layer_rejects_cross_mismatch(dev):
+    """enc must be given exactly when the layer holds cross-attention weights."""
+    r = np.random.default_rng(3)
+    H, Nh, Nkv, D, I = 256, 4, 2, 128, 512
+    q8 = lambda a: ops.Q8(to_dev(a))  # noqa: E731
+    ones = lambda n: to_dev(np.ones(n, np.float32))  # noqa: E731
+    layer = DiTLayer(q8(_w(r, (Nh + 2 * Nkv) * D, H)), q8(_w(r, H, Nh * D)), q8(_w(r, 2 * I, H)), q8(_w(r, H, I)),
+                     ones(H), ones(H), ones(D), ones(D), H, Nh, Nkv, D, I)
+    h = to_dev(np.zeros((1, 8, H), np.float32))
+    with pytest.raises(ValueError):
+        layer.forward(h, to_dev(np.zeros((6, H), np.float32)), DiTLayer.positions(1, 8),
+                      enc=to_dev(np.zeros((1, 4, H), np.float32)))
+    with pytest.raises(ValueError):
+        DiTLayer(q8(_w(r, (Nh + 2 * Nkv) * D, H)), q8(_w(r, H, Nh * D)), q8(_w(r, 2 * I, H)), q8(_w(r, H, I)),
+                 ones(H), ones(H), ones(D), ones(D), H, Nh, Nkv, D, I, w_ca_q=q8(_w(r, Nh * D, H)))
