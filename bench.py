@@ -1163,6 +1163,81 @@ def prefill_layer_bench_kv(steps: int, kv_type: str, N: int = 2, S: int = 512, S
     device.synchronize()
 
 
+# ---------------------------------------------------------------------------
+# One whole DiT layer (dit_ggml_build_layer, dit-graph.h:367-448) on the device:
+# the DiT's shape (H 2048, 16/8 heads x 128, I 6144, Q8_0 weights, F32
+# activations) over the CFG pair of S = 3000 latent tokens, with the cross
+# attention over 512 encoder rows (the last 40 padding), as the two layer
+# types run: a sliding window of 128 on the even layers and the padding mask
+# (all zero) on the odd ones (dit-sampler.h:253-274). A graph of `steps` layer
+# calls, replayed once untimed and once timed.
+# ---------------------------------------------------------------------------
+def dit_layer_bench(steps: int):
+    from acestep_ops import device, ops
+    from acestep_ops.device import DTensor, Event, Graph, Stream
+    from acestep_ops.dit import DiTLayer
+
+    H, Nh, Nkv, D, I, N, S, E, WIN = 2048, 16, 8, 128, 6144, 2, 3000, 512, 128
+    rng = np.random.default_rng(23)
+    st = Stream()
+    sh = st.handle
+
+    def q8w(n, k):
+        nbk = k // 32
+        b = np.empty((n, nbk, 34), np.uint8)
+        b[:, :, 2:] = rng.integers(-127, 128, (n, nbk, 32), dtype=np.int8).view(np.uint8)
+        b[:, :, :2] = (rng.uniform(0.5, 1.0, (n, nbk)) * 2e-3).astype(np.float16).view(np.uint8).reshape(n, nbk, 2)
+        return ops.Q8(DTensor.from_numpy(b.reshape(n, nbk * 34)))
+
+    ones = lambda n: DTensor.from_numpy(np.ones(n, np.float32))  # noqa: E731
+    layer = DiTLayer(q8w((Nh + 2 * Nkv) * D, H), q8w(H, Nh * D), q8w(2 * I, H), q8w(H, I), ones(H), ones(H),
+                     ones(D), ones(D), H, Nh, Nkv, D, I, w_ca_q=q8w(Nh * D, H), w_ca_kv=q8w(2 * Nkv * D, H),
+                     w_ca_o=q8w(H, Nh * D), ca_norm_w=ones(H), ca_q_norm_w=ones(D), ca_k_norm_w=ones(D), stream=sh)
+    hidden = DTensor.from_numpy(rng.standard_normal((N, S, H), dtype=np.float32))
+    enc = DTensor.from_numpy(rng.standard_normal((N, E, H), dtype=np.float32))
+    adaln = DTensor.from_numpy((0.1 * rng.standard_normal((6, H))).astype(np.float32))
+    out = DTensor.empty((N, S, H), "f32")
+    pos = DiTLayer.positions(N, S)
+    ii = np.arange(S)
+    win = np.where(np.abs(ii[None, :] - ii[:, None]) <= WIN // 2, 0.0, -np.inf).astype(np.float16)
+    wmask = DTensor.from_numpy(np.ascontiguousarray(np.broadcast_to(win, (N, 1, S, S))).view(np.uint16), "f16")
+    del win
+    zmask = DTensor.zeros((N, 1, S, S), "f16")
+    pm = np.zeros((N, 1, S, E), np.float16)
+    pm[..., E - 40:] = -np.inf
+    cmask = DTensor.from_numpy(pm.view(np.uint16), "f16")
+    T = N * S
+    gemm = 2 * T * sum(w.n * w.k for name, w in layer.w.items() if name != "ca_kv") + \
+        2 * N * E * layer.w["ca_kv"].n * layer.w["ca_kv"].k
+    ca_pairs = 4 * D * Nh * N * S * (E - 40)
+    for label, mk, live in ((f"sliding window {WIN}", wmask, None), ("padding mask (all zero)", zmask, S)):
+        call = lambda: layer.forward(hidden, adaln, pos, sa_mask=mk, enc=enc, ca_mask=cmask, out=out)  # noqa: E731
+        call()  # allocates the layer's buffers outside the graph
+        st.synchronize()
+        g = Graph()
+        with g.capture(st):
+            for _ in range(steps):
+                call()
+        g.launch()
+        st.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(sh)
+        g.launch()
+        e1.record(sh)
+        e1.synchronize()
+        us = 1000.0 * e0.elapsed_ms(e1) / steps
+        pairs = S * S if live else sum(min(S, i + WIN // 2 + 1) - max(0, i - WIN // 2) for i in range(S))
+        sa = 4 * D * Nh * N * pairs
+        print(json.dumps({"config": f"DiT layer, S={S} x {N}, H={H}, {Nh}/{Nkv} heads x {D}, I={I}, Q8_0 weights, "
+                                    f"F32 activations, self attention under the {label}, cross attention over {E} "
+                                    "encoder rows (40 padding), every op on the device",
+                          "us_per_layer": round(us, 1), "gemm_flop": gemm, "attn_flop_live": sa + ca_pairs,
+                          "TFLOP/s": round((gemm + sa + ca_pairs) / (us * 1e-6) / 1e12, 1)}), flush=True)
+        del g
+    del layer
+    device.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1187,6 +1262,9 @@ def main():
     ap.add_argument("--prefill-layer", action="store_true",
                     help="time one whole Qwen3-4B decoder layer in prefill (2 CFG sequences x 512 tokens; F16 and "
                          "Q8_0 KV caches), all on the device")
+    ap.add_argument("--dit-layer", action="store_true",
+                    help="time one whole DiT layer (S=3000 x 2, cross attention, both self-attention masks), all on "
+                         "the device")
     ap.add_argument("--gemv", action="store_true",
                     help="time the Q8_0 mul_mat of the Qwen3-4B decode projections and LM head at batch 8")
     args = ap.parse_args()
@@ -1222,6 +1300,9 @@ def main():
         return
     if args.prefill_layer:
         prefill_layer_bench(args.steps)
+        return
+    if args.dit_layer:
+        dit_layer_bench(args.steps)
         return
     kb = block_bytes(ROWS, cross=True)
     kb_f = block_bytes(ROWS, fused=True)
