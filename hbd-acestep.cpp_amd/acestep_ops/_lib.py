@@ -121,6 +121,8 @@ PROTOTYPES = {
                                  ctypes.c_size_t, _VP],
     "mi_mul_mat_q8_0_add_rms_norm": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, _TP, _TP, ctypes.c_float, _TP, _TP,
                                      _VP, ctypes.c_size_t, _VP],
+    "mi_mul_mat_q8_0_adaln": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, _TP, _TP, _TP, _TP, _TP, ctypes.c_float, _TP,
+                              _TP, _VP, ctypes.c_size_t, _VP],
     "mi_mul_mat_q8_0_swiglu_workspace": [ctypes.c_int64, ctypes.c_int64, _TP, ctypes.POINTER(ctypes.c_size_t)],
     "mi_mul_mat_q8_0_swiglu": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, ctypes.c_int, _TP, _VP, ctypes.c_size_t,
                                _VP],

@@ -18,9 +18,11 @@ dit_ggml_build_cross_attn, 274-354, and the MLP of dit_ggml_build_mlp, 249-268):
   norm_ffn = modulate(rms_norm(hidden) * mlp_norm, scale_ffn, shift_ffn)  (437-438)
   hidden   = hidden + mul_mat(W_down, swiglu(mul_mat(W_gate_up, norm_ffn))) * gate_ffn  (439-440)
 
-Each gated (or plain) residual add runs in one launch with the norm after it
-(mi_add_rms_norm), and the SwiGLU inside the quantization of the down
-product's x (mi_mul_mat_q8_0_swiglu). The six AdaLN vectors come in as one F32
+Each norm (with the gated or plain residual add before it and the modulate
+after it) runs inside the quantization of the next product's x
+(mi_mul_mat_q8_0_adaln: the normalized rows never go to memory), and the
+SwiGLU inside the quantization of the down product's x
+(mi_mul_mat_q8_0_swiglu). The six AdaLN vectors come in as one F32
 (6, H) tensor: scale_shift_table + the timestep projection (dit-graph.h:384-399),
 rows shift_sa, scale_sa, gate_sa, shift_ffn, scale_ffn, gate_ffn.
 
@@ -91,12 +93,10 @@ class DiTLayer:
         h2 = hidden.view(T, H)
         shift_sa, scale_sa, gate_sa, shift_ffn, scale_ffn, gate_ffn = (adaln[i] for i in range(6))
 
-        # self attention
-        norm_sa = ops.rms_norm_modulate(h2, self.sa_norm_w, scale_sa, shift_sa, self.eps,
-                                        out=self._buf("norm_sa", (T, H)), stream=st)
+        # self attention: norm -> modulate -> the QKV product in one call
         qkv_dim = (Nh + 2 * Nkv) * D
-        qkv = ops.mul_mat_q8_0(self.w["sa_qkv"], norm_sa, out=self._buf("qkv", (T, qkv_dim)),
-                               workspace=self._ws("sa_qkv", norm_sa), stream=st)
+        qkv = ops.mul_mat_q8_0_adaln(self.w["sa_qkv"], h2, self.sa_norm_w, self.eps, scale=scale_sa, shift=shift_sa,
+                                     out=self._buf("qkv", (T, qkv_dim)), workspace=self._ws("sa_qkv", h2), stream=st)
         q = qkv[:, 0:Nh * D].unflatten(1, (Nh, D))
         k = qkv[:, Nh * D:(Nh + Nkv) * D].unflatten(1, (Nkv, D))
         v = qkv[:, (Nh + Nkv) * D:qkv_dim].unflatten(1, (Nkv, D))
@@ -110,23 +110,21 @@ class DiTLayer:
         sa_out = ops.mul_mat_q8_0(self.w["sa_o"], attn.view(T, Nh * D), out=self._buf("sa_out", (T, H)),
                                   workspace=self._ws("sa_o", attn.view(T, Nh * D)), stream=st)
         if self.cross:
-            # the gated residual and the cross-attention norm in one launch
-            h1, norm_ca = ops.add_rms_norm(h2, sa_out, self.eps, gate=gate_sa, w=self.ca_norm_w,
-                                           out_sum=self._buf("h1", (T, H)), out_norm=self._buf("norm_ca", (T, H)),
-                                           stream=st)
-            ca_out = self._cross(norm_ca, enc, ca_mask, N, S)
-            # the cross-attention residual and the FFN norm -> modulate in one launch
-            h2b, norm_ffn = ops.add_rms_norm(h1, ca_out, self.eps, w=self.mlp_norm_w, scale=scale_ffn,
+            # the gated residual, the cross-attention norm and the cross Q product in one call
+            h1, qc = ops.mul_mat_q8_0_adaln(self.w["ca_q"], h2, self.ca_norm_w, self.eps, b=sa_out, gate=gate_sa,
+                                            out_sum=self._buf("h1", (T, H)), out=self._buf("ca_q", (T, Nh * D)),
+                                            workspace=self._ws("ca_q", h2), stream=st)
+            ca_out = self._cross(qc, enc, ca_mask, N, S)
+            # the cross-attention residual, the FFN norm -> modulate and the gate/up product in one call
+            h2b, gu = ops.mul_mat_q8_0_adaln(self.w["gu"], h1, self.mlp_norm_w, self.eps, b=ca_out, scale=scale_ffn,
                                              shift=shift_ffn, out_sum=self._buf("h2", (T, H)),
-                                             out_norm=self._buf("norm_ffn", (T, H)), stream=st)
+                                             out=self._buf("gu", (T, 2 * I)), workspace=self._ws("gu", h1), stream=st)
         else:
-            # the gated residual and the FFN norm -> modulate in one launch
-            h2b, norm_ffn = ops.add_rms_norm(h2, sa_out, self.eps, gate=gate_sa, w=self.mlp_norm_w, scale=scale_ffn,
-                                             shift=shift_ffn, out_sum=self._buf("h2", (T, H)),
-                                             out_norm=self._buf("norm_ffn", (T, H)), stream=st)
-        # the MLP: gate/up, then SwiGLU inside the down product's quantization
-        gu = ops.mul_mat_q8_0(self.w["gu"], norm_ffn, out=self._buf("gu", (T, 2 * I)),
-                              workspace=self._ws("gu", norm_ffn), stream=st)
+            # the gated residual, the FFN norm -> modulate and the gate/up product in one call
+            h2b, gu = ops.mul_mat_q8_0_adaln(self.w["gu"], h2, self.mlp_norm_w, self.eps, b=sa_out, gate=gate_sa,
+                                             scale=scale_ffn, shift=shift_ffn, out_sum=self._buf("h2", (T, H)),
+                                             out=self._buf("gu", (T, 2 * I)), workspace=self._ws("gu", h2), stream=st)
+        # the MLP: SwiGLU inside the down product's quantization
         need = ops.mul_mat_q8_0_swiglu_workspace(self.w["down"], gu)
         ffn = ops.mul_mat_q8_0_swiglu(self.w["down"], gu, out=self._buf("ffn", (T, H)),
                                       workspace=self._buf("ws_down", (max(need, 1),), "u8"), stream=st)
@@ -134,15 +132,14 @@ class DiTLayer:
         ops.gated_add(h2b, ffn, gate_ffn, out=y, stream=st)
         return y.view(N, S, H)
 
-    def _cross(self, norm_ca, enc, ca_mask, N: int, S: int):
-        """Cross attention of the layer's rows over the encoder states: its O product (T, H)."""
+    def _cross(self, qc, enc, ca_mask, N: int, S: int):
+        """Cross attention of the layer's rows (their Q product qc (T, Nh * D)) over the
+        encoder states: its O product (T, H)."""
         Nh, Nkv, D, H = self.Nh, self.Nkv, self.D, self.H
         st = self.stream
         T = N * S
         E = enc.shape[1]
         e2 = enc.view(N * E, H)
-        qc = ops.mul_mat_q8_0(self.w["ca_q"], norm_ca, out=self._buf("ca_q", (T, Nh * D)),
-                              workspace=self._ws("ca_q", norm_ca), stream=st)
         kvc = ops.mul_mat_q8_0(self.w["ca_kv"], e2, out=self._buf("ca_kv", (N * E, 2 * Nkv * D)),
                                workspace=self._ws("ca_kv", e2), stream=st)
         qn = ops.rms_norm(qc.unflatten(1, (Nh, D)), self.eps, w=self.ca_q_norm_w,

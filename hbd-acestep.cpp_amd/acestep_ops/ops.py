@@ -356,6 +356,25 @@ def mul_mat_q8_0_add_rms_norm(w: Q8R64, a, b, norm_w, eps: float, out_sum=None, 
     return sm, y
 
 
+def mul_mat_q8_0_adaln(w: Q8R64, a, norm_w, eps: float, b=None, gate=None, scale=None, shift=None, out_sum=None,
+                       out=None, workspace=None, stream=None):
+    """The DiT's norm -> product pair in one call (mi_mul_mat_q8_0_adaln): sum = a + b [* gate]
+    (with b), x' = rms_norm(sum or a) * norm_w [* (scale + 1) + shift], y = ggml_mul_mat(w, x').
+    Returns (sum, y) when b is given, else y; equal to add_rms_norm / rms_norm_modulate
+    followed by mul_mat_q8_0."""
+    sm = _out(out_sum, a.shape, "f32") if b is not None else None
+    y = _out(out, tuple(a.shape[:-1]) + (w.n,), "f32")
+    need = mul_mat_q8_0_workspace(w, a)
+    ws = workspace
+    if need and ws is None:
+        ws = DTensor.empty((need,), "u8")
+    wp = ctypes.c_void_p(ws.ptr) if ws is not None else None
+    wn = ws.numel() * ws.es if ws is not None else 0
+    _lib.call("mi_mul_mat_q8_0_adaln", ctypes.c_void_p(w.data.ptr), w.k, w.n, _p(a), _p(b), _p(gate), _p(norm_w),
+              _p(scale), _p(shift), ctypes.c_float(eps), _p(sm), _p(y), wp, wn, _s(stream))
+    return (sm, y) if b is not None else y
+
+
 def mul_mat_q8_0(w: Q8R64, x, out=None, workspace=None, stream=None):
     """ggml_mul_mat(w, x): x F32 (m, k) with m <= 8 -> F32 (m, n)."""
     y = _out(out, tuple(x.shape[:-1]) + (w.n,), "f32")

@@ -1180,14 +1180,40 @@ int mi_mul_mat_q8_0_swiglu_add(const void * w, int64_t k, int64_t n, const mi_te
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 
+// an F32 vector of k contiguous elements (the norm weight, a gate, a modulate scale or shift)
+static int mm_vec(const mi_tensor * v, int64_t k) {
+    MI_TRY(check(v));
+    if (v->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (v->ne[0] != k || nrows(*v) != 1 || v->nb[0] != 4) {
+        return MI_ERR_SHAPE;
+    }
+    return MI_OK;
+}
+
 static int mm_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * b,
                    const mi_tensor * norm_w, float eps, const mi_tensor * sum, const mi_tensor * y, void * workspace,
-                   size_t workspace_bytes, mi_stream stream) {
+                   size_t workspace_bytes, mi_stream stream, const mi_tensor * gate = nullptr,
+                   const mi_tensor * scale = nullptr, const mi_tensor * shift = nullptr) {
     if (!y || !norm_w) {
+        return MI_ERR_NULL;
+    }
+    if ((scale == nullptr) != (shift == nullptr) || (gate && !b)) {
         return MI_ERR_NULL;
     }
     MmvArgs a;
     MI_TRY(mm_desc(w, k, n, x, y, a));
+    if (gate) {
+        MI_TRY(mm_vec(gate, k));
+        a.gate = (const float *) gate->data;
+    }
+    if (scale) {
+        MI_TRY(mm_vec(scale, k));
+        MI_TRY(mm_vec(shift, k));
+        a.msc = (const float *) scale->data;
+        a.msh = (const float *) shift->data;
+    }
     if (b) {  // the residual addend and the sum: F32 rows of x's shape, uniformly strided
         if (!sum) {
             return MI_ERR_NULL;
@@ -1218,13 +1244,7 @@ static int mm_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, co
         a.sum1 = (int64_t) sum->nb[1];
         a.xvec = a.xvec && aligned(b->data, 16) && (a.m <= 1 || b->nb[1] % 16 == 0);
     }
-    MI_TRY(check(norm_w));
-    if (norm_w->type != MI_TYPE_F32) {
-        return MI_ERR_TYPE;
-    }
-    if (norm_w->ne[0] != k || nrows(*norm_w) != 1 || norm_w->nb[0] != 4) {
-        return MI_ERR_SHAPE;
-    }
+    MI_TRY(mm_vec(norm_w, k));
     if (!(eps >= 0.0f)) {
         return MI_ERR_PARAM;
     }
@@ -1262,6 +1282,14 @@ int mi_mul_mat_q8_0_add_rms_norm(const void * w, int64_t k, int64_t n, const mi_
         return MI_ERR_NULL;
     }
     return mm_norm(w, k, n, a, b, norm_w, eps, sum, y, workspace, workspace_bytes, stream);
+}
+
+int mi_mul_mat_q8_0_adaln(const void * w, int64_t k, int64_t n, const mi_tensor * a, const mi_tensor * b,
+                          const mi_tensor * gate, const mi_tensor * norm_w, const mi_tensor * scale,
+                          const mi_tensor * shift, float eps, const mi_tensor * sum, const mi_tensor * y,
+                          void * workspace, size_t workspace_bytes, mi_stream stream) {
+    return mm_norm(w, k, n, a, b, norm_w, eps, b ? sum : nullptr, y, workspace, workspace_bytes, stream, gate, scale,
+                   shift);
 }
 
 // F32 [oc, t, n] contiguous, the velocity/latent layout of the sampler

@@ -196,6 +196,9 @@ struct MmvArgs {
     float        eps;
     const char * ab;           // non-null (with nw): x = x + ab first, rows at stride ab1,
     int64_t      ab1;          // the sum written to sum (rows at stride sum1)
+    const float * gate;        // non-null (with ab): x = x + ab * gate (the DiT's gated residual)
+    const float * msc;         // non-null (with nw): the normalized rows modulated,
+    const float * msh;         // (x' * (msc + 1)) + msh (the DiT's AdaLN)
     char *       sum;
     int64_t      sum1;
     int          glu;          // 1: x = silu(g) * u (the SwiGLU prologue), rows at stride gu1

@@ -142,7 +142,10 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x(const MmvArgs a) {
 // k_mmv_quant_x does, 8 lanes per 32-element block. With an addend (a.ab), x is
 // the residual sum a.x + a.ab, written to a.sum in the first pass (the
 // arithmetic of mi_add_rms_norm) and formed again from the two inputs in the
-// second.
+// second. With a gate (a.gate) the addend is scaled first, x + ab * gate (the
+// arithmetic of mi_add_rms_norm's gated form); with a modulate (a.msc, a.msh)
+// the normalized rows become (x' * (msc + 1)) + msh, each step rounded as
+// mi_rms_norm_modulate rounds it.
 __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
     __shared__ double red[4];
     __shared__ float  scl;
@@ -170,6 +173,12 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
         if (br) {
             float b4[4];
             ld4(br + (size_t) i * 4, b4);
+            if (a.gate) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    b4[e] = b4[e] * a.gate[i + e];
+                }
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 v[e] = v[e] + b4[e];
@@ -212,6 +221,13 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
             const float v = f[e] * scale;
             f[e]          = v * a.nw[i0 + e];
         }
+        if (a.msc) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                f[e] = f[e] * (a.msc[i0 + e] + 1.0f);
+                f[e] = f[e] + a.msh[i0 + e];
+            }
+        }
         float amax = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
         amax       = group_max<8>(amax);
         const float d  = mm_div127(amax);
@@ -238,8 +254,8 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm(const MmvArgs a) {
 // quants of one block as one 256-byte run of the block-major layout (one
 // workgroup per row wrote 32-byte pieces 32 * mp bytes apart). With an addend
 // the residual sum is formed once and written in the first pass (ADD: a.ab is
-// given, so that the plain prologue holds no registers for it). Rows of x are
-// at most 4 * NBW blocks.
+// given, so that the plain prologue holds no registers for it); the gate and
+// the modulate as in k_mmv_quant_x_norm. Rows of x are at most 4 * NBW blocks.
 template <int NBW, bool ADD>
 __global__ void __launch_bounds__(256) k_mmv_quant_x_norm8(const MmvArgs a) {
     __shared__ double red[4][8];
@@ -282,6 +298,12 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm8(const MmvArgs a) {
         const uint32_t b = (uint32_t) wv + 4u * (uint32_t) j;
         if (b < a.nbk && rv) {
             if constexpr (ADD) {
+                if (a.gate) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        u[j][e] = u[j][e] * a.gate[b * 32u + sub * 4u + e];
+                    }
+                }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     v[j][e] = v[j][e] + u[j][e];
@@ -318,6 +340,13 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm8(const MmvArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             f[e] = (v[j][e] * scale) * a.nw[i0 + e];
+        }
+        if (a.msc) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                f[e] = f[e] * (a.msc[i0 + e] + 1.0f);
+                f[e] = f[e] + a.msh[i0 + e];
+            }
         }
         float amax = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
         amax       = group_max<8>(amax);

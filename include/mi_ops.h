@@ -348,6 +348,25 @@ int mi_mul_mat_q8_0_add_rms_norm(const void * w, int64_t k, int64_t n, const mi_
                                  const mi_tensor * norm_w, float eps, const mi_tensor * sum, const mi_tensor * y,
                                  void * workspace, size_t workspace_bytes, mi_stream stream);
 
+/* The DiT's norm -> product pairs as one call (dit_ggml_build_layer,
+ * dit-graph.h:402-439): the optional residual add before the norm, gated or
+ * plain (sum = a + b * gate, or a + b; written to sum, F32 [k, m], for the next
+ * residual), the RMSNorm * norm_w, the optional AdaLN modulate
+ * ((x' * (scale + 1)) + shift, dit_ggml_adaln, dit-graph.h:54-64), then
+ * y = ggml_mul_mat(w, x'). Replaces the node chains feeding the QKV projection
+ * (404-405, norm -> modulate), the cross-attention Q projection (415 and 424,
+ * gated add -> norm) and the gate/up projection (415 or 427, then 437-438,
+ * add -> norm -> modulate). b, gate and sum may be null (no add; gate needs b);
+ * scale and shift are both given or both null; gate, norm_w, scale, shift:
+ * F32 [k]. Every step is rounded as mi_add_rms_norm / mi_rms_norm_modulate round
+ * it, so y equals that call followed by mi_mul_mat_q8_0 and the normalized rows
+ * never go to memory. Same operand rules and workspace as
+ * mi_mul_mat_q8_0_add_rms_norm. */
+int mi_mul_mat_q8_0_adaln(const void * w, int64_t k, int64_t n, const mi_tensor * a, const mi_tensor * b,
+                          const mi_tensor * gate, const mi_tensor * norm_w, const mi_tensor * scale,
+                          const mi_tensor * shift, float eps, const mi_tensor * sum, const mi_tensor * y,
+                          void * workspace, size_t workspace_bytes, mi_stream stream);
+
 /* The DiT sampler's per-step math on the device (dit_ggml_generate,
  * dit-sampler.h:408-640), so the latents stay resident across steps.
  * Latents and velocities are F32 [Oc, T, N], contiguous.

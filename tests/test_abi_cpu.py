@@ -272,6 +272,19 @@ def test_mul_mat_q8_0_validation():
     assert ma(W, k, n, R(x), R(_t([k, m + 1])), R(nw), eps, R(_t([k, m])), R(y), None, 0, NULL_S) == -3
     assert ma(W, k, n, R(x), R(_t([k, m], BF16)), R(nw), eps, R(_t([k, m])), R(y), None, 0, NULL_S) == -2
     assert ma(W, k, n, R(x), R(_t([k, m])), R(nw), eps, R(x), R(y), None, 0, NULL_S) == -6   # sum aliases a
+    # the AdaLN prologue: gate needs b, scale and shift come together, each F32 [k]
+    md = L.mi_mul_mat_q8_0_adaln
+    b2, s2 = _t([k, m]), _t([k, m])
+    assert md(W, k, n, R(x), None, R(nw), R(nw), None, None, eps, None, R(y), None, 0, NULL_S) == -1  # gate, no b
+    assert md(W, k, n, R(x), None, None, R(nw), R(nw), None, eps, None, R(y), None, 0, NULL_S) == -1  # scale alone
+    assert md(W, k, n, R(x), None, None, R(nw), None, R(nw), eps, None, R(y), None, 0, NULL_S) == -1  # shift alone
+    assert md(W, k, n, R(x), R(b2), R(nw), R(nw), None, None, eps, None, R(y), None, 0, NULL_S) == -1  # b, no sum
+    assert md(W, k, n, R(x), R(b2), R(_t([k + 32])), R(nw), None, None, eps, R(s2), R(y), None, 0, NULL_S) == -3
+    assert md(W, k, n, R(x), R(b2), R(_t([k], BF16)), R(nw), None, None, eps, R(s2), R(y), None, 0, NULL_S) == -2
+    assert md(W, k, n, R(x), None, None, R(nw), R(_t([k, 2])), R(nw), eps, None, R(y), None, 0, NULL_S) == -3
+    assert md(W, k, n, R(x), None, None, R(nw), R(nw), R(_t([k], BF16)), eps, None, R(y), None, 0, NULL_S) == -2
+    assert md(W, k, n, R(x), R(b2), R(nw), R(nw), R(nw), R(nw), eps, R(b2), R(y), None, 0, NULL_S) == -6  # sum aliases b
+    assert md(W, k, n, R(x), R(b2), R(nw), R(nw), R(nw), R(nw), eps, R(s2), R(y), None, 0, NULL_S) == -6  # no workspace
     # the SwiGLU prologue: gu [2k, m]
     gu = _t([2 * k, m])
     mg = L.mi_mul_mat_q8_0_swiglu

@@ -1,16 +1,19 @@
 """A whole ACE-Step DiT layer on the device (acestep_ops.dit.DiTLayer: AdaLN
-norm -> modulate, Q8_0 QKV product, QK-norm + rope, F16 casts, flash attention
-under the sliding-window or padding mask, O product, gated residual fused with
-the next norm, the cross attention over encoder states, the MLP with the
+norm -> modulate inside the Q8_0 QKV product, QK-norm + rope, F16 casts, flash
+attention under the sliding-window or padding mask, O product, gated residual
+and the next norm inside the next product, the cross attention over encoder states, the MLP with the
 SwiGLU inside the down product, the last gated residual) against the oracle,
 stage by stage (dit_ggml_build_layer, dit-graph.h:367-448), at a small size and
 at the DiT's layer shape (H 2048, 16/8 heads x 128, I 6144).
 
 Every stage is checked against the oracle applied to the device's own inputs
 of that stage, at that op's own bar:
-  norm -> modulate, QK-norm -> rope, the cross-attention norms   1e-5 (row floor
+  QK-norm -> rope, the cross-attention per-head norms             1e-5 (row floor
                                                                  where values cancel)
   Q8_0 products (QKV, O, cross Q, cross K/V, gate/up, down)      Q8_0 product bound
+                                                                 (those fed by a fused
+                                                                 norm on the oracle's
+                                                                 normalized rows)
   F16 casts of K and V                                           bit-exact
   attention                                                      the matrix-core
                                                                  kernel's derived bound
@@ -87,10 +90,10 @@ def test_dit_layer_stage_by_stage(dev, size, cross, window):
         assert np.all(np.isfinite(got)), name
         assert np.all(np.abs(got - ref) <= bound), name
 
-    # 1. norm -> modulate; the QKV product on the device's norm
-    assert_f32_close(b["norm_sa"], orc.rms_norm_modulate(h2, nw["sa"], scale_sa, shift_sa, eps), row_floor=True)
+    # 1. norm -> modulate -> the QKV product (one call: the normalized rows are made
+    # inside the quantization of x, with the arithmetic of mi_rms_norm_modulate)
     qkv = b["qkv"]
-    assert_mul_mat_q8_0(qkv, W["sa_qkv"], b["norm_sa"])
+    assert_mul_mat_q8_0(qkv, W["sa_qkv"], orc.rms_norm_modulate(h2, nw["sa"], scale_sa, shift_sa, eps))
     # 2. QK-norm -> rope; the F16 casts of K and V bit-exact
     q = qkv[:, :Nh * D].reshape(T, Nh, D)
     k = qkv[:, Nh * D:(Nh + Nkv) * D].reshape(T, Nkv, D)
@@ -103,13 +106,13 @@ def test_dit_layer_stage_by_stage(dev, size, cross, window):
     attention("attn", b["qo"], b["k16"], b["v16"], S, sa_m)
     assert_mul_mat_q8_0(b["sa_out"], W["sa_o"], b["attn"].reshape(T, Nh * D))
     if cross:
-        # 4. the gated residual (bit-exact) and the cross-attention norm
+        # 4. the gated residual (bit-exact), the cross-attention norm and the cross Q
+        # product (one call)
         h1 = orc.gated_add(h2, b["sa_out"], gate_sa)
         assert np.array_equal(b["h1"], h1)
-        assert_f32_close(b["norm_ca"], orc.rms_norm_mul(h1, nw["ca"], eps))
-        # 5. cross Q from the layer's rows, K/V from the encoder states; the
-        # per-head norms; the F16 casts; attention under the padding mask
-        assert_mul_mat_q8_0(b["ca_q"], W["ca_q"], b["norm_ca"])
+        assert_mul_mat_q8_0(b["ca_q"], W["ca_q"], orc.rms_norm_mul(h1, nw["ca"], eps))
+        # 5. K/V from the encoder states; the per-head norms; the F16 casts;
+        # attention under the padding mask
         assert_mul_mat_q8_0(b["ca_kv"], W["ca_kv"], enc.reshape(N * E, H))
         kv = b["ca_kv"]
         assert_f32_close(b["ca_qn"], orc.rms_norm_mul(b["ca_q"].reshape(T, Nh, D), nw["cqn"], eps))
@@ -118,15 +121,15 @@ def test_dit_layer_stage_by_stage(dev, size, cross, window):
         assert np.array_equal(b["ca_v16"], orc.f32_to_f16(kv[:, Nkv * D:].reshape(N * E, Nkv, D)))
         attention("ca_attn", b["ca_qn"], b["ca_k16"], b["ca_v16"], E, ca_m)
         assert_mul_mat_q8_0(b["ca_out"], W["ca_o"], b["ca_attn"].reshape(T, Nh * D))
-        # 6. the plain residual (bit-exact), then the FFN norm -> modulate
+        # 6. the plain residual (bit-exact)
         hf = orc.add(h1, b["ca_out"])
     else:
         hf = orc.gated_add(h2, b["sa_out"], gate_sa)
     assert np.array_equal(b["h2"], hf)
-    assert_f32_close(b["norm_ffn"], orc.rms_norm_modulate(hf, nw["mlp"], scale_ff, shift_ff, eps), row_floor=True)
-    # 7. gate/up; the down product on the device's SwiGLU values (the prologue
-    # quantizes silu(g)*u as mi_swiglu computes it, within ~1 ulp of the oracle's)
-    assert_mul_mat_q8_0(b["gu"], W["gu"], b["norm_ffn"])
+    # 7. the FFN norm -> modulate -> gate/up (one call); the down product on the
+    # device's SwiGLU values (the prologue quantizes silu(g)*u as mi_swiglu computes
+    # it, within ~1 ulp of the oracle's)
+    assert_mul_mat_q8_0(b["gu"], W["gu"], orc.rms_norm_modulate(hf, nw["mlp"], scale_ff, shift_ff, eps))
     sw = to_np(ops.swiglu(layer._bufs["gu"]))
     assert_f32_close(sw, orc.swiglu(b["gu"]))
     assert_mul_mat_q8_0(b["ffn"], W["down"], sw)

@@ -229,6 +229,49 @@ def test_rms_norm_prologue_matches_norm_then_mul_mat(dev, n, k, m, view):
     _check(y_f, w, to_np(norm))
 
 
+@pytest.mark.parametrize("n,k,m,add,gated,mod", [
+    (4096, 2048, 8, False, False, True),     # decode kernel, norm -> modulate
+    (640, 256, 129, False, False, True),     # matrix kernel, a workgroup per row
+    (96, 2048, 4100, False, False, True),    # 8 rows per workgroup, ragged last group
+    (640, 256, 129, True, True, False),      # gated add -> norm (the cross-attention norm)
+    (64, 2048, 4103, True, True, False),
+    (640, 256, 129, True, True, True),       # gated add -> norm -> modulate (the FFN norm)
+    (64, 2048, 4096, True, True, True),
+    (300, 256, 3, True, False, True),        # plain add -> norm -> modulate (after cross attention)
+    (64, 256, 4104, True, False, True),
+])
+def test_adaln_prologue_matches_unfused(dev, n, k, m, add, gated, mod):
+    """mi_mul_mat_q8_0_adaln (the DiT's residual add, gated or plain, the RMSNorm*w
+    and the AdaLN modulate made inside the quantization of x) against
+    mi_add_rms_norm / mi_rms_norm_modulate / mi_rms_norm followed by
+    mi_mul_mat_q8_0: the sum and the product bit-identical, for the decode and
+    matrix kernels, a workgroup per row and per 8 rows; then the product against
+    the oracle on the normalized rows the device produced."""
+    print(f"mul_mat q8_0 adaln n={n} k={k} m={m} add={add} gated={gated} mod={mod}", flush=True)
+    r = np.random.default_rng(n + k + m + 3)
+    w = orc.quantize_q8_0((r.standard_normal((n, k)) * 0.05).astype(np.float32))
+    a = r.standard_normal((m, k)).astype(np.float32)
+    a *= np.float32(10.0) ** r.integers(-2, 3, (m, 1)).astype(np.float32)
+    b = (r.standard_normal((m, k)) * 0.3).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    g = (0.5 * r.standard_normal(k)).astype(np.float32)
+    sc = (0.3 * r.standard_normal(k)).astype(np.float32)
+    sh = (0.3 * r.standard_normal(k)).astype(np.float32)
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    da, db, dnw, dg, dsc, dsh = (to_dev(v) for v in (a, b, nw, g, sc, sh))
+    kw = {"gate": dg if gated else None, "scale": dsc if mod else None, "shift": dsh if mod else None}
+    if add:
+        s_f, y_f = ops.mul_mat_q8_0_adaln(wr, da, dnw, 1e-6, b=db, **kw)
+        s_u, n_u = ops.add_rms_norm(da, db, 1e-6, w=dnw, **kw)
+        assert np.array_equal(to_np(s_f), to_np(s_u))
+    else:
+        y_f = ops.mul_mat_q8_0_adaln(wr, da, dnw, 1e-6, scale=dsc, shift=dsh)
+        n_u = ops.rms_norm_modulate(da, dnw, dsc, dsh, 1e-6)
+    y_u = to_np(ops.mul_mat_q8_0(wr, n_u))
+    assert np.array_equal(to_np(y_f), y_u)
+    _check(to_np(y_f), w, to_np(n_u))
+
+
 @pytest.mark.parametrize("n,k,m", [(19456, 2560, 8), (300, 256, 3), (640, 256, 129), (64, 2560, 4103),
                                    (64, 4096, 4096), (64, 256, 4104)])
 def test_add_rms_norm_prologue_matches_add_norm_then_mul_mat(dev, n, k, m):
