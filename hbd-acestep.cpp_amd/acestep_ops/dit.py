@@ -81,14 +81,40 @@ class DiTLayer:
         """The rope positions: 0..S-1 for each of the N sequences (dit-graph.h:186-195)."""
         return DTensor.from_numpy(np.tile(np.arange(S, dtype=np.int32), N))
 
-    def forward(self, hidden, adaln, pos, sa_mask=None, enc=None, ca_mask=None, out=None):
+    def encode(self, enc):
+        """The cross attention's K and V of the encoder states enc (N, enc_S, H) F32: the
+        fused K/V product, the per-head K norm and both F16 casts (dit-graph.h:302-307,
+        326-330, 338-343), as (k16, v16), each (N, enc_S, Nkv, D) F16. The encoder states
+        are the same for every sampler step, so a caller may compute these once per
+        generation and pass them to forward as enc_kv (the reference recomputes them in
+        every step's graph; the values are the same). The tensors are the layer's own
+        buffers: the next encode overwrites them."""
+        if not self.cross:
+            raise ValueError("encode: the layer has no cross-attention weights")
+        Nkv, D, H = self.Nkv, self.D, self.H
+        st = self.stream
+        N, E = enc.shape[0], enc.shape[1]
+        e2 = enc.view(N * E, H)
+        kvc = ops.mul_mat_q8_0(self.w["ca_kv"], e2, out=self._buf("ca_kv", (N * E, 2 * Nkv * D)),
+                               workspace=self._ws("ca_kv", e2), stream=st)
+        kn = ops.rms_norm(kvc[:, 0:Nkv * D].unflatten(1, (Nkv, D)), self.eps, w=self.ca_k_norm_w,
+                          out=self._buf("ca_kn", (N * E, Nkv, D)), stream=st)
+        k16 = ops.cpy(kn, self._buf("ca_k16", (N * E, Nkv, D), "f16"), stream=st)
+        v16 = ops.cpy(kvc[:, Nkv * D:2 * Nkv * D].unflatten(1, (Nkv, D)), self._buf("ca_v16", (N * E, Nkv, D), "f16"),
+                      stream=st)
+        return k16.view(N, E, Nkv, D), v16.view(N, E, Nkv, D)
+
+    def forward(self, hidden, adaln, pos, sa_mask=None, enc=None, ca_mask=None, out=None, enc_kv=None):
         """hidden (N, S, H) F32 -> new hidden (N, S, H); adaln (6, H) F32; pos from
-        positions(N, S); enc (N, enc_S, H) F32 when the layer has cross attention."""
+        positions(N, S); for a layer with cross attention, the encoder states enc (N,
+        enc_S, H) F32, or their K and V from encode() as enc_kv."""
         N, S, H = hidden.shape
         Nh, Nkv, D, I = self.Nh, self.Nkv, self.D, self.I
         st = self.stream
-        if self.cross != (enc is not None):
-            raise ValueError("enc is given exactly when the layer has cross-attention weights")
+        if enc is not None and enc_kv is not None:
+            raise ValueError("give enc or enc_kv, not both")
+        if self.cross != (enc is not None or enc_kv is not None):
+            raise ValueError("enc (or enc_kv) is given exactly when the layer has cross-attention weights")
         T = N * S
         h2 = hidden.view(T, H)
         shift_sa, scale_sa, gate_sa, shift_ffn, scale_ffn, gate_ffn = (adaln[i] for i in range(6))
@@ -114,7 +140,7 @@ class DiTLayer:
             h1, qc = ops.mul_mat_q8_0_adaln(self.w["ca_q"], h2, self.ca_norm_w, self.eps, b=sa_out, gate=gate_sa,
                                             out_sum=self._buf("h1", (T, H)), out=self._buf("ca_q", (T, Nh * D)),
                                             workspace=self._ws("ca_q", h2), stream=st)
-            ca_out = self._cross(qc, enc, ca_mask, N, S)
+            ca_out = self._cross(qc, enc_kv if enc_kv is not None else self.encode(enc), ca_mask, N, S)
             # the cross-attention residual, the FFN norm -> modulate and the gate/up product in one call
             h2b, gu = ops.mul_mat_q8_0_adaln(self.w["gu"], h1, self.mlp_norm_w, self.eps, b=ca_out, scale=scale_ffn,
                                              shift=shift_ffn, out_sum=self._buf("h2", (T, H)),
@@ -132,24 +158,19 @@ class DiTLayer:
         ops.gated_add(h2b, ffn, gate_ffn, out=y, stream=st)
         return y.view(N, S, H)
 
-    def _cross(self, qc, enc, ca_mask, N: int, S: int):
+    def _cross(self, qc, enc_kv, ca_mask, N: int, S: int):
         """Cross attention of the layer's rows (their Q product qc (T, Nh * D)) over the
-        encoder states: its O product (T, H)."""
+        encoder K and V (from encode): its O product (T, H)."""
         Nh, Nkv, D, H = self.Nh, self.Nkv, self.D, self.H
         st = self.stream
         T = N * S
-        E = enc.shape[1]
-        e2 = enc.view(N * E, H)
-        kvc = ops.mul_mat_q8_0(self.w["ca_kv"], e2, out=self._buf("ca_kv", (N * E, 2 * Nkv * D)),
-                               workspace=self._ws("ca_kv", e2), stream=st)
+        k16, v16 = enc_kv
+        E = k16.shape[1]
+        if k16.shape != (N, E, Nkv, D) or v16.shape != (N, E, Nkv, D):
+            raise ValueError(f"enc_kv: K and V (N={N}, enc_S, {Nkv}, {D}) F16")
         qn = ops.rms_norm(qc.unflatten(1, (Nh, D)), self.eps, w=self.ca_q_norm_w,
                           out=self._buf("ca_qn", (T, Nh, D)), stream=st)
-        kn = ops.rms_norm(kvc[:, 0:Nkv * D].unflatten(1, (Nkv, D)), self.eps, w=self.ca_k_norm_w,
-                          out=self._buf("ca_kn", (N * E, Nkv, D)), stream=st)
-        k16 = ops.cpy(kn, self._buf("ca_k16", (N * E, Nkv, D), "f16"), stream=st)
-        v16 = ops.cpy(kvc[:, Nkv * D:2 * Nkv * D].unflatten(1, (Nkv, D)), self._buf("ca_v16", (N * E, Nkv, D), "f16"),
-                      stream=st)
-        attn = self._fa("ca", qn.view(N, S, Nh, D).permute(0, 2, 1, 3), k16.view(N, E, Nkv, D).permute(0, 2, 1, 3),
-                        v16.view(N, E, Nkv, D).permute(0, 2, 1, 3), ca_mask, self._buf("ca_attn", (N, S, Nh, D)))
+        attn = self._fa("ca", qn.view(N, S, Nh, D).permute(0, 2, 1, 3), k16.permute(0, 2, 1, 3),
+                        v16.permute(0, 2, 1, 3), ca_mask, self._buf("ca_attn", (N, S, Nh, D)))
         return ops.mul_mat_q8_0(self.w["ca_o"], attn.view(T, Nh * D), out=self._buf("ca_out", (T, H)),
                                 workspace=self._ws("ca_o", attn.view(T, Nh * D)), stream=st)

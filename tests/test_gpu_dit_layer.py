@@ -138,6 +138,35 @@ def test_dit_layer_stage_by_stage(dev, size, cross, window):
     assert np.all(np.isfinite(y))
 
 
+def test_dit_layer_encoder_kv_once(dev):
+    """The cross attention's K and V computed once (DiTLayer.encode) and reused over two
+    steps give the same layer outputs, bit for bit, as recomputing them from the
+    encoder states in each step."""
+    print("dit layer encoder K/V once", flush=True)
+    r = np.random.default_rng(61)
+    H, Nh, Nkv, D, I, S, N, E = SIZES["small"]
+    q8 = lambda a: ops.Q8(to_dev(a))  # noqa: E731
+    nw = lambda n: to_dev((1 + 0.1 * r.standard_normal(n)).astype(np.float32))  # noqa: E731
+    layer = DiTLayer(q8(_w(r, (Nh + 2 * Nkv) * D, H)), q8(_w(r, H, Nh * D)), q8(_w(r, 2 * I, H)), q8(_w(r, H, I)),
+                     nw(H), nw(H), nw(D), nw(D), H, Nh, Nkv, D, I, w_ca_q=q8(_w(r, Nh * D, H)),
+                     w_ca_kv=q8(_w(r, 2 * Nkv * D, H)), w_ca_o=q8(_w(r, H, Nh * D)), ca_norm_w=nw(H),
+                     ca_q_norm_w=nw(D), ca_k_norm_w=nw(D))
+    enc = to_dev((r.standard_normal((N, E, H)) * 0.8).astype(np.float32))
+    ca_m = np.zeros((N, 1, S, E), np.float32)
+    ca_m[0, :, :, E - 5:] = -np.inf
+    cmask = _f16_mask(ca_m)
+    pos = DiTLayer.positions(N, S)
+    adaln = to_dev((0.3 * r.standard_normal((6, H))).astype(np.float32))
+    steps = [to_dev((r.standard_normal((N, S, H)) * 0.8).astype(np.float32)) for _ in range(2)]
+    ref = [to_np(layer.forward(h, adaln, pos, enc=enc, ca_mask=cmask)) for h in steps]
+    kv = layer.encode(enc)
+    for h, y_ref in zip(steps, ref):
+        y = to_np(layer.forward(h, adaln, pos, ca_mask=cmask, enc_kv=kv))
+        assert np.array_equal(y, y_ref)
+    with pytest.raises(ValueError):
+        layer.forward(steps[0], adaln, pos, enc=enc, ca_mask=cmask, enc_kv=kv)
+
+
 def test_dit_layer_rejects_cross_mismatch(dev):
     """enc must be given exactly when the layer holds cross-attention weights."""
     r = np.random.default_rng(3)
