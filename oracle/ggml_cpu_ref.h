@@ -5,7 +5,7 @@
  * arithmetic that acestep.cpp's graph builders invoke (ggml itself is an
  * empty submodule in the reference checkout, so it cannot be built here).
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load this library, and only as the checker or the timed CPU baseline --
+ * load this library, and only as the parity reference or the timed CPU baseline --
  * never as part of the product path.
  *
  * Every function is one ggml graph node, computed the way ggml-cpu computes

@@ -3,7 +3,7 @@
 numpy front end over ``oracle/_build/liborc.so`` (plain-C restatement of the
 ggml-cpu arithmetic, ``oracle/ggml_cpu_ref.c``). Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg may import
-this module, and only as the checker or the timed CPU baseline.
+this module, and only as the parity reference or the timed CPU baseline.
 
 Each primitive below is one ggml graph node. The chain functions at the end
 call them in the order the reference's graph builders emit them, citing the
@@ -42,7 +42,7 @@ def build() -> str:
 
 
 def use_isa(isa: str) -> str:
-    """Load the x86-64-v3 build ("v3", the checker's) or the x86-64-v4 build
+    """Load the x86-64-v3 build ("v3", the one the tests use) or the x86-64-v4 build
     ("v4", AVX-512) of the same source; only before the first call into it."""
     global _LIB_PATH
     path = os.path.join(_HERE, "_build", "liborc.so" if isa == "v3" else f"liborc_{isa}.so")

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker (CPU only).
+"""Pins the CPU oracle before the tests trust it as their reference (CPU only).
 
 ggml is absent from the reference checkout and the reference's tests hold no
 golden vectors for these ops, so each oracle function is pinned here by
