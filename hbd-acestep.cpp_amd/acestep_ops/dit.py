@@ -22,7 +22,8 @@ Each norm (with the gated or plain residual add before it and the modulate
 after it) runs inside the quantization of the next product's x
 (mi_mul_mat_q8_0_adaln: the normalized rows never go to memory), and the
 SwiGLU inside the quantization of the down product's x
-(mi_mul_mat_q8_0_swiglu). The six AdaLN vectors come in as one F32
+(mi_mul_mat_q8_0_swiglu); QK-norm -> rope writes K and V as F16 in the same
+launch (mi_qk_norm_rope_kv_store). The six AdaLN vectors come in as one F32
 (6, H) tensor: scale_shift_table + the timestep projection (dit-graph.h:384-399),
 rows shift_sa, scale_sa, gate_sa, shift_ffn, scale_ffn, gate_ffn.
 
@@ -76,6 +77,13 @@ class DiTLayer:
         ws = self._buf("ws_fa_" + name, (max(need, 1),), "u8")
         return ops.flash_attn_ext(q, k, v, mask, 1.0 / math.sqrt(self.D), out=out, workspace=ws, stream=self.stream)
 
+    def _seq_inputs(self, N: int):
+        """Each sequence's first slot (0) and set (its index), for the K/V store."""
+        key = ("seq", N)
+        if key not in self._bufs:
+            self._bufs[key] = (DTensor.from_numpy(np.zeros(N, np.int32)), DTensor.from_numpy(np.arange(N, dtype=np.int32)))
+        return self._bufs[key]
+
     @staticmethod
     def positions(N: int, S: int) -> DTensor:
         """The rope positions: 0..S-1 for each of the N sequences (dit-graph.h:186-195)."""
@@ -126,13 +134,16 @@ class DiTLayer:
         q = qkv[:, 0:Nh * D].unflatten(1, (Nh, D))
         k = qkv[:, Nh * D:(Nh + Nkv) * D].unflatten(1, (Nkv, D))
         v = qkv[:, (Nh + Nkv) * D:qkv_dim].unflatten(1, (Nkv, D))
-        qo, ko = ops.qk_norm_rope(q, self.sa_q_norm_w, pos, self.eps, D, self.theta, k=k, k_w=self.sa_k_norm_w,
-                                  q_out=self._buf("qo", (T, Nh, D)), k_out=self._buf("ko", (T, Nkv, D)), stream=st)
-        k16 = ops.cpy(ko, self._buf("k16", (T, Nkv, D), "f16"), stream=st)
-        v16 = ops.cpy(v, self._buf("v16", (T, Nkv, D), "f16"), stream=st)
-        # (N, heads, S, D) views, ggml's permute(x, 0, 2, 1, 3) (dit-graph.h:206-208)
-        attn = self._fa("sa", qo.view(N, S, Nh, D).permute(0, 2, 1, 3), k16.view(N, S, Nkv, D).permute(0, 2, 1, 3),
-                        v16.view(N, S, Nkv, D).permute(0, 2, 1, 3), sa_mask, self._buf("attn", (N, S, Nh, D)))
+        # QK-norm -> rope and the F16 casts of K and V in one launch: K and V go to
+        # F16 tensors laid out as a KV cache, (N, Nkv, S, D) with sequence b's token t
+        # at slot t of set b -- the (N, heads, S, D) order flash attention reads
+        # (ggml's permute(x, 0, 2, 1, 3), dit-graph.h:206-208)
+        k16, v16 = self._buf("k16", (N, Nkv, S, D), "f16"), self._buf("v16", (N, Nkv, S, D), "f16")
+        qo = ops.qk_norm_rope_kv_store(q, self.sa_q_norm_w, k, self.sa_k_norm_w, v, pos, self.eps, D, self.theta,
+                                       k16, v16, self._seq_inputs(N)[0], sets=self._seq_inputs(N)[1],
+                                       q_out=self._buf("qo", (T, Nh, D)), stream=st)
+        attn = self._fa("sa", qo.view(N, S, Nh, D).permute(0, 2, 1, 3), k16, v16, sa_mask,
+                        self._buf("attn", (N, S, Nh, D)))
         sa_out = ops.mul_mat_q8_0(self.w["sa_o"], attn.view(T, Nh * D), out=self._buf("sa_out", (T, H)),
                                   workspace=self._ws("sa_o", attn.view(T, Nh * D)), stream=st)
         if self.cross:

@@ -75,7 +75,7 @@ def test_dit_layer_stage_by_stage(dev, size, cross, window):
     pos = np.tile(np.arange(S, dtype=np.int32), N)
     y = to_np(layer.forward(to_dev(hidden), to_dev(adaln), DiTLayer.positions(N, S), sa_mask=_f16_mask(sa_m),
                             enc=to_dev(enc) if cross else None, ca_mask=_f16_mask(ca_m) if cross else None))
-    b = {k: to_np(v) for k, v in layer._bufs.items() if not k.startswith("ws")}
+    b = {k: to_np(v) for k, v in layer._bufs.items() if isinstance(k, str) and not k.startswith("ws")}
     h2 = hidden.reshape(T, H)
     scale = 1.0 / np.sqrt(D)
     mfma = "prefill" if S * (Nh // Nkv) >= 64 else False
@@ -98,12 +98,21 @@ def test_dit_layer_stage_by_stage(dev, size, cross, window):
     q = qkv[:, :Nh * D].reshape(T, Nh, D)
     k = qkv[:, Nh * D:(Nh + Nkv) * D].reshape(T, Nkv, D)
     v = qkv[:, (Nh + Nkv) * D:].reshape(T, Nkv, D)
+    # (the roped K, which the fused launch sends only to its F16 copy, recomputed by
+    # mi_qk_norm_rope on the layer's QKV buffer: the fused launch equals it bit for bit)
+    dq = layer._bufs["qkv"]
+    _, ko = ops.qk_norm_rope(dq[:, :Nh * D].unflatten(1, (Nh, D)), to_dev(nw["qn"]), to_dev(pos), eps, D, theta,
+                             k=dq[:, Nh * D:(Nh + Nkv) * D].unflatten(1, (Nkv, D)), k_w=to_dev(nw["kn"]))
+    ko = to_np(ko)
     assert_f32_close(b["qo"], orc.qk_norm_rope(q, nw["qn"], pos, eps, D, theta), row_floor=True)
-    assert_f32_close(b["ko"], orc.qk_norm_rope(k, nw["kn"], pos, eps, D, theta), row_floor=True)
-    assert np.array_equal(b["k16"], orc.f32_to_f16(b["ko"]))
-    assert np.array_equal(b["v16"], orc.f32_to_f16(v))
+    assert_f32_close(ko, orc.qk_norm_rope(k, nw["kn"], pos, eps, D, theta), row_floor=True)
+    # K and V in F16, (N, Nkv, S, D)
+    to_kv = lambda a: a.reshape(N, S, Nkv, D).transpose(0, 2, 1, 3)  # noqa: E731
+    assert np.array_equal(b["k16"], to_kv(orc.f32_to_f16(ko)))
+    assert np.array_equal(b["v16"], to_kv(orc.f32_to_f16(v)))
     # 3. self attention under its mask; the O product
-    attention("attn", b["qo"], b["k16"], b["v16"], S, sa_m)
+    attention("attn", b["qo"], np.ascontiguousarray(b["k16"].transpose(0, 2, 1, 3)),
+              np.ascontiguousarray(b["v16"].transpose(0, 2, 1, 3)), S, sa_m)
     assert_mul_mat_q8_0(b["sa_out"], W["sa_o"], b["attn"].reshape(T, Nh * D))
     if cross:
         # 4. the gated residual (bit-exact), the cross-attention norm and the cross Q
