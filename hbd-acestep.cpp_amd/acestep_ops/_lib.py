@@ -128,6 +128,8 @@ PROTOTYPES = {
                                _VP],
     "mi_mul_mat_q8_0_swiglu_add": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, ctypes.c_int, _TP, ctypes.c_int, _F, _F,
                                    _TP, _VP, ctypes.c_size_t, _VP],
+    "mi_mul_mat_q8_0_swiglu_gated_add": [_VP, ctypes.c_int64, ctypes.c_int64, _TP, ctypes.c_int, _TP, _TP, _TP, _VP,
+                                         ctypes.c_size_t, _VP],
     "mi_apg_buffer_bytes": [_TP, ctypes.POINTER(ctypes.c_size_t)],
     "mi_apg_forward": [_TP, _TP, _F, _F, _F, _VP, ctypes.c_size_t, _I, _TP, _VP],
     "mi_flow_step": [_I, _TP, _TP, _F, _F, _I, _TP, _TP, _VP],

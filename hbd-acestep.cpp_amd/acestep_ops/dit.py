@@ -21,8 +21,8 @@ dit_ggml_build_cross_attn, 274-354, and the MLP of dit_ggml_build_mlp, 249-268):
 Each norm (with the gated or plain residual add before it and the modulate
 after it) runs inside the quantization of the next product's x
 (mi_mul_mat_q8_0_adaln: the normalized rows never go to memory), and the
-SwiGLU inside the quantization of the down product's x
-(mi_mul_mat_q8_0_swiglu); QK-norm -> rope writes K and V as F16 in the same
+SwiGLU inside the quantization of the down product's x with the last gated
+residual where its outputs are formed (mi_mul_mat_q8_0_swiglu_gated_add); QK-norm -> rope writes K and V as F16 in the same
 launch (mi_qk_norm_rope_kv_store). The six AdaLN vectors come in as one F32
 (6, H) tensor: scale_shift_table + the timestep projection (dit-graph.h:384-399),
 rows shift_sa, scale_sa, gate_sa, shift_ffn, scale_ffn, gate_ffn.
@@ -161,12 +161,12 @@ class DiTLayer:
             h2b, gu = ops.mul_mat_q8_0_adaln(self.w["gu"], h2, self.mlp_norm_w, self.eps, b=sa_out, gate=gate_sa,
                                              scale=scale_ffn, shift=shift_ffn, out_sum=self._buf("h2", (T, H)),
                                              out=self._buf("gu", (T, 2 * I)), workspace=self._ws("gu", h2), stream=st)
-        # the MLP: SwiGLU inside the down product's quantization
+        # the MLP: SwiGLU inside the down product's quantization, the gated residual
+        # where the product's outputs are formed
         need = ops.mul_mat_q8_0_swiglu_workspace(self.w["down"], gu)
-        ffn = ops.mul_mat_q8_0_swiglu(self.w["down"], gu, out=self._buf("ffn", (T, H)),
-                                      workspace=self._buf("ws_down", (max(need, 1),), "u8"), stream=st)
         y = out.view(T, H) if out is not None else self._buf("out", (T, H))
-        ops.gated_add(h2b, ffn, gate_ffn, out=y, stream=st)
+        ops.mul_mat_q8_0_swiglu_gated_add(self.w["down"], gu, h2b, gate_ffn, out=y,
+                                          workspace=self._buf("ws_down", (max(need, 1),), "u8"), stream=st)
         return y.view(N, S, H)
 
     def _cross(self, qc, enc_kv, ca_mask, N: int, S: int):

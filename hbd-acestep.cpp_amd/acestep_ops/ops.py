@@ -309,6 +309,22 @@ def mul_mat_q8_0_swiglu_add(w: Q8R64, gu, r, clamp=None, swapped: bool = False, 
     return y
 
 
+def mul_mat_q8_0_swiglu_gated_add(w: Q8R64, gu, r, gate, swapped: bool = False, out=None, workspace=None,
+                                  stream=None):
+    """r + ggml_mul_mat(w, ggml_swiglu(gu)) * gate in one call (the DiT's gated
+    residual after the MLP): bit-identical to mul_mat_q8_0_swiglu followed by gated_add."""
+    y = _out(out, tuple(gu.shape[:-1]) + (w.n,), "f32")
+    need = mul_mat_q8_0_swiglu_workspace(w, gu)
+    ws = workspace
+    if need and ws is None:
+        ws = DTensor.empty((need,), "u8")
+    wp = ctypes.c_void_p(ws.ptr) if ws is not None else None
+    wn = ws.numel() * ws.es if ws is not None else 0
+    _lib.call("mi_mul_mat_q8_0_swiglu_gated_add", ctypes.c_void_p(w.data.ptr), w.k, w.n, _p(gu), int(bool(swapped)),
+              _p(r), _p(gate), _p(y), wp, wn, _s(stream))
+    return y
+
+
 def mul_mat_q8_0_swiglu(w: Q8R64, gu, swapped: bool = False, out=None, workspace=None, stream=None):
     """ggml_mul_mat(w, ggml_swiglu(gu)) in one call: gu F32 (m, 2k) -> F32 (m, n),
     bit-identical to swiglu followed by mul_mat_q8_0."""

@@ -1138,14 +1138,30 @@ int mi_mul_mat_q8_0_swiglu(const void * w, int64_t k, int64_t n, const mi_tensor
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 
-int mi_mul_mat_q8_0_swiglu_add(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
-                               const mi_tensor * r, int clamp, float lo, float hi, const mi_tensor * y, void * workspace,
-                               size_t workspace_bytes, mi_stream stream) {
+// an F32 vector of k contiguous elements (the norm weight, a gate, a modulate scale or shift)
+static int mm_vec(const mi_tensor * v, int64_t k) {
+    MI_TRY(check(v));
+    if (v->type != MI_TYPE_F32) {
+        return MI_ERR_TYPE;
+    }
+    if (v->ne[0] != k || nrows(*v) != 1 || v->nb[0] != 4) {
+        return MI_ERR_SHAPE;
+    }
+    return MI_OK;
+}
+
+static int mm_swiglu_res(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped, const mi_tensor * r,
+                         const mi_tensor * gate, int clamp, float lo, float hi, const mi_tensor * y, void * workspace,
+                         size_t workspace_bytes, mi_stream stream) {
     if (!y || !r) {
         return MI_ERR_NULL;
     }
     MmvArgs a;
     MI_TRY(mm_glu_desc(w, k, n, gu, swapped, y, a));
+    if (gate) {
+        MI_TRY(mm_vec(gate, n));
+        a.rgate = (const float *) gate->data;
+    }
     MI_TRY(check(r));
     if (r->type != MI_TYPE_F32) {
         return MI_ERR_TYPE;
@@ -1180,17 +1196,21 @@ int mi_mul_mat_q8_0_swiglu_add(const void * w, int64_t k, int64_t n, const mi_te
     return finish(launch_mul_mat_q8_0(a, (hipStream_t) stream));
 }
 
-// an F32 vector of k contiguous elements (the norm weight, a gate, a modulate scale or shift)
-static int mm_vec(const mi_tensor * v, int64_t k) {
-    MI_TRY(check(v));
-    if (v->type != MI_TYPE_F32) {
-        return MI_ERR_TYPE;
-    }
-    if (v->ne[0] != k || nrows(*v) != 1 || v->nb[0] != 4) {
-        return MI_ERR_SHAPE;
-    }
-    return MI_OK;
+int mi_mul_mat_q8_0_swiglu_add(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
+                               const mi_tensor * r, int clamp, float lo, float hi, const mi_tensor * y, void * workspace,
+                               size_t workspace_bytes, mi_stream stream) {
+    return mm_swiglu_res(w, k, n, gu, swapped, r, nullptr, clamp, lo, hi, y, workspace, workspace_bytes, stream);
 }
+
+int mi_mul_mat_q8_0_swiglu_gated_add(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
+                                     const mi_tensor * r, const mi_tensor * gate, const mi_tensor * y, void * workspace,
+                                     size_t workspace_bytes, mi_stream stream) {
+    if (!gate) {
+        return MI_ERR_NULL;
+    }
+    return mm_swiglu_res(w, k, n, gu, swapped, r, gate, 0, 0.0f, 0.0f, y, workspace, workspace_bytes, stream);
+}
+
 
 static int mm_norm(const void * w, int64_t k, int64_t n, const mi_tensor * x, const mi_tensor * b,
                    const mi_tensor * norm_w, float eps, const mi_tensor * sum, const mi_tensor * y, void * workspace,

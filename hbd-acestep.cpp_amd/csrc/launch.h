@@ -209,6 +209,7 @@ struct MmvArgs {
     int64_t      res1;         // then clamped to [rlo, rhi] when rclamp (ggml_clamp)
     int          rclamp;
     float        rlo, rhi;
+    const float * rgate;       // non-null (with res): y = res + y * rgate[n] (the DiT's gated residual)
     char *       xq;           // workspace: quantized x [m][k]
     float *      xd;           //            scales [m][nbk]
     float *      part;         //            partials [splits][m][npad] (splits > 1)

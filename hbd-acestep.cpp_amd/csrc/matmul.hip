@@ -376,6 +376,9 @@ __global__ void __launch_bounds__(256) k_mmv_quant_x_norm8(const MmvArgs a) {
 // as the separate add; the add is commutative, so the operand order is ggml's)
 __device__ __forceinline__ float mm_epilogue(const MmvArgs & a, uint32_t m, uint32_t n, float v) {
     if (a.res != nullptr) {
+        if (a.rgate) {
+            v = v * a.rgate[n];  // ggml_add(res, ggml_mul(product, gate)): the product rounded first
+        }
         v = v + *(const float *) (a.res + (int64_t) m * a.res1 + (int64_t) n * 4);
         if (a.rclamp) {
             v = clamp_ggml(v, a.rlo, a.rhi);
@@ -390,7 +393,10 @@ __device__ __forceinline__ float mm_epilogue(const MmvArgs & a, uint32_t m, uint
 __device__ __forceinline__ float mm_res(const MmvArgs & a, uint32_t m, uint32_t n) {
     return *(const float *) (a.res + (int64_t) m * a.res1 + (int64_t) n * 4);
 }
-__device__ __forceinline__ float mm_add_res(const MmvArgs & a, float v, float r) {
+__device__ __forceinline__ float mm_add_res(const MmvArgs & a, float v, float r, uint32_t n) {
+    if (a.rgate) {
+        v = v * a.rgate[n];
+    }
     v = v + r;
     return a.rclamp ? clamp_ggml(v, a.rlo, a.rhi) : v;
 }
@@ -493,7 +499,7 @@ __global__ void __launch_bounds__(512) k_mmv_q8_0(const MmvArgs a) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 if (row < a.n) {
-                    *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = mm_add_res(a, acc[m], r[m]);
+                    *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) row * 4) = mm_add_res(a, acc[m], r[m], row);
                 }
             }
             return;
@@ -735,7 +741,7 @@ __global__ void __launch_bounds__(256) k_mmq_q8_0(const MmvArgs a) {
                     if (m < a.m) {
                         const float v = acc[i][j][4 * q + e];
                         *(float *) (a.y + (int64_t) m * a.y1 + (int64_t) n * 4) =
-                            a.res != nullptr ? mm_add_res(a, v, r[4 * q + e]) : v;
+                            a.res != nullptr ? mm_add_res(a, v, r[4 * q + e], n) : v;
                     }
                 }
             }

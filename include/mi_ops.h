@@ -326,6 +326,15 @@ int mi_mul_mat_q8_0_swiglu_add(const void * w, int64_t k, int64_t n, const mi_te
                                const mi_tensor * r, int clamp, float lo, float hi, const mi_tensor * y, void * workspace,
                                size_t workspace_bytes, mi_stream stream);
 
+/* The DiT's MLP tail as one call: y = r + ggml_mul_mat(w, ggml_swiglu(gu)) *
+ * gate (dit_ggml_gated_add after dit_ggml_build_mlp, dit-graph.h:439-440, 68-76:
+ * the product multiplied by the F32 [n] gate vector, rounded, then added to r),
+ * bit-identical to mi_mul_mat_q8_0_swiglu followed by mi_gated_add. Operands and
+ * workspace as mi_mul_mat_q8_0_swiglu_add (without the clamp); y may be r. */
+int mi_mul_mat_q8_0_swiglu_gated_add(const void * w, int64_t k, int64_t n, const mi_tensor * gu, int swapped,
+                                     const mi_tensor * r, const mi_tensor * gate, const mi_tensor * y, void * workspace,
+                                     size_t workspace_bytes, mi_stream stream);
+
 /* The RMSNorm -> product pair as one call: y = ggml_mul_mat(w,
  * ggml_mul(ggml_rms_norm(x, eps), norm_w)) (qwen3-lm.h:632-639, the input norm
  * feeding the fused QKV projection; qwen3_rms_norm, qwen3-enc.h:114-120). x F32

@@ -310,6 +310,14 @@ def test_mul_mat_q8_0_validation():
     assert mr(W, k, n, R(gu), 0, R(r), 1, hi, lo, R(y), None, 0, NULL_S) == -6     # lo > hi
     assert mr(W, k, n, R(gu), 0, R(r), 1, lo, hi, R(y), ctypes.c_void_p(1 << 20), wsn - 1, NULL_S) == -6
     assert mr(W, k, n, R(gu), 0, R(r), 1, lo, hi, R(y), ctypes.c_void_p((1 << 20) + 16), wsn, NULL_S) == -5
+    # with the gated residual: gate F32 [n]
+    mgg = L.mi_mul_mat_q8_0_swiglu_gated_add
+    gv = _t([n])
+    assert mgg(W, k, n, R(gu), 0, R(r), None, R(y), None, 0, NULL_S) == -1
+    assert mgg(W, k, n, R(gu), 0, None, R(gv), R(y), None, 0, NULL_S) == -1
+    assert mgg(W, k, n, R(gu), 0, R(r), R(_t([n + 1])), R(y), None, 0, NULL_S) == -3
+    assert mgg(W, k, n, R(gu), 0, R(r), R(_t([n], BF16)), R(y), None, 0, NULL_S) == -2
+    assert mgg(W, k, n, R(gu), 0, R(r), R(gv), R(y), ctypes.c_void_p(1 << 20), wsn - 1, NULL_S) == -6
 
 
 def test_sampler_validation():

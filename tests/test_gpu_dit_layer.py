@@ -135,15 +135,17 @@ def test_dit_layer_stage_by_stage(dev, size, cross, window):
     else:
         hf = orc.gated_add(h2, b["sa_out"], gate_sa)
     assert np.array_equal(b["h2"], hf)
-    # 7. the FFN norm -> modulate -> gate/up (one call); the down product on the
-    # device's SwiGLU values (the prologue quantizes silu(g)*u as mi_swiglu computes
-    # it, within ~1 ulp of the oracle's)
+    # 7. the FFN norm -> modulate -> gate/up (one call); the down product (recomputed
+    # by mi_mul_mat_q8_0_swiglu, which the layer's fused call equals before its gated
+    # add) on the device's SwiGLU values (the prologue quantizes silu(g)*u as mi_swiglu
+    # computes it, within ~1 ulp of the oracle's)
     assert_mul_mat_q8_0(b["gu"], W["gu"], orc.rms_norm_modulate(hf, nw["mlp"], scale_ff, shift_ff, eps))
     sw = to_np(ops.swiglu(layer._bufs["gu"]))
     assert_f32_close(sw, orc.swiglu(b["gu"]))
-    assert_mul_mat_q8_0(b["ffn"], W["down"], sw)
+    mlp = to_np(ops.mul_mat_q8_0_swiglu(layer.w["down"], layer._bufs["gu"]))
+    assert_mul_mat_q8_0(mlp, W["down"], sw)
     # 8. the last gated residual, bit-exact
-    assert np.array_equal(y.reshape(T, H), orc.gated_add(hf, b["ffn"], gate_ff))
+    assert np.array_equal(y.reshape(T, H), orc.gated_add(hf, mlp, gate_ff))
     assert np.all(np.isfinite(y))
 
 

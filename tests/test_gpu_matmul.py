@@ -189,6 +189,31 @@ def test_swiglu_down_with_residual_add(dev, n, k, m, clamp, inplace):
         assert (np.abs(res) > 65504.0).any() and np.abs(y_f).max() <= 65504.0
 
 
+@pytest.mark.parametrize("n,k,m,inplace", [
+    (2048, 6144, 8, False),     # decode kernel: splits added in LDS, the gate in the store
+    (2048, 6144, 8, True),
+    (640, 256, 129, False),     # the matrix kernel
+    (2048, 6144, 200, True),    # the matrix kernel with key splits: the gate in the split sum
+    (16448, 256, 4, False),     # 257 row groups
+])
+def test_swiglu_down_with_gated_add(dev, n, k, m, inplace):
+    """mi_mul_mat_q8_0_swiglu_gated_add against mi_mul_mat_q8_0_swiglu then
+    mi_gated_add: bit-identical on every path that forms the product's sum."""
+    print(f"mul_mat q8_0 swiglu + gated add n={n} k={k} m={m} inplace={inplace}", flush=True)
+    r = np.random.default_rng(n + k + m + 7)
+    w = orc.quantize_q8_0((r.standard_normal((n, k)) * 0.05).astype(np.float32))
+    gu = (r.standard_normal((m, 2 * k)) * 2.0).astype(np.float32)
+    res = r.standard_normal((m, n)).astype(np.float32)
+    gate = (0.7 * r.standard_normal(n)).astype(np.float32)
+    wr = ops.q8_0_repack(ops.Q8(to_dev(w)))
+    dgu, dres, dg = to_dev(gu), to_dev(res), to_dev(gate)
+    y_f = to_np(ops.mul_mat_q8_0_swiglu_gated_add(wr, dgu, dres, dg, out=dres if inplace else None))
+    mlp = ops.mul_mat_q8_0_swiglu(wr, dgu)
+    y_u = to_np(ops.gated_add(to_dev(res), mlp, dg))
+    assert np.array_equal(y_f, y_u)
+    assert np.array_equal(y_u, orc.gated_add(res, to_np(mlp), gate))
+
+
 def test_swiglu_prologue_strided_rows(dev):
     """gu rows at a stride that is not a multiple of 16 bytes (element loads)."""
     print("mul_mat q8_0 swiglu strided", flush=True)
