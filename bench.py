@@ -1172,7 +1172,8 @@ def prefill_layer_bench_kv(steps: int, kv_type: str, N: int = 2, S: int = 512, S
 # (all zero) on the odd ones (dit-sampler.h:253-274). A graph of `steps` layer
 # calls, replayed once untimed and once timed.
 # ---------------------------------------------------------------------------
-def dit_layer_bench(steps: int):
+def dit_layer_bench(steps: int, emit: bool = True):
+    """One JSON line per (mask, encoder K/V) variant, or (emit False) their figures as a list."""
     from acestep_ops import device, ops
     from acestep_ops.device import DTensor, Event, Graph, Stream
     from acestep_ops.dit import DiTLayer
@@ -1210,6 +1211,7 @@ def dit_layer_bench(steps: int):
     gemm = 2 * T * sum(w.n * w.k for name, w in layer.w.items() if name != "ca_kv") + \
         2 * N * E * layer.w["ca_kv"].n * layer.w["ca_kv"].k
     ca_pairs = 4 * D * Nh * N * S * (E - 40)
+    results = []
     kv = layer.encode(enc)  # the encoder K/V once, for the runs that reuse them
     st.synchronize()
     for (label, mk, live), once in ((m, o) for m in ((f"sliding window {WIN}", wmask, None),
@@ -1235,16 +1237,20 @@ def dit_layer_bench(steps: int):
         pairs = S * S if live else sum(min(S, i + WIN // 2 + 1) - max(0, i - WIN // 2) for i in range(S))
         sa = 4 * D * Nh * N * pairs
         fl = gemm - (2 * N * E * layer.w["ca_kv"].n * layer.w["ca_kv"].k if once else 0) + sa + ca_pairs
-        print(json.dumps({"config": f"DiT layer, S={S} x {N}, H={H}, {Nh}/{Nkv} heads x {D}, I={I}, Q8_0 weights, "
-                                    f"F32 activations, self attention under the {label}, cross attention over {E} "
-                                    "encoder rows (40 padding), the encoder K/V "
-                                    + ("computed once per generation" if once else "recomputed in the step")
-                                    + ", every op on the device",
-                          "us_per_layer": round(us, 1), "gemm_flop": gemm, "attn_flop_live": sa + ca_pairs,
-                          "TFLOP/s": round(fl / (us * 1e-6) / 1e12, 1)}), flush=True)
+        rec = {"config": f"DiT layer, S={S} x {N}, H={H}, {Nh}/{Nkv} heads x {D}, I={I}, Q8_0 weights, "
+                         f"F32 activations, self attention under the {label}, cross attention over {E} "
+                         "encoder rows (40 padding), the encoder K/V "
+                         + ("computed once per generation" if once else "recomputed in the step")
+                         + ", every op on the device",
+               "us_per_layer": round(us, 1), "gemm_flop": gemm, "attn_flop_live": sa + ca_pairs,
+               "TFLOP/s": round(fl / (us * 1e-6) / 1e12, 1)}
+        if emit:
+            print(json.dumps(rec), flush=True)
+        results.append(rec)
         del g
     del layer
     device.synchronize()
+    return results
 
 
 def main():
@@ -1255,7 +1261,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=ROWS, help="rows of the block the CPU baseline runs")
     ap.add_argument("--cpu-reps", type=int, default=64, help="timed CPU repetitions (about 10 s on 8 threads)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-configs", action="store_true", help="leave the Qwen3 layer chains out of the default line")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave the Qwen3 layer chains and the DiT layer out of the default line")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="launch each block kernel once plus a copy of known size, for counter collection")
     ap.add_argument("--pmc-configs", action="store_true",
@@ -1328,6 +1335,9 @@ def main():
     # prefill 4x4096, C5 4B prefill 8x2048 into a Q8_0 KV cache), timed in the
     # same run; they do not enter value
     cfg = None if args.no_configs else configs_bench(min(args.steps, 20), args.warmup, emit=False)
+    # a whole DiT layer (products, attention and the fused ops) over the same run's
+    # clock; it does not enter value
+    ditl = None if args.no_configs else dit_layer_bench(min(args.steps, 10), emit=False)
 
     # HBM bytes per launch of the dominant kernel from the committed counter
     # summary (FETCH_SIZE and WRITE_SIZE, each scaled by a copy of known size)
@@ -1418,6 +1428,7 @@ def main():
                                "sequence on the bench stream (includes ~2.5-3 us of event and dispatch time that "
                                "rocprof's kernel duration leaves out)"},
         "configs": cfg,
+        "dit_layer": ditl,
         "cpu_baseline": cpu,
         "wall_s": round(wall, 4),
     }
